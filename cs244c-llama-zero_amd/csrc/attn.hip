@@ -1,0 +1,850 @@
+// Causal grouped-query attention, flash style, on CDNA4 matrix cores
+// (reference: model/llama.py:72-133 GroupedQueryAttention.forward with
+// F.scaled_dot_product_attention(is_causal=True), K/V heads shared by
+// H/KV query heads through repeat_interleave).
+//
+// Layouts (elements):
+//   q/k/v : rows b*S + s of ld elements; head h occupies [h*hd, (h+1)*hd).  The
+//           three may be column ranges of one fused QKV projection.
+//   o     : same row layout with H heads.
+//   lse   : [B, H, S] fp32, natural-log log-sum-exp of the scaled scores.
+//   *t    : transposed copies [B, heads, hd, S] (reduction index innermost).
+// The kv head of query head h is h / (H/KV); K/V are never expanded.
+//
+// MFMA tiling (v_mfma_f32_32x32x16_bf16).  The score tile is computed as
+// S^T = K . Q^T so that each lane owns one query column: row statistics need
+// one cross-half shuffle, and the probabilities already sit in the B-operand
+// layout for O^T += V^T . P^T (the k-slots of the two operands are the same
+// permutation of the 16 keys).  The backward splits into a dK/dV pass (one
+// workgroup per 128 keys of a kv head, looping over the query heads of its
+// group and the query blocks at or after the diagonal) and a dQ pass (one
+// workgroup per 128 queries, looping over key blocks up to the diagonal); no
+// atomics, deterministic.
+#include "lz_common.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t ldq, ldk, ldv;
+  uint16_t* o;
+  int64_t ldo;
+  float* lse;
+  const uint16_t* vt;  // fwd: V^T [B,KV,hd,S]
+  // backward
+  const uint16_t* qt;   // [B,H,hd,S]
+  const uint16_t* kt;   // [B,KV,hd,S]
+  const uint16_t* dout; // rows like o
+  int64_t lddo;
+  const uint16_t* dot;  // dO^T [B,H,hd,S]
+  const float* delta;   // [B,H,S] rowsum(dO*O)
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t lddq, lddk, lddv;
+  int B, S, H, KV;
+  float scale;
+};
+
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
+  uint4 w;
+  w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+  w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+  w.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+  w.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+  return __builtin_bit_cast(bf16x8_t, w);
+}
+
+__device__ __forceinline__ bf16x8_t lds_frag16(const char* p) {
+  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
+}
+
+// Two 4-element runs (8 bytes each) -> one 8-element fragment.
+__device__ __forceinline__ bf16x8_t lds_frag_2x4(const char* p0, const char* p1) {
+  const uint2 a = *reinterpret_cast<const uint2*>(p0);
+  const uint2 b = *reinterpret_cast<const uint2*>(p1);
+  return __builtin_bit_cast(bf16x8_t, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+// 8 consecutive elements of a row of length `len` starting at `idx` (multiple
+// of 8), zero outside [0, len).
+__device__ __forceinline__ uint4 load8(const uint16_t* row, int64_t idx, int64_t len) {
+  if (idx + 8 <= len && ((reinterpret_cast<uintptr_t>(row + idx) & 15) == 0))
+    return *reinterpret_cast<const uint4*>(row + idx);
+  uint16_t t[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) t[e] = (idx + e < len) ? row[idx + e] : (uint16_t)0;
+  return make_uint4((uint32_t)t[0] | ((uint32_t)t[1] << 16), (uint32_t)t[2] | ((uint32_t)t[3] << 16),
+                    (uint32_t)t[4] | ((uint32_t)t[5] << 16), (uint32_t)t[6] | ((uint32_t)t[7] << 16));
+}
+
+__device__ __forceinline__ void store_bf16x4(uint16_t* p, float a, float b, float c, float d) {
+  uint2 w;
+  w.x = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  w.y = (uint32_t)f2bf(c) | ((uint32_t)f2bf(d) << 16);
+  *reinterpret_cast<uint2*>(p) = w;
+}
+
+// Row tile [rows][HD] (row stride `rb` bytes) from a [S, ld] row-major source.
+template <int HD, int ROWS, int NT>
+__device__ __forceinline__ void load_rows(char* dst, int rb, const uint16_t* src, int64_t ld, int64_t r0, int64_t nrows,
+                                          int tid) {
+  constexpr int kChunks = ROWS * HD / 8;
+#pragma unroll
+  for (int i = 0; i < (kChunks + NT - 1) / NT; ++i) {
+    const int c = tid + i * NT;
+    if (c < kChunks) {
+      const int row = c / (HD / 8), ch = c % (HD / 8);
+      const int64_t r = r0 + row;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (r < nrows) val = *reinterpret_cast<const uint4*>(src + r * ld + ch * 8);
+      *reinterpret_cast<uint4*>(dst + row * rb + ch * 16) = val;
+    }
+  }
+}
+
+// Transposed tile [HD][COLS] (row stride `rb` bytes, a multiple of 8) from a
+// [HD, S] source, columns c0.. (zero beyond S).
+template <int HD, int COLS, int NT>
+__device__ __forceinline__ void load_trows(char* dst, int rb, const uint16_t* src, int64_t S, int64_t c0, int tid) {
+  constexpr int kChunks = HD * COLS / 8;
+#pragma unroll
+  for (int i = 0; i < (kChunks + NT - 1) / NT; ++i) {
+    const int c = tid + i * NT;
+    if (c < kChunks) {
+      const int row = c / (COLS / 8), ch = c % (COLS / 8);
+      const uint4 val = load8(src + (int64_t)row * S, c0 + ch * 8, S);
+      uint2* d = reinterpret_cast<uint2*>(dst + row * rb + ch * 16);
+      d[0] = make_uint2(val.x, val.y);
+      d[1] = make_uint2(val.z, val.w);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  256 threads; 128 queries per workgroup (32 per wave); 64-key steps.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
+  constexpr int BQ = 128, BKV = 64, NT = 256;
+  constexpr int KROW = HD * 2 + 16;
+  constexpr int VROW = BKV * 2 + 8;
+  __shared__ __attribute__((aligned(16))) char smem[BKV * KROW + HD * VROW];
+  char* Ks = smem;
+  char* Vts = smem + BKV * KROW;
+
+  const int S = a.S, H = a.H, KV = a.KV;
+  const int nqb = (S + BQ - 1) / BQ;
+  const int bh = a.B * H;
+  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
+  const int rem = blockIdx.x % bh;
+  const int b = rem / H, h = rem % H;
+  const int g = h / (H / KV);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
+  const int qrow = qw0 + l32;
+
+  bf16x8_t qf[HD / 16];
+  {
+    const uint16_t* qp = a.q + ((int64_t)b * S + min(qrow, S - 1)) * a.ldq + (int64_t)h * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qp + kk * 16));
+  }
+  f32x16_t o[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float c = a.scale * kLog2e;
+
+  const int kv_end = min(S, q0 + BQ);
+  const int kv_end_w = min(S, qw0 + 32);
+  const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
+  const uint16_t* vtbase = a.vt + (int64_t)(b * KV + g) * HD * S;
+
+  for (int k0 = 0; k0 < kv_end; k0 += BKV) {
+    load_rows<HD, BKV, NT>(Ks, KROW, kbase, a.ldk, k0, S, tid);
+    load_trows<HD, BKV, NT>(Vts, VROW, vtbase, S, k0, tid);
+    __syncthreads();
+    if (k0 < kv_end_w) {
+      f32x16_t s[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; ++kk) {
+          const bf16x8_t af = lds_frag16(Ks + (t * 32 + l32) * KROW + kk * 32 + half * 16);
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[kk], s[t], 0, 0, 0);
+        }
+      }
+      const bool need_mask = (k0 + BKV - 1 > qw0) || (k0 + BKV > S);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = s[t][r] * c;
+          if (need_mask) {
+            const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (kv > qrow || kv >= S) x = -INFINITY;
+          }
+          s[t][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m, mx);
+      const float alpha = exp2f(m - m_new);
+      float rs = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = exp2f(s[t][r] - m_new);
+          s[t][r] = p;
+          rs += p;
+        }
+      rs += __shfl_xor(rs, 32, 64);
+      l = l * alpha + rs;
+      m = m_new;
+#pragma unroll
+      for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+#pragma unroll
+      for (int ks = 0; ks < BKV / 16; ++ks) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = s[ks >> 1][8 * (ks & 1) + e];
+        const bf16x8_t pb = pack_bf16x8(pv);
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i) {
+          const char* row = Vts + (i * 32 + l32) * VROW;
+          const bf16x8_t av = lds_frag_2x4(row + (16 * ks + 4 * half) * 2, row + (16 * ks + 8 + 4 * half) * 2);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb, o[i], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (qrow < S) {
+    const float inv_l = 1.0f / l;
+    uint16_t* op = a.o + ((int64_t)b * S + qrow) * a.ldo + (int64_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(op + hd, o[i][4 * q4] * inv_l, o[i][4 * q4 + 1] * inv_l, o[i][4 * q4 + 2] * inv_l,
+                     o[i][4 * q4 + 3] * inv_l);
+      }
+    if (half == 0) a.lse[((int64_t)b * H + h) * S + qrow] = (m + log2f(l)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, dK/dV pass.  256 threads; 128 keys per workgroup (32 per wave);
+// 64-query steps over every query head of the kv head's group.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(AttnArgs a) {
+  constexpr int BKV = 128, BQ = 64, NT = 256;
+  constexpr int KROW = HD * 2 + 16;
+  constexpr int TROW = BQ * 2 + 8;
+  __shared__ __attribute__((aligned(16))) char smem[2 * BQ * KROW + 2 * HD * TROW + 2 * BQ * 4];
+  char* Qs = smem;
+  char* dOs = Qs + BQ * KROW;
+  char* Qts = dOs + BQ * KROW;
+  char* dOts = Qts + HD * TROW;
+  float* lse2s = reinterpret_cast<float*>(dOts + HD * TROW);
+  float* Ds = lse2s + BQ;
+
+  const int S = a.S, H = a.H, KV = a.KV, rep = H / KV;
+  const int bkv = a.B * KV;
+  const int kvb = blockIdx.x / bkv;
+  const int rem = blockIdx.x % bkv;
+  const int b = rem / KV, g = rem % KV;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int k0 = kvb * BKV, kw0 = k0 + 32 * wave;
+  const int kvrow = kw0 + l32;
+  const float c = a.scale * kLog2e;
+
+  bf16x8_t kf[HD / 16], vf[HD / 16];
+  {
+    const int64_t r = (int64_t)b * S + min(kvrow, S - 1);
+    const uint16_t* kp = a.k + r * a.ldk + (int64_t)g * HD + 8 * half;
+    const uint16_t* vp = a.v + r * a.ldv + (int64_t)g * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      kf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kp + kk * 16));
+      vf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(vp + kk * 16));
+    }
+  }
+  f32x16_t dk[HD / 32], dv[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[i][r] = 0.f;
+      dv[i][r] = 0.f;
+    }
+
+  const int qstart = (k0 / BQ) * BQ;
+  for (int hq = 0; hq < rep; ++hq) {
+    const int h = g * rep + hq;
+    const uint16_t* qbase = a.q + (int64_t)b * S * a.ldq + (int64_t)h * HD;
+    const uint16_t* dobase = a.dout + (int64_t)b * S * a.lddo + (int64_t)h * HD;
+    const uint16_t* qtbase = a.qt + (int64_t)(b * H + h) * HD * S;
+    const uint16_t* dotbase = a.dot + (int64_t)(b * H + h) * HD * S;
+    const float* lsep = a.lse + (int64_t)(b * H + h) * S;
+    const float* dp_ = a.delta + (int64_t)(b * H + h) * S;
+    for (int q0 = qstart; q0 < S; q0 += BQ) {
+      load_rows<HD, BQ, NT>(Qs, KROW, qbase, a.ldq, q0, S, tid);
+      load_rows<HD, BQ, NT>(dOs, KROW, dobase, a.lddo, q0, S, tid);
+      load_trows<HD, BQ, NT>(Qts, TROW, qtbase, S, q0, tid);
+      load_trows<HD, BQ, NT>(dOts, TROW, dotbase, S, q0, tid);
+      if (tid < BQ) {
+        const int q = q0 + tid;
+        lse2s[tid] = q < S ? lsep[q] * kLog2e : 0.f;
+        Ds[tid] = q < S ? dp_[q] : 0.f;
+      }
+      __syncthreads();
+      if (q0 + BQ - 1 >= kw0 && kw0 < S) {
+        f32x16_t s[2], dp[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            s[t][r] = 0.f;
+            dp[t][r] = 0.f;
+          }
+#pragma unroll
+          for (int kk = 0; kk < HD / 16; ++kk) {
+            const bf16x8_t aq = lds_frag16(Qs + (t * 32 + l32) * KROW + kk * 32 + half * 16);
+            s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[kk], s[t], 0, 0, 0);
+            const bf16x8_t ado = lds_frag16(dOs + (t * 32 + l32) * KROW + kk * 32 + half * 16);
+            dp[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ado, vf[kk], dp[t], 0, 0, 0);
+          }
+        }
+        // lane holds key column kvrow; query rows ql = t*32 + 8*(r/4) + 4*half + r%4
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int qlb = t * 32 + 8 * r4 + 4 * half;
+            const float4 l4 = *reinterpret_cast<const float4*>(lse2s + qlb);
+            const float4 d4 = *reinterpret_cast<const float4*>(Ds + qlb);
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+            const float dvv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * r4 + e;
+              const int q = q0 + qlb + e;
+              const bool ok = q < S && kvrow <= q && kvrow < S;
+              const float p = ok ? exp2f(s[t][r] * c - lv[e]) : 0.f;
+              dp[t][r] = p * (dp[t][r] - dvv[e]);
+              s[t][r] = p;
+            }
+          }
+#pragma unroll
+        for (int ks = 0; ks < BQ / 16; ++ks) {
+          float pv[8], dsv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            pv[e] = s[ks >> 1][8 * (ks & 1) + e];
+            dsv[e] = dp[ks >> 1][8 * (ks & 1) + e];
+          }
+          const bf16x8_t pb = pack_bf16x8(pv);
+          const bf16x8_t dsb = pack_bf16x8(dsv);
+#pragma unroll
+          for (int i = 0; i < HD / 32; ++i) {
+            const char* dorow = dOts + (i * 32 + l32) * TROW;
+            const bf16x8_t ado = lds_frag_2x4(dorow + (16 * ks + 4 * half) * 2, dorow + (16 * ks + 8 + 4 * half) * 2);
+            dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ado, pb, dv[i], 0, 0, 0);
+            const char* qrow_ = Qts + (i * 32 + l32) * TROW;
+            const bf16x8_t aq = lds_frag_2x4(qrow_ + (16 * ks + 4 * half) * 2, qrow_ + (16 * ks + 8 + 4 * half) * 2);
+            dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, dsb, dk[i], 0, 0, 0);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (kvrow < S) {
+    uint16_t* dkp = a.dk + ((int64_t)b * S + kvrow) * a.lddk + (int64_t)g * HD;
+    uint16_t* dvp = a.dv + ((int64_t)b * S + kvrow) * a.lddv + (int64_t)g * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(dkp + hd, dk[i][4 * q4] * a.scale, dk[i][4 * q4 + 1] * a.scale, dk[i][4 * q4 + 2] * a.scale,
+                     dk[i][4 * q4 + 3] * a.scale);
+        store_bf16x4(dvp + hd, dv[i][4 * q4], dv[i][4 * q4 + 1], dv[i][4 * q4 + 2], dv[i][4 * q4 + 3]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, dQ pass.  256 threads; 128 queries per workgroup; 64-key steps.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
+  constexpr int BQ = 128, BKV = 64, NT = 256;
+  constexpr int KROW = HD * 2 + 16;
+  constexpr int TROW = BKV * 2 + 8;
+  __shared__ __attribute__((aligned(16))) char smem[2 * BKV * KROW + HD * TROW];
+  char* Ks = smem;
+  char* Vs = Ks + BKV * KROW;
+  char* Kts = Vs + BKV * KROW;
+
+  const int S = a.S, H = a.H, KV = a.KV;
+  const int nqb = (S + BQ - 1) / BQ;
+  const int bh = a.B * H;
+  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
+  const int rem = blockIdx.x % bh;
+  const int b = rem / H, h = rem % H;
+  const int g = h / (H / KV);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
+  const int qrow = qw0 + l32;
+  const int qc = min(qrow, S - 1);
+  const float c = a.scale * kLog2e;
+
+  bf16x8_t qf[HD / 16], df[HD / 16];
+  {
+    const uint16_t* qp = a.q + ((int64_t)b * S + qc) * a.ldq + (int64_t)h * HD + 8 * half;
+    const uint16_t* dp_ = a.dout + ((int64_t)b * S + qc) * a.lddo + (int64_t)h * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qp + kk * 16));
+      df[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(dp_ + kk * 16));
+    }
+  }
+  const float lse2 = a.lse[((int64_t)b * H + h) * S + qc] * kLog2e;
+  const float Dq = a.delta[((int64_t)b * H + h) * S + qc];
+  f32x16_t dq[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+
+  const int kv_end = min(S, q0 + BQ);
+  const int kv_end_w = min(S, qw0 + 32);
+  const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
+  const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
+  const uint16_t* ktbase = a.kt + (int64_t)(b * KV + g) * HD * S;
+
+  for (int k0 = 0; k0 < kv_end; k0 += BKV) {
+    load_rows<HD, BKV, NT>(Ks, KROW, kbase, a.ldk, k0, S, tid);
+    load_rows<HD, BKV, NT>(Vs, KROW, vbase, a.ldv, k0, S, tid);
+    load_trows<HD, BKV, NT>(Kts, TROW, ktbase, S, k0, tid);
+    __syncthreads();
+    if (k0 < kv_end_w) {
+      f32x16_t st[2], dpt[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          st[t][r] = 0.f;
+          dpt[t][r] = 0.f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; ++kk) {
+          const bf16x8_t ak = lds_frag16(Ks + (t * 32 + l32) * KROW + kk * 32 + half * 16);
+          st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[kk], st[t], 0, 0, 0);
+          const bf16x8_t av = lds_frag16(Vs + (t * 32 + l32) * KROW + kk * 32 + half * 16);
+          dpt[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[kk], dpt[t], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool ok = kv <= qrow && kv < S && qrow < S;
+          const float p = ok ? exp2f(st[t][r] * c - lse2) : 0.f;
+          dpt[t][r] = p * (dpt[t][r] - Dq);
+        }
+#pragma unroll
+      for (int ks = 0; ks < BKV / 16; ++ks) {
+        float dsv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsv[e] = dpt[ks >> 1][8 * (ks & 1) + e];
+        const bf16x8_t dsb = pack_bf16x8(dsv);
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i) {
+          const char* row = Kts + (i * 32 + l32) * TROW;
+          const bf16x8_t ak = lds_frag_2x4(row + (16 * ks + 4 * half) * 2, row + (16 * ks + 8 + 4 * half) * 2);
+          dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, dsb, dq[i], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (qrow < S) {
+    uint16_t* dqp = a.dq + ((int64_t)b * S + qrow) * a.lddq + (int64_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(dqp + hd, dq[i][4 * q4] * a.scale, dq[i][4 * q4 + 1] * a.scale, dq[i][4 * q4 + 2] * a.scale,
+                     dq[i][4 * q4 + 3] * a.scale);
+      }
+  }
+}
+
+// delta[b,h,s] = sum_d dO[b,s,h,d] * O[b,s,h,d]; one wave per (b, s, h) row.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_delta_kernel(const T* __restrict__ o, int64_t ldo, const T* __restrict__ dout,
+                                                          int64_t lddo, float* __restrict__ delta, int B, int S, int H,
+                                                          int hd) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t total = (int64_t)B * S * H;
+  if (row >= total) return;
+  const int64_t bs = row / H;
+  const int h = (int)(row - bs * H);
+  const T* op = o + bs * ldo + (int64_t)h * hd;
+  const T* dp = dout + bs * lddo + (int64_t)h * hd;
+  float acc = 0.f;
+  for (int d = lane; d < hd; d += 64) acc = fmaf(Elem<T>::load(op, d), Elem<T>::load(dp, d), acc);
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    const int64_t b = bs / S, s = bs - b * S;
+    delta[(b * H + h) * S + s] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic path (any even head dim up to 256, bf16 or fp32): one wave per
+// query row (forward, dQ) or key row (dK/dV), lanes split the head dim, fp32
+// online softmax.  Used where the MFMA tiling does not apply.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct GenArgs {
+  const T* q;
+  const T* k;
+  const T* v;
+  int64_t ldq, ldk, ldv;
+  T* o;
+  int64_t ldo;
+  float* lse;
+  const T* dout;
+  int64_t lddo;
+  const float* delta;
+  T* dq;
+  T* dk;
+  T* dv;
+  int64_t lddq, lddk, lddv;
+  int B, S, H, KV, hd;
+  float scale;
+};
+
+constexpr int kGenMax = 4;  // head dim up to 64 * kGenMax
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_fwd_generic_kernel(GenArgs<T> a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t total = (int64_t)a.B * a.H * a.S;
+  if (row >= total) return;
+  const int s = (int)(row % a.S);
+  const int64_t bh = row / a.S;
+  const int h = (int)(bh % a.H), b = (int)(bh / a.H);
+  const int g = h / (a.H / a.KV);
+  const T* qp = a.q + ((int64_t)b * a.S + s) * a.ldq + (int64_t)h * a.hd;
+  float qv[kGenMax], ov[kGenMax];
+#pragma unroll
+  for (int j = 0; j < kGenMax; ++j) {
+    const int d = lane + 64 * j;
+    qv[j] = d < a.hd ? Elem<T>::load(qp, d) : 0.f;
+    ov[j] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  for (int kv = 0; kv <= s; ++kv) {
+    const T* kp = a.k + ((int64_t)b * a.S + kv) * a.ldk + (int64_t)g * a.hd;
+    const T* vp = a.v + ((int64_t)b * a.S + kv) * a.ldv + (int64_t)g * a.hd;
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < kGenMax; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.hd) dot = fmaf(qv[j], Elem<T>::load(kp, d), dot);
+    }
+    const float sc = wave_sum(dot) * a.scale;
+    const float m_new = fmaxf(m, sc);
+    const float corr = expf(m - m_new), p = expf(sc - m_new);
+    l = l * corr + p;
+#pragma unroll
+    for (int j = 0; j < kGenMax; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.hd) ov[j] = ov[j] * corr + p * Elem<T>::load(vp, d);
+    }
+    m = m_new;
+  }
+  T* op = a.o + ((int64_t)b * a.S + s) * a.ldo + (int64_t)h * a.hd;
+#pragma unroll
+  for (int j = 0; j < kGenMax; ++j) {
+    const int d = lane + 64 * j;
+    if (d < a.hd) Elem<T>::store(op, d, ov[j] / l);
+  }
+  if (lane == 0) a.lse[((int64_t)b * a.H + h) * a.S + s] = m + logf(l);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_bwd_dq_generic_kernel(GenArgs<T> a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t total = (int64_t)a.B * a.H * a.S;
+  if (row >= total) return;
+  const int s = (int)(row % a.S);
+  const int64_t bh = row / a.S;
+  const int h = (int)(bh % a.H), b = (int)(bh / a.H);
+  const int g = h / (a.H / a.KV);
+  const T* qp = a.q + ((int64_t)b * a.S + s) * a.ldq + (int64_t)h * a.hd;
+  const T* dop = a.dout + ((int64_t)b * a.S + s) * a.lddo + (int64_t)h * a.hd;
+  float qv[kGenMax], dov[kGenMax], acc[kGenMax];
+#pragma unroll
+  for (int j = 0; j < kGenMax; ++j) {
+    const int d = lane + 64 * j;
+    qv[j] = d < a.hd ? Elem<T>::load(qp, d) : 0.f;
+    dov[j] = d < a.hd ? Elem<T>::load(dop, d) : 0.f;
+    acc[j] = 0.f;
+  }
+  const float lse = a.lse[((int64_t)b * a.H + h) * a.S + s];
+  const float D = a.delta[((int64_t)b * a.H + h) * a.S + s];
+  for (int kv = 0; kv <= s; ++kv) {
+    const T* kp = a.k + ((int64_t)b * a.S + kv) * a.ldk + (int64_t)g * a.hd;
+    const T* vp = a.v + ((int64_t)b * a.S + kv) * a.ldv + (int64_t)g * a.hd;
+    float dot = 0.f, dpd = 0.f;
+#pragma unroll
+    for (int j = 0; j < kGenMax; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.hd) {
+        dot = fmaf(qv[j], Elem<T>::load(kp, d), dot);
+        dpd = fmaf(dov[j], Elem<T>::load(vp, d), dpd);
+      }
+    }
+    const float p = expf(wave_sum(dot) * a.scale - lse);
+    const float ds = p * (wave_sum(dpd) - D);
+#pragma unroll
+    for (int j = 0; j < kGenMax; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.hd) acc[j] = fmaf(ds, Elem<T>::load(kp, d), acc[j]);
+    }
+  }
+  T* dqp = a.dq + ((int64_t)b * a.S + s) * a.lddq + (int64_t)h * a.hd;
+#pragma unroll
+  for (int j = 0; j < kGenMax; ++j) {
+    const int d = lane + 64 * j;
+    if (d < a.hd) Elem<T>::store(dqp, d, acc[j] * a.scale);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_bwd_dkdv_generic_kernel(GenArgs<T> a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t total = (int64_t)a.B * a.KV * a.S;
+  if (row >= total) return;
+  const int kv = (int)(row % a.S);
+  const int64_t bg = row / a.S;
+  const int g = (int)(bg % a.KV), b = (int)(bg / a.KV);
+  const int rep = a.H / a.KV;
+  const T* kp = a.k + ((int64_t)b * a.S + kv) * a.ldk + (int64_t)g * a.hd;
+  const T* vp = a.v + ((int64_t)b * a.S + kv) * a.ldv + (int64_t)g * a.hd;
+  float kvv[kGenMax], vvv[kGenMax], dka[kGenMax], dva[kGenMax];
+#pragma unroll
+  for (int j = 0; j < kGenMax; ++j) {
+    const int d = lane + 64 * j;
+    kvv[j] = d < a.hd ? Elem<T>::load(kp, d) : 0.f;
+    vvv[j] = d < a.hd ? Elem<T>::load(vp, d) : 0.f;
+    dka[j] = 0.f;
+    dva[j] = 0.f;
+  }
+  for (int hq = 0; hq < rep; ++hq) {
+    const int h = g * rep + hq;
+    for (int s = kv; s < a.S; ++s) {
+      const T* qp = a.q + ((int64_t)b * a.S + s) * a.ldq + (int64_t)h * a.hd;
+      const T* dop = a.dout + ((int64_t)b * a.S + s) * a.lddo + (int64_t)h * a.hd;
+      float dot = 0.f, dpd = 0.f;
+#pragma unroll
+      for (int j = 0; j < kGenMax; ++j) {
+        const int d = lane + 64 * j;
+        if (d < a.hd) {
+          dot = fmaf(Elem<T>::load(qp, d), kvv[j], dot);
+          dpd = fmaf(Elem<T>::load(dop, d), vvv[j], dpd);
+        }
+      }
+      const int64_t li = ((int64_t)b * a.H + h) * a.S + s;
+      const float p = expf(wave_sum(dot) * a.scale - a.lse[li]);
+      const float ds = p * (wave_sum(dpd) - a.delta[li]);
+#pragma unroll
+      for (int j = 0; j < kGenMax; ++j) {
+        const int d = lane + 64 * j;
+        if (d < a.hd) {
+          dva[j] = fmaf(p, Elem<T>::load(dop, d), dva[j]);
+          dka[j] = fmaf(ds, Elem<T>::load(qp, d), dka[j]);
+        }
+      }
+    }
+  }
+  T* dkp = a.dk + ((int64_t)b * a.S + kv) * a.lddk + (int64_t)g * a.hd;
+  T* dvp = a.dv + ((int64_t)b * a.S + kv) * a.lddv + (int64_t)g * a.hd;
+#pragma unroll
+  for (int j = 0; j < kGenMax; ++j) {
+    const int d = lane + 64 * j;
+    if (d < a.hd) {
+      Elem<T>::store(dkp, d, dka[j] * a.scale);
+      Elem<T>::store(dvp, d, dva[j]);
+    }
+  }
+}
+
+bool mfma_ok(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, const void* q, const void* k,
+             const void* v, const void* o) {
+  return dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 &&
+         lz_aligned16(q) && lz_aligned16(k) && lz_aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7) == 0;
+}
+
+int check_shape(int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd) {
+  LZ_REQUIRE(B > 0 && S > 0 && H > 0 && KV > 0 && hd > 0, "attention: bad shape");
+  LZ_REQUIRE(H % KV == 0, "attention: H (%lld) must be a multiple of KV (%lld)", (long long)H, (long long)KV);
+  LZ_REQUIRE(hd <= 64 * kGenMax, "attention: head dim %lld > %d", (long long)hd, 64 * kGenMax);
+  LZ_REQUIRE(B * H * lz_cdiv(S, 64) < (1ll << 31) && S < (1 << 30), "attention: problem too large");
+  return LZ_OK;
+}
+
+}  // namespace
+
+// Which path lz_attn_fwd/bwd take for these arguments: 1 = MFMA tiles (needs
+// the transposed operand buffers), 0 = generic.
+LZ_EXPORT int lz_attn_uses_mfma(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
+  return dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0;
+}
+
+// Forward.  vt: V^T [B,KV,hd,S] (needed on the MFMA path only).
+LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                          const void* vt, void* o, int64_t ldo, float* lse, int64_t B, int64_t S, int64_t H, int64_t KV,
+                          int64_t hd, float scale, int dtype, void* stream) {
+  int rc = check_shape(B, S, H, KV, hd);
+  if (rc) return rc;
+  LZ_REQUIRE(q && k && v && o && lse, "lz_attn_fwd: null pointer");
+  hipStream_t s = lz_stream(stream);
+  if (mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o)) {
+    LZ_REQUIRE(vt && lz_aligned16(vt), "lz_attn_fwd: MFMA path needs an aligned V^T buffer");
+    AttnArgs a{};
+    a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv;
+    a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse; a.vt = (const uint16_t*)vt;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
+    const unsigned grid = (unsigned)(lz_cdiv(S, 128) * B * H);
+    if (hd == 128) attn_fwd_kernel<128><<<grid, 256, 0, s>>>(a);
+    else attn_fwd_kernel<64><<<grid, 256, 0, s>>>(a);
+    return lz_check_launch("lz_attn_fwd");
+  }
+  const unsigned grid = (unsigned)lz_cdiv(B * H * S, 4);
+  if (dtype == LZ_BF16) {
+    GenArgs<uint16_t> a{};
+    a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+    attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F32) {
+    GenArgs<float> a{};
+    a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.o = (float*)o; a.ldo = ldo; a.lse = lse;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+    attn_fwd_generic_kernel<float><<<grid, 256, 0, s>>>(a);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_attn_fwd: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_attn_fwd(generic)");
+}
+
+LZ_EXPORT int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_t lddo, float* delta, int64_t B, int64_t S,
+                            int64_t H, int64_t hd, int dtype, void* stream) {
+  LZ_REQUIRE(B > 0 && S > 0 && H > 0 && hd > 0 && delta, "lz_attn_delta: bad arguments");
+  const unsigned grid = (unsigned)lz_cdiv(B * S * H, 4);
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_BF16)
+    attn_delta_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)o, ldo, (const uint16_t*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);
+  else if (dtype == LZ_F32)
+    attn_delta_kernel<float><<<grid, 256, 0, s>>>((const float*)o, ldo, (const float*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);
+  else
+    return lz_set_error(LZ_EINVAL, "lz_attn_delta: bad dtype %d", dtype);
+  return lz_check_launch("lz_attn_delta");
+}
+
+// Backward.  On the MFMA path qt [B,H,hd,S], kt [B,KV,hd,S] and dot [B,H,hd,S]
+// are required; delta comes from lz_attn_delta.  dq/dk/dv are written (not
+// accumulated).
+LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                          const void* dout, int64_t lddo, const float* lse, const float* delta, const void* qt,
+                          const void* kt, const void* dot, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
+                          int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale, int dtype,
+                          void* stream) {
+  int rc = check_shape(B, S, H, KV, hd);
+  if (rc) return rc;
+  LZ_REQUIRE(q && k && v && dout && lse && delta && dq && dk && dv, "lz_attn_bwd: null pointer");
+  hipStream_t s = lz_stream(stream);
+  if (mfma_ok(dtype, hd, ldq, ldk, ldv, lddo, q, k, v, dout) && lddq % 4 == 0 && lddk % 4 == 0 && lddv % 4 == 0) {
+    LZ_REQUIRE(qt && kt && dot, "lz_attn_bwd: MFMA path needs the transposed Q, K and dO buffers");
+    AttnArgs a{};
+    a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv;
+    a.lse = const_cast<float*>(lse);
+    a.qt = (const uint16_t*)qt; a.kt = (const uint16_t*)kt; a.dout = (const uint16_t*)dout; a.lddo = lddo;
+    a.dot = (const uint16_t*)dot; a.delta = delta;
+    a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
+    a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
+    const unsigned grid_kv = (unsigned)(lz_cdiv(S, 128) * B * KV);
+    const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
+    if (hd == 128) {
+      attn_bwd_dkdv_kernel<128><<<grid_kv, 256, 0, s>>>(a);
+      attn_bwd_dq_kernel<128><<<grid_q, 256, 0, s>>>(a);
+    } else {
+      attn_bwd_dkdv_kernel<64><<<grid_kv, 256, 0, s>>>(a);
+      attn_bwd_dq_kernel<64><<<grid_q, 256, 0, s>>>(a);
+    }
+    return lz_check_launch("lz_attn_bwd");
+  }
+  const unsigned grid_q = (unsigned)lz_cdiv(B * H * S, 4);
+  const unsigned grid_kv = (unsigned)lz_cdiv(B * KV * S, 4);
+  if (dtype == LZ_BF16) {
+    GenArgs<uint16_t> a{};
+    a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.lse = const_cast<float*>(lse);
+    a.dout = (const uint16_t*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+    attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F32) {
+    GenArgs<float> a{};
+    a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.lse = const_cast<float*>(lse);
+    a.dout = (const float*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (float*)dq; a.dk = (float*)dk; a.dv = (float*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+    attn_bwd_dq_generic_kernel<float><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_generic_kernel<float><<<grid_kv, 256, 0, s>>>(a);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_attn_bwd: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_attn_bwd(generic)");
+}

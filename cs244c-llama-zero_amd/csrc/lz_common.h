@@ -1,0 +1,121 @@
+// Shared definitions for the llama-zero gfx950 kernels.
+//
+// Every exported entry point is `extern "C"`, takes raw device pointers,
+// int64 sizes and a hipStream_t passed as `void*`, launches asynchronously on
+// that stream and returns 0 on success or a negative status.  The message of
+// the last failure on the calling thread is available from lz_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#define LZ_OK 0
+#define LZ_EINVAL -1
+#define LZ_ELAUNCH -2
+#define LZ_ERUNTIME -3
+
+// dtype codes shared with the Python side.
+#define LZ_F32 0
+#define LZ_BF16 1
+
+#define LZ_EXPORT extern "C" __attribute__((visibility("default")))
+
+// Records `msg` as the last error of this thread and returns `code`.
+int lz_set_error(int code, const char* fmt, ...);
+// Converts a pending launch error into a status.
+int lz_check_launch(const char* what);
+
+#define LZ_REQUIRE(cond, ...)                          \
+  do {                                                 \
+    if (!(cond)) return lz_set_error(LZ_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+static inline hipStream_t lz_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static inline bool lz_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__host__ __device__ static inline int64_t lz_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// bfloat16 <-> float.  Storage is uint16_t; conversion is round-to-nearest-even
+// with NaN preserved, which is what torch's `.to(torch.bfloat16)` does.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Rounds a float to the nearest bfloat16 value, kept as float.
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+  // Rounding to the storage type (identity for fp32).
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+
+template <>
+struct Elem<uint16_t> {
+  static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
+  static __device__ __forceinline__ float round(float v) { return round_bf(v); }
+};
+
+// ---------------------------------------------------------------------------
+// Wavefront (64-lane) and block reductions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over the whole block; every thread gets the result.  `scratch` must
+// hold blockDim.x/64 floats.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int i = 0; i < nw; ++i) r += scratch[i];
+  return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  float r = -INFINITY;
+  for (int i = 0; i < nw; ++i) r = fmaxf(r, scratch[i]);
+  return r;
+}
+
+// Number of compute units of the current device (cached per device).
+int lz_num_cus();

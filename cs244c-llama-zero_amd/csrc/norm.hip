@@ -1,0 +1,304 @@
+// RMSNorm forward and backward (reference: model/llama.py:14-22).
+//
+//   y = x * rsqrt(mean(x^2) + eps) * w        (statistics in fp32)
+//
+// One 64-lane wavefront per row; each lane keeps its slice of the row in
+// registers (8 elements per 16-byte access), so x is read once and y written
+// once: 4 B/element in bf16.  The backward reads x and dy, writes dx (and an
+// optional residual-gradient add), 6 B/element, and reduces dw through per-wave
+// fp32 partials and a second column-sum kernel.
+#include "lz_common.h"
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one wave per row
+constexpr int kThreads = 64 * kRowsPerBlock;
+
+template <typename T>
+struct Pack8;
+
+template <>
+struct Pack8<uint16_t> {
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&r)[8]) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    r[0] = bf2f(v.x & 0xffff); r[1] = bf2f(v.x >> 16);
+    r[2] = bf2f(v.y & 0xffff); r[3] = bf2f(v.y >> 16);
+    r[4] = bf2f(v.z & 0xffff); r[5] = bf2f(v.z >> 16);
+    r[6] = bf2f(v.w & 0xffff); r[7] = bf2f(v.w >> 16);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float (&r)[8]) {
+    uint4 v;
+    v.x = (uint32_t)f2bf(r[0]) | ((uint32_t)f2bf(r[1]) << 16);
+    v.y = (uint32_t)f2bf(r[2]) | ((uint32_t)f2bf(r[3]) << 16);
+    v.z = (uint32_t)f2bf(r[4]) | ((uint32_t)f2bf(r[5]) << 16);
+    v.w = (uint32_t)f2bf(r[6]) | ((uint32_t)f2bf(r[7]) << 16);
+    *reinterpret_cast<uint4*>(p) = v;
+  }
+};
+
+template <>
+struct Pack8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&r)[8]) {
+    float4 a = reinterpret_cast<const float4*>(p)[0];
+    float4 b = reinterpret_cast<const float4*>(p)[1];
+    r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+    r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&r)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(r[0], r[1], r[2], r[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(r[4], r[5], r[6], r[7]);
+  }
+};
+
+// NC = number of 8-element chunks per lane; cols == NC * 512 at most, and the
+// row is processed as chunks c = lane + 64*j.
+template <typename T, int NC>
+__global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                                T* __restrict__ y, float* __restrict__ rstd_out,
+                                                                int64_t rows, int cols, int64_t ldx, int64_t ldy,
+                                                                float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nchunk = cols >> 3;
+  const T* xr = x + row * ldx;
+  float v[NC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nchunk) {
+      Pack8<T>::load(xr + 8 * c, v[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)cols + eps);
+  if (lane == 0 && rstd_out) rstd_out[row] = r;
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nchunk) {
+      float wv[8], o[8];
+      Pack8<T>::load(w + 8 * c, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (v[j][e] * r) * wv[e];
+      Pack8<T>::store(yr + 8 * c, o);
+    }
+  }
+}
+
+// Generic path for any cols (scalar accesses, two passes over the row).
+template <typename T>
+__global__ void __launch_bounds__(kThreads) rmsnorm_fwd_scalar_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                                       T* __restrict__ y, float* __restrict__ rstd_out,
+                                                                       int64_t rows, int cols, int64_t ldx, int64_t ldy,
+                                                                       float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int c = lane; c < cols; c += 64) {
+    float t = Elem<T>::load(xr, c);
+    ss = fmaf(t, t, ss);
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)cols + eps);
+  if (lane == 0 && rstd_out) rstd_out[row] = r;
+  T* yr = y + row * ldy;
+  for (int c = lane; c < cols; c += 64) Elem<T>::store(yr, c, (Elem<T>::load(xr, c) * r) * Elem<T>::load(w, c));
+}
+
+// Backward.  Each wave walks rows row = wave_id, wave_id + nwaves, ... and keeps
+// its dw contribution per owned column in registers; at the end it writes one
+// fp32 partial row (dw_part[wave_id][cols]).
+template <typename T, int NC>
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                                const float* __restrict__ rstd, const T* __restrict__ dy,
+                                                                const T* __restrict__ dres, T* __restrict__ dx,
+                                                                float* __restrict__ dw_part, int64_t rows, int cols,
+                                                                int64_t ldx, int64_t lddy, int64_t lddx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * kRowsPerBlock;
+  const int nchunk = cols >> 3;
+  float wv[NC][8];
+  float dwacc[NC][8];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dwacc[j][e] = 0.f;
+    if (c < nchunk) Pack8<T>::load(w + 8 * c, wv[j]);
+  }
+  const float inv_n = 1.0f / (float)cols;
+  for (int64_t row = wave; row < rows; row += nwaves) {
+    const float r = rstd[row];
+    float xv[NC][8], gv[NC][8];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk) {
+        Pack8<T>::load(x + row * ldx + 8 * c, xv[j]);
+        Pack8<T>::load(dy + row * lddy + 8 * c, gv[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dot = fmaf(gv[j][e] * wv[j][e], xv[j][e], dot);
+          dwacc[j][e] = fmaf(gv[j][e], xv[j][e] * r, dwacc[j][e]);
+        }
+      }
+    }
+    dot = wave_sum(dot);
+    const float coef = dot * r * r * r * inv_n;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = r * wv[j][e] * gv[j][e] - coef * xv[j][e];
+        if (dres) {
+          float rv[8];
+          Pack8<T>::load(dres + row * lddx + 8 * c, rv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] += rv[e];
+        }
+        Pack8<T>::store(dx + row * lddx + 8 * c, o);
+      }
+    }
+  }
+  float* part = dw_part + wave * cols;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nchunk) {
+      reinterpret_cast<float4*>(part + 8 * c)[0] = make_float4(dwacc[j][0], dwacc[j][1], dwacc[j][2], dwacc[j][3]);
+      reinterpret_cast<float4*>(part + 8 * c)[1] = make_float4(dwacc[j][4], dwacc[j][5], dwacc[j][6], dwacc[j][7]);
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_scalar_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                                       const float* __restrict__ rstd, const T* __restrict__ dy,
+                                                                       const T* __restrict__ dres, T* __restrict__ dx,
+                                                                       float* __restrict__ dw_part, int64_t rows, int cols,
+                                                                       int64_t ldx, int64_t lddy, int64_t lddx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * kRowsPerBlock;
+  float* part = dw_part + wave * cols;
+  for (int c = lane; c < cols; c += 64) part[c] = 0.f;
+  const float inv_n = 1.0f / (float)cols;
+  for (int64_t row = wave; row < rows; row += nwaves) {
+    const float r = rstd[row];
+    float dot = 0.f;
+    for (int c = lane; c < cols; c += 64)
+      dot = fmaf(Elem<T>::load(dy + row * lddy, c) * Elem<T>::load(w, c), Elem<T>::load(x + row * ldx, c), dot);
+    dot = wave_sum(dot);
+    const float coef = dot * r * r * r * inv_n;
+    for (int c = lane; c < cols; c += 64) {
+      const float xv = Elem<T>::load(x + row * ldx, c), gv = Elem<T>::load(dy + row * lddy, c);
+      float o = r * Elem<T>::load(w, c) * gv - coef * xv;
+      if (dres) o += Elem<T>::load(dres + row * lddx, c);
+      Elem<T>::store(dx + row * lddx, c, o);
+      part[c] += gv * (xv * r);
+    }
+  }
+}
+
+// dw[c] (+)= sum over partial rows.
+template <typename T>
+__global__ void dw_reduce_kernel(const float* __restrict__ part, int64_t nparts, int cols, T* __restrict__ dw,
+                                 int accumulate) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int64_t p = 0; p < nparts; ++p) s += part[p * cols + c];
+  if (accumulate) s += Elem<T>::load(dw, c);
+  Elem<T>::store(dw, c, s);
+}
+
+template <typename T>
+int fwd_dispatch(const void* x, const void* w, void* y, float* rstd, int64_t rows, int cols, int64_t ldx, int64_t ldy,
+                 float eps, hipStream_t s) {
+  const int grid = (int)lz_cdiv(rows, kRowsPerBlock);
+  const bool vec = cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(y) &&
+                   (ldx * (int64_t)sizeof(T)) % 16 == 0 && (ldy * (int64_t)sizeof(T)) % 16 == 0;
+  const T* xp = (const T*)x;
+  const T* wp = (const T*)w;
+  T* yp = (T*)y;
+  if (vec && cols <= 512) rmsnorm_fwd_kernel<T, 1><<<grid, kThreads, 0, s>>>(xp, wp, yp, rstd, rows, cols, ldx, ldy, eps);
+  else if (vec && cols <= 1024) rmsnorm_fwd_kernel<T, 2><<<grid, kThreads, 0, s>>>(xp, wp, yp, rstd, rows, cols, ldx, ldy, eps);
+  else if (vec && cols <= 2048) rmsnorm_fwd_kernel<T, 4><<<grid, kThreads, 0, s>>>(xp, wp, yp, rstd, rows, cols, ldx, ldy, eps);
+  else if (vec && cols <= 4096) rmsnorm_fwd_kernel<T, 8><<<grid, kThreads, 0, s>>>(xp, wp, yp, rstd, rows, cols, ldx, ldy, eps);
+  else rmsnorm_fwd_scalar_kernel<T><<<grid, kThreads, 0, s>>>(xp, wp, yp, rstd, rows, cols, ldx, ldy, eps);
+  return lz_check_launch("lz_rmsnorm_fwd");
+}
+
+template <typename T>
+int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
+                 int dw_accumulate, float* ws, int64_t ws_bytes, int64_t rows, int cols, int64_t ldx, int64_t lddy,
+                 int64_t lddx, hipStream_t s) {
+  // number of waves = number of fp32 partial rows held in the workspace
+  int64_t max_parts = ws_bytes / ((int64_t)cols * 4);
+  int64_t nwaves = std::min<int64_t>({(int64_t)lz_num_cus() * 4 * kRowsPerBlock, max_parts, rows});
+  nwaves = (nwaves / kRowsPerBlock) * kRowsPerBlock;
+  LZ_REQUIRE(nwaves >= kRowsPerBlock, "lz_rmsnorm_bwd: workspace too small (%lld bytes)", (long long)ws_bytes);
+  const int grid = (int)(nwaves / kRowsPerBlock);
+  const bool vec = cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(dy) && lz_aligned16(dx) &&
+                   (dres == nullptr || lz_aligned16(dres)) && (ldx * (int64_t)sizeof(T)) % 16 == 0 &&
+                   (lddy * (int64_t)sizeof(T)) % 16 == 0 && (lddx * (int64_t)sizeof(T)) % 16 == 0;
+  const T *xp = (const T*)x, *wp = (const T*)w, *gp = (const T*)dy, *rp = (const T*)dres;
+  T* dxp = (T*)dx;
+  if (vec && cols <= 512) rmsnorm_bwd_kernel<T, 1><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else if (vec && cols <= 1024) rmsnorm_bwd_kernel<T, 2><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else if (vec && cols <= 2048) rmsnorm_bwd_kernel<T, 4><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else if (vec && cols <= 4096) rmsnorm_bwd_kernel<T, 8><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else rmsnorm_bwd_scalar_kernel<T><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  int rc = lz_check_launch("lz_rmsnorm_bwd");
+  if (rc) return rc;
+  if (dw) {
+    dw_reduce_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(ws, nwaves, cols, (T*)dw, dw_accumulate);
+    rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
+  }
+  return rc;
+}
+
+}  // namespace
+
+LZ_EXPORT int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int dtype, int64_t rows, int64_t cols,
+                             int64_t ldx, int64_t ldy, float eps, void* stream) {
+  LZ_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30), "lz_rmsnorm_fwd: bad shape");
+  LZ_REQUIRE(ldx >= cols && ldy >= cols, "lz_rmsnorm_fwd: bad leading dimension");
+  if (rows == 0) return LZ_OK;
+  if (dtype == LZ_BF16) return fwd_dispatch<uint16_t>(x, w, y, rstd, rows, (int)cols, ldx, ldy, eps, lz_stream(stream));
+  if (dtype == LZ_F32) return fwd_dispatch<float>(x, w, y, rstd, rows, (int)cols, ldx, ldy, eps, lz_stream(stream));
+  return lz_set_error(LZ_EINVAL, "lz_rmsnorm_fwd: bad dtype %d", dtype);
+}
+
+// Workspace bytes the backward wants for its dw partials.
+LZ_EXPORT int64_t lz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
+  int64_t nwaves = std::min<int64_t>((int64_t)lz_num_cus() * 4 * kRowsPerBlock, std::max<int64_t>(rows, kRowsPerBlock));
+  return nwaves * cols * 4;
+}
+
+LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,
+                             void* dw, int dw_accumulate, void* workspace, int64_t workspace_bytes, int dtype, int64_t rows,
+                             int64_t cols, int64_t ldx, int64_t lddy, int64_t lddx, void* stream) {
+  LZ_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30), "lz_rmsnorm_bwd: bad shape");
+  LZ_REQUIRE(ldx >= cols && lddy >= cols && lddx >= cols, "lz_rmsnorm_bwd: bad leading dimension");
+  LZ_REQUIRE(workspace != nullptr, "lz_rmsnorm_bwd: null workspace");
+  if (rows == 0) return LZ_OK;
+  if (dtype == LZ_BF16)
+    return bwd_dispatch<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (float*)workspace, workspace_bytes, rows,
+                                  (int)cols, ldx, lddy, lddx, lz_stream(stream));
+  if (dtype == LZ_F32)
+    return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (float*)workspace, workspace_bytes, rows,
+                               (int)cols, ldx, lddy, lddx, lz_stream(stream));
+  return lz_set_error(LZ_EINVAL, "lz_rmsnorm_bwd: bad dtype %d", dtype);
+}

@@ -1,0 +1,471 @@
+// Optimizer-path kernels: fused AdamW over a flat fp32 master, gradient
+// sum-of-squares and clip factor, fills, casts, accumulates, and the
+// multi-tensor gather/scatter between per-parameter storages and flat buffers.
+//
+// All are HBM-bound streaming kernels: 16-byte vector accesses where the
+// pointers allow it, grid-stride loops sized to a few waves of workgroups per
+// compute unit.
+#include <algorithm>
+
+#include "lz_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline int stream_grid(int64_t work_items) {
+  int64_t blocks = lz_cdiv(work_items, kThreads);
+  int64_t cap = (int64_t)lz_num_cus() * 8;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
+struct AdamArgs {
+  float beta1, beta2;
+  float omb1, omb2;     // 1 - beta1, 1 - beta2
+  float wd_factor;      // 1 - lr * weight_decay
+  float sqrt_bc2;       // sqrt(1 - beta2^t)
+  float eps;
+  float neg_step;       // -lr / (1 - beta1^t)
+  int apply_wd;
+};
+
+// One AdamW element update, in the operation order of the reference update
+// (zero/stage0_ddp.py:73-88): moments, decoupled decay, then the
+// bias-corrected step.
+__device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g, const AdamArgs& a) {
+  m = fmaf(a.omb1, g, m * a.beta1);
+  v = fmaf(a.omb2 * g, g, v * a.beta2);
+  if (a.apply_wd) p = p * a.wd_factor;
+  const float denom = sqrtf(v) / a.sqrt_bc2 + a.eps;
+  p = fmaf(a.neg_step, m / denom, p);
+}
+
+template <typename G, typename PO>
+__global__ void __launch_bounds__(kThreads) adamw_scalar_kernel(float* __restrict__ p, float* __restrict__ m,
+                                                                 float* __restrict__ v, const G* __restrict__ g,
+                                                                 PO* __restrict__ pout, int64_t n, AdamArgs a,
+                                                                 const float* __restrict__ scale_ptr) {
+  const float scale = scale_ptr ? *scale_ptr : 1.0f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float pp = p[i], mm = m[i], vv = v[i];
+    float gg = Elem<G>::load(g, i);
+    if (scale_ptr) gg = gg * scale;
+    adam_elem(pp, mm, vv, gg, a);
+    p[i] = pp;
+    m[i] = mm;
+    v[i] = vv;
+    if (pout) Elem<PO>::store(pout, i, pp);
+  }
+}
+
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<float> {
+  using type = float4;
+  static __device__ __forceinline__ void load(const float* p, int64_t i, float (&r)[4]) {
+    float4 x = *reinterpret_cast<const float4*>(p + i);
+    r[0] = x.x; r[1] = x.y; r[2] = x.z; r[3] = x.w;
+  }
+  static __device__ __forceinline__ void store(float* p, int64_t i, const float (&r)[4]) {
+    *reinterpret_cast<float4*>(p + i) = make_float4(r[0], r[1], r[2], r[3]);
+  }
+};
+template <>
+struct Vec4<uint16_t> {
+  static __device__ __forceinline__ void load(const uint16_t* p, int64_t i, float (&r)[4]) {
+    uint2 x = *reinterpret_cast<const uint2*>(p + i);
+    r[0] = bf2f(x.x & 0xffff); r[1] = bf2f(x.x >> 16); r[2] = bf2f(x.y & 0xffff); r[3] = bf2f(x.y >> 16);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, const float (&r)[4]) {
+    uint2 x;
+    x.x = (uint32_t)f2bf(r[0]) | ((uint32_t)f2bf(r[1]) << 16);
+    x.y = (uint32_t)f2bf(r[2]) | ((uint32_t)f2bf(r[3]) << 16);
+    *reinterpret_cast<uint2*>(p + i) = x;
+  }
+};
+
+template <typename G, typename PO>
+__global__ void __launch_bounds__(kThreads) adamw_vec_kernel(float* __restrict__ p, float* __restrict__ m,
+                                                              float* __restrict__ v, const G* __restrict__ g,
+                                                              PO* __restrict__ pout, int64_t n, AdamArgs a,
+                                                              const float* __restrict__ scale_ptr) {
+  const float scale = scale_ptr ? *scale_ptr : 1.0f;
+  const int64_t n4 = n >> 2;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < n4; q += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = q << 2;
+    float pp[4], mm[4], vv[4], gg[4];
+    Vec4<float>::load(p, i, pp);
+    Vec4<float>::load(m, i, mm);
+    Vec4<float>::load(v, i, vv);
+    Vec4<G>::load(g, i, gg);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float gj = scale_ptr ? gg[j] * scale : gg[j];
+      adam_elem(pp[j], mm[j], vv[j], gj, a);
+    }
+    Vec4<float>::store(p, i, pp);
+    Vec4<float>::store(m, i, mm);
+    Vec4<float>::store(v, i, vv);
+    if (pout) Vec4<PO>::store(pout, i, pp);
+  }
+  // Tail (n % 4 elements) handled by the first block.
+  if (blockIdx.x == 0) {
+    for (int64_t i = (n4 << 2) + threadIdx.x; i < n; i += blockDim.x) {
+      float pp = p[i], mm = m[i], vv = v[i];
+      float gj = Elem<G>::load(g, i);
+      if (scale_ptr) gj = gj * scale;
+      adam_elem(pp, mm, vv, gj, a);
+      p[i] = pp;
+      m[i] = mm;
+      v[i] = vv;
+      if (pout) Elem<PO>::store(pout, i, pp);
+    }
+  }
+}
+
+template <typename G, typename PO>
+int launch_adamw(float* p, float* m, float* v, const void* g, void* pout, int64_t n, const AdamArgs& a,
+                 const float* scale, hipStream_t s) {
+  const G* gp = static_cast<const G*>(g);
+  PO* po = static_cast<PO*>(pout);
+  const bool vec = lz_aligned16(p) && lz_aligned16(m) && lz_aligned16(v) &&
+                   ((reinterpret_cast<uintptr_t>(g) & (4 * sizeof(G) - 1)) == 0) &&
+                   (pout == nullptr || (reinterpret_cast<uintptr_t>(pout) & (4 * sizeof(PO) - 1)) == 0);
+  if (vec) {
+    int grid = stream_grid(n / 4 + 1);
+    adamw_vec_kernel<G, PO><<<grid, kThreads, 0, s>>>(p, m, v, gp, po, n, a, scale);
+  } else {
+    int grid = stream_grid(n);
+    adamw_scalar_kernel<G, PO><<<grid, kThreads, 0, s>>>(p, m, v, gp, po, n, a, scale);
+  }
+  return lz_check_launch("lz_adamw");
+}
+
+// ---------------------------------------------------------------------------
+// Sum of squares, accumulated into a device double.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kThreads) sumsq_kernel(const T* __restrict__ x, int64_t n, double* __restrict__ acc) {
+  __shared__ double red[kThreads / 64];
+  float local = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float t = Elem<T>::load(x, i);
+    local = fmaf(t, t, local);
+  }
+  double d = wave_sum_d((double)local);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = d;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    atomicAdd(acc, s);
+  }
+}
+
+__global__ void sumsq_vec4_f32_kernel(const float* __restrict__ x, int64_t n, double* __restrict__ acc) {
+  __shared__ double red[kThreads / 64];
+  float local = 0.f;
+  const int64_t n4 = n >> 2;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < n4; q += (int64_t)gridDim.x * blockDim.x) {
+    float4 t = reinterpret_cast<const float4*>(x)[q];
+    local = fmaf(t.x, t.x, local);
+    local = fmaf(t.y, t.y, local);
+    local = fmaf(t.z, t.z, local);
+    local = fmaf(t.w, t.w, local);
+  }
+  if (blockIdx.x == 0)
+    for (int64_t i = (n4 << 2) + threadIdx.x; i < n; i += blockDim.x) local = fmaf(x[i], x[i], local);
+  double d = wave_sum_d((double)local);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = d;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    atomicAdd(acc, s);
+  }
+}
+
+// norm = sqrt(sum of squares) rounded to fp32 (the reference reads an fp32
+// norm with .item()); scale = max/(norm + 1e-6) when clipping applies, else 1
+// (zero/stage0_ddp.py:66-71).
+__global__ void clip_finalize_kernel(const double* __restrict__ acc, float max_norm, float* __restrict__ norm_out,
+                                     float* __restrict__ scale_out) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const float norm = (float)sqrt(*acc);
+    float scale = 1.0f;
+    if (max_norm > 0.0f && norm > max_norm) scale = (float)((double)max_norm / ((double)norm + 1e-6));
+    if (norm_out) *norm_out = norm;
+    if (scale_out) *scale_out = scale;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fill, cast, accumulate.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void fill_kernel(T* __restrict__ x, int64_t n, T value) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) x[i] = value;
+}
+
+__global__ void fill16_kernel(uint4* __restrict__ x, int64_t n16, uint4 value) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) x[i] = value;
+}
+
+template <typename S, typename D>
+__global__ void cast_kernel(const S* __restrict__ src, D* __restrict__ dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    Elem<D>::store(dst, i, Elem<S>::load(src, i));
+}
+
+// dst(f32) += alpha * src
+template <typename S>
+__global__ void axpy_f32_kernel(float* __restrict__ dst, const S* __restrict__ src, int64_t n, float alpha, int unit_alpha) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = Elem<S>::load(src, i);
+    dst[i] = unit_alpha ? dst[i] + s : fmaf(alpha, s, dst[i]);
+  }
+}
+
+// dst = round_T(dst + src), both in the storage type T (torch's in-place add).
+template <typename T>
+__global__ void add_inplace_kernel(T* __restrict__ dst, const T* __restrict__ src, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(dst, i, Elem<T>::load(dst, i) + Elem<T>::load(src, i));
+}
+
+// x *= alpha (in the storage type).
+template <typename T>
+__global__ void scale_kernel(T* __restrict__ x, int64_t n, float alpha) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(x, i, Elem<T>::load(x, i) * alpha);
+}
+
+// ---------------------------------------------------------------------------
+// Multi-tensor gather/scatter.  `table` is a device int64 array of nseg
+// records {ptr, numel, flat_offset}, sorted by flat_offset.  A record with a
+// null ptr reads as zeros (a parameter without a gradient).
+// ---------------------------------------------------------------------------
+constexpr int64_t kChunk = 8192;
+
+__device__ __forceinline__ int find_segment(const int64_t* table, int nseg, int64_t pos) {
+  // first segment whose end is > pos
+  int lo = 0, hi = nseg;
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (table[3 * mid + 2] + table[3 * mid + 1] <= pos) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// mode 0: dst = src ; mode 1: dst(f32) += src
+template <typename S, typename D>
+__global__ void __launch_bounds__(kThreads) mt_gather_kernel(const int64_t* __restrict__ table, int nseg, D* __restrict__ dst,
+                                                              int64_t begin, int64_t end, int mode) {
+  const int64_t nchunks = lz_cdiv(end - begin, kChunk);
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t c0 = begin + c * kChunk;
+    const int64_t c1 = min(c0 + kChunk, end);
+    for (int s = find_segment(table, nseg, c0); s < nseg; ++s) {
+      const S* ptr = reinterpret_cast<const S*>(table[3 * s]);
+      const int64_t numel = table[3 * s + 1], off = table[3 * s + 2];
+      if (off >= c1) break;
+      const int64_t lo = max(c0, off), hi = min(c1, off + numel);
+      for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        float val = ptr ? Elem<S>::load(ptr, i - off) : 0.0f;
+        if (mode == 1) {
+          float* d = reinterpret_cast<float*>(dst);
+          d[i - begin] += val;
+        } else {
+          Elem<D>::store(dst, i - begin, val);
+        }
+      }
+    }
+  }
+}
+
+template <typename S, typename D>
+__global__ void __launch_bounds__(kThreads) mt_scatter_kernel(const S* __restrict__ src, const int64_t* __restrict__ table,
+                                                               int nseg, int64_t begin, int64_t end) {
+  const int64_t nchunks = lz_cdiv(end - begin, kChunk);
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t c0 = begin + c * kChunk;
+    const int64_t c1 = min(c0 + kChunk, end);
+    for (int s = find_segment(table, nseg, c0); s < nseg; ++s) {
+      D* ptr = reinterpret_cast<D*>(table[3 * s]);
+      const int64_t numel = table[3 * s + 1], off = table[3 * s + 2];
+      if (off >= c1) break;
+      if (!ptr) continue;
+      const int64_t lo = max(c0, off), hi = min(c1, off + numel);
+      for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) Elem<D>::store(ptr, i - off, Elem<S>::load(src, i - begin));
+    }
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// Exported entry points.
+// ===========================================================================
+
+// Fused AdamW over n elements of an fp32 master (p), moments (m, v) and a
+// gradient (g, fp32 or bf16), optionally scaled by *grad_scale (the clip factor,
+// read on the device) and optionally writing the updated parameter in a low
+// precision copy (p_out).  Hyper-parameters arrive as doubles, like the
+// reference's Python floats; bias corrections use `step` (1-based).
+LZ_EXPORT int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype,
+                            int64_t n, double lr, double beta1, double beta2, double eps, double weight_decay,
+                            int64_t step, const float* grad_scale, void* stream) {
+  LZ_REQUIRE(step >= 1, "lz_adamw: step must be >= 1");
+  if (n == 0) return LZ_OK;
+  LZ_REQUIRE(p && m && v && g && n > 0, "lz_adamw: bad arguments");
+  const double bc1 = 1.0 - pow(beta1, (double)step);
+  const double bc2 = 1.0 - pow(beta2, (double)step);
+  AdamArgs a;
+  a.beta1 = (float)beta1;
+  a.beta2 = (float)beta2;
+  a.omb1 = (float)(1.0 - beta1);
+  a.omb2 = (float)(1.0 - beta2);
+  a.wd_factor = (float)(1.0 - lr * weight_decay);
+  a.apply_wd = weight_decay != 0.0;
+  a.sqrt_bc2 = (float)sqrt(bc2);
+  a.eps = (float)eps;
+  a.neg_step = (float)(-(lr / bc1));
+  hipStream_t s = lz_stream(stream);
+  const bool gb = g_dtype == LZ_BF16;
+  LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32, "lz_adamw: bad grad dtype %d", g_dtype);
+  if (p_out == nullptr || p_out_dtype == LZ_F32) {
+    return gb ? launch_adamw<uint16_t, float>(p, m, v, g, p_out, n, a, grad_scale, s)
+              : launch_adamw<float, float>(p, m, v, g, p_out, n, a, grad_scale, s);
+  }
+  LZ_REQUIRE(p_out_dtype == LZ_BF16, "lz_adamw: bad output dtype %d", p_out_dtype);
+  return gb ? launch_adamw<uint16_t, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, s)
+            : launch_adamw<float, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, s);
+}
+
+LZ_EXPORT int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* stream) {
+  LZ_REQUIRE(n >= 0 && acc, "lz_sumsq: bad arguments");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_F32) {
+    if (lz_aligned16(x)) sumsq_vec4_f32_kernel<<<stream_grid(n / 4 + 1), kThreads, 0, s>>>((const float*)x, n, acc);
+    else sumsq_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((const float*)x, n, acc);
+  } else if (dtype == LZ_BF16) {
+    sumsq_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((const uint16_t*)x, n, acc);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_sumsq: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_sumsq");
+}
+
+LZ_EXPORT int lz_clip_finalize(const double* acc, float max_norm, float* norm_out, float* scale_out, void* stream) {
+  LZ_REQUIRE(acc, "lz_clip_finalize: null accumulator");
+  clip_finalize_kernel<<<1, 64, 0, lz_stream(stream)>>>(acc, max_norm, norm_out, scale_out);
+  return lz_check_launch("lz_clip_finalize");
+}
+
+LZ_EXPORT int lz_fill(void* x, int dtype, int64_t n, double value, void* stream) {
+  LZ_REQUIRE(n >= 0, "lz_fill: negative n");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_F32) {
+    const float f = (float)value;
+    if (lz_aligned16(x) && n % 4 == 0) {
+      uint32_t u = __builtin_bit_cast(uint32_t, f);
+      fill16_kernel<<<stream_grid(n / 4), kThreads, 0, s>>>((uint4*)x, n / 4, make_uint4(u, u, u, u));
+    } else {
+      fill_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)x, n, f);
+    }
+  } else if (dtype == LZ_BF16) {
+    // host-side RNE rounding of the fill value
+    uint32_t u = __builtin_bit_cast(uint32_t, (float)value);
+    uint16_t h = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    if (lz_aligned16(x) && n % 8 == 0) {
+      uint32_t w = (uint32_t)h | ((uint32_t)h << 16);
+      fill16_kernel<<<stream_grid(n / 8), kThreads, 0, s>>>((uint4*)x, n / 8, make_uint4(w, w, w, w));
+    } else {
+      fill_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, h);
+    }
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_fill: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_fill");
+}
+
+LZ_EXPORT int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream) {
+  LZ_REQUIRE(n >= 0, "lz_cast: negative n");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  const int g = stream_grid(n);
+  if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) cast_kernel<float, uint16_t><<<g, kThreads, 0, s>>>((const float*)src, (uint16_t*)dst, n);
+  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) cast_kernel<uint16_t, float><<<g, kThreads, 0, s>>>((const uint16_t*)src, (float*)dst, n);
+  else if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) cast_kernel<float, float><<<g, kThreads, 0, s>>>((const float*)src, (float*)dst, n);
+  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_BF16) cast_kernel<uint16_t, uint16_t><<<g, kThreads, 0, s>>>((const uint16_t*)src, (uint16_t*)dst, n);
+  else return lz_set_error(LZ_EINVAL, "lz_cast: bad dtypes %d->%d", src_dtype, dst_dtype);
+  return lz_check_launch("lz_cast");
+}
+
+LZ_EXPORT int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n, float alpha, void* stream) {
+  LZ_REQUIRE(n >= 0 && dst, "lz_axpy_f32: bad arguments");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  const int unit = alpha == 1.0f;
+  if (src_dtype == LZ_BF16) axpy_f32_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>(dst, (const uint16_t*)src, n, alpha, unit);
+  else if (src_dtype == LZ_F32) axpy_f32_kernel<float><<<stream_grid(n), kThreads, 0, s>>>(dst, (const float*)src, n, alpha, unit);
+  else return lz_set_error(LZ_EINVAL, "lz_axpy_f32: bad dtype %d", src_dtype);
+  return lz_check_launch("lz_axpy_f32");
+}
+
+LZ_EXPORT int lz_add_inplace(void* dst, const void* src, int dtype, int64_t n, void* stream) {
+  LZ_REQUIRE(n >= 0, "lz_add_inplace: negative n");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_BF16) add_inplace_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)dst, (const uint16_t*)src, n);
+  else if (dtype == LZ_F32) add_inplace_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)dst, (const float*)src, n);
+  else return lz_set_error(LZ_EINVAL, "lz_add_inplace: bad dtype %d", dtype);
+  return lz_check_launch("lz_add_inplace");
+}
+
+LZ_EXPORT int lz_scale_inplace(void* x, int dtype, int64_t n, float alpha, void* stream) {
+  LZ_REQUIRE(n >= 0, "lz_scale_inplace: negative n");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_BF16) scale_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, alpha);
+  else if (dtype == LZ_F32) scale_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)x, n, alpha);
+  else return lz_set_error(LZ_EINVAL, "lz_scale_inplace: bad dtype %d", dtype);
+  return lz_check_launch("lz_scale_inplace");
+}
+
+LZ_EXPORT int lz_mt_gather(const int64_t* table, int nseg, int src_dtype, void* dst, int dst_dtype, int64_t begin,
+                           int64_t end, int accumulate, void* stream) {
+  LZ_REQUIRE(table && nseg > 0 && begin <= end, "lz_mt_gather: bad arguments");
+  LZ_REQUIRE(!accumulate || dst_dtype == LZ_F32, "lz_mt_gather: accumulate requires an fp32 destination");
+  if (begin == end) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  const int grid = (int)std::min<int64_t>(lz_cdiv(end - begin, kChunk), (int64_t)lz_num_cus() * 8);
+  if (src_dtype == LZ_BF16 && dst_dtype == LZ_BF16) mt_gather_kernel<uint16_t, uint16_t><<<grid, kThreads, 0, s>>>(table, nseg, (uint16_t*)dst, begin, end, 0);
+  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) mt_gather_kernel<uint16_t, float><<<grid, kThreads, 0, s>>>(table, nseg, (float*)dst, begin, end, accumulate);
+  else if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) mt_gather_kernel<float, float><<<grid, kThreads, 0, s>>>(table, nseg, (float*)dst, begin, end, accumulate);
+  else if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) mt_gather_kernel<float, uint16_t><<<grid, kThreads, 0, s>>>(table, nseg, (uint16_t*)dst, begin, end, 0);
+  else return lz_set_error(LZ_EINVAL, "lz_mt_gather: bad dtypes");
+  return lz_check_launch("lz_mt_gather");
+}
+
+LZ_EXPORT int lz_mt_scatter(const void* src, int src_dtype, const int64_t* table, int nseg, int dst_dtype, int64_t begin,
+                            int64_t end, void* stream) {
+  LZ_REQUIRE(table && nseg > 0 && begin <= end, "lz_mt_scatter: bad arguments");
+  if (begin == end) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  const int grid = (int)std::min<int64_t>(lz_cdiv(end - begin, kChunk), (int64_t)lz_num_cus() * 8);
+  if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) mt_scatter_kernel<float, uint16_t><<<grid, kThreads, 0, s>>>((const float*)src, table, nseg, begin, end);
+  else if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) mt_scatter_kernel<float, float><<<grid, kThreads, 0, s>>>((const float*)src, table, nseg, begin, end);
+  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_BF16) mt_scatter_kernel<uint16_t, uint16_t><<<grid, kThreads, 0, s>>>((const uint16_t*)src, table, nseg, begin, end);
+  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) mt_scatter_kernel<uint16_t, float><<<grid, kThreads, 0, s>>>((const uint16_t*)src, table, nseg, begin, end);
+  else return lz_set_error(LZ_EINVAL, "lz_mt_scatter: bad dtypes");
+  return lz_check_launch("lz_mt_scatter");
+}

@@ -1,0 +1,149 @@
+// SwiGLU pointwise part (reference: model/llama.py:136-146):
+//   h = silu(g) * u,   silu(g) = g / (1 + exp(-g))
+// with the reference's rounding in the activation dtype: silu's result is
+// rounded before the product, the product rounded again.  The backward
+// follows autograd of the same two ops:
+//   ds = r(dh * u),  du = r(dh * r(silu(g))),
+//   dg = r(ds * sig * (1 + g * (1 - sig))).
+// Gate and up may be two column ranges of one fused [T, 2*ffn] projection.
+// HBM-bound: forward 6 B/element (read g,u; write h), backward 10 B/element.
+#include "lz_common.h"
+
+namespace {
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+template <typename T>
+__global__ void swiglu_fwd_kernel(const T* __restrict__ g, int64_t ldg, const T* __restrict__ u, int64_t ldu,
+                                  T* __restrict__ h, int64_t ldh, int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / cols, c = idx - r * cols;
+    const float gv = Elem<T>::load(g + r * ldg, c);
+    const float uv = Elem<T>::load(u + r * ldu, c);
+    const float s = Elem<T>::round(silu_f(gv));
+    Elem<T>::store(h + r * ldh, c, s * uv);
+  }
+}
+
+// Vector path: 8 bf16 per thread (16-byte accesses).
+__global__ void swiglu_fwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t ldg, const uint16_t* __restrict__ u,
+                                         int64_t ldu, uint16_t* __restrict__ h, int64_t ldh, int64_t rows, int64_t cols) {
+  const int64_t cpr = cols >> 3;
+  const int64_t total = rows * cpr;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / cpr, c = (idx - r * cpr) << 3;
+    const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
+    const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float g0 = bf2f(gw[k] & 0xffff), g1 = bf2f(gw[k] >> 16);
+      const float u0 = bf2f(uw[k] & 0xffff), u1 = bf2f(uw[k] >> 16);
+      const float h0 = round_bf(silu_f(g0)) * u0, h1 = round_bf(silu_f(g1)) * u1;
+      ow[k] = (uint32_t)f2bf(h0) | ((uint32_t)f2bf(h1) << 16);
+    }
+    *reinterpret_cast<uint4*>(h + r * ldh + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void swiglu_bwd_elem(float gv, float uv, float dh, float& dg, float& du) {
+  const float sig = 1.0f / (1.0f + expf(-gv));
+  const float s = Elem<T>::round(gv / (1.0f + expf(-gv)));
+  const float ds = Elem<T>::round(dh * uv);
+  du = dh * s;
+  dg = ds * sig * (1.0f + gv * (1.0f - sig));
+}
+
+template <typename T>
+__global__ void swiglu_bwd_kernel(const T* __restrict__ g, int64_t ldg, const T* __restrict__ u, int64_t ldu,
+                                  const T* __restrict__ dh, int64_t lddh, T* __restrict__ dg, int64_t lddg,
+                                  T* __restrict__ du, int64_t lddu, int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / cols, c = idx - r * cols;
+    float a, b;
+    swiglu_bwd_elem<T>(Elem<T>::load(g + r * ldg, c), Elem<T>::load(u + r * ldu, c), Elem<T>::load(dh + r * lddh, c), a, b);
+    Elem<T>::store(dg + r * lddg, c, a);
+    Elem<T>::store(du + r * lddu, c, b);
+  }
+}
+
+__global__ void swiglu_bwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t ldg, const uint16_t* __restrict__ u,
+                                         int64_t ldu, const uint16_t* __restrict__ dh, int64_t lddh,
+                                         uint16_t* __restrict__ dg, int64_t lddg, uint16_t* __restrict__ du,
+                                         int64_t lddu, int64_t rows, int64_t cols) {
+  const int64_t cpr = cols >> 3;
+  const int64_t total = rows * cpr;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / cpr, c = (idx - r * cpr) << 3;
+    const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
+    const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
+    const uint4 hv = *reinterpret_cast<const uint4*>(dh + r * lddh + c);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    uint32_t ga[4], ua[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float dg0, du0, dg1, du1;
+      swiglu_bwd_elem<uint16_t>(bf2f(gw[k] & 0xffff), bf2f(uw[k] & 0xffff), bf2f(hw[k] & 0xffff), dg0, du0);
+      swiglu_bwd_elem<uint16_t>(bf2f(gw[k] >> 16), bf2f(uw[k] >> 16), bf2f(hw[k] >> 16), dg1, du1);
+      ga[k] = (uint32_t)f2bf(dg0) | ((uint32_t)f2bf(dg1) << 16);
+      ua[k] = (uint32_t)f2bf(du0) | ((uint32_t)f2bf(du1) << 16);
+    }
+    *reinterpret_cast<uint4*>(dg + r * lddg + c) = make_uint4(ga[0], ga[1], ga[2], ga[3]);
+    *reinterpret_cast<uint4*>(du + r * lddu + c) = make_uint4(ua[0], ua[1], ua[2], ua[3]);
+  }
+}
+
+inline int grid_for(int64_t n) {
+  int64_t b = lz_cdiv(n, 256);
+  int64_t cap = (int64_t)lz_num_cus() * 16;
+  return (int)std::max<int64_t>(1, std::min(b, cap));
+}
+
+inline bool vec_ok(const void* p, int64_t ld) { return lz_aligned16(p) && (ld % 8) == 0; }
+
+}  // namespace
+
+LZ_EXPORT int lz_swiglu_fwd(const void* g, int64_t ldg, const void* u, int64_t ldu, void* h, int64_t ldh, int64_t rows,
+                            int64_t cols, int dtype, void* stream) {
+  LZ_REQUIRE(rows >= 0 && cols >= 0 && ldg >= cols && ldu >= cols && ldh >= cols, "lz_swiglu_fwd: bad shape");
+  if (rows == 0 || cols == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_BF16) {
+    if (cols % 8 == 0 && vec_ok(g, ldg) && vec_ok(u, ldu) && vec_ok(h, ldh))
+      swiglu_fwd_bf16x8_kernel<<<grid_for(rows * cols / 8), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)h, ldh, rows, cols);
+    else
+      swiglu_fwd_kernel<uint16_t><<<grid_for(rows * cols), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)h, ldh, rows, cols);
+  } else if (dtype == LZ_F32) {
+    swiglu_fwd_kernel<float><<<grid_for(rows * cols), 256, 0, s>>>((const float*)g, ldg, (const float*)u, ldu, (float*)h, ldh, rows, cols);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_swiglu_fwd: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_swiglu_fwd");
+}
+
+LZ_EXPORT int lz_swiglu_bwd(const void* g, int64_t ldg, const void* u, int64_t ldu, const void* dh, int64_t lddh,
+                            void* dg, int64_t lddg, void* du, int64_t lddu, int64_t rows, int64_t cols, int dtype,
+                            void* stream) {
+  LZ_REQUIRE(rows >= 0 && cols >= 0 && ldg >= cols && ldu >= cols && lddh >= cols && lddg >= cols && lddu >= cols,
+             "lz_swiglu_bwd: bad shape");
+  if (rows == 0 || cols == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_BF16) {
+    if (cols % 8 == 0 && vec_ok(g, ldg) && vec_ok(u, ldu) && vec_ok(dh, lddh) && vec_ok(dg, lddg) && vec_ok(du, lddu))
+      swiglu_bwd_bf16x8_kernel<<<grid_for(rows * cols / 8), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (const uint16_t*)dh, lddh, (uint16_t*)dg, lddg, (uint16_t*)du, lddu, rows, cols);
+    else
+      swiglu_bwd_kernel<uint16_t><<<grid_for(rows * cols), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (const uint16_t*)dh, lddh, (uint16_t*)dg, lddg, (uint16_t*)du, lddu, rows, cols);
+  } else if (dtype == LZ_F32) {
+    swiglu_bwd_kernel<float><<<grid_for(rows * cols), 256, 0, s>>>((const float*)g, ldg, (const float*)u, ldu, (const float*)dh, lddh, (float*)dg, lddg, (float*)du, lddu, rows, cols);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_swiglu_bwd: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_swiglu_bwd");
+}

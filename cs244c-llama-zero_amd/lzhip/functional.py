@@ -1,0 +1,306 @@
+"""Autograd functions of the LLaMA training step, each backed by the HIP kernels.
+
+The model modules call these; every forward and backward pass below runs the
+gfx950 kernels of libllamazero_hip.so (through lzhip.ops).  Activations are 2-D
+row views [tokens, features]; projections that the reference computes as
+separate nn.Linear calls on the same input (q/k/v, gate/up) run as one GEMM
+over the concatenated weight rows.
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+from torch.autograd import Function
+
+from . import ops
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """[..., C] -> [rows, C] view (copies only if the layout cannot be viewed)."""
+    if not t.is_contiguous():
+        t = t.contiguous()
+    return t.view(-1, t.shape[-1])
+
+
+def fused_weight(weights: Sequence[torch.Tensor]) -> torch.Tensor:
+    """Concatenation of weight matrices along their output rows.  When the
+    storages are already adjacent (parameters that are views of one flat
+    buffer in registration order) this is a view; otherwise a copy."""
+    w0 = weights[0]
+    if len(weights) == 1:
+        return w0
+    k = w0.shape[1]
+    n_total = sum(w.shape[0] for w in weights)
+    adjacent = all(w.is_contiguous() and w.dtype == w0.dtype and w.shape[1] == k for w in weights)
+    if adjacent:
+        expect = w0.data_ptr()
+        for w in weights:
+            if w.data_ptr() != expect:
+                adjacent = False
+                break
+            expect += w.numel() * w.element_size()
+    if adjacent:
+        return w0.as_strided((n_total, k), (k, 1), w0.storage_offset())
+    out = torch.empty((n_total, k), dtype=w0.dtype, device=w0.device)
+    r = 0
+    for w in weights:
+        ops.copy2d(w.view(w.shape[0], k), out[r : r + w.shape[0]])
+        r += w.shape[0]
+    return out
+
+
+def _linear_fwd(x2: torch.Tensor, w: torch.Tensor, residual2: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return ops.gemm_nt(ops.nt_operand(x2), ops.nt_operand(w), residual=residual2)
+
+
+def _linear_bwd(dy2: torch.Tensor, x2: torch.Tensor, w: torch.Tensor, need_dx: bool, need_dw: bool
+                ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """dx = dy . W (NT against W^T), dW = dy^T . x (NT against x^T)."""
+    dx = dw = None
+    if need_dx:
+        wt = ops.transpose_padded(w)              # [K, N8]
+        dx = ops.gemm_nt(ops.nt_operand(dy2), wt)  # [M, K]
+    if need_dw:
+        dyt = ops.transpose_padded(dy2)           # [N, M8]
+        xt = ops.transpose_padded(x2)             # [K, M8]
+        dw = ops.gemm_nt(dyt, xt, out_dtype=w.dtype)  # [N, K]
+    return dx, dw
+
+
+class LinearFn(Function):
+    """y = x . W^T (+ residual) — nn.Linear without bias (model/llama.py:81-84,
+    133, 139-141, 178) with the block's residual add folded into the GEMM
+    epilogue (model/llama.py:158-159)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor]):
+        x2 = _rows(x)
+        r2 = _rows(residual) if residual is not None else None
+        y = _linear_fwd(x2, weight, r2)
+        ctx.save_for_backward(x2, weight)
+        ctx.has_residual = residual is not None
+        ctx.in_shape = x.shape
+        return y.view(*x.shape[:-1], weight.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        x2, weight = ctx.saved_tensors
+        dy2 = _rows(dy)
+        dx, dw = _linear_bwd(dy2, x2, weight, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        if dx is not None:
+            dx = dx.view(ctx.in_shape)
+        dres = dy if (ctx.has_residual and ctx.needs_input_grad[2]) else None
+        return dx, dw, dres
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return LinearFn.apply(x, weight, residual)
+
+
+class RMSNormFn(Function):
+    """RMSNorm (model/llama.py:14-22) forward/backward kernels."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
+        x2 = _rows(x)
+        y, rstd = ops.rmsnorm_fwd(x2, weight, eps)
+        ctx.save_for_backward(x2, weight, rstd)
+        ctx.in_shape = x.shape
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        x2, weight, rstd = ctx.saved_tensors
+        dx, dw = ops.rmsnorm_bwd(x2, weight, rstd, _rows(dy), need_dw=ctx.needs_input_grad[1])
+        return dx.view(ctx.in_shape), dw, None
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    return RMSNormFn.apply(x, weight, eps)
+
+
+class RopeFn(Function):
+    """apply_rotary_pos_emb on a [..., S, hd] tensor (model/llama.py:25-39)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+        seq, hd = x.shape[-2], x.shape[-1]
+        out = x.contiguous().clone() if x.is_contiguous() else x.contiguous()
+        ops.rope_(out.view(-1, hd), seq, 1, hd, cos, sin)
+        ctx.save_for_backward(cos, sin)
+        ctx.seq, ctx.hd = seq, hd
+        return out
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        cos, sin = ctx.saved_tensors
+        g = dy.contiguous().clone() if dy.is_contiguous() else dy.contiguous()
+        ops.rope_(g.view(-1, ctx.hd), ctx.seq, 1, ctx.hd, cos, sin, backward=True)
+        return g, None, None
+
+
+class AttnProjFn(Function):
+    """Fused QKV projection + RoPE + causal GQA flash attention
+    (model/llama.py:95-117).  Input h [B, S, d] (the normed residual stream),
+    weights Wq [H*hd, d], Wk/Wv [KV*hd, d]; returns the attention output
+    [B, S, H*hd] that o_proj consumes."""
+
+    @staticmethod
+    def forward(ctx, h, wq, wk, wv, cos, sin, n_heads: int, n_kv: int, scale: float):
+        B, S, d = h.shape
+        hd = wq.shape[0] // n_heads
+        h2 = _rows(h)
+        w = fused_weight([wq, wk, wv])
+        qkv = _linear_fwd(h2, w)                         # [B*S, (H+2KV)*hd]
+        ops.rope_(qkv, S, n_heads + n_kv, hd, cos, sin)  # q and k heads, in place
+        H, KV = n_heads, n_kv
+        q2 = qkv[:, : H * hd]
+        k2 = qkv[:, H * hd : (H + KV) * hd]
+        v2 = qkv[:, (H + KV) * hd :]
+        ld = qkv.shape[1]
+        vt = None
+        if ops.attn_uses_mfma(qkv.dtype, hd, ld, ld, ld, H * hd):
+            vt = ops.transpose_heads(qkv, B, S, KV, hd, col0=(H + KV) * hd)
+        o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
+        ctx.save_for_backward(h2, wq, wk, wv, qkv, o, lse, cos, sin)
+        ctx.meta = (B, S, H, KV, hd, scale)
+        return o.view(B, S, H * hd)
+
+    @staticmethod
+    def backward(ctx, do):
+        h2, wq, wk, wv, qkv, o, lse, cos, sin = ctx.saved_tensors
+        B, S, H, KV, hd, scale = ctx.meta
+        do2 = _rows(do)
+        ld = qkv.shape[1]
+        dqkv = torch.empty_like(qkv)
+        qt = kt = dot = None
+        if ops.attn_uses_mfma(qkv.dtype, hd, ld, ld, ld, do2.stride(0)):
+            qt = ops.transpose_heads(qkv, B, S, H, hd, col0=0)
+            kt = ops.transpose_heads(qkv, B, S, KV, hd, col0=H * hd)
+            dot = ops.transpose_heads(do2, B, S, H, hd, col0=0)
+        ops.attn_bwd(
+            qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :], o, do2, lse,
+            B, S, H, KV, hd, scale,
+            dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :],
+            qt=qt, kt=kt, dot=dot,
+        )
+        ops.rope_(dqkv, S, H + KV, hd, cos, sin, backward=True)
+        need_w = any(ctx.needs_input_grad[1:4])
+        w = fused_weight([wq, wk, wv])
+        dh2, dw = _linear_bwd(dqkv, h2, w, ctx.needs_input_grad[0], need_w)
+        dwq = dwk = dwv = None
+        if dw is not None:
+            nq, nk = wq.shape[0], wk.shape[0]
+            dwq, dwk, dwv = dw[:nq], dw[nq : nq + nk], dw[nq + nk :]
+        dh = dh2.view(B, S, -1) if dh2 is not None else None
+        return dh, dwq, dwk, dwv, None, None, None, None, None
+
+
+class MLPFn(Function):
+    """SwiGLU MLP (model/llama.py:136-146): down(silu(gate x) * up x), gate and
+    up as one GEMM, with an optional residual added in the down projection's
+    epilogue."""
+
+    @staticmethod
+    def forward(ctx, x, wg, wu, wd, residual):
+        x2 = _rows(x)
+        F_ = wg.shape[0]
+        w = fused_weight([wg, wu])
+        gu = _linear_fwd(x2, w)                 # [T, 2F]
+        m = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
+        r2 = _rows(residual) if residual is not None else None
+        y = _linear_fwd(m, wd, r2)
+        ctx.save_for_backward(x2, wg, wu, wd, gu, m)
+        ctx.has_residual = residual is not None
+        ctx.in_shape = x.shape
+        return y.view(*x.shape[:-1], wd.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, wg, wu, wd, gu, m = ctx.saved_tensors
+        F_ = wg.shape[0]
+        dy2 = _rows(dy)
+        dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3])
+        dgu = torch.empty_like(gu)
+        ops.swiglu_bwd(gu[:, :F_], gu[:, F_:], dm, dgu[:, :F_], dgu[:, F_:])
+        w = fused_weight([wg, wu])
+        need_w = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
+        dx2, dw = _linear_bwd(dgu, x2, w, ctx.needs_input_grad[0], need_w)
+        dwg = dwu = None
+        if dw is not None:
+            dwg, dwu = dw[:F_], dw[F_:]
+        dx = dx2.view(ctx.in_shape) if dx2 is not None else None
+        dres = dy if (ctx.has_residual and ctx.needs_input_grad[4]) else None
+        return dx, dwg, dwu, dwd, dres
+
+
+class SwiGLUPointwiseFn(Function):
+    """silu(g) * u alone (for callers that keep the projections separate)."""
+
+    @staticmethod
+    def forward(ctx, g, u):
+        h = ops.swiglu_fwd(_rows(g), _rows(u))
+        ctx.save_for_backward(g, u)
+        return h.view(g.shape)
+
+    @staticmethod
+    def backward(ctx, dh):
+        g, u = ctx.saved_tensors
+        g2, u2 = _rows(g), _rows(u)
+        dg = torch.empty_like(g2)
+        du = torch.empty_like(u2)
+        ops.swiglu_bwd(g2, u2, _rows(dh), dg, du)
+        return dg.view(g.shape), du.view(u.shape)
+
+
+class EmbeddingFn(Function):
+    """Token embedding lookup (model/llama.py:174,212)."""
+
+    @staticmethod
+    def forward(ctx, ids, weight):
+        out = ops.embedding_fwd(ids, weight)
+        ctx.save_for_backward(ids)
+        ctx.vocab, ctx.dtype = weight.shape[0], weight.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (ids,) = ctx.saved_tensors
+        if not ctx.needs_input_grad[1]:
+            return None, None
+        grad = ops.embedding_bwd(ids, _rows(dout), ctx.vocab, ctx.dtype)
+        return None, grad
+
+
+class CrossEntropyFn(Function):
+    """Mean shifted cross entropy of [B, S, V] logits against labels [B, S]
+    (model/llama.py:273-302).  clamp=True divides by max(count, 1) (the chunked
+    variant); clamp=False divides by count (F.cross_entropy's mean).  With
+    inplace=True the backward writes the logits gradient over the saved logits
+    (only when no one else reads them)."""
+
+    @staticmethod
+    def forward(ctx, logits, labels, clamp: bool, inplace: bool):
+        B, S, V = logits.shape
+        l2 = _rows(logits)
+        lab = labels.contiguous()
+        lse, row_loss = ops.ce_fwd(l2, lab, S)
+        loss, count = ops.ce_reduce(row_loss, lab, B * S, S, V, clamp)
+        ctx.save_for_backward(l2, lab, lse, count)
+        ctx.shape = (B, S, V)
+        ctx.inplace = inplace
+        return loss
+
+    @staticmethod
+    def backward(ctx, gloss):
+        l2, lab, lse, count = ctx.saved_tensors
+        B, S, V = ctx.shape
+        out = l2 if ctx.inplace else None
+        d = ops.ce_bwd(l2, lab, S, lse, gloss.reshape(1), count, out=out)
+        return d.view(B, S, V), None, None, None
+
+
+def cross_entropy(logits: torch.Tensor, labels: torch.Tensor, clamp: bool, inplace: bool = False) -> torch.Tensor:
+    return CrossEntropyFn.apply(logits, labels, clamp, inplace)

@@ -1,0 +1,463 @@
+"""Tensor-level wrappers over the C ABI.
+
+Every function takes and returns torch tensors that live on a ROCm GPU,
+validates shapes/dtypes/strides on the host, allocates outputs from torch's
+caching allocator and enqueues the HIP kernel on torch's current stream.  A CPU
+tensor or an unsupported dtype raises: there is no fallback computation.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F32
+
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"llama-zero HIP kernels support float32 and bfloat16 tensors, got {t.dtype}") from None
+
+
+def require_gpu(*tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                f"llama-zero HIP kernels run on a ROCm GPU; got a tensor on {t.device}. "
+                "Move the model and inputs to 'cuda'."
+            )
+
+
+def stream_ptr(device: Optional[torch.device] = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _row_stride(t: torch.Tensor) -> int:
+    """Leading dimension of a 2-D row-major view (last stride must be 1)."""
+    if t.dim() != 2:
+        raise ValueError(f"expected a 2-D view, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.size(1) > 1:
+        raise ValueError("expected unit stride in the last dimension")
+    return max(t.stride(0), t.size(1)) if t.size(0) > 1 else t.size(1)
+
+
+# ---------------------------------------------------------------------------
+# optimizer path
+# ---------------------------------------------------------------------------
+
+def adamw_(
+    p: torch.Tensor,
+    m: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    step: int,
+    grad_scale: Optional[torch.Tensor] = None,
+    p_out: Optional[torch.Tensor] = None,
+) -> None:
+    """In-place fused AdamW on flat fp32 p/m/v with gradient g (fp32 or bf16)."""
+    require_gpu(p, m, v, g, grad_scale, p_out)
+    n = p.numel()
+    for t, name in ((m, "exp_avg"), (v, "exp_avg_sq"), (g, "grad")):
+        if t.numel() != n:
+            raise ValueError(f"{name} has {t.numel()} elements, expected {n}")
+    for t in (p, m, v):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("AdamW master/moment buffers must be contiguous float32")
+    if not g.is_contiguous():
+        raise ValueError("gradient must be contiguous")
+    if grad_scale is not None and (grad_scale.dtype != torch.float32 or grad_scale.numel() < 1):
+        raise ValueError("grad_scale must be a float32 device scalar")
+    if p_out is not None and (p_out.numel() != n or not p_out.is_contiguous()):
+        raise ValueError("p_out must be contiguous with the same number of elements")
+    _lib.call(
+        "lz_adamw",
+        p.data_ptr(), m.data_ptr(), v.data_ptr(), g.data_ptr(), dtype_code(g),
+        _ptr(p_out), dtype_code(p_out) if p_out is not None else F32, n,
+        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(step),
+        _ptr(grad_scale), stream_ptr(p.device),
+    )
+
+
+def sumsq_(x: torch.Tensor, acc: torch.Tensor) -> None:
+    """acc (float64 device scalar) += sum(x^2)."""
+    require_gpu(x, acc)
+    if acc.dtype != torch.float64:
+        raise ValueError("accumulator must be float64")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous")
+    _lib.call("lz_sumsq", x.data_ptr(), dtype_code(x), x.numel(), acc.data_ptr(), stream_ptr(x.device))
+
+
+def clip_finalize(acc: torch.Tensor, max_norm: float, norm_out: torch.Tensor, scale_out: torch.Tensor) -> None:
+    require_gpu(acc, norm_out, scale_out)
+    _lib.call(
+        "lz_clip_finalize", acc.data_ptr(), float(max_norm), norm_out.data_ptr(), scale_out.data_ptr(),
+        stream_ptr(acc.device),
+    )
+
+
+def fill_(x: torch.Tensor, value: float) -> torch.Tensor:
+    require_gpu(x)
+    if not x.is_contiguous():
+        raise ValueError("fill_ needs a contiguous tensor")
+    _lib.call("lz_fill", x.data_ptr(), dtype_code(x), x.numel(), float(value), stream_ptr(x.device))
+    return x
+
+
+def zeros(shape, dtype: torch.dtype, device) -> torch.Tensor:
+    t = torch.empty(shape, dtype=dtype, device=device)
+    if t.numel():
+        fill_(t, 0.0)
+    return t
+
+
+def cast(src: torch.Tensor, dtype: torch.dtype, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    require_gpu(src, out)
+    if not src.is_contiguous():
+        raise ValueError("cast needs a contiguous source")
+    if out is None:
+        out = torch.empty(src.shape, dtype=dtype, device=src.device)
+    if out.numel() != src.numel() or not out.is_contiguous():
+        raise ValueError("cast output must be contiguous with the same number of elements")
+    _lib.call("lz_cast", src.data_ptr(), dtype_code(src), out.data_ptr(), dtype_code(out), src.numel(),
+              stream_ptr(src.device))
+    return out
+
+
+def axpy_f32_(dst: torch.Tensor, src: torch.Tensor, alpha: float = 1.0) -> None:
+    require_gpu(dst, src)
+    if dst.dtype != torch.float32 or not dst.is_contiguous() or not src.is_contiguous():
+        raise ValueError("axpy_f32_ needs a contiguous float32 destination and contiguous source")
+    if dst.numel() != src.numel():
+        raise ValueError(f"size mismatch {dst.numel()} vs {src.numel()}")
+    _lib.call("lz_axpy_f32", dst.data_ptr(), src.data_ptr(), dtype_code(src), dst.numel(), float(alpha),
+              stream_ptr(dst.device))
+
+
+def add_(dst: torch.Tensor, src: torch.Tensor) -> None:
+    require_gpu(dst, src)
+    if dst.dtype != src.dtype or dst.numel() != src.numel() or not dst.is_contiguous() or not src.is_contiguous():
+        raise ValueError("add_ needs contiguous tensors of one dtype and size")
+    _lib.call("lz_add_inplace", dst.data_ptr(), src.data_ptr(), dtype_code(dst), dst.numel(), stream_ptr(dst.device))
+
+
+def scale_(x: torch.Tensor, alpha: float) -> None:
+    require_gpu(x)
+    if not x.is_contiguous():
+        raise ValueError("scale_ needs a contiguous tensor")
+    _lib.call("lz_scale_inplace", x.data_ptr(), dtype_code(x), x.numel(), float(alpha), stream_ptr(x.device))
+
+
+class SegmentTable:
+    """Device table of {ptr, numel, flat_offset} records for the multi-tensor
+    gather/scatter kernels.  Built on the host, uploaded once per call site."""
+
+    def __init__(self, records: Sequence[Tuple[int, int, int]], device: torch.device) -> None:
+        if not records:
+            raise ValueError("empty segment table")
+        host = torch.tensor([v for rec in records for v in rec], dtype=torch.int64)
+        self.nseg = len(records)
+        self.device = device
+        self.tensor = host.to(device, non_blocking=False)
+
+    @classmethod
+    def from_tensors(cls, tensors: Sequence[Optional[torch.Tensor]], offsets: Sequence[int],
+                     numels: Sequence[int], device: torch.device) -> "SegmentTable":
+        recs = []
+        for t, off, n in zip(tensors, offsets, numels):
+            if t is not None:
+                require_gpu(t)
+                if not t.is_contiguous():
+                    raise ValueError("segment tensors must be contiguous")
+                if t.numel() != n:
+                    raise ValueError(f"segment has {t.numel()} elements, expected {n}")
+            recs.append((0 if t is None else t.data_ptr(), int(n), int(off)))
+        return cls(recs, device)
+
+
+def mt_gather(table: SegmentTable, src_dtype: torch.dtype, dst: torch.Tensor, begin: int, end: int,
+              accumulate: bool = False) -> None:
+    require_gpu(dst)
+    if dst.numel() < end - begin or not dst.is_contiguous():
+        raise ValueError("gather destination too small or not contiguous")
+    _lib.call("lz_mt_gather", table.tensor.data_ptr(), table.nseg, _DTYPES[src_dtype], dst.data_ptr(),
+              dtype_code(dst), int(begin), int(end), int(bool(accumulate)), stream_ptr(dst.device))
+
+
+def mt_scatter(src: torch.Tensor, table: SegmentTable, dst_dtype: torch.dtype, begin: int, end: int) -> None:
+    require_gpu(src)
+    if src.numel() < end - begin or not src.is_contiguous():
+        raise ValueError("scatter source too small or not contiguous")
+    _lib.call("lz_mt_scatter", src.data_ptr(), dtype_code(src), table.tensor.data_ptr(), table.nseg,
+              _DTYPES[dst_dtype], int(begin), int(end), stream_ptr(src.device))
+
+
+# ---------------------------------------------------------------------------
+# model ops
+# ---------------------------------------------------------------------------
+
+def rmsnorm_fwd(x2: torch.Tensor, w: torch.Tensor, eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    require_gpu(x2, w)
+    rows, cols = x2.shape
+    if w.numel() != cols or w.dtype != x2.dtype or not w.is_contiguous():
+        raise ValueError("RMSNorm weight must be contiguous, of the activation dtype and size dim")
+    y = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
+    rstd = torch.empty((rows,), dtype=torch.float32, device=x2.device)
+    _lib.call("lz_rmsnorm_fwd", x2.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr(), dtype_code(x2), rows, cols,
+              _row_stride(x2), cols, float(eps), stream_ptr(x2.device))
+    return y, rstd
+
+
+def rmsnorm_bwd(x2: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy2: torch.Tensor,
+                dres: Optional[torch.Tensor] = None, need_dw: bool = True) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    require_gpu(x2, w, rstd, dy2, dres)
+    rows, cols = x2.shape
+    dx = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
+    dw = torch.empty((cols,), dtype=w.dtype, device=w.device) if need_dw else None
+    lib = _lib.load()
+    ws_bytes = int(lib.lz_rmsnorm_bwd_workspace(rows, cols))
+    ws = torch.empty((max(ws_bytes, 16) + 3) // 4, dtype=torch.float32, device=x2.device)
+    if dres is not None and (dres.shape != dx.shape or dres.dtype != dx.dtype):
+        raise ValueError("residual gradient must match dx")
+    _lib.call("lz_rmsnorm_bwd", x2.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(), _ptr(dres), dx.data_ptr(),
+              _ptr(dw), 0, ws.data_ptr(), ws.numel() * 4, dtype_code(x2), rows, cols, _row_stride(x2),
+              _row_stride(dy2), cols if dres is None else _row_stride(dres), stream_ptr(x2.device))
+    return dx, dw
+
+
+def rope_table(seq: int, hd: int, inv_freq: torch.Tensor, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin [seq, hd] in `dtype` from the hd/2 inverse frequencies; the
+    position and angle are formed in inv_freq's dtype."""
+    require_gpu(inv_freq)
+    if inv_freq.numel() != hd // 2 or not inv_freq.is_contiguous():
+        raise ValueError("inv_freq must hold hd/2 contiguous values")
+    cos = torch.empty((seq, hd), dtype=dtype, device=inv_freq.device)
+    sin = torch.empty((seq, hd), dtype=dtype, device=inv_freq.device)
+    _lib.call("lz_rope_table", cos.data_ptr(), sin.data_ptr(), _DTYPES[dtype], seq, hd, inv_freq.data_ptr(),
+              dtype_code(inv_freq), stream_ptr(cos.device))
+    return cos, sin
+
+
+def rope_(x2: torch.Tensor, seq: int, nheads: int, hd: int, cos: torch.Tensor, sin: torch.Tensor,
+          backward: bool = False, pos_offset: int = 0) -> None:
+    """In place on the first nheads*hd columns of every row of x2 (rows b*S+s)."""
+    require_gpu(x2, cos, sin)
+    if cos.dtype != x2.dtype or sin.dtype != x2.dtype:
+        raise ValueError("RoPE tables must have the activation dtype")
+    if cos.size(0) < seq + pos_offset or cos.size(1) != hd:
+        raise ValueError("RoPE table too short")
+    rows = x2.size(0)
+    _lib.call("lz_rope", x2.data_ptr(), dtype_code(x2), _row_stride(x2), rows, seq, nheads, hd, cos.data_ptr(),
+              sin.data_ptr(), int(pos_offset), int(bool(backward)), stream_ptr(x2.device))
+
+
+def swiglu_fwd(g2: torch.Tensor, u2: torch.Tensor) -> torch.Tensor:
+    require_gpu(g2, u2)
+    rows, cols = g2.shape
+    h = torch.empty((rows, cols), dtype=g2.dtype, device=g2.device)
+    _lib.call("lz_swiglu_fwd", g2.data_ptr(), _row_stride(g2), u2.data_ptr(), _row_stride(u2), h.data_ptr(), cols,
+              rows, cols, dtype_code(g2), stream_ptr(g2.device))
+    return h
+
+
+def swiglu_bwd(g2: torch.Tensor, u2: torch.Tensor, dh2: torch.Tensor, dg2: torch.Tensor, du2: torch.Tensor) -> None:
+    require_gpu(g2, u2, dh2, dg2, du2)
+    rows, cols = g2.shape
+    _lib.call("lz_swiglu_bwd", g2.data_ptr(), _row_stride(g2), u2.data_ptr(), _row_stride(u2), dh2.data_ptr(),
+              _row_stride(dh2), dg2.data_ptr(), _row_stride(dg2), du2.data_ptr(), _row_stride(du2), rows, cols,
+              dtype_code(g2), stream_ptr(g2.device))
+
+
+def embedding_fwd(ids: torch.Tensor, table: torch.Tensor, bad_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    require_gpu(ids, table)
+    if ids.dtype != torch.int64:
+        raise TypeError("token ids must be int64")
+    ids_c = ids.contiguous()
+    vocab, dim = table.shape
+    out = torch.empty((*ids.shape, dim), dtype=table.dtype, device=table.device)
+    _lib.call("lz_embedding_fwd", ids_c.data_ptr(), ids_c.numel(), table.data_ptr(), vocab, dim, out.data_ptr(), dim,
+              dtype_code(table), _ptr(bad_flag), stream_ptr(table.device))
+    return out
+
+
+def embedding_bwd(ids: torch.Tensor, dout2: torch.Tensor, vocab: int, dtype: torch.dtype,
+                  grad: Optional[torch.Tensor] = None) -> torch.Tensor:
+    require_gpu(ids, dout2)
+    ids_c = ids.contiguous()
+    dim = dout2.size(1)
+    out = torch.empty((vocab, dim), dtype=dtype, device=dout2.device) if grad is None else grad
+    ws = torch.empty((vocab * dim,), dtype=torch.float32, device=dout2.device)
+    _lib.call("lz_embedding_bwd", ids_c.data_ptr(), ids_c.numel(), dout2.data_ptr(), _row_stride(dout2), vocab, dim,
+              out.data_ptr(), int(grad is not None), ws.data_ptr(), _DTYPES[dtype], stream_ptr(dout2.device))
+    return out
+
+
+def transpose2d(src: torch.Tensor, out: Optional[torch.Tensor] = None, ld_out: Optional[int] = None) -> torch.Tensor:
+    """dst[c, r] = src[r, c] for a 2-D row-major view."""
+    require_gpu(src)
+    rows, cols = src.shape
+    if out is None:
+        ld = ld_out or rows
+        out = torch.empty((cols, ld), dtype=src.dtype, device=src.device)
+    ld = out.stride(0)
+    _lib.call("lz_transpose", src.data_ptr(), out.data_ptr(), dtype_code(src), 1, 1, rows, cols, _row_stride(src), 0, 0,
+              ld, 0, 0, stream_ptr(src.device))
+    return out
+
+
+def transpose_heads(x2: torch.Tensor, B: int, S: int, nheads: int, hd: int, col0: int = 0) -> torch.Tensor:
+    """[B*S, ld] rows holding heads at columns col0 + h*hd  ->  [B, nheads, hd, S]."""
+    require_gpu(x2)
+    ld = _row_stride(x2)
+    out = torch.empty((B, nheads, hd, S), dtype=x2.dtype, device=x2.device)
+    base = x2.data_ptr() + col0 * x2.element_size()
+    _lib.call("lz_transpose", base, out.data_ptr(), dtype_code(x2), B, nheads, S, hd, ld, S * ld, hd, S,
+              nheads * hd * S, hd * S, stream_ptr(x2.device))
+    return out
+
+
+def copy2d(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+    """dst[:rows, :cols] = src for two 2-D row-major views of one dtype."""
+    require_gpu(src, dst)
+    if src.dtype != dst.dtype:
+        raise ValueError("copy2d needs one dtype")
+    rows, cols = src.shape
+    _lib.call("lz_copy2d", src.data_ptr(), _row_stride(src), dst.data_ptr(), _row_stride(dst), rows, cols,
+              dtype_code(src), stream_ptr(src.device))
+    return dst
+
+
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+def nt_operand(t2: torch.Tensor) -> torch.Tensor:
+    """Returns t2, or a zero-padded copy, as a [rows, K8] view whose leading
+    dimension and reduction length are multiples of 8 with a 16-byte aligned
+    base (what the MFMA GEMM requires).  Padding columns are zero, so they do
+    not change the product."""
+    rows, k = t2.shape
+    ld = _row_stride(t2)
+    if k % 8 == 0 and ld % 8 == 0 and t2.data_ptr() % 16 == 0:
+        return t2
+    k8 = _round8(k)
+    buf = torch.empty((rows, k8), dtype=t2.dtype, device=t2.device)
+    if k8 != k:
+        fill_(buf, 0.0)
+    copy2d(t2, buf[:, :k])
+    return buf
+
+
+def transpose_padded(src2: torch.Tensor) -> torch.Tensor:
+    """[R, C] -> [C, R8] with zero columns R..R8 (an NT operand whose reduction
+    dimension is R)."""
+    rows, cols = src2.shape
+    r8 = _round8(rows)
+    out = torch.empty((cols, r8), dtype=src2.dtype, device=src2.device)
+    if r8 != rows:
+        fill_(out, 0.0)
+    transpose2d(src2, out=out)
+    return out
+
+
+def gemm_nt(a2: torch.Tensor, b2: torch.Tensor, out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+            residual: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """out[M,N] = alpha * a2[M,K] . b2[N,K]^T (+ beta*out) (+ residual)."""
+    require_gpu(a2, b2, out, residual)
+    if a2.dtype != torch.bfloat16 or b2.dtype != torch.bfloat16:
+        raise TypeError(
+            f"the MFMA GEMM takes bfloat16 operands (got {a2.dtype}, {b2.dtype}); "
+            "run the model in bfloat16 (--dtype bfloat16)"
+        )
+    M, K = a2.shape
+    N, K2 = b2.shape
+    if K != K2:
+        raise ValueError(f"GEMM reduction mismatch {K} vs {K2}")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or a2.dtype, device=a2.device)
+    if residual is not None and (residual.dtype != torch.bfloat16 or tuple(residual.shape) != (M, N)):
+        raise ValueError("residual must be a bf16 [M, N] view")
+    _lib.call("lz_gemm_nt", a2.data_ptr(), _row_stride(a2), b2.data_ptr(), _row_stride(b2), out.data_ptr(),
+              _row_stride(out), dtype_code(out), _ptr(residual), _row_stride(residual) if residual is not None else 0,
+              M, N, K, float(alpha), float(beta), stream_ptr(a2.device))
+    return out
+
+
+def ce_fwd(logits2: torch.Tensor, labels: torch.Tensor, seq: int, ignore_index: int = -100
+           ) -> Tuple[torch.Tensor, torch.Tensor]:
+    require_gpu(logits2, labels)
+    rows, vocab = logits2.shape
+    lse = torch.empty((rows,), dtype=torch.float32, device=logits2.device)
+    row_loss = torch.empty((rows,), dtype=torch.float32, device=logits2.device)
+    _lib.call("lz_ce_fwd", logits2.data_ptr(), _row_stride(logits2), rows, vocab, dtype_code(logits2),
+              labels.data_ptr(), seq, ignore_index, lse.data_ptr(), row_loss.data_ptr(), stream_ptr(logits2.device))
+    return lse, row_loss
+
+
+def ce_reduce(row_loss: torch.Tensor, labels: torch.Tensor, rows: int, seq: int, vocab: int, clamp: bool,
+              ignore_index: int = -100) -> Tuple[torch.Tensor, torch.Tensor]:
+    loss = torch.empty((), dtype=torch.float32, device=row_loss.device)
+    count = torch.empty((), dtype=torch.float32, device=row_loss.device)
+    _lib.call("lz_ce_reduce", row_loss.data_ptr(), labels.data_ptr(), rows, seq, vocab, ignore_index, loss.data_ptr(),
+              count.data_ptr(), int(bool(clamp)), stream_ptr(row_loss.device))
+    return loss, count
+
+
+def ce_bwd(logits2: torch.Tensor, labels: torch.Tensor, seq: int, lse: torch.Tensor, grad_loss: torch.Tensor,
+           count: torch.Tensor, out: Optional[torch.Tensor] = None, ignore_index: int = -100) -> torch.Tensor:
+    require_gpu(logits2, labels, lse, grad_loss, count, out)
+    rows, vocab = logits2.shape
+    if out is None:
+        out = torch.empty((rows, vocab), dtype=logits2.dtype, device=logits2.device)
+    g = grad_loss.to(torch.float32) if grad_loss.dtype != torch.float32 else grad_loss
+    g = g.contiguous()
+    _lib.call("lz_ce_bwd", logits2.data_ptr(), _row_stride(logits2), rows, vocab, dtype_code(logits2), labels.data_ptr(),
+              seq, ignore_index, lse.data_ptr(), g.data_ptr(), count.data_ptr(), out.data_ptr(), _row_stride(out),
+              dtype_code(out), stream_ptr(logits2.device))
+    return out
+
+
+def attn_uses_mfma(dtype: torch.dtype, hd: int, ldq: int, ldk: int, ldv: int, ldo: int) -> bool:
+    if dtype not in _DTYPES:
+        return False
+    return bool(_lib.load().lz_attn_uses_mfma(_DTYPES[dtype], hd, ldq, ldk, ldv, ldo))
+
+
+def attn_fwd(q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, B: int, S: int, H: int, KV: int, hd: int,
+             scale: float, vt: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """q2/k2/v2: [B*S, ld] row views (head h at columns h*hd).  Returns
+    o [B*S, H*hd] and lse [B, H, S]."""
+    require_gpu(q2, k2, v2, vt)
+    o = torch.empty((B * S, H * hd), dtype=q2.dtype, device=q2.device)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
+    _lib.call("lz_attn_fwd", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
+              _row_stride(v2), _ptr(vt), o.data_ptr(), H * hd, lse.data_ptr(), B, S, H, KV, hd, float(scale),
+              dtype_code(q2), stream_ptr(q2.device))
+    return o, lse
+
+
+def attn_bwd(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt=None, kt=None, dot=None) -> None:
+    require_gpu(q2, k2, v2, o2, do2, lse, dq2, dk2, dv2)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
+    _lib.call("lz_attn_delta", o2.data_ptr(), _row_stride(o2), do2.data_ptr(), _row_stride(do2), delta.data_ptr(),
+              B, S, H, hd, dtype_code(o2), stream_ptr(q2.device))
+    _lib.call("lz_attn_bwd", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
+              _row_stride(v2), do2.data_ptr(), _row_stride(do2), lse.data_ptr(), delta.data_ptr(), _ptr(qt), _ptr(kt),
+              _ptr(dot), dq2.data_ptr(), _row_stride(dq2), dk2.data_ptr(), _row_stride(dk2), dv2.data_ptr(),
+              _row_stride(dv2), B, S, H, KV, hd, float(scale), dtype_code(q2), stream_ptr(q2.device))

@@ -1,0 +1,180 @@
+/*
+ * llamazero_hip.h — C ABI of libllamazero_hip.so, the gfx950 (MI355X) kernels
+ * behind the single-GPU LLaMA training step of the llama-zero harness.
+ *
+ * Conventions shared by every entry point:
+ *   - pointers are device pointers; sizes and leading dimensions are element
+ *     counts (int64_t); `stream` is a hipStream_t passed as void*;
+ *   - work is enqueued asynchronously on `stream`; nothing here synchronizes
+ *     the host;
+ *   - return 0 on success, a negative status on invalid arguments (-1) or a
+ *     launch failure (-2); lz_last_error() returns the calling thread's last
+ *     message;
+ *   - nothing allocates device memory: every buffer, including workspaces, is
+ *     passed in by the caller;
+ *   - dtype codes: LZ_F32 = 0, LZ_BF16 = 1 (bf16 stored as uint16 bits).
+ *
+ * The reference (dannyadkins/cs244c-llama-zero) is pure PyTorch and has no
+ * FFI; each declaration names the reference code whose computation it
+ * replaces.  The Python binding is cs244c-llama-zero_amd/lzhip/_lib.py.
+ */
+#ifndef LLAMAZERO_HIP_H
+#define LLAMAZERO_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LZ_F32 0
+#define LZ_BF16 1
+
+/* ---- library ------------------------------------------------------------ */
+const char* lz_last_error(void);
+int lz_version(void);
+int lz_device_cus(void); /* compute units of the current device */
+
+/* ---- optimizer path ----------------------------------------------------- */
+
+/* Fused AdamW over a flat fp32 master partition, one pass:
+ *   g' = g * (*grad_scale)   (grad_scale may be NULL)
+ *   m = b1*m + (1-b1)*g';  v = b2*v + (1-b2)*g'^2;  p *= 1 - lr*wd;
+ *   p -= lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps)
+ * and optionally writes p in p_out_dtype to p_out (the model's parameters).
+ * Replaces the unfused update of zero/stage0_ddp.py:73-88 (identical in
+ * zero/stage1_optimizer.py:73-88, zero/stage2_optimizer.py:145-160,
+ * zero/stage3_optimizer.py:454-470) and the .to(param_dtype) +
+ * assign_flat_params write-back of zero/common.py:202-216. */
+int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype, int64_t n,
+             double lr, double beta1, double beta2, double eps, double weight_decay, int64_t step,
+             const float* grad_scale, void* stream);
+
+/* *acc += sum(x^2) (acc is a device double).  Replaces flat_grads.norm(2)
+ * (zero/stage0_ddp.py:66) and sum(g*g) (zero/stage2_optimizer.py:162-166,
+ * zero/stage3_optimizer.py:438-444). */
+int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* stream);
+
+/* norm = sqrt(*acc); scale = max/(norm+1e-6) if 0 < max < norm else 1.
+ * Replaces the clip decision of zero/stage0_ddp.py:66-71 (and stage1/2/3). */
+int lz_clip_finalize(const double* acc, float max_norm, float* norm_out, float* scale_out, void* stream);
+
+/* Multi-tensor gather: dst[i-begin] = src_seg[i-off] for flat i in [begin,end).
+ * table: device int64 records {ptr, numel, flat_offset} sorted by offset; a
+ * NULL ptr reads as zeros; accumulate=1 adds into an fp32 dst.  Replaces the
+ * torch.cat flattens of zero/common.py:132-200 and
+ * zero/stage3_optimizer.py:32-40 (and builds the 25M-element gradient buckets). */
+int lz_mt_gather(const int64_t* table, int nseg, int src_dtype, void* dst, int dst_dtype, int64_t begin, int64_t end,
+                 int accumulate, void* stream);
+
+/* Multi-tensor scatter: dst_seg[i-off] = src[i-begin] with a cast.  Replaces
+ * assign_flat_params (zero/common.py:202-216) and the ZeRO-3 materialise
+ * (zero/stage3_optimizer.py:65-74). */
+int lz_mt_scatter(const void* src, int src_dtype, const int64_t* table, int nseg, int dst_dtype, int64_t begin,
+                  int64_t end, void* stream);
+
+/* dst(fp32) += alpha * src.  Replaces grad_shard.add_(local_grads.to(fp32))
+ * (zero/stage3_optimizer.py:98-103, zero/stage2_optimizer.py:134-139). */
+int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n, float alpha, void* stream);
+
+/* dst = dst + src in the storage dtype.  Replaces the post-accumulate hook add
+ * flat_grad_buffer[start:end].add_(grad) (zero/stage2_optimizer.py:109-114). */
+int lz_add_inplace(void* dst, const void* src, int dtype, int64_t n, void* stream);
+
+/* x *= alpha in the storage dtype (grad averaging / clipping in place). */
+int lz_scale_inplace(void* x, int dtype, int64_t n, float alpha, void* stream);
+
+/* Fill / cast.  Replace torch.zeros(...) for gradient buffers
+ * (zero/stage2_optimizer.py:88-89) and dtype casts (.to()). */
+int lz_fill(void* x, int dtype, int64_t n, double value, void* stream);
+int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
+
+/* ---- model ops ----------------------------------------------------------- */
+
+/* RMSNorm (model/llama.py:14-22): y = x * rsqrt(mean(x^2)+eps) * w, rstd[row]
+ * saved (fp32).  x, w, y in `dtype`. */
+int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int dtype, int64_t rows, int64_t cols,
+                   int64_t ldx, int64_t ldy, float eps, void* stream);
+/* Backward: dx = rstd*w*dy - rstd^3/n * (sum dy*w*x) * x (+ dres); dw (=/+=)
+ * sum over rows of dy*x*rstd.  workspace >= lz_rmsnorm_bwd_workspace(rows, cols)
+ * bytes. */
+int64_t lz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols);
+int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
+                   int dw_accumulate, void* workspace, int64_t workspace_bytes, int dtype, int64_t rows, int64_t cols,
+                   int64_t ldx, int64_t lddy, int64_t lddx, void* stream);
+
+/* RoPE table (model/llama.py:42-69 RotaryEmbedding._build_cache): cos/sin
+ * [seq, hd] in dtype from the module's inv_freq buffer (hd/2 values of
+ * freq_dtype); position, angle and cos/sin are rounded to freq_dtype, as the
+ * reference's cache is after Module.to(dtype) casts that buffer. */
+int lz_rope_table(void* cos_t, void* sin_t, int dtype, int64_t seq, int64_t hd, const void* inv_freq, int freq_dtype,
+                  void* stream);
+/* In-place rotary embedding of `nheads` heads per row (model/llama.py:25-39
+ * rotate_half/apply_rotary_pos_emb); backward=1 applies the transpose. */
+int lz_rope(void* x, int dtype, int64_t ld, int64_t rows, int64_t seq, int64_t nheads, int64_t hd, const void* cos_t,
+            const void* sin_t, int64_t pos_offset, int backward, void* stream);
+
+/* SwiGLU pointwise part (model/llama.py:145): h = silu(g) * u, and its
+ * backward. */
+int lz_swiglu_fwd(const void* g, int64_t ldg, const void* u, int64_t ldu, void* h, int64_t ldh, int64_t rows,
+                  int64_t cols, int dtype, void* stream);
+int lz_swiglu_bwd(const void* g, int64_t ldg, const void* u, int64_t ldu, const void* dh, int64_t lddh, void* dg,
+                  int64_t lddg, void* du, int64_t lddu, int64_t rows, int64_t cols, int dtype, void* stream);
+
+/* Embedding gather (model/llama.py:174,212) and gradient (fp32 atomics into a
+ * vocab*dim fp32 workspace, then written/added in dtype).  bad_flag (nullable)
+ * is set to 1 when an id is out of range. */
+int lz_embedding_fwd(const int64_t* ids, int64_t ntok, const void* table, int64_t vocab, int64_t dim, void* out,
+                     int64_t ldo, int dtype, int* bad_flag, void* stream);
+int lz_embedding_bwd(const int64_t* ids, int64_t ntok, const void* dout, int64_t ldo, int64_t vocab, int64_t dim,
+                     void* grad, int accumulate, float* workspace, int dtype, void* stream);
+
+/* Shifted cross entropy (model/llama.py:273-302, ignore_index -100):
+ * lse/row_loss per row, lz_ce_reduce forms the mean (clamp_count=1 gives the
+ * chunked variant's division by max(count,1)), lz_ce_bwd writes
+ * (softmax - onehot) * grad/count (may run in place over the logits). */
+int lz_ce_fwd(const void* logits, int64_t ld, int64_t rows, int64_t vocab, int dtype, const int64_t* labels,
+              int64_t seq, int64_t ignore_index, float* lse, float* row_loss, void* stream);
+int lz_ce_reduce(const float* row_loss, const int64_t* labels, int64_t rows, int64_t seq, int64_t vocab,
+                 int64_t ignore_index, float* loss_out, float* count_out, int clamp_count, void* stream);
+int lz_ce_bwd(const void* logits, int64_t ld, int64_t rows, int64_t vocab, int dtype, const int64_t* labels,
+              int64_t seq, int64_t ignore_index, const float* lse, const float* grad_loss, const float* count,
+              void* dlogits, int64_t ldd, int ddtype, void* stream);
+
+/* Batched transpose dst[b1][b2][c][r] = src[b1][b2][r][c] (operand layout
+ * for the backward GEMMs and attention; replaces the .transpose(1, 2) views
+ * of model/llama.py:97-99,132). */
+int lz_transpose(const void* src, void* dst, int dtype, int64_t nb1, int64_t nb2, int64_t rows, int64_t cols,
+                 int64_t lds, int64_t sb1s, int64_t sb2s, int64_t ldd, int64_t sb1d, int64_t sb2d, void* stream);
+
+/* dst[r][c] = src[r][c] over a rows x cols window (re-strides an operand whose
+ * leading dimension the GEMM cannot take, and concatenates weights; replaces
+ * torch.cat / .contiguous() copies). */
+int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows, int64_t cols, int dtype,
+              void* stream);
+
+/* bf16 MFMA GEMM C = alpha*A.B^T (+beta*C) (+R): the nn.Linear products of
+ * model/llama.py:81-84,133,139-141,178 and their gradients.  K, lda, ldb
+ * multiples of 8; A, B 16-byte aligned; C bf16 or fp32. */
+int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype, const void* R,
+               int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* stream);
+
+/* Causal GQA flash attention (model/llama.py:88-117: repeat_kv +
+ * F.scaled_dot_product_attention(is_causal=True)).  1 if the MFMA path applies
+ * (bf16, hd 64 or 128), which needs the transposed operand buffers. */
+int lz_attn_uses_mfma(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo);
+int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* vt,
+                void* o, int64_t ldo, float* lse, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
+                int dtype, void* stream);
+int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_t lddo, float* delta, int64_t B, int64_t S,
+                  int64_t H, int64_t hd, int dtype, void* stream);
+int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
+                int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
+                void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
+                int64_t H, int64_t KV, int64_t hd, float scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLAMAZERO_HIP_H */

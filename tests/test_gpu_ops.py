@@ -1,0 +1,409 @@
+"""Kernel-level parity: every HIP entry point against the CPU oracle (or, for
+floating-point GEMM products, a float32/float64 CPU matmul of the same op).
+
+Tolerances:
+  - integer/index/byte work (gather/scatter, transpose, embedding forward):
+    bit-exact;
+  - fp32 kernels (AdamW, sum of squares): 1e-5 relative;
+  - RoPE in bf16 reproduces the reference's per-op rounding: bit-exact given
+    the same cos/sin tables;
+  - bf16 kernels: within a few bf16 ulps of the float64 oracle (stated per test).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from lzhip import _lib, ops
+from oracle import ops as R
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def _seed(s):
+    torch.manual_seed(s)
+    return torch.Generator().manual_seed(s)
+
+
+def _rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def test_library_is_the_in_tree_build():
+    lib = _lib.load()
+    assert lib.lz_version() == 1
+    assert torch.cuda.is_available()
+    assert lib.lz_device_cus() > 0
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize(
+    "M,N,K",
+    [(64, 64, 64), (256, 256, 128), (300, 200, 72), (1000, 520, 136), (2048, 2048, 2048), (4096, 1536, 768)],
+)
+def test_gemm_nt_bf16_and_fp32_out(M, N, K):
+    g = _seed(M + N + K)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    ref = a.double() @ b.double().t()
+    c32 = ops.gemm_nt(a.to(DEV), b.to(DEV), out_dtype=torch.float32).cpu()
+    # fp32 accumulation of exact bf16 products: error ~ sqrt(K) * eps32 * |terms|
+    tol = 1e-5 * math.sqrt(K) * float(a.float().abs().max() * b.float().abs().max()) * 4
+    assert float((c32.double() - ref).abs().max()) <= tol
+    c16 = ops.gemm_nt(a.to(DEV), b.to(DEV)).cpu()
+    assert c16.dtype == torch.bfloat16
+    # one bf16 rounding of the fp32 result
+    assert torch.allclose(c16.double(), c32.double(), rtol=2 ** -8, atol=1e-6)
+
+
+def test_gemm_residual_alpha_beta():
+    g = _seed(7)
+    M, N, K = 384, 256, 192
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    c0 = torch.randn(M, N, generator=g).to(DEV)
+    ab = a.double().cpu() @ b.double().cpu().t()
+    out = ops.gemm_nt(a, b, residual=r).cpu().double()
+    assert torch.allclose(out, ab + r.double().cpu(), rtol=2 ** -7, atol=1e-3)
+    acc = c0.clone()
+    ops.gemm_nt(a, b, out=acc, alpha=0.5, beta=1.0)
+    assert torch.allclose(acc.cpu().double(), 0.5 * ab + c0.double().cpu(), rtol=1e-5, atol=1e-3)
+
+
+def test_gemm_strided_views_and_padding_helpers():
+    g = _seed(11)
+    M, N, K = 200, 96, 40  # K not a multiple of 64
+    big = torch.randn(M, K + 24, generator=g).to(torch.bfloat16).to(DEV)
+    a = big[:, 8 : 8 + K]  # row stride K+24, offset 8 elements (16 B)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    c = ops.gemm_nt(a, b, out_dtype=torch.float32).cpu().double()
+    ref = a.cpu().double() @ b.cpu().double().t()
+    assert torch.allclose(c, ref, rtol=1e-5, atol=1e-3)
+    # odd reduction length through the padding helpers
+    x = torch.randn(37, 13, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(29, 13, generator=g).to(torch.bfloat16).to(DEV)
+    y = ops.gemm_nt(ops.nt_operand(x), ops.nt_operand(w), out_dtype=torch.float32).cpu().double()
+    assert torch.allclose(y, x.cpu().double() @ w.cpu().double().t(), rtol=1e-5, atol=1e-3)
+    xt = ops.transpose_padded(x)
+    assert xt.shape == (13, 40)
+    assert torch.equal(xt[:, :37].cpu(), x.cpu().t())
+    assert torch.count_nonzero(xt[:, 37:]) == 0
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols,dtype", [(64, 64, torch.float32), (333, 768, torch.bfloat16),
+                                             (16 * 1024, 2048, torch.bfloat16), (50, 100, torch.float32),
+                                             (128, 4096, torch.bfloat16)])
+def test_rmsnorm_fwd_bwd(rows, cols, dtype):
+    g = _seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    w = (1.0 + 0.02 * torch.randn(cols, generator=g)).to(dtype)
+    dy = torch.randn(rows, cols, generator=g).to(dtype)
+    y, rstd = ops.rmsnorm_fwd(x.to(DEV), w.to(DEV), 1e-5)
+    # reference: fp32 statistics, (x*r)*w in fp32, one rounding to the dtype
+    xd, wd = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    yref = R.rmsnorm(xd, wd, 1e-5)
+    if dtype == torch.float32:
+        assert _rel_err(y, yref) < 1e-6
+    else:
+        assert float((y.cpu().double() - yref.detach()).abs().max()) <= 2 ** -8 * float(yref.abs().max())
+    rref = torch.rsqrt(x.double().pow(2).mean(-1) + 1e-5)
+    assert _rel_err(rstd, rref) < 1e-6
+    dx, dw = ops.rmsnorm_bwd(x.to(DEV), w.to(DEV), rstd, dy.to(DEV))
+    yref.backward(dy.double())
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _rel_err(dx, xd.grad) < tol
+    assert _rel_err(dw, wd.grad) < tol
+
+
+# ---------------------------------------------------------------------------
+# RoPE: bit-exact against the reference's bf16 op sequence given equal tables
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S,hd,theta", [(1024, 128, 10000.0), (128, 32, 10000.0), (16, 16, 500000.0)])
+def test_rope_matches_reference_ops(dtype, S, hd, theta):
+    g = _seed(S + hd)
+    B, nh = 2, 3
+    cos, sin = R.rope_tables(S, hd, theta, dtype=dtype)
+    # the kernel's table, from the same fp32 inv_freq buffer, agrees with the
+    # reference table to one rounding of cos/sin; with a bf16 buffer (the
+    # reference after Module.to(bfloat16)) positions and angles are bf16 too
+    for angle_dtype in (torch.float32, torch.bfloat16):
+        rc, rs = R.rope_tables(S, hd, theta, dtype=dtype, angle_dtype=angle_dtype)
+        inv = R.inv_freq(hd, theta).to(angle_dtype).to(DEV)
+        kc, ks = ops.rope_table(S, hd, inv, dtype)
+        ulp = 2 ** -8 if (dtype == torch.bfloat16 or angle_dtype == torch.bfloat16) else 2 ** -23
+        assert float((kc.cpu().double() - rc.double()).abs().max()) <= ulp
+        assert float((ks.cpu().double() - rs.double()).abs().max()) <= ulp
+        if dtype == torch.bfloat16:
+            # after rounding to bf16 the device and host cos/sin agree almost everywhere
+            assert float((kc.cpu() == rc).double().mean()) > 0.99
+    x = torch.randn(B, S, nh, hd, generator=g).to(dtype)
+    xg = x.clone().to(DEV)
+    ops.rope_(xg.view(B * S, nh * hd), S, nh, hd, cos.to(DEV), sin.to(DEV))
+    ref = R.apply_rope(x.transpose(1, 2), cos, sin).transpose(1, 2)
+    assert torch.equal(xg.cpu(), ref)
+    # backward = autograd of the same ops in the same dtype
+    xr = x.transpose(1, 2).clone().requires_grad_(True)
+    dy = torch.randn(B, nh, S, hd, generator=g).to(dtype)
+    R.apply_rope(xr, cos, sin).backward(dy)
+    dg = dy.transpose(1, 2).contiguous().to(DEV)
+    ops.rope_(dg.view(B * S, nh * hd), S, nh, hd, cos.to(DEV), sin.to(DEV), backward=True)
+    assert torch.equal(dg.cpu(), xr.grad.transpose(1, 2))
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU pointwise
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols,dtype", [(1024, 5632, torch.bfloat16), (77, 130, torch.bfloat16),
+                                             (64, 96, torch.float32)])
+def test_swiglu_fwd_bwd(rows, cols, dtype):
+    g = _seed(rows * 3 + cols)
+    gu = torch.randn(rows, 2 * cols, generator=g).to(dtype)
+    dh = torch.randn(rows, cols, generator=g).to(dtype)
+    gd = gu.to(DEV)
+    h = ops.swiglu_fwd(gd[:, :cols], gd[:, cols:])
+    gate, up = gu[:, :cols], gu[:, cols:]
+    # reference op sequence in the activation dtype: silu rounded, product rounded
+    href = F.silu(gate) * up
+    diff = (h.cpu().double() - href.double()).abs()
+    assert float(diff.max()) <= 2 ** -7 * float(href.double().abs().max() + 1)
+    if dtype == torch.bfloat16:
+        assert float((diff == 0).double().mean()) > 0.99
+    dgu = torch.empty_like(gd)
+    ops.swiglu_bwd(gd[:, :cols], gd[:, cols:], dh.to(DEV), dgu[:, :cols], dgu[:, cols:])
+    gr = gate.double().requires_grad_(True)
+    ur = up.double().requires_grad_(True)
+    R.swiglu(gr, ur).backward(dh.double())
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _rel_err(dgu[:, :cols], gr.grad) < tol
+    assert _rel_err(dgu[:, cols:], ur.grad) < tol
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize(
+    "B,S,H,KV,hd",
+    [(2, 128, 4, 2, 64), (1, 256, 4, 1, 128), (2, 200, 4, 4, 64), (1, 130, 2, 2, 128), (2, 64, 8, 4, 32),
+     (2, 16, 4, 2, 16), (1, 1024, 16, 8, 128)],
+)
+def test_attention_fwd_bwd(B, S, H, KV, hd):
+    g = _seed(B * S + H * hd)
+    ld = (H + 2 * KV) * hd
+    qkv = torch.randn(B * S, ld, generator=g).to(torch.bfloat16)
+    d = qkv.to(DEV)
+    q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
+    scale = hd**-0.5
+    mfma = ops.attn_uses_mfma(torch.bfloat16, hd, ld, ld, ld, H * hd)
+    vt = ops.transpose_heads(d, B, S, KV, hd, col0=(H + KV) * hd) if mfma else None
+    o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
+
+    def heads(t, n):
+        return t.double().view(B, S, n, hd).transpose(1, 2).requires_grad_(True)
+
+    qr, kr, vr = heads(qkv[:, : H * hd], H), heads(qkv[:, H * hd : (H + KV) * hd], KV), heads(qkv[:, (H + KV) * hd :], KV)
+    oref = R.causal_gqa_attention(qr, kr, vr, scale)
+    o4 = o.cpu().double().view(B, S, H, hd).transpose(1, 2)
+    assert _rel_err(o4, oref) < 1e-2
+    kk = kr.repeat_interleave(H // KV, dim=1)
+    sc = (qr @ kk.transpose(-1, -2)) * scale
+    sc = sc.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    lse_ref = torch.logsumexp(sc, dim=-1)
+    assert float((lse.cpu().double() - lse_ref.detach()).abs().max()) < 2e-2
+
+    do = torch.randn(B * S, H * hd, generator=g).to(torch.bfloat16)
+    dqkv = torch.zeros_like(d)
+    qt = kt = dot = None
+    if mfma:
+        qt = ops.transpose_heads(d, B, S, H, hd, col0=0)
+        kt = ops.transpose_heads(d, B, S, KV, hd, col0=H * hd)
+        dot = ops.transpose_heads(do.to(DEV), B, S, H, hd, col0=0)
+    ops.attn_bwd(q2, k2, v2, o, do.to(DEV), lse, B, S, H, KV, hd, scale,
+                 dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :], qt=qt, kt=kt, dot=dot)
+    oref.backward(do.double().view(B, S, H, hd).transpose(1, 2))
+    dq = dqkv[:, : H * hd].cpu().double().view(B, S, H, hd).transpose(1, 2)
+    dk = dqkv[:, H * hd : (H + KV) * hd].cpu().double().view(B, S, KV, hd).transpose(1, 2)
+    dv = dqkv[:, (H + KV) * hd :].cpu().double().view(B, S, KV, hd).transpose(1, 2)
+    assert _rel_err(dq, qr.grad) < 2e-2
+    assert _rel_err(dk, kr.grad) < 2e-2
+    assert _rel_err(dv, vr.grad) < 2e-2
+
+
+def test_attention_fp32_generic():
+    g = _seed(5)
+    B, S, H, KV, hd = 2, 40, 4, 2, 24
+    q = torch.randn(B, S, H, hd, generator=g)
+    k = torch.randn(B, S, KV, hd, generator=g)
+    v = torch.randn(B, S, KV, hd, generator=g)
+    o, lse = ops.attn_fwd(q.view(B * S, -1).to(DEV), k.view(B * S, -1).to(DEV), v.view(B * S, -1).to(DEV),
+                          B, S, H, KV, hd, hd**-0.5, None)
+    oref = R.causal_gqa_attention(q.double().transpose(1, 2), k.double().transpose(1, 2), v.double().transpose(1, 2))
+    assert _rel_err(o.cpu().view(B, S, H, hd).transpose(1, 2), oref) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Cross entropy
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,S,V,dtype", [(2, 17, 97, torch.float32), (4, 64, 32000, torch.bfloat16),
+                                         (2, 9, 1000, torch.bfloat16)])
+def test_cross_entropy_fwd_bwd(B, S, V, dtype):
+    g = _seed(B * S + V)
+    logits = (3 * torch.randn(B, S, V, generator=g)).to(dtype)
+    labels = torch.randint(0, V, (B, S), generator=g)
+    labels[0, 3] = -100
+    lg = logits.to(DEV).view(B * S, V)
+    lab = labels.to(DEV)
+    lse, row_loss = ops.ce_fwd(lg, lab, S)
+    loss, count = ops.ce_reduce(row_loss, lab, B * S, S, V, clamp=False)
+    lr = logits.double().requires_grad_(True)
+    ref = R.shifted_cross_entropy(lr, labels)
+    assert abs(float(loss) - float(ref)) <= 1e-5 * abs(float(ref))
+    assert int(count) == int(labels[:, 1:].ne(-100).sum())
+    ref_lib = F.cross_entropy(logits.double()[:, :-1].transpose(1, 2), labels[:, 1:], ignore_index=-100)
+    assert abs(float(ref) - float(ref_lib)) < 1e-10
+    ref.backward(torch.tensor(0.5, dtype=torch.float64))
+    d = ops.ce_bwd(lg, lab, S, lse, torch.tensor([0.5], device=DEV), count)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _rel_err(d.view(B, S, V), lr.grad) < tol
+    # clamp semantics with no valid targets
+    none = torch.full((B, S), -100, dtype=torch.long, device=DEV)
+    _, rl = ops.ce_fwd(lg, none, S)
+    l0, c0 = ops.ce_reduce(rl, none, B * S, S, V, clamp=True)
+    assert float(l0) == 0.0 and float(c0) == 1.0
+
+
+# ---------------------------------------------------------------------------
+# Embedding
+# ---------------------------------------------------------------------------
+def test_embedding_fwd_exact_bwd_close():
+    g = _seed(3)
+    V, d, B, S = 1000, 256, 4, 64
+    table = torch.randn(V, d, generator=g).to(torch.bfloat16)
+    ids = torch.randint(0, V, (B, S), generator=g)
+    ids[0, :8] = 5  # repeated ids
+    out = ops.embedding_fwd(ids.to(DEV), table.to(DEV))
+    assert torch.equal(out.cpu(), table[ids])
+    dout = torch.randn(B * S, d, generator=g).to(torch.bfloat16)
+    grad = ops.embedding_bwd(ids.to(DEV), dout.to(DEV), V, torch.bfloat16)
+    ref = torch.zeros(V, d, dtype=torch.float64).index_add_(0, ids.view(-1), dout.double())
+    assert float((grad.cpu().double() - ref).abs().max()) <= 2 ** -8 * float(ref.abs().max())
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    bad = ids.clone()
+    bad[1, 1] = V + 5
+    out2 = ops.embedding_fwd(bad.to(DEV), table.to(DEV), bad_flag=flag)
+    assert int(flag.item()) == 1
+    assert torch.count_nonzero(out2[1, 1]) == 0
+
+
+# ---------------------------------------------------------------------------
+# Optimizer path
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,gdtype", [(1_000_003, torch.float32), (262_147, torch.bfloat16), (5, torch.float32)])
+def test_adamw_matches_reference_update(n, gdtype):
+    g = _seed(n)
+    p = 0.02 * torch.randn(n, generator=g)
+    m = torch.zeros(n)
+    v = torch.zeros(n)
+    pd, md, vd = p.to(DEV), m.to(DEV), v.to(DEV)
+    out = torch.empty(n, dtype=torch.bfloat16, device=DEV)
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    for step in range(1, 11):
+        gr = (1e-3 * torch.randn(n, generator=g)).to(gdtype)
+        ops.adamw_(pd, md, vd, gr.to(DEV), step=step, p_out=out, **hp)
+        R.adamw_update(p, m, v, gr.float(), step=step, **hp)
+    assert _rel_err(pd, p) < 1e-5
+    assert _rel_err(md, m) < 1e-5
+    assert _rel_err(vd, v) < 1e-5
+    assert torch.equal(out.cpu(), pd.cpu().to(torch.bfloat16))
+
+
+def test_adamw_grad_scale_and_unaligned_views():
+    g = _seed(9)
+    n = 10_001
+    p = 0.02 * torch.randn(n + 1, generator=g)
+    gr = 1e-2 * torch.randn(n + 1, generator=g)
+    pd = p.to(DEV)[1:]
+    md = torch.zeros(n + 1, device=DEV)[1:]
+    vd = torch.zeros(n + 1, device=DEV)[1:]
+    scale = torch.tensor([0.25], device=DEV)
+    ops.adamw_(pd, md, vd, gr.to(DEV)[1:], lr=1e-3, beta1=0.9, beta2=0.99, eps=1e-8, weight_decay=0.0, step=1,
+               grad_scale=scale)
+    pr, mr, vr = p[1:].clone(), torch.zeros(n), torch.zeros(n)
+    R.adamw_update(pr, mr, vr, gr[1:] * 0.25, lr=1e-3, beta1=0.9, beta2=0.99, eps=1e-8, weight_decay=0.0, step=1)
+    assert _rel_err(pd, pr) < 1e-5
+
+
+def test_sumsq_and_clip():
+    g = _seed(4)
+    a = torch.randn(3_000_001, generator=g)
+    b = torch.randn(1001, generator=g).to(torch.bfloat16)
+    acc = torch.zeros(1, dtype=torch.float64, device=DEV)
+    ops.sumsq_(a.to(DEV), acc)
+    ops.sumsq_(b.to(DEV), acc)
+    ref = float(a.double().pow(2).sum() + b.double().pow(2).sum())
+    assert abs(float(acc.item()) - ref) <= 1e-6 * ref
+    norm = torch.empty(1, device=DEV)
+    scale = torch.empty(1, device=DEV)
+    ops.clip_finalize(acc, 1.0, norm, scale)
+    n = math.sqrt(ref)
+    assert abs(float(norm.item()) - n) <= 1e-6 * n
+    assert abs(float(scale.item()) - 1.0 / (n + 1e-6)) <= 1e-6
+    ops.clip_finalize(acc, 1e9, norm, scale)
+    assert float(scale.item()) == 1.0
+    ops.clip_finalize(acc, 0.0, norm, scale)
+    assert float(scale.item()) == 1.0
+
+
+def test_multi_tensor_gather_scatter_bit_exact():
+    g = _seed(8)
+    shapes = [(7,), (33, 5), (1,), (4096, 3), (2, 2, 2), (100_000,)]
+    ts = [torch.randn(*s, generator=g).to(torch.bfloat16).to(DEV) for s in shapes]
+    numels = [t.numel() for t in ts]
+    offs = [sum(numels[:i]) for i in range(len(ts))]
+    total = sum(numels)
+    tensors = list(ts)
+    tensors[2] = None  # a missing gradient reads as zeros
+    table = ops.SegmentTable.from_tensors(tensors, offs, numels, DEV)
+    flat = torch.empty(total, dtype=torch.bfloat16, device=DEV)
+    ops.mt_gather(table, torch.bfloat16, flat, 0, total)
+    ref = torch.cat([(torch.zeros(n, dtype=torch.bfloat16) if t is None else t.cpu().view(-1))
+                     for t, n in zip(tensors, numels)])
+    assert torch.equal(flat.cpu(), ref)
+    # a bucket window in the middle, accumulated into fp32
+    acc = torch.ones(5000, device=DEV)
+    ops.mt_gather(table, torch.bfloat16, acc, 100, 5100, accumulate=True)
+    assert torch.equal(acc.cpu(), ref[100:5100].float() + 1.0)
+    # scatter fp32 -> bf16 storages
+    src = torch.randn(total, generator=g).to(DEV)
+    outs = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shapes]
+    t2 = ops.SegmentTable.from_tensors(outs, offs, numels, DEV)
+    ops.mt_scatter(src, t2, torch.bfloat16, 0, total)
+    got = torch.cat([o.cpu().view(-1) for o in outs])
+    assert torch.equal(got, src.cpu().to(torch.bfloat16))
+
+
+def test_transpose_and_cast_exact():
+    g = _seed(12)
+    x = torch.randn(130, 70, generator=g).to(torch.bfloat16).to(DEV)
+    assert torch.equal(ops.transpose2d(x).cpu(), x.cpu().t())
+    B, S, nh, hd = 2, 65, 3, 32
+    y = torch.randn(B * S, 5 * hd, generator=g).to(torch.bfloat16).to(DEV)
+    t = ops.transpose_heads(y, B, S, nh, hd, col0=hd)
+    ref = y.cpu()[:, hd : hd + nh * hd].view(B, S, nh, hd).permute(0, 2, 3, 1)
+    assert torch.equal(t.cpu(), ref)
+    f = torch.randn(1001, generator=g).to(DEV)
+    assert torch.equal(ops.cast(f, torch.bfloat16).cpu(), f.cpu().to(torch.bfloat16))
+    z = ops.zeros((37,), torch.float32, DEV)
+    assert torch.count_nonzero(z) == 0
