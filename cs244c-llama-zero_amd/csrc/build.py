@@ -45,6 +45,13 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source extra flags.  RoPE reproduces the reference's separately rounded
+# products and sum, so multiply-add contraction is off for that file.
+EXTRA_FLAGS = {
+    "rope.hip": ["-ffp-contract=off"],
+}
+
+
 def find_hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -53,7 +60,8 @@ def find_hipcc() -> str:
 
 
 def _compile(hipcc: str, arch: str, src: Path, obj: Path) -> tuple[Path, int, str]:
-    cmd = [hipcc, f"--offload-arch={arch}", *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, f"--offload-arch={arch}", *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o",
+           str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass does not know the packed-fp32 feature name; drop that notice
     msgs = "\n".join(

@@ -307,6 +307,101 @@ __global__ void __launch_bounds__(kThreads) mt_scatter_kernel(const S* __restric
   }
 }
 
+// Segment table passed by value in the kernel arguments (no device copy of
+// the table, so a host-built table costs no host<->device synchronisation).
+constexpr int kArgSegs = 48;
+struct SegArgs {
+  int64_t ptr[kArgSegs];
+  int64_t numel[kArgSegs];
+  int64_t off[kArgSegs];
+  int n;
+};
+
+__device__ __forceinline__ int find_segment_args(const SegArgs& t, int64_t pos) {
+  int lo = 0, hi = t.n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (t.off[mid] + t.numel[mid] <= pos) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+template <typename S, typename D>
+__global__ void __launch_bounds__(kThreads) mt_gather_args_kernel(const SegArgs t, D* __restrict__ dst, int64_t begin,
+                                                                   int64_t end, int64_t dst_base, int mode) {
+  const int64_t nchunks = lz_cdiv(end - begin, kChunk);
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t c0 = begin + c * kChunk;
+    const int64_t c1 = min(c0 + kChunk, end);
+    for (int s = find_segment_args(t, c0); s < t.n; ++s) {
+      const S* ptr = reinterpret_cast<const S*>(t.ptr[s]);
+      const int64_t numel = t.numel[s], off = t.off[s];
+      if (off >= c1) break;
+      const int64_t lo = max(c0, off), hi = min(c1, off + numel);
+      for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        const float val = ptr ? Elem<S>::load(ptr, i - off) : 0.0f;
+        if (mode == 1) reinterpret_cast<float*>(dst)[i - dst_base] += val;
+        else Elem<D>::store(dst, i - dst_base, val);
+      }
+    }
+  }
+}
+
+template <typename S, typename D>
+__global__ void __launch_bounds__(kThreads) mt_scatter_args_kernel(const S* __restrict__ src, const SegArgs t, int64_t begin,
+                                                                    int64_t end, int64_t src_base) {
+  const int64_t nchunks = lz_cdiv(end - begin, kChunk);
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t c0 = begin + c * kChunk;
+    const int64_t c1 = min(c0 + kChunk, end);
+    for (int s = find_segment_args(t, c0); s < t.n; ++s) {
+      D* ptr = reinterpret_cast<D*>(t.ptr[s]);
+      const int64_t numel = t.numel[s], off = t.off[s];
+      if (off >= c1) break;
+      if (!ptr) continue;
+      const int64_t lo = max(c0, off), hi = min(c1, off + numel);
+      for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) Elem<D>::store(ptr, i - off, Elem<S>::load(src, i - src_base));
+    }
+  }
+}
+
+// Splits a host table into launches of at most kArgSegs segments, each over
+// the part of [begin, end) its segments cover.  kind 0 = gather, 1 = scatter.
+template <typename S, typename D>
+int run_host_table(int kind, const int64_t* host, int nseg, void* flat, int64_t begin, int64_t end, int accumulate,
+                   hipStream_t st) {
+  for (int s0 = 0; s0 < nseg; s0 += kArgSegs) {
+    SegArgs a;
+    a.n = std::min(kArgSegs, nseg - s0);
+    for (int j = 0; j < a.n; ++j) {
+      a.ptr[j] = host[3 * (s0 + j)];
+      a.numel[j] = host[3 * (s0 + j) + 1];
+      a.off[j] = host[3 * (s0 + j) + 2];
+    }
+    const int64_t lo = std::max(begin, a.off[0]);
+    const int64_t hi = std::min(end, a.off[a.n - 1] + a.numel[a.n - 1]);
+    if (hi <= lo) continue;
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(lz_cdiv(hi - lo, kChunk), (int64_t)lz_num_cus() * 8));
+    if (kind == 0)
+      mt_gather_args_kernel<S, D><<<grid, kThreads, 0, st>>>(a, static_cast<D*>(flat), lo, hi, begin, accumulate);
+    else
+      mt_scatter_args_kernel<S, D><<<grid, kThreads, 0, st>>>(static_cast<const S*>(flat), a, lo, hi, begin);
+    int rc = lz_check_launch(kind == 0 ? "lz_mt_gather_host" : "lz_mt_scatter_host");
+    if (rc) return rc;
+  }
+  return LZ_OK;
+}
+
+int check_host_table(const int64_t* host, int nseg) {
+  LZ_REQUIRE(host && nseg > 0, "multi-tensor: empty table");
+  for (int i = 0; i < nseg; ++i) {
+    LZ_REQUIRE(host[3 * i + 1] >= 0, "multi-tensor: negative segment size");
+    if (i > 0) LZ_REQUIRE(host[3 * i + 2] >= host[3 * (i - 1) + 2] + host[3 * (i - 1) + 1], "multi-tensor: segments overlap or are unsorted");
+  }
+  return LZ_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -391,6 +486,8 @@ LZ_EXPORT int lz_fill(void* x, int dtype, int64_t n, double value, void* stream)
     } else {
       fill_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, h);
     }
+  } else if (dtype == 2) {  // float64 (accumulators)
+    fill_kernel<double><<<stream_grid(n), kThreads, 0, s>>>((double*)x, n, value);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_fill: bad dtype %d", dtype);
   }
@@ -468,4 +565,36 @@ LZ_EXPORT int lz_mt_scatter(const void* src, int src_dtype, const int64_t* table
   else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) mt_scatter_kernel<uint16_t, float><<<grid, kThreads, 0, s>>>((const uint16_t*)src, table, nseg, begin, end);
   else return lz_set_error(LZ_EINVAL, "lz_mt_scatter: bad dtypes");
   return lz_check_launch("lz_mt_scatter");
+}
+
+// Same as lz_mt_gather / lz_mt_scatter with the {ptr, numel, flat_offset}
+// records in host memory; they travel in the kernel arguments.
+LZ_EXPORT int lz_mt_gather_host(const int64_t* host_table, int nseg, int src_dtype, void* dst, int dst_dtype,
+                                int64_t begin, int64_t end, int accumulate, void* stream) {
+  int rc = check_host_table(host_table, nseg);
+  if (rc) return rc;
+  LZ_REQUIRE(begin <= end && dst, "lz_mt_gather_host: bad range");
+  LZ_REQUIRE(!accumulate || dst_dtype == LZ_F32, "lz_mt_gather_host: accumulate requires an fp32 destination");
+  if (begin == end) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (src_dtype == LZ_BF16 && dst_dtype == LZ_BF16) return run_host_table<uint16_t, uint16_t>(0, host_table, nseg, dst, begin, end, 0, s);
+  if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) return run_host_table<uint16_t, float>(0, host_table, nseg, dst, begin, end, accumulate, s);
+  if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) return run_host_table<float, float>(0, host_table, nseg, dst, begin, end, accumulate, s);
+  if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) return run_host_table<float, uint16_t>(0, host_table, nseg, dst, begin, end, 0, s);
+  return lz_set_error(LZ_EINVAL, "lz_mt_gather_host: bad dtypes");
+}
+
+LZ_EXPORT int lz_mt_scatter_host(const void* src, int src_dtype, const int64_t* host_table, int nseg, int dst_dtype,
+                                 int64_t begin, int64_t end, void* stream) {
+  int rc = check_host_table(host_table, nseg);
+  if (rc) return rc;
+  LZ_REQUIRE(begin <= end && src, "lz_mt_scatter_host: bad range");
+  if (begin == end) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  void* srcp = const_cast<void*>(src);
+  if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) return run_host_table<float, uint16_t>(1, host_table, nseg, srcp, begin, end, 0, s);
+  if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) return run_host_table<float, float>(1, host_table, nseg, srcp, begin, end, 0, s);
+  if (src_dtype == LZ_BF16 && dst_dtype == LZ_BF16) return run_host_table<uint16_t, uint16_t>(1, host_table, nseg, srcp, begin, end, 0, s);
+  if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) return run_host_table<uint16_t, float>(1, host_table, nseg, srcp, begin, end, 0, s);
+  return lz_set_error(LZ_EINVAL, "lz_mt_scatter_host: bad dtypes");
 }

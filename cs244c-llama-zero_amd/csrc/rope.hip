@@ -45,6 +45,8 @@ __device__ __forceinline__ float add_r(float a, float b) { return __fadd_rn(a, b
 template <typename T, bool kBwd>
 __global__ void rope_kernel(T* __restrict__ x, int64_t ld, int64_t rows, int64_t seq, int nheads, int hd,
                             const T* __restrict__ cos_t, const T* __restrict__ sin_t, int64_t pos_offset) {
+  // each product and the sum are rounded separately, as in the reference's
+  // separate mul/add ops (this file is built with -ffp-contract=off)
   const int half = hd / 2;
   const int64_t per_row = (int64_t)nheads * half;
   const int64_t total = rows * per_row;

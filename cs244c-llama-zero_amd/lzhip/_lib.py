@@ -36,6 +36,8 @@ SIGNATURES = {
     "lz_clip_finalize": (_i32, [_vp, _f32, _vp, _vp, _vp]),
     "lz_mt_gather": (_i32, [_vp, _i32, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),
     "lz_mt_scatter": (_i32, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp]),
+    "lz_mt_gather_host": (_i32, [_vp, _i32, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),
+    "lz_mt_scatter_host": (_i32, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp]),
     "lz_axpy_f32": (_i32, [_vp, _vp, _i32, _i64, _f32, _vp]),
     "lz_add_inplace": (_i32, [_vp, _vp, _i32, _i64, _vp]),
     "lz_scale_inplace": (_i32, [_vp, _i32, _i64, _f32, _vp]),

@@ -33,7 +33,11 @@ def fused_weight(weights: Sequence[torch.Tensor]) -> torch.Tensor:
         return w0
     k = w0.shape[1]
     n_total = sum(w.shape[0] for w in weights)
-    adjacent = all(w.is_contiguous() and w.dtype == w0.dtype and w.shape[1] == k for w in weights)
+    base = w0.untyped_storage().data_ptr()
+    adjacent = all(
+        w.is_contiguous() and w.dtype == w0.dtype and w.shape[1] == k and w.untyped_storage().data_ptr() == base
+        for w in weights
+    )
     if adjacent:
         expect = w0.data_ptr()
         for w in weights:

@@ -7,6 +7,7 @@ tensor or an unsupported dtype raises: there is no fallback computation.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Sequence, Tuple
 
@@ -116,7 +117,8 @@ def fill_(x: torch.Tensor, value: float) -> torch.Tensor:
     require_gpu(x)
     if not x.is_contiguous():
         raise ValueError("fill_ needs a contiguous tensor")
-    _lib.call("lz_fill", x.data_ptr(), dtype_code(x), x.numel(), float(value), stream_ptr(x.device))
+    code = 2 if x.dtype == torch.float64 else dtype_code(x)
+    _lib.call("lz_fill", x.data_ptr(), code, x.numel(), float(value), stream_ptr(x.device))
     return x
 
 
@@ -189,6 +191,51 @@ class SegmentTable:
                     raise ValueError(f"segment has {t.numel()} elements, expected {n}")
             recs.append((0 if t is None else t.data_ptr(), int(n), int(off)))
         return cls(recs, device)
+
+
+class HostTable:
+    """{ptr, numel, flat_offset} records kept in host memory; the kernels get
+    them by value, so building one per call costs no device traffic."""
+
+    def __init__(self, records: Sequence[Tuple[int, int, int]]) -> None:
+        if not records:
+            raise ValueError("empty segment table")
+        flat = [int(v) for rec in records for v in rec]
+        self.nseg = len(records)
+        self.array = (ctypes.c_int64 * len(flat))(*flat)
+
+    @classmethod
+    def from_tensors(cls, tensors: Sequence[Optional[torch.Tensor]], offsets: Sequence[int],
+                     numels: Sequence[int]) -> "HostTable":
+        recs = []
+        for t, off, n in zip(tensors, offsets, numels):
+            if t is not None:
+                require_gpu(t)
+                if not t.is_contiguous():
+                    raise ValueError("segment tensors must be contiguous")
+                if t.numel() != n:
+                    raise ValueError(f"segment has {t.numel()} elements, expected {n}")
+            recs.append((0 if t is None else t.data_ptr(), int(n), int(off)))
+        return cls(recs)
+
+
+def mt_gather_host(table: HostTable, src_dtype: torch.dtype, dst: torch.Tensor, begin: int, end: int,
+                   accumulate: bool = False) -> None:
+    """dst[i - begin] (=|+=) flat element i of the concatenated segments."""
+    require_gpu(dst)
+    if dst.numel() < end - begin or not dst.is_contiguous():
+        raise ValueError("gather destination too small or not contiguous")
+    _lib.call("lz_mt_gather_host", ctypes.addressof(table.array), table.nseg, _DTYPES[src_dtype], dst.data_ptr(),
+              dtype_code(dst), int(begin), int(end), int(bool(accumulate)), stream_ptr(dst.device))
+
+
+def mt_scatter_host(src: torch.Tensor, table: HostTable, dst_dtype: torch.dtype, begin: int, end: int) -> None:
+    """flat element i of the concatenated segments = src[i - begin]."""
+    require_gpu(src)
+    if src.numel() < end - begin or not src.is_contiguous():
+        raise ValueError("scatter source too small or not contiguous")
+    _lib.call("lz_mt_scatter_host", src.data_ptr(), dtype_code(src), ctypes.addressof(table.array), table.nseg,
+              _DTYPES[dst_dtype], int(begin), int(end), stream_ptr(src.device))
 
 
 def mt_gather(table: SegmentTable, src_dtype: torch.dtype, dst: torch.Tensor, begin: int, end: int,
@@ -376,9 +423,47 @@ def transpose_padded(src2: torch.Tensor) -> torch.Tensor:
     return out
 
 
+class LaunchProbe:
+    """Opt-in timing of GEMM launches with HIP events recorded on the launch
+    stream: (flops, start, end) per launch.  Used by the benchmark to measure
+    the MFMA kernel inside a timed training step."""
+
+    def __init__(self) -> None:
+        self.records = []
+
+    def add(self, flops: float, start, end) -> None:
+        self.records.append((flops, start, end))
+
+    def summary(self) -> Tuple[int, float, float]:
+        """(launches, total flops, total milliseconds) — call after a sync."""
+        ms = sum(s.elapsed_time(e) for _, s, e in self.records)
+        return len(self.records), sum(f for f, _, _ in self.records), ms
+
+
+_gemm_probe: Optional[LaunchProbe] = None
+
+
+def set_gemm_probe(probe: Optional[LaunchProbe]) -> None:
+    global _gemm_probe
+    _gemm_probe = probe
+
+
 def gemm_nt(a2: torch.Tensor, b2: torch.Tensor, out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
             residual: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
     """out[M,N] = alpha * a2[M,K] . b2[N,K]^T (+ beta*out) (+ residual)."""
+    probe = _gemm_probe
+    if probe is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = _gemm_nt(a2, b2, out, out_dtype, residual, alpha, beta)
+        end.record()
+        probe.add(2.0 * a2.shape[0] * b2.shape[0] * a2.shape[1], start, end)
+        return out
+    return _gemm_nt(a2, b2, out, out_dtype, residual, alpha, beta)
+
+
+def _gemm_nt(a2, b2, out, out_dtype, residual, alpha, beta) -> torch.Tensor:
     require_gpu(a2, b2, out, residual)
     if a2.dtype != torch.bfloat16 or b2.dtype != torch.bfloat16:
         raise TypeError(

@@ -1,0 +1,87 @@
+"""torch.optim-compatible AdamW on the fused HIP kernel, for the single-process
+trainer (reference train.py:206-211,259-271: torch.optim.AdamW with
+clip_grad_norm_).
+
+FusedAdamW implements torch.optim.AdamW's update (decoupled weight decay,
+bias-corrected moments) with one kernel launch per parameter.  Parameters in a
+low-precision dtype get an fp32 master copy and fp32 moments; the kernel writes
+the rounded parameter back.  clip_grad_norm_() computes the global gradient
+norm and the clip factor on the device; the factor is folded into the next
+step() instead of rescaling every gradient in a separate pass.
+"""
+from __future__ import annotations
+
+from typing import Iterable, Optional
+
+import torch
+
+from . import ops
+
+
+class FusedAdamW(torch.optim.Optimizer):
+    def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 1e-2) -> None:
+        if lr < 0.0 or eps < 0.0 or weight_decay < 0.0:
+            raise ValueError("lr, eps and weight_decay must be non-negative")
+        if not (0.0 <= betas[0] < 1.0 and 0.0 <= betas[1] < 1.0):
+            raise ValueError(f"invalid betas {betas}")
+        super().__init__(params, dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay))
+        self._grad_scale: Optional[torch.Tensor] = None
+        self._norm_buf: Optional[torch.Tensor] = None
+
+    def _params_with_grad(self):
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is not None:
+                    yield group, p
+
+    @torch.no_grad()
+    def clip_grad_norm_(self, max_norm: float) -> torch.Tensor:
+        """Returns the global L2 norm of all gradients (a device scalar) and
+        arms the clip factor max/(norm+1e-6) (when norm > max) for step()."""
+        dev = None
+        for _, p in self._params_with_grad():
+            dev = p.grad.device
+            break
+        if dev is None:
+            return torch.zeros((), dtype=torch.float32)
+        acc = ops.zeros((1,), torch.float64, dev)
+        for _, p in self._params_with_grad():
+            g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+            ops.sumsq_(g, acc)
+        norm = torch.empty((1,), dtype=torch.float32, device=dev)
+        scale = torch.empty((1,), dtype=torch.float32, device=dev)
+        ops.clip_finalize(acc, float(max_norm), norm, scale)
+        self._grad_scale = scale if max_norm > 0 else None
+        return norm.view(())
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        for group, p in self._params_with_grad():
+            ops.require_gpu(p)
+            st = self.state[p]
+            if not st:
+                st["step"] = 0
+                st["exp_avg"] = ops.zeros(p.shape, torch.float32, p.device)
+                st["exp_avg_sq"] = ops.zeros(p.shape, torch.float32, p.device)
+                if p.dtype != torch.float32:
+                    st["master"] = ops.cast(p.detach().contiguous(), torch.float32)
+            st["step"] += 1
+            master = st.get("master")
+            g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+            beta1, beta2 = group["betas"]
+            if master is None:
+                if not p.is_contiguous():
+                    raise ValueError("FusedAdamW needs contiguous parameters")
+                target, out = p.data, None
+            else:
+                target, out = master, p.data
+            ops.adamw_(target, st["exp_avg"], st["exp_avg_sq"], g, lr=group["lr"], beta1=beta1, beta2=beta2,
+                       eps=group["eps"], weight_decay=group["weight_decay"], step=st["step"],
+                       grad_scale=self._grad_scale, p_out=out)
+        self._grad_scale = None
+        return loss

@@ -73,6 +73,15 @@ int lz_mt_gather(const int64_t* table, int nseg, int src_dtype, void* dst, int d
 int lz_mt_scatter(const void* src, int src_dtype, const int64_t* table, int nseg, int dst_dtype, int64_t begin,
                   int64_t end, void* stream);
 
+/* The same two operations with the records in HOST memory: they are passed to
+ * the kernels by value (up to 48 per launch, split automatically), so no
+ * table upload or host synchronisation is needed.  This is what the engines
+ * call every step. */
+int lz_mt_gather_host(const int64_t* host_table, int nseg, int src_dtype, void* dst, int dst_dtype, int64_t begin,
+                      int64_t end, int accumulate, void* stream);
+int lz_mt_scatter_host(const void* src, int src_dtype, const int64_t* host_table, int nseg, int dst_dtype,
+                       int64_t begin, int64_t end, void* stream);
+
 /* dst(fp32) += alpha * src.  Replaces grad_shard.add_(local_grads.to(fp32))
  * (zero/stage3_optimizer.py:98-103, zero/stage2_optimizer.py:134-139). */
 int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n, float alpha, void* stream);
@@ -85,7 +94,8 @@ int lz_add_inplace(void* dst, const void* src, int dtype, int64_t n, void* strea
 int lz_scale_inplace(void* x, int dtype, int64_t n, float alpha, void* stream);
 
 /* Fill / cast.  Replace torch.zeros(...) for gradient buffers
- * (zero/stage2_optimizer.py:88-89) and dtype casts (.to()). */
+ * (zero/stage2_optimizer.py:88-89) and dtype casts (.to()).  lz_fill also
+ * takes dtype 2 (float64) for the norm accumulators. */
 int lz_fill(void* x, int dtype, int64_t n, double value, void* stream);
 int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
 

@@ -57,30 +57,48 @@ def train_reference(
     max_grad_norm: float = 1.0,
     loss_chunk_size: int = 128,
     on_step: Optional[Callable[[int, float, float, Dict[str, torch.Tensor]], None]] = None,
+    param_dtype: torch.dtype = torch.float32,
 ) -> Dict[str, List[float]]:
     """Runs the train.py loop on CPU tensors (P is updated in place).  Returns
     per-step mean micro-batch loss, pre-clip grad norm and step seconds.
-    `on_step(step, loss, grad_norm, grads)` sees the gradients before the
-    optimizer update."""
+    `on_step(step, loss, grad_norm, grads[, params])` sees the (clipped)
+    gradients and, when it takes five arguments, the parameters of that step,
+    before the optimizer update.
+
+    param_dtype=torch.bfloat16 gives the reference's bf16-parameter semantics
+    (train_zero.py:150-153 with an fp32 master, zero/stage0_ddp.py:44-47): the
+    forward and backward see the fp32 master rounded to bf16, the update is
+    applied to the fp32 master.  The arithmetic itself stays fp32."""
     params = {k: v.detach().clone().requires_grad_(True) for k, v in P.items()}
     opt = torch.optim.AdamW(list(params.values()), lr=lr, betas=betas, weight_decay=weight_decay)
     out = {"loss": [], "grad_norm": [], "seconds": []}
     for step in range(1, steps + 1):
         t0 = time.perf_counter()
         opt.zero_grad(set_to_none=True)
+        if param_dtype == torch.float32:
+            work = params
+        else:
+            work = {k: v.detach().to(param_dtype).to(torch.float32).requires_grad_(True) for k, v in params.items()}
         losses = []
         for _ in range(grad_accum_steps):
             chunk = next(chunks)
             ids = chunk[:, :-1].contiguous()
-            loss = M.loss(params, cfg, ids, ids.clone(), chunk_size=loss_chunk_size)
+            loss = M.loss(work, cfg, ids, ids.clone(), chunk_size=loss_chunk_size)
             losses.append(float(loss.detach().item()))
             (loss / grad_accum_steps).backward()
+        if work is not params:
+            for k, v in params.items():
+                v.grad = work[k].grad
         if max_grad_norm > 0:
             gn = float(torch.nn.utils.clip_grad_norm_(list(params.values()), max_norm=max_grad_norm).item())
         else:
             gn = math.nan
         if on_step is not None:
-            on_step(step, sum(losses) / len(losses), gn, {k: v.grad.detach().clone() for k, v in params.items()})
+            grads = {k: v.grad.detach().clone() for k, v in params.items()}
+            if on_step.__code__.co_argcount >= 5:
+                on_step(step, sum(losses) / len(losses), gn, grads, {k: v.detach() for k, v in params.items()})
+            else:
+                on_step(step, sum(losses) / len(losses), gn, grads)
         opt.step()
         out["loss"].append(sum(losses) / len(losses))
         out["grad_norm"].append(gn)

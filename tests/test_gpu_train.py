@@ -1,0 +1,182 @@
+"""End-to-end training on the GPU.
+
+- The plumbing workload (d256, 4 layers, 8/4 heads, ffn 688, vocab 32000,
+  theta 1e4, seed 0, uniform ids, B=4, S=128, GA=2, AdamW lr 3e-4, clip 1.0)
+  for 100 steps through the HIP path in bf16, against the oracle's train.py
+  loop on the CPU (torch.optim.AdamW + clip_grad_norm_), once with the
+  reference's bf16-parameter semantics and once on its fp32 path.
+- The drop-in CLIs (train.py, train_zero.py stage 1 and 3) run and print the
+  reference's step lines.
+"""
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from lzhip.optim import FusedAdamW
+from model import LlamaForCausalLM, build_config
+from oracle import data as OD
+from oracle import engine as OE
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+ROOT = Path(__file__).resolve().parents[1]
+PKG = ROOT / "cs244c-llama-zero_amd"
+STEP_RE = re.compile(r"\[step\s+(\d+)\]\s+loss=([0-9.]+).*tokens/s=([0-9,]+)")
+
+
+def _flat_grad(named_grads, order):
+    return torch.cat([named_grads[n].double().reshape(-1).cpu() for n in order])
+
+
+def _plumbing_run(oracle_param_dtype, angle_dtype):
+    """100 steps of the plumbing workload through the HIP path (bf16) and
+    through the oracle; returns per-step (loss rel diff, grad cosine) and the
+    oracle losses."""
+    steps, B, S, GA = 100, 4, 128, 2
+    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg)
+    ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
+                  n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta,
+                  rope_angle_dtype=angle_dtype)
+    P = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
+    order = [n for n, _ in model.named_parameters()]
+    model = model.to(device=DEV, dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+
+    ref_losses, ref_grads = [], []
+
+    def on_step(step, loss, gn, grads):
+        ref_losses.append(loss)
+        ref_grads.append(_flat_grad(grads, order))
+
+    OE.train_reference(ocfg, P, OD.uniform_chunks(S, cfg.vocab_size, B, seed=0), steps=steps, grad_accum_steps=GA,
+                       lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1.0, loss_chunk_size=128,
+                       on_step=on_step, param_dtype=oracle_param_dtype)
+    chunks = OD.uniform_chunks(S, cfg.vocab_size, B, seed=0)
+    rel, cos = [], []
+    for step in range(steps):
+        opt.zero_grad(set_to_none=True)
+        losses = []
+        for _ in range(GA):
+            ids = next(chunks)[:, :-1].contiguous().to(DEV)
+            loss = model(input_ids=ids, labels=ids, return_logits=False).loss
+            losses.append(float(loss))
+            (loss / GA).backward()
+        g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
+        opt.clip_grad_norm_(1.0)
+        opt.step()
+        mean = sum(losses) / GA
+        rel.append(abs(mean - ref_losses[step]) / abs(ref_losses[step]))
+        cos.append(float(F.cosine_similarity(g, ref_grads[step], dim=0)))
+    print("per-step grad cosine:", " ".join(f"{c:.5f}" for c in cos))
+    print(f"max loss rel diff {max(rel):.2e}, min grad cosine {min(cos):.5f} (step {cos.index(min(cos)) + 1}), "
+          f"oracle loss {ref_losses[0]:.3f} -> {ref_losses[-1]:.3f}")
+    return rel, cos
+
+
+def test_plumbing_100_steps_gradient_fidelity():
+    """At every one of 100 training steps of the plumbing workload, the HIP
+    path's loss and gradient at the reference trainer's current parameters
+    (rounded to bf16): loss within 1e-2 relative, gradient cosine >= 0.999.
+    The reference trainer runs with the reference's bf16-parameter semantics
+    (fp32 master, bf16 parameters and RoPE angles)."""
+    steps, B, S, GA = 100, 4, 128, 2
+    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg)
+    ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
+                  n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta,
+                  rope_angle_dtype=torch.bfloat16)
+    P = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
+    order = [n for n, _ in model.named_parameters()]
+    model = model.to(device=DEV, dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    batches = []
+    gen = OD.uniform_chunks(S, cfg.vocab_size, B, seed=0)
+    for _ in range(steps * GA):
+        batches.append(next(gen))
+    rel, cos = [], []
+
+    def on_step(step, loss, gn, grads, params):
+        with torch.no_grad():
+            sd = {k: v.to(torch.bfloat16) for k, v in params.items()}
+            model.load_state_dict(sd, strict=False)
+        model.zero_grad(set_to_none=True)
+        losses = []
+        for i in range(GA):
+            ids = batches[(step - 1) * GA + i][:, :-1].contiguous().to(DEV)
+            l = model(input_ids=ids, labels=ids, return_logits=False).loss
+            losses.append(float(l))
+            (l / GA).backward()
+        g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
+        rel.append(abs(sum(losses) / GA - loss) / abs(loss))
+        cos.append(float(F.cosine_similarity(g, _flat_grad(grads, order), dim=0)))
+
+    OE.train_reference(ocfg, P, iter(batches), steps=steps, grad_accum_steps=GA, lr=3e-4, betas=(0.9, 0.95),
+                       weight_decay=0.1, max_grad_norm=1.0, loss_chunk_size=128, on_step=on_step,
+                       param_dtype=torch.bfloat16)
+    print("per-step grad cosine:", " ".join(f"{c:.5f}" for c in cos))
+    print(f"max loss rel diff {max(rel):.2e}, min grad cosine {min(cos):.5f}")
+    assert len(cos) == steps
+    assert max(rel) <= 1e-2
+    assert min(cos) >= 0.999
+
+
+def test_plumbing_100_steps_free_running():
+    """Both trainers on their own trajectories for 100 steps (HIP path in
+    bf16; reference semantics with bf16 parameters / its fp32 path): loss
+    within 1e-2 at every step.  The gradients agree to cosine 0.9999 at step 1
+    and then drift as Adam amplifies rounding-level differences of tiny
+    gradient components (measured minimum about 0.9989-0.9990 over 100 steps);
+    the bar here is 0.998."""
+    for pdt in (torch.bfloat16, torch.float32):
+        rel, cos = _plumbing_run(pdt, pdt)
+        assert max(rel) <= 1e-2
+        assert cos[0] >= 0.9999
+        assert min(cos) >= 0.998
+
+
+def _run(args, timeout=600):
+    env = dict(os.environ)
+    env["PYTHONPATH"] = f"{PKG}:{ROOT}:" + env.get("PYTHONPATH", "")
+    proc = subprocess.run([sys.executable, *args], cwd=str(PKG), env=env, capture_output=True, text=True,
+                          timeout=timeout)
+    assert proc.returncode == 0, proc.stdout[-3000:] + proc.stderr[-3000:]
+    return proc.stdout
+
+
+def test_train_py_cli(tmp_path):
+    out = _run(["train.py", "--model-size", "plumbing", "--data-mode", "synthetic-uniform", "--synthetic-vocab-size",
+                "32000", "--seq-len", "128", "--batch-size", "4", "--grad-accum-steps", "2", "--max-steps", "3",
+                "--seed", "0", "--log-interval", "1", "--save-dir", str(tmp_path)])
+    lines = [m for m in STEP_RE.finditer(out)]
+    assert len(lines) == 3, out
+    assert (tmp_path / "step_000003.pt").exists()
+
+
+@pytest.mark.parametrize("stage", [1, 3])
+def test_train_zero_cli(stage, tmp_path):
+    prof = tmp_path / "profile.json"
+    out = _run(["train_zero.py", "--zero-stage", str(stage), "--model-size", "plumbing", "--dtype", "bfloat16",
+                "--data-mode", "synthetic-uniform", "--synthetic-vocab-size", "32000", "--seq-len", "128",
+                "--batch-size", "4", "--max-steps", "3", "--log-interval", "1", "--max-grad-norm", "1.0",
+                "--checkpoint-interval", "0", "--profile-json", str(prof), "--profile-collectives",
+                "--measure-memory-step", "--memory-warmup-steps", "1"])
+    assert len(STEP_RE.findall(out)) == 3, out
+    assert "fb_ms=" in out and "tflops=" in out
+    import json
+
+    payload = json.loads(prof.read_text())
+    assert payload["stage"] == stage and len(payload["steps"]) == 3
+    assert payload["measured_step_memory"]["peak_allocated_mb"] > 0
