@@ -211,16 +211,41 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_scalar_kernel(const T* _
   }
 }
 
-// dw[c] (+)= sum over partial rows.
+// dw reduction over the per-wave partial rows, in two parallel levels:
+// (column block of 64) x (slice of the partial rows) workgroups sum their
+// slice with 4 rows of 64 coalesced lanes, then one pass adds the slices.
+constexpr int kSlices = 16;
+
+__global__ void __launch_bounds__(256) dw_slice_kernel(const float* __restrict__ part, int64_t nparts, int cols,
+                                                        float* __restrict__ slices) {
+  __shared__ float red[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + tx;
+  const int64_t per = lz_cdiv(nparts, kSlices);
+  const int64_t p0 = (int64_t)blockIdx.y * per, p1 = min(p0 + per, nparts);
+  float s = 0.f;
+  if (c < cols)
+    for (int64_t p = p0 + ty; p < p1; p += 4) s += part[p * cols + c];
+  red[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && c < cols) slices[(int64_t)blockIdx.y * cols + c] = red[0][tx] + red[1][tx] + red[2][tx] + red[3][tx];
+}
+
 template <typename T>
-__global__ void dw_reduce_kernel(const float* __restrict__ part, int64_t nparts, int cols, T* __restrict__ dw,
-                                 int accumulate) {
+__global__ void dw_final_kernel(const float* __restrict__ slices, int cols, T* __restrict__ dw, int accumulate) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= cols) return;
   float s = 0.f;
-  for (int64_t p = 0; p < nparts; ++p) s += part[p * cols + c];
+#pragma unroll
+  for (int k = 0; k < kSlices; ++k) s += slices[(int64_t)k * cols + c];
   if (accumulate) s += Elem<T>::load(dw, c);
   Elem<T>::store(dw, c, s);
+}
+
+inline int64_t bwd_waves(int64_t rows) {
+  // two workgroups (8 waves) per compute unit, at most one wave per row
+  int64_t n = std::min<int64_t>((int64_t)lz_num_cus() * 2 * kRowsPerBlock, std::max<int64_t>(rows, kRowsPerBlock));
+  return std::max<int64_t>(kRowsPerBlock, (n / kRowsPerBlock) * kRowsPerBlock);
 }
 
 template <typename T>
@@ -244,11 +269,10 @@ template <typename T>
 int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
                  int dw_accumulate, float* ws, int64_t ws_bytes, int64_t rows, int cols, int64_t ldx, int64_t lddy,
                  int64_t lddx, hipStream_t s) {
-  // number of waves = number of fp32 partial rows held in the workspace
-  int64_t max_parts = ws_bytes / ((int64_t)cols * 4);
-  int64_t nwaves = std::min<int64_t>({(int64_t)lz_num_cus() * 4 * kRowsPerBlock, max_parts, rows});
-  nwaves = (nwaves / kRowsPerBlock) * kRowsPerBlock;
-  LZ_REQUIRE(nwaves >= kRowsPerBlock, "lz_rmsnorm_bwd: workspace too small (%lld bytes)", (long long)ws_bytes);
+  // workspace: one fp32 partial row per wave, then kSlices rows of slice sums
+  const int64_t nwaves = bwd_waves(rows);
+  LZ_REQUIRE(ws_bytes >= (nwaves + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
+             (long long)ws_bytes);
   const int grid = (int)(nwaves / kRowsPerBlock);
   const bool vec = cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(dy) && lz_aligned16(dx) &&
                    (dres == nullptr || lz_aligned16(dres)) && (ldx * (int64_t)sizeof(T)) % 16 == 0 &&
@@ -263,7 +287,9 @@ int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy
   int rc = lz_check_launch("lz_rmsnorm_bwd");
   if (rc) return rc;
   if (dw) {
-    dw_reduce_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(ws, nwaves, cols, (T*)dw, dw_accumulate);
+    float* slices = ws + nwaves * (int64_t)cols;
+    dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(ws, nwaves, cols, slices);
+    dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, (T*)dw, dw_accumulate);
     rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
   }
   return rc;
@@ -283,8 +309,7 @@ LZ_EXPORT int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,
 
 // Workspace bytes the backward wants for its dw partials.
 LZ_EXPORT int64_t lz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
-  int64_t nwaves = std::min<int64_t>((int64_t)lz_num_cus() * 4 * kRowsPerBlock, std::max<int64_t>(rows, kRowsPerBlock));
-  return nwaves * cols * 4;
+  return (bwd_waves(rows) + kSlices) * cols * 4;
 }
 
 LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,

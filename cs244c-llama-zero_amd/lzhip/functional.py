@@ -125,6 +125,34 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return RMSNormFn.apply(x, weight, eps)
 
 
+class RMSNormResidualFn(Function):
+    """(rmsnorm(x), x): the pre-norm block reads x twice — through the norm
+    and as the residual.  Returning x from here makes this function the only
+    consumer of x, so its backward adds the residual gradient inside the
+    RMSNorm backward kernel instead of autograd summing two gradients."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
+        x2 = _rows(x)
+        y, rstd = ops.rmsnorm_fwd(x2, weight, eps)
+        ctx.save_for_backward(x2, weight, rstd)
+        ctx.in_shape = x.shape
+        return y.view(x.shape), x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor, dres: Optional[torch.Tensor]):
+        x2, weight, rstd = ctx.saved_tensors
+        if dy is None:
+            return dres, None, None
+        r2 = _rows(dres) if dres is not None else None
+        dx, dw = ops.rmsnorm_bwd(x2, weight, rstd, _rows(dy), dres=r2, need_dw=ctx.needs_input_grad[1])
+        return dx.view(ctx.in_shape), dw, None
+
+
+def rms_norm_with_residual(x: torch.Tensor, weight: torch.Tensor, eps: float):
+    return RMSNormResidualFn.apply(x, weight, eps)
+
+
 class RopeFn(Function):
     """apply_rotary_pos_emb on a [..., S, hd] tensor (model/llama.py:25-39)."""
 

@@ -280,11 +280,14 @@ def rmsnorm_bwd(x2: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy2: torc
     lib = _lib.load()
     ws_bytes = int(lib.lz_rmsnorm_bwd_workspace(rows, cols))
     ws = torch.empty((max(ws_bytes, 16) + 3) // 4, dtype=torch.float32, device=x2.device)
-    if dres is not None and (dres.shape != dx.shape or dres.dtype != dx.dtype):
-        raise ValueError("residual gradient must match dx")
+    if dres is not None:
+        if dres.shape != dx.shape or dres.dtype != dx.dtype:
+            raise ValueError("residual gradient must match dx")
+        if _row_stride(dres) != cols or dres.stride(-1) != 1:
+            dres = dres.contiguous()  # the kernel reads dres with dx's row stride
     _lib.call("lz_rmsnorm_bwd", x2.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(), _ptr(dres), dx.data_ptr(),
               _ptr(dw), 0, ws.data_ptr(), ws.numel() * 4, dtype_code(x2), rows, cols, _row_stride(x2),
-              _row_stride(dy2), cols if dres is None else _row_stride(dres), stream_ptr(x2.device))
+              _row_stride(dy2), cols, stream_ptr(x2.device))
     return dx, dw
 
 

@@ -57,6 +57,11 @@ class RMSNorm(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return LF.rms_norm(x, self.weight, self.eps)
 
+    def forward_with_residual(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(norm(x), x) for a pre-norm residual block; the residual gradient is
+        added inside the norm's backward kernel."""
+        return LF.rms_norm_with_residual(x, self.weight, self.eps)
+
 
 def rotate_half(x: torch.Tensor) -> torch.Tensor:
     """cat(-x2, x1) over the last dimension (model/llama.py:25-28); a tensor
@@ -174,9 +179,12 @@ class TransformerBlock(nn.Module):
         self.mlp = SwiGLU(cfg)
 
     def forward(self, x: torch.Tensor, attention_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        # x + attn(norm(x)); then x + mlp(norm(x)) — residual adds in the GEMM epilogues
-        x = self.attn(self.input_norm(x), attention_mask=attention_mask, residual=x)
-        return self.mlp(self.post_attn_norm(x), residual=x)
+        # x + attn(norm(x)); then x + mlp(norm(x)) — residual adds in the GEMM
+        # epilogues, residual gradients inside the norm backward
+        h, x = self.input_norm.forward_with_residual(x)
+        x = self.attn(h, attention_mask=attention_mask, residual=x)
+        h, x = self.post_attn_norm.forward_with_residual(x)
+        return self.mlp(h, residual=x)
 
 
 @dataclass
