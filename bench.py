@@ -226,7 +226,7 @@ def main() -> int:
         "llama_125m_zero1": res_125m,
         "adamw_124m": adamw,
         "roofline": {
-            "kernel": "gemm_nt_kernel (bf16 MFMA GEMM, all launches of the timed steps)",
+            "kernel": "gemm_kernel (bf16 MFMA GEMM, all launches of the timed steps)",
             "bound": "mfma",
             "achieved": gemm_tflops,
             "peak": PEAK_BF16_TFLOPS,

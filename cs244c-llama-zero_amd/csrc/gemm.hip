@@ -1,22 +1,29 @@
-// bf16 "NT" GEMM on CDNA4 matrix cores:
+// bf16 GEMM on CDNA4 matrix cores:
 //
-//   C[M,N] = alpha * A[M,K] . B[N,K]^T  (+ beta * C)  (+ R)
+//   C[M,N] = alpha * sum_k A(m,k) B(n,k)  (+ beta * C)  (+ R)
 //
-// A and B are row-major with the reduction dimension K innermost, which is the
-// layout of nn.Linear's forward (x . W^T, reference model/llama.py:81-84,
-// 139-141, 178).  fp32 accumulation, bf16 or fp32 output, optional residual
-// add (the block's `x + f(x)`, model/llama.py:158-159) and optional
-// accumulation into an existing fp32 C (gradient accumulation).
+// Each operand is stored either K-major (A(m,k) = A[m*lda + k], the layout of
+// nn.Linear's x . W^T, reference model/llama.py:81-84, 139-141, 178) or
+// M/N-major (A(m,k) = A[k*lda + m]).  The three products of a linear layer
+// map onto one kernel without transposing anything in HBM:
+//   forward      y  = x  . W^T : A = x  K-major, B = W  K-major
+//   input grad   dx = dy . W   : A = dy K-major, B = W  N-major
+//   weight grad  dW = dy^T . x : A = dy M-major, B = x  N-major
+// fp32 accumulation, bf16 or fp32 output, optional residual add (the block's
+// `x + f(x)`, model/llama.py:158-159) and optional accumulation into an
+// existing C (gradient accumulation).
 //
-// Tiling: a workgroup computes a BM x BN tile with 64-wide K steps staged
-// through double-buffered LDS (rows padded by 16 bytes so the 16-byte fragment
-// reads of 8 consecutive lanes hit distinct banks).  Each wave owns a
-// (BM/WM) x (BN/WN) sub-tile made of 32x32 v_mfma_f32_32x32x16_bf16 tiles.
-// The MFMA computes D = B_tile . A_tile^T so that each lane ends up holding 4
-// consecutive output columns of one output row, which are stored as one 8- or
-// 16-byte write.  Global loads for step k+1 are in flight while step k's MFMAs
-// run.  Workgroup ids are remapped so that consecutive tiles of one M-band land
-// on the same XCD (its L2 then serves the shared A rows).
+// Tiling: a workgroup computes a BM x BN tile in 64-deep K steps staged
+// through double-buffered LDS.  LDS always holds K-major rows padded to 144
+// bytes, so the 16-byte fragment reads of 8 (or 16) consecutive lanes fall on
+// distinct banks.  An M/N-major operand is loaded as 8x8 blocks (8 K rows of
+// 8 contiguous elements) and transposed in registers before the LDS write.
+// Each wave owns a (BM/WM) x (BN/WN) sub-tile of 32x32
+// v_mfma_f32_32x32x16_bf16 tiles; the MFMA computes D = B_tile . A_tile^T so
+// each lane ends up holding 4 consecutive output columns of one output row.
+// Global loads for step k+1 are in flight while step k's MFMAs run.
+// Workgroup ids are remapped so that consecutive tiles of one M-band land on
+// the same XCD (its L2 then serves the shared operand rows).
 #include "lz_common.h"
 
 namespace {
@@ -37,7 +44,19 @@ struct GemmArgs {
   float alpha, beta;
   int c_f32;      // output dtype fp32 (else bf16)
   int vec_store;  // N, ldc, ldr multiples of 4 and pointers aligned
+  int64_t kper;   // K range of one split (multiple of 64); blockIdx.y is the split
+  int64_t slab;   // elements between the fp32 partial slabs of consecutive splits
 };
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 (round to nearest even) packed low/high, one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const float2 f = make_float2(lo, hi);
+  const bf16x2_t b = __builtin_convertvector(__builtin_bit_cast(__attribute__((ext_vector_type(2))) float, f), bf16x2_t);
+  return __builtin_bit_cast(uint32_t, b);
+}
 
 __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t n, const float (&v)[4]) {
   float o[4] = {v[0] * g.alpha, v[1] * g.alpha, v[2] * g.alpha, v[3] * g.alpha};
@@ -95,10 +114,9 @@ __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t
 // workgroup i on XCD i % 8; the remap gives each XCD a contiguous range of
 // logical tiles, and the logical order walks groups of kGroupM M-tiles across
 // all N-tiles so an XCD's concurrently running tiles share A rows and B rows.
-__device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
+__device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
   constexpr int kXcd = 8, kGroupM = 8;
   const int64_t nblk = tiles_m * tiles_n;
-  int64_t pid = blockIdx.x;
   if (nblk % kXcd == 0) pid = (pid % kXcd) * (nblk / kXcd) + pid / kXcd;
   const int64_t per_group = (int64_t)kGroupM * tiles_n;
   const int64_t group = pid / per_group;
@@ -109,15 +127,199 @@ __device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, in
   tn = in_group / gsize;
 }
 
+// One operand tile (ROWS rows of the M or N dimension x 64 K) moving from HBM
+// through registers into a K-major LDS buffer.
+template <int ROWS, int THREADS, bool KMAJOR>
+struct TileLoader {
+  // K-major: ROWS*8 chunks of 16 bytes (8 K values of one row).
+  // M/N-major: ROWS 8x8 blocks (8 K rows x 8 contiguous M/N values).
+  static constexpr int kUnits = ROWS * 8 / (KMAJOR ? 1 : 8);
+  static constexpr int kPer = (kUnits + THREADS - 1) / THREADS;
+  static constexpr int kRegs = KMAJOR ? kPer : kPer * 8;
+  static constexpr bool kFull = kUnits % THREADS == 0;
+  uint4 r[kRegs];
+
+  // CHECK=false: the whole tile (rows and 64 K) is in range.  CHECK=true:
+  // addresses are clamped into the operand and out-of-range data is zeroed
+  // with a mask, so no load sits behind a branch.
+  template <bool CHECK>
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ p, int64_t ld, int64_t row0, int64_t nrows,
+                                       int64_t k0, int64_t kend, int tid) {
+    if constexpr (KMAJOR) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = tid + i * THREADS;
+        const int row = c >> 3, ch = c & 7;
+        const int64_t gr = row0 + row, gk = k0 + ch * 8;
+        if constexpr (!CHECK) {
+          r[i] = *reinterpret_cast<const uint4*>(p + gr * ld + gk);
+        } else {
+          const uint32_t msk = ((kFull || c < kUnits) && gr < nrows && gk < kend) ? ~0u : 0u;
+          const uint4 v = *reinterpret_cast<const uint4*>(p + min(gr, nrows - 1) * ld + min(gk, kend - 8));
+          r[i] = make_uint4(v.x & msk, v.y & msk, v.z & msk, v.w & msk);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int b = tid + i * THREADS;
+        const int kb = b & 7, rb = b >> 3;  // 8 consecutive lanes: 8 K blocks of one row block
+        const int64_t gr = row0 + rb * 8;
+        if constexpr (!CHECK) {
+          const int64_t rr = (kFull || b < kUnits) ? gr : row0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) r[i * 8 + j] = *reinterpret_cast<const uint4*>(p + (k0 + kb * 8 + j) * ld + rr);
+        } else {
+          const bool ok = (kFull || b < kUnits) && gr < nrows;
+          const int64_t grc = min(gr, nrows - 8);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int64_t gk = k0 + kb * 8 + j;
+            const uint32_t msk = (ok && gk < kend) ? ~0u : 0u;
+            const uint4 v = *reinterpret_cast<const uint4*>(p + min(gk, kend - 1) * ld + grc);
+            r[i * 8 + j] = make_uint4(v.x & msk, v.y & msk, v.z & msk, v.w & msk);
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(char* lds, int tid) {
+    if constexpr (KMAJOR) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = tid + i * THREADS;
+        if (kFull || c < kUnits) *reinterpret_cast<uint4*>(lds + (c >> 3) * kRowBytes + (c & 7) * 16) = r[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int b = tid + i * THREADS;
+        if (!kFull && b >= kUnits) continue;
+        const int kb = b & 7, rb = b >> 3;
+        // r[i*8 + j] holds K row j, elements e = 0..7 as dwords (e=2q, 2q+1);
+        // output row e needs K = 0..7 of element e.
+        const uint32_t* x = reinterpret_cast<const uint32_t*>(&r[i * 8]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int q = e >> 1;
+          uint32_t w[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const uint32_t lo = x[(2 * jj) * 4 + q], hi = x[(2 * jj + 1) * 4 + q];
+            w[jj] = (e & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+          }
+          *reinterpret_cast<uint4*>(lds + (rb * 8 + e) * kRowBytes + kb * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+    }
+  }
+};
+
+// Writes a workgroup's BM x BN accumulator tile.  Lane layout of the
+// accumulators: output row m = lane % 32 of each 32x32 tile, columns
+// n = 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Interior tiles store each
+// lane's 4-column groups straight from the accumulators (8 or 16 bytes) with
+// the row address formed once per 32-row band; edge tiles go through LDS one
+// 32-row band at a time and are written as whole rows with bounds checks, so
+// the accumulators are never indexed dynamically.  `smem` must be free and at
+// least WM*WN*32*(BN/WN+4)*4 bytes.
 template <int BM, int BN, int WM, int WN>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_nt_kernel(GemmArgs g) {
+__device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0,
+                                           int64_t n0, char* smem, int lane, int wave) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  const int wm = wave / WN, wn = wave % WN;
+  const int frag_row = lane & 31, half = lane >> 5;
+  if (m0 + BM <= go.M && n0 + BN <= go.N && go.vec_store) {
+    const int64_t ncol0 = n0 + wn * TN + half * 4;
+    if (go.c_f32) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int64_t m = m0 + wm * TM + i * 32 + frag_row;
+        float* crow = static_cast<float*>(go.C) + m * go.ldc + ncol0;
+        const uint16_t* rrow = go.R ? go.R + m * go.ldr + ncol0 : nullptr;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float4 o = make_float4(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
+                                   acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha);
+            float4* cp = reinterpret_cast<float4*>(crow + j * 32 + q * 8);
+            if (go.beta != 0.f) {
+              const float4 c = *cp;
+              o.x = fmaf(go.beta, c.x, o.x); o.y = fmaf(go.beta, c.y, o.y);
+              o.z = fmaf(go.beta, c.z, o.z); o.w = fmaf(go.beta, c.w, o.w);
+            }
+            if (rrow) {
+              const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
+              o.x += bf2f(r.x & 0xffff); o.y += bf2f(r.x >> 16); o.z += bf2f(r.y & 0xffff); o.w += bf2f(r.y >> 16);
+            }
+            *cp = o;
+          }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int64_t m = m0 + wm * TM + i * 32 + frag_row;
+        uint16_t* crow = static_cast<uint16_t*>(go.C) + m * go.ldc + ncol0;
+        const uint16_t* rrow = go.R ? go.R + m * go.ldr + ncol0 : nullptr;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float o[4] = {acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
+                          acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha};
+            uint2* cp = reinterpret_cast<uint2*>(crow + j * 32 + q * 8);
+            if (go.beta != 0.f) {
+              const uint2 c = *cp;
+              o[0] = fmaf(go.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, bf2f(c.x >> 16), o[1]);
+              o[2] = fmaf(go.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, bf2f(c.y >> 16), o[3]);
+            }
+            if (rrow) {
+              const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
+              o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+            }
+            *cp = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+          }
+      }
+    }
+    return;
+  }
+  constexpr int kPitch = TN + 4;  // floats; 16-byte aligned, staggers the banks of consecutive rows
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(stage + frag_row * kPitch + j * 32 + q * 8 + half * 4) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    __syncthreads();
+    const int64_t mband = m0 + wm * TM + i * 32, nband = n0 + wn * TN;
+    for (int it = lane; it < 32 * (TN / 4); it += 64) {
+      const int r = it / (TN / 4), c4 = it % (TN / 4);
+      const int64_t m = mband + r, n = nband + c4 * 4;
+      if (m < go.M && n < go.N) {
+        const float4 v4 = *reinterpret_cast<const float4*>(stage + r * kPitch + c4 * 4);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        store_out4(go, m, n, v);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Register-staged kernel: any operand layouts.  Global loads for K step k+1
+// are in flight in registers while step k's MFMAs run, then written to the
+// other LDS buffer (transposed on the way for an M/N-major operand).
+template <int BM, int BN, int WM, int WN, bool AK, bool BK>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   constexpr int kThreads = 64 * WM * WN;
-  constexpr int TM = BM / WM, TN = BN / WN;      // wave sub-tile
-  constexpr int FM = TM / 32, FN = TN / 32;      // 32x32 MFMA tiles per wave
-  constexpr int kChunksA = BM * (kBK / 8) / kThreads;  // 16-byte chunks per thread per stage
-  constexpr int kChunksB = BN * (kBK / 8) / kThreads;
+  constexpr int TM = BM / WM, TN = BN / WN;  // wave sub-tile
+  constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA tiles per wave
   constexpr int kStageBytes = (BM + BN) * kRowBytes;
-  static_assert(kChunksA * kThreads == BM * kBK / 8 && kChunksB * kThreads == BN * kBK / 8, "tile/thread mismatch");
+  static_assert(WM * WN * 32 * (TN + 4) * 4 <= 2 * kStageBytes, "epilogue staging does not fit");
 
   __shared__ __attribute__((aligned(16))) char smem[2 * kStageBytes];
 
@@ -125,41 +327,22 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt_kernel(GemmArgs g) {
   const int wm = wave / WN, wn = wave % WN;
   const int64_t tiles_m = lz_cdiv(g.M, BM), tiles_n = lz_cdiv(g.N, BN);
   int64_t tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = tm * BM, n0 = tn * BN;
-  const int64_t ktiles = lz_cdiv(g.K, kBK);
+  const int64_t kbeg = (int64_t)blockIdx.y * g.kper, kend = min(g.K, kbeg + g.kper);
+  const int64_t ktiles = kend > kbeg ? lz_cdiv(kend - kbeg, kBK) : 0;
+  // uniform per workgroup: the whole tile lies inside the operands
+  const bool interior = m0 + BM <= g.M && n0 + BN <= g.N && (kend - kbeg) % kBK == 0;
 
-  // global->register staging
-  uint4 ra[kChunksA], rb[kChunksB];
-  auto gload = [&](int64_t kt) {
-    const int64_t kbase = kt * kBK;
-#pragma unroll
-    for (int i = 0; i < kChunksA; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c >> 3, ch = c & 7;
-      const int64_t gm = m0 + row, gk = kbase + ch * 8;
-      ra[i] = (gm < g.M && gk < g.K) ? *reinterpret_cast<const uint4*>(g.A + gm * g.lda + gk) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < kChunksB; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c >> 3, ch = c & 7;
-      const int64_t gn = n0 + row, gk = kbase + ch * 8;
-      rb[i] = (gn < g.N && gk < g.K) ? *reinterpret_cast<const uint4*>(g.B + gn * g.ldb + gk) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto sstore = [&](int stage) {
-    char* As = smem + stage * kStageBytes;
-    char* Bs = As + BM * kRowBytes;
-#pragma unroll
-    for (int i = 0; i < kChunksA; ++i) {
-      const int c = tid + i * kThreads;
-      *reinterpret_cast<uint4*>(As + (c >> 3) * kRowBytes + (c & 7) * 16) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kChunksB; ++i) {
-      const int c = tid + i * kThreads;
-      *reinterpret_cast<uint4*>(Bs + (c >> 3) * kRowBytes + (c & 7) * 16) = rb[i];
+  TileLoader<BM, kThreads, AK> la;
+  TileLoader<BN, kThreads, BK> lb;
+  auto gload = [&](int64_t k0) {
+    if (interior) {
+      la.template load<false>(g.A, g.lda, m0, g.M, k0, kend, tid);
+      lb.template load<false>(g.B, g.ldb, n0, g.N, k0, kend, tid);
+    } else {
+      la.template load<true>(g.A, g.lda, m0, g.M, k0, kend, tid);
+      lb.template load<true>(g.B, g.ldb, n0, g.N, k0, kend, tid);
     }
   };
 
@@ -171,16 +354,18 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  gload(0);
-  sstore(0);
+  if (ktiles > 0) {
+    gload(kbeg);
+    la.store(smem, tid);
+    lb.store(smem + BM * kRowBytes, tid);
+  }
   __syncthreads();
 
   const int frag_row = lane & 31;
   const int frag_k = (lane >> 5) * 16;  // byte offset of this lane's 8 K values
-
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < ktiles) gload(kt + 1);
+    if (kt + 1 < ktiles) gload(kbeg + (kt + 1) * kBK);
     const char* As = smem + cur * kStageBytes;
     const char* Bs = As + BM * kRowBytes;
 #pragma unroll
@@ -199,56 +384,311 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < ktiles) sstore(cur ^ 1);
+    if (kt + 1 < ktiles) {
+      char* nxt = smem + (cur ^ 1) * kStageBytes;
+      la.store(nxt, tid);
+      lb.store(nxt + BM * kRowBytes, tid);
+    }
     __syncthreads();
   }
 
-  // Epilogue: lane holds output row m = (lane % 32) of each 32x32 tile and
-  // columns n = 8*(r/4) + 4*(lane/32) + r%4.
-  const int half = lane >> 5;
+  GemmArgs go = g;  // split-K: this split's fp32 slab
+  if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
+  store_tile<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS kernel for two K-major operands (the forward product).
+//
+// Global data goes straight into LDS with global_load_lds_dwordx4 (each lane's
+// 16 bytes land at the wave-uniform destination + 16*lane), so staging takes
+// no registers and no LDS-write instructions.  K advances DBK per stage over
+// NST LDS stages: the loads for stage k+NST-1 are issued right after the
+// barrier that opens stage k, and each wave waits only for its own loads of
+// the stage it is about to read (explicit vmcnt, then a bare s_barrier: a
+// __syncthreads() fence would wait for every load in flight).  LDS rows are
+// DBK*2 bytes without padding, XOR-swizzled by swz().  Rows past M or N are
+// clamped to the last row (they only feed outputs that are not stored); K
+// must be a multiple of DBK in every split.
+// ---------------------------------------------------------------------------
+// LDS row swizzle: chunk c (8 K values) of row r sits in slot c ^ swz(r).
+// For 4-chunk (64-byte) and 8-chunk (128-byte) rows this keeps the 16-byte
+// reads of 8 or 16 consecutive rows on distinct banks.
+template <int kChunks>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (kChunks == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+  else return ((r >> 1) ^ ((r & 1) << 2)) & 7;
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are
+// outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+// left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+
+// Issues one stage's loads for this wave: kPerWave 1 KB wave loads of A rows
+// then of B rows into the stage at `base`, K offset `k0` of the split.
+template <int kPerWave, int kOpBytes, int kRowB>
+__device__ __forceinline__ void dma_stage(const uint16_t* const (&pa)[kPerWave], const uint16_t* const (&pb)[kPerWave],
+                                          char* base, int wave, int64_t k0) {
+  constexpr int kRowsPerLoad = 1024 / kRowB;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int64_t m = m0 + wm * TM + i * 32 + frag_row;
-    if (m >= g.M) continue;
+  for (int q = 0; q < kPerWave; ++q)
+    __builtin_amdgcn_global_load_lds(pa[q] + k0, base + (wave * kPerWave + q) * kRowsPerLoad * kRowB, 16, 0, 0);
+#pragma unroll
+  for (int q = 0; q < kPerWave; ++q)
+    __builtin_amdgcn_global_load_lds(pb[q] + k0, base + kOpBytes + (wave * kPerWave + q) * kRowsPerLoad * kRowB, 16,
+                                     0, 0);
+}
+
+template <int WM, int WN, int DBK, int NST>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int kWaves = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int kRowB = DBK * 2;                 // bytes per LDS row
+  constexpr int kChunks = DBK / 8;               // 16-byte chunks per row
+  constexpr int kRowsPerLoad = 1024 / kRowB;     // rows covered by one wave load
+  constexpr int kOpBytes = BM * kRowB;           // one operand, one stage
+  constexpr int kStage = 2 * kOpBytes;
+  constexpr int kPerWave = kOpBytes / 1024 / kWaves;  // wave loads per operand per stage
+  constexpr int kDmaPerStage = 2 * kPerWave;          // per wave
+  static_assert(kPerWave * kWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
+  static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
+  static_assert(NST >= 2 && NST * kStage <= 160 * 1024, "LDS stages do not fit");
+
+  __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t tiles_m = lz_cdiv(g.M, BM), tiles_n = lz_cdiv(g.N, BN);
+  int64_t tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  const int64_t kbeg = (int64_t)blockIdx.y * g.kper, kend = min(g.K, kbeg + g.kper);
+  const int ktiles = kend > kbeg ? (int)((kend - kbeg) / DBK) : 0;
+
+  // This lane's source rows: wave load q covers LDS rows
+  // (wave*kPerWave+q)*kRowsPerLoad + lane/kChunks, slot lane%kChunks holding
+  // chunk slot ^ swz(row).
+  const uint16_t* pa[kPerWave];
+  const uint16_t* pb[kPerWave];
+#pragma unroll
+  for (int q = 0; q < kPerWave; ++q) {
+    const int r = (wave * kPerWave + q) * kRowsPerLoad + lane / kChunks;
+    const int c = (lane % kChunks) ^ swz<kChunks>(r);
+    pa[q] = g.A + min(m0 + r, g.M - 1) * g.lda + kbeg + c * 8;
+    pb[q] = g.B + min(n0 + r, g.N - 1) * g.ldb + kbeg + c * 8;
+  }
+
+  // fragment byte offsets within a stage, per 16-deep sub-step
+  constexpr int kSub = DBK / 16;
+  const int frag_row = lane & 31, frag_half = lane >> 5;
+  int offa[FM][kSub], offb[FN][kSub];
+#pragma unroll
+  for (int kk = 0; kk < kSub; ++kk) {
+    const int c = kk * 2 + frag_half;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = wm * TM + i * 32 + frag_row;
+      offa[i][kk] = r * kRowB + ((c ^ swz<kChunks>(r)) << 4);
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
+      const int r = wn * TN + j * 32 + frag_row;
+      offb[j][kk] = kOpBytes + r * kRowB + ((c ^ swz<kChunks>(r)) << 4);
+    }
+  }
+
+  f32x16_t acc[FM][FN];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wn * TN + j * 32 + q * 8 + half * 4;
-        if (n >= g.N) continue;
-        const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-        store_out4(g, m, n, v);
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < ktiles) dma_stage<kPerWave, kOpBytes, kRowB>(pa, pb, smem + s * kStage, wave, (int64_t)s * DBK);
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // this wave's loads of stage kt are done once at most the loads of the
+    // stages issued after it are outstanding; the barrier then publishes every
+    // wave's part and retires the reads of stage kt-1, whose slot is refilled
+    const int later = min(ktiles - 1 - kt, NST - 2);
+    if (later >= 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kDmaPerStage));
+    else if (later == 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaPerStage));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_barrier();
+    if (kt + NST - 1 < ktiles)
+      dma_stage<kPerWave, kOpBytes, kRowB>(pa, pb, smem + ((kt + NST - 1) % NST) * kStage, wave,
+                                          (int64_t)(kt + NST - 1) * DBK);
+    const char* st = smem + (kt % NST) * kStage;
+#pragma unroll
+    for (int kk = 0; kk < kSub; ++kk) {
+      bf16x8_t fa[FN], fb[FM];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) fa[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + offb[j][kk]));
+#pragma unroll
+      for (int i = 0; i < FM; ++i) fb[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + offa[i][kk]));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave is done with the stages before the epilogue may reuse LDS
+
+  GemmArgs go = g;  // split-K: this split's fp32 slab
+  if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
+  store_tile<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+}
+
+// Sums the fp32 partial slabs of a split-K product and applies the epilogue
+// (alpha, beta*C, R) to the real output, 4 columns per thread, in a fixed
+// order so results do not depend on scheduling.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const float* __restrict__ slabs, int splits) {
+  const int64_t n4 = lz_cdiv(g.N, 4);
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= g.M * n4) return;
+  const int64_t m = idx / n4, n = (idx - m * n4) * 4;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t mn = g.M * g.N;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* row = slabs + sp * mn + m * g.N;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < g.N) v[e] += row[n + e];
+  }
+  store_out4(g, m, n, v);
+}
+
+// Tile configurations: 0 = 256x256 with 8 waves (128x64 per wave),
+// 1 = 256x256 with 4 waves (128x128 per wave, accumulators in AGPRs),
+// 2 = 128x128 with 4 waves; 5 = the direct-to-LDS kernel (both operands
+// K-major, 8 waves, 2 stages of 64 K).
+struct Plan {
+  int cfg;
+  int splits;
+  int64_t kper;
+};
+
+Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
+  const int cus = lz_num_cus();
+  const int64_t big = lz_cdiv(M, 256) * lz_cdiv(N, 256);
+  const int64_t small = lz_cdiv(M, 128) * lz_cdiv(N, 128);
+  // K-major A: the 8-wave tile; M-major A (weight gradients): the 4-wave
+  // tile, whose larger per-wave sub-tile holds up better with the in-register
+  // transposes of both operands.
+  Plan p{ak ? 0 : 1, 1, K};
+  if (ak && bk) {
+    // Both K-major: the 8-wave 256x256 tile (one per CU) is the faster tile;
+    // 128x128 tiles (two per CU) win when they fill the chip in fewer rounds.
+    // Relative speeds measured on MI355X: 0.85 and 0.75.
+    const double c256 = (double)lz_cdiv(big, cus) * 4.0 / 0.85;
+    const double c128 = (double)lz_cdiv(small, 2 * cus) * 2.0 / 0.75;
+    // the direct-to-LDS kernel needs whole 64-deep K steps
+    p.cfg = c128 < c256 ? 2 : (K % 64 == 0 ? 5 : 0);
+  }
+  if (p.cfg != 2 && big < 2 * cus && K >= 2048) {
+    // Long K over few output tiles: split K so the grid covers the chip.
+    // Cost in units of one un-split tile: rounds of the grid over the CUs,
+    // each 1/S as long, plus a small charge per split for the slab traffic.
+    double best = 1e30;
+    for (int sp = 1; sp <= 8; ++sp) {
+      const int64_t kper = lz_cdiv(lz_cdiv(K, sp), 64) * 64;
+      if (sp > 1 && kper < 512) break;
+      if (lz_cdiv(K, kper) != sp) continue;
+      const double cost = (double)lz_cdiv(big * sp, cus) / sp + 0.05 * (sp - 1);
+      if (cost < best - 1e-9) {
+        best = cost;
+        p.splits = sp;
+        p.kper = kper;
       }
     }
   }
+  return p;
 }
 
-template <int BM, int BN, int WM, int WN>
-int launch(const GemmArgs& g, hipStream_t s) {
+int64_t plan_workspace(const Plan& p, int64_t M, int64_t N) { return p.splits > 1 ? p.splits * M * N * 4 : 0; }
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BK>
+int launch(const GemmArgs& g, int splits, hipStream_t s) {
   const int64_t tiles = lz_cdiv(g.M, BM) * lz_cdiv(g.N, BN);
   LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
-  gemm_nt_kernel<BM, BN, WM, WN><<<(unsigned)tiles, 64 * WM * WN, 0, s>>>(g);
-  return lz_check_launch("lz_gemm_nt");
+  gemm_kernel<BM, BN, WM, WN, AK, BK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  return lz_check_launch("lz_gemm");
+}
+
+template <int WM, int WN, int DBK, int NST>
+int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
+  const int64_t tiles = lz_cdiv(g.M, 256) * lz_cdiv(g.N, 256);
+  LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
+  gemm_dma_kernel<WM, WN, DBK, NST><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  return lz_check_launch("lz_gemm");
+}
+
+template <bool AK, bool BK>
+int dispatch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
+  if constexpr (AK && BK) {
+    if (cfg == 5) return launch_dma<2, 4, 64, 2>(g, splits, s);
+  }
+  switch (cfg) {
+    case 0:
+      return launch<256, 256, 2, 4, AK, BK>(g, splits, s);
+    case 1:
+      return launch<256, 256, 2, 2, AK, BK>(g, splits, s);
+    default:
+      return launch<128, 128, 2, 2, AK, BK>(g, splits, s);
+  }
+}
+
+int dispatch_layout(const GemmArgs& g, bool ak, bool bk, int cfg, int splits, hipStream_t s) {
+  if (ak && bk) return dispatch<true, true>(g, cfg, splits, s);
+  if (ak) return dispatch<true, false>(g, cfg, splits, s);
+  if (bk) return dispatch<false, true>(g, cfg, splits, s);
+  return dispatch<false, false>(g, cfg, splits, s);
 }
 
 }  // namespace
 
-// C = alpha * A . B^T (+ beta*C) (+ R).  A: [M,K] bf16 (lda), B: [N,K] bf16
-// (ldb), C: [M,N] bf16 or fp32 (ldc), R: optional [M,N] bf16 (ldr).
-// Requirements: K % 8 == 0, lda % 8 == 0, ldb % 8 == 0, A and B 16-byte aligned.
-LZ_EXPORT int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype,
-                         const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta,
-                         void* stream) {
-  LZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lz_gemm_nt: negative shape");
+// Workspace bytes lz_gemm uses for this shape and layout (0 when the product
+// is not split along K).
+LZ_EXPORT int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return plan_workspace(make_plan(M, N, K, a_kmajor != 0, b_kmajor != 0), M, N);
+}
+
+// C = alpha * sum_k A(m,k) B(n,k) (+ beta*C) (+ R), see the top of this file
+// for the operand layouts.  C: [M,N] bf16 or fp32 (ldc), R: optional [M,N]
+// bf16 (ldr).  Requirements: A and B 16-byte aligned, lda and ldb multiples
+// of 8; K % 8 == 0 for a K-major operand; M % 8 == 0 (N % 8 == 0) for an
+// M-major A (N-major B).  `ws` (16-byte aligned, ws_bytes long, may be null)
+// holds the fp32 partial products when K is split; with less workspace than
+// lz_gemm_workspace() reports the product runs unsplit.
+LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb, int b_kmajor, void* C,
+                      int64_t ldc, int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha,
+                      float beta, void* ws, int64_t ws_bytes, void* stream) {
+  LZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lz_gemm: negative shape");
   if (M == 0 || N == 0) return LZ_OK;
-  LZ_REQUIRE(A && B && C, "lz_gemm_nt: null pointer");
-  LZ_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0, "lz_gemm_nt: K (%lld), lda, ldb must be multiples of 8",
-             (long long)K);
-  LZ_REQUIRE(lz_aligned16(A) && lz_aligned16(B), "lz_gemm_nt: A and B must be 16-byte aligned");
-  LZ_REQUIRE(lda >= K && ldb >= K && ldc >= N && (R == nullptr || ldr >= N), "lz_gemm_nt: bad leading dimension");
-  LZ_REQUIRE(c_dtype == LZ_BF16 || c_dtype == LZ_F32, "lz_gemm_nt: bad output dtype %d", c_dtype);
+  LZ_REQUIRE(A && B && C, "lz_gemm: null pointer");
+  LZ_REQUIRE(lda % 8 == 0 && ldb % 8 == 0, "lz_gemm: lda (%lld) and ldb (%lld) must be multiples of 8",
+             (long long)lda, (long long)ldb);
+  LZ_REQUIRE((!a_kmajor && !b_kmajor) || K % 8 == 0, "lz_gemm: K (%lld) must be a multiple of 8", (long long)K);
+  LZ_REQUIRE(a_kmajor || M % 8 == 0, "lz_gemm: M-major A needs M %% 8 == 0 (M = %lld)", (long long)M);
+  LZ_REQUIRE(b_kmajor || N % 8 == 0, "lz_gemm: N-major B needs N %% 8 == 0 (N = %lld)", (long long)N);
+  LZ_REQUIRE(lz_aligned16(A) && lz_aligned16(B), "lz_gemm: A and B must be 16-byte aligned");
+  LZ_REQUIRE(lda >= (a_kmajor ? K : M) && ldb >= (b_kmajor ? K : N) && ldc >= N && (R == nullptr || ldr >= N),
+             "lz_gemm: bad leading dimension");
+  LZ_REQUIRE(c_dtype == LZ_BF16 || c_dtype == LZ_F32, "lz_gemm: bad output dtype %d", c_dtype);
+  LZ_REQUIRE(ws_bytes >= 0 && (ws == nullptr || lz_aligned16(ws)), "lz_gemm: workspace must be 16-byte aligned");
   GemmArgs g;
   g.A = (const uint16_t*)A;
   g.B = (const uint16_t*)B;
@@ -267,11 +707,37 @@ LZ_EXPORT int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb,
   const int esz = g.c_f32 ? 4 : 2;
   g.vec_store = (N % 4 == 0) && (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & (4 * esz - 1)) == 0) &&
                 (R == nullptr || ((ldr % 4 == 0) && (reinterpret_cast<uintptr_t>(R) & 7) == 0));
+  g.kper = K > 0 ? K : 1;
+  g.slab = 0;
   hipStream_t s = lz_stream(stream);
-  if (K == 0) {
-    // nothing to reduce: C = beta*C + R handled by the epilogue with zero accumulators
+  const bool ak = a_kmajor != 0, bk = b_kmajor != 0;
+  Plan p = make_plan(M, N, K, ak, bk);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_workspace(p, M, N))) {
+    p.splits = 1;
+    p.kper = g.kper;
   }
-  const int64_t big_tiles = lz_cdiv(M, 256) * lz_cdiv(N, 256);
-  if (big_tiles >= lz_num_cus()) return launch<256, 256, 2, 4>(g, s);
-  return launch<128, 128, 2, 2>(g, s);
+  if (p.splits == 1) return dispatch_layout(g, ak, bk, p.cfg, 1, s);
+  GemmArgs gs = g;  // partial products into fp32 slabs [splits][M][N]
+  gs.C = ws;
+  gs.ldc = N;
+  gs.c_f32 = 1;
+  gs.alpha = 1.f;
+  gs.beta = 0.f;
+  gs.R = nullptr;
+  gs.vec_store = N % 4 == 0;
+  gs.kper = p.kper;
+  gs.slab = M * N;
+  int rc = dispatch_layout(gs, ak, bk, p.cfg, p.splits, s);
+  if (rc) return rc;
+  const int64_t work = M * lz_cdiv(N, 4);
+  splitk_reduce_kernel<<<(unsigned)lz_cdiv(work, 256), 256, 0, s>>>(g, static_cast<const float*>(ws), p.splits);
+  return lz_check_launch("lz_gemm(split-K reduce)");
+}
+
+// C = alpha * A . B^T (+ beta*C) (+ R) with A: [M,K] and B: [N,K] row-major,
+// never split along K (no workspace).
+LZ_EXPORT int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype,
+                         const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                         void* stream) {
+  return lz_gemm(A, lda, 1, B, ldb, 1, C, ldc, c_dtype, R, ldr, M, N, K, alpha, beta, nullptr, 0, stream);
 }

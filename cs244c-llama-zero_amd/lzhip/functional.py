@@ -56,20 +56,18 @@ def fused_weight(weights: Sequence[torch.Tensor]) -> torch.Tensor:
 
 
 def _linear_fwd(x2: torch.Tensor, w: torch.Tensor, residual2: Optional[torch.Tensor] = None) -> torch.Tensor:
-    return ops.gemm_nt(ops.nt_operand(x2), ops.nt_operand(w), residual=residual2)
+    return ops.gemm(x2, w, residual=residual2)
 
 
 def _linear_bwd(dy2: torch.Tensor, x2: torch.Tensor, w: torch.Tensor, need_dx: bool, need_dw: bool
                 ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
-    """dx = dy . W (NT against W^T), dW = dy^T . x (NT against x^T)."""
+    """dx = dy . W (W read N-major), dW = dy^T . x (both read M/N-major): the
+    GEMM consumes the stored layouts directly, nothing is transposed."""
     dx = dw = None
     if need_dx:
-        wt = ops.transpose_padded(w)              # [K, N8]
-        dx = ops.gemm_nt(ops.nt_operand(dy2), wt)  # [M, K]
+        dx = ops.gemm(dy2, w, b_kmajor=False)  # [M, K]
     if need_dw:
-        dyt = ops.transpose_padded(dy2)           # [N, M8]
-        xt = ops.transpose_padded(x2)             # [K, M8]
-        dw = ops.gemm_nt(dyt, xt, out_dtype=w.dtype)  # [N, K]
+        dw = ops.gemm(dy2, x2, a_kmajor=False, b_kmajor=False, out_dtype=w.dtype)  # [N, K]
     return dx, dw
 
 

@@ -454,36 +454,68 @@ def set_gemm_probe(probe: Optional[LaunchProbe]) -> None:
 def gemm_nt(a2: torch.Tensor, b2: torch.Tensor, out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
             residual: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
     """out[M,N] = alpha * a2[M,K] . b2[N,K]^T (+ beta*out) (+ residual)."""
+    return gemm(a2, b2, True, True, out=out, out_dtype=out_dtype, residual=residual, alpha=alpha, beta=beta)
+
+
+def _gemm_operand(t: torch.Tensor, kmajor: bool) -> Tuple[torch.Tensor, bool]:
+    """Returns (operand, kmajor) satisfying the kernel's layout rules.  A
+    K-major operand is zero-padded along K when needed (nt_operand); an
+    M/N-major operand [K, R] whose R, row stride or base is not 8-element
+    aligned is transposed into a K-major padded copy instead."""
+    if kmajor:
+        return nt_operand(t), True
+    k, r = t.shape
+    if r % 8 == 0 and _row_stride(t) % 8 == 0 and t.data_ptr() % 16 == 0 and t.stride(-1) == 1:
+        return t, False
+    return transpose_padded(t), True
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool = True,
+         out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+         residual: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """out[M,N] = alpha * sum_k A(m,k) B(n,k) (+ beta*out) (+ residual), bf16
+    operands, fp32 accumulation.  `a` is [M,K] when a_kmajor else [K,M];
+    `b` is [N,K] when b_kmajor else [K,N].  So x.W^T is gemm(x, W),
+    dy.W is gemm(dy, W, b_kmajor=False) and dy^T.x is
+    gemm(dy, x, a_kmajor=False, b_kmajor=False)."""
+    require_gpu(a, b, out, residual)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError(
+            f"the MFMA GEMM takes bfloat16 operands (got {a.dtype}, {b.dtype}); "
+            "run the model in bfloat16 (--dtype bfloat16)"
+        )
+    M, K = a.shape if a_kmajor else (a.shape[1], a.shape[0])
+    N, K2 = b.shape if b_kmajor else (b.shape[1], b.shape[0])
+    if K != K2:
+        raise ValueError(f"GEMM reduction mismatch {K} vs {K2}")
+    a, a_kmajor = _gemm_operand(a, a_kmajor)
+    b, b_kmajor = _gemm_operand(b, b_kmajor)
+    if K % 8 and (a_kmajor or b_kmajor):
+        # a K-major operand is zero-padded to K8: bring the other one to the same K
+        if not a_kmajor:
+            a, a_kmajor = transpose_padded(a), True
+        if not b_kmajor:
+            b, b_kmajor = transpose_padded(b), True
+    Kp = _round8(K) if (a_kmajor or b_kmajor) else K
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or a.dtype, device=a.device)
+    if residual is not None and (residual.dtype != torch.bfloat16 or tuple(residual.shape) != (M, N)):
+        raise ValueError("residual must be a bf16 [M, N] view")
+    lib = _lib.load()
+    ws_bytes = int(lib.lz_gemm_workspace(M, N, Kp, int(a_kmajor), int(b_kmajor)))
+    ws = torch.empty(((ws_bytes + 15) // 16) * 4, dtype=torch.float32, device=a.device) if ws_bytes else None
     probe = _gemm_probe
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
-        out = _gemm_nt(a2, b2, out, out_dtype, residual, alpha, beta)
+    _lib.call("lz_gemm", a.data_ptr(), _row_stride(a), int(a_kmajor), b.data_ptr(), _row_stride(b), int(b_kmajor),
+              out.data_ptr(), _row_stride(out), dtype_code(out), _ptr(residual),
+              _row_stride(residual) if residual is not None else 0, M, N, Kp, float(alpha), float(beta), _ptr(ws),
+              ws_bytes if ws is not None else 0, stream_ptr(a.device))
+    if probe is not None:
         end.record()
-        probe.add(2.0 * a2.shape[0] * b2.shape[0] * a2.shape[1], start, end)
-        return out
-    return _gemm_nt(a2, b2, out, out_dtype, residual, alpha, beta)
-
-
-def _gemm_nt(a2, b2, out, out_dtype, residual, alpha, beta) -> torch.Tensor:
-    require_gpu(a2, b2, out, residual)
-    if a2.dtype != torch.bfloat16 or b2.dtype != torch.bfloat16:
-        raise TypeError(
-            f"the MFMA GEMM takes bfloat16 operands (got {a2.dtype}, {b2.dtype}); "
-            "run the model in bfloat16 (--dtype bfloat16)"
-        )
-    M, K = a2.shape
-    N, K2 = b2.shape
-    if K != K2:
-        raise ValueError(f"GEMM reduction mismatch {K} vs {K2}")
-    if out is None:
-        out = torch.empty((M, N), dtype=out_dtype or a2.dtype, device=a2.device)
-    if residual is not None and (residual.dtype != torch.bfloat16 or tuple(residual.shape) != (M, N)):
-        raise ValueError("residual must be a bf16 [M, N] view")
-    _lib.call("lz_gemm_nt", a2.data_ptr(), _row_stride(a2), b2.data_ptr(), _row_stride(b2), out.data_ptr(),
-              _row_stride(out), dtype_code(out), _ptr(residual), _row_stride(residual) if residual is not None else 0,
-              M, N, K, float(alpha), float(beta), stream_ptr(a2.device))
+        probe.add(2.0 * M * N * K, start, end)
     return out
 
 

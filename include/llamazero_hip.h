@@ -163,9 +163,22 @@ int lz_transpose(const void* src, void* dst, int dtype, int64_t nb1, int64_t nb2
 int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows, int64_t cols, int dtype,
               void* stream);
 
-/* bf16 MFMA GEMM C = alpha*A.B^T (+beta*C) (+R): the nn.Linear products of
- * model/llama.py:81-84,133,139-141,178 and their gradients.  K, lda, ldb
- * multiples of 8; A, B 16-byte aligned; C bf16 or fp32. */
+/* bf16 MFMA GEMM C[M,N] = alpha * sum_k A(m,k) B(n,k) (+beta*C) (+R): the
+ * nn.Linear products of model/llama.py:81-84,133,139-141,178 and their
+ * gradients, fp32 accumulation, C bf16 or fp32, R an optional bf16 residual.
+ *   a_kmajor = 1: A(m,k) = A[m*lda + k]   a_kmajor = 0: A(m,k) = A[k*lda + m]
+ *   b_kmajor = 1: B(n,k) = B[n*ldb + k]   b_kmajor = 0: B(n,k) = B[k*ldb + n]
+ * so y = x.W^T is (1,1), dx = dy.W is (1,0) and dW = dy^T.x is (0,0).
+ * A and B 16-byte aligned, lda and ldb multiples of 8, K % 8 == 0 when an
+ * operand is K-major, M % 8 == 0 (N % 8 == 0) for an M-major A (N-major B).
+ * When few output tiles meet a long K the product is split along K into
+ * fp32 partial slabs in `ws` (lz_gemm_workspace bytes) and summed in a fixed
+ * order; with a smaller workspace it runs unsplit. */
+int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor);
+int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb, int b_kmajor, void* C, int64_t ldc,
+            int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* ws,
+            int64_t ws_bytes, void* stream);
+/* lz_gemm with both operands K-major and no workspace. */
 int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype, const void* R,
                int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* stream);
 

@@ -99,6 +99,68 @@ def test_gemm_strided_views_and_padding_helpers():
     assert torch.count_nonzero(xt[:, 37:]) == 0
 
 
+def _layout_operand(t, kmajor):
+    """t is the logical [rows, K] operand; returns the stored tensor."""
+    return t.to(DEV) if kmajor else t.t().contiguous().to(DEV)
+
+
+@pytest.mark.parametrize("a_kmajor,b_kmajor", [(True, True), (True, False), (False, True), (False, False)])
+@pytest.mark.parametrize(
+    "M,N,K",
+    [(64, 64, 64), (520, 264, 200), (1000, 1000, 520), (2048, 1024, 1536),
+     # few output tiles, long K: split along K (K not a multiple of 64 in the last case)
+     (512, 384, 8192), (1024, 768, 8200)],
+)
+def test_gemm_layouts(M, N, K, a_kmajor, b_kmajor):
+    g = _seed(M * 3 + N + K + 2 * a_kmajor + b_kmajor)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    ref = a.double() @ b.double().t()
+    A, B = _layout_operand(a, a_kmajor), _layout_operand(b, b_kmajor)
+    c32 = ops.gemm(A, B, a_kmajor, b_kmajor, out_dtype=torch.float32).cpu()
+    tol = 1e-5 * math.sqrt(K) * float(a.float().abs().max() * b.float().abs().max()) * 4
+    assert float((c32.double() - ref).abs().max()) <= tol
+    c16 = ops.gemm(A, B, a_kmajor, b_kmajor).cpu()
+    assert torch.allclose(c16.double(), c32.double(), rtol=2 ** -8, atol=1e-6)
+    # accumulation into an existing fp32 C and a bf16 residual, split or not
+    c0 = torch.randn(M, N, generator=g)
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    acc = c0.to(DEV)
+    ops.gemm(A, B, a_kmajor, b_kmajor, out=acc, alpha=0.5, beta=1.0, residual=r.to(DEV))
+    want = 0.5 * ref + c0.double() + r.double()
+    assert float((acc.cpu().double() - want).abs().max()) <= 0.5 * tol + 1e-5 * float(want.abs().max())
+
+
+def test_gemm_split_k_workspace_and_determinism():
+    lib = ops._lib.load()
+    M, N, K = 512, 384, 8192
+    assert lib.lz_gemm_workspace(M, N, K, 0, 0) > 0  # the plan splits this shape
+    assert lib.lz_gemm_workspace(16384, 4096, 2048, 1, 1) == 0
+    g = _seed(5)
+    a = torch.randn(K, M, generator=g).to(torch.bfloat16).to(DEV)
+    b = torch.randn(K, N, generator=g).to(torch.bfloat16).to(DEV)
+    c1 = ops.gemm(a, b, False, False, out_dtype=torch.float32)
+    c2 = ops.gemm(a, b, False, False, out_dtype=torch.float32)
+    assert torch.equal(c1, c2)
+    # without a workspace the same product runs unsplit (same values up to summation order)
+    c3 = torch.empty_like(c1)
+    ops._lib.call("lz_gemm", a.data_ptr(), M, 0, b.data_ptr(), N, 0, c3.data_ptr(), N, 0, 0, 0, M, N, K, 1.0, 0.0,
+                  0, 0, ops.stream_ptr(a.device))
+    assert torch.allclose(c1, c3, rtol=1e-4, atol=1e-3)
+
+
+def test_gemm_unaligned_mn_major_operands_fall_back():
+    g = _seed(13)
+    M, N, K = 37, 29, 45
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    ref = a.double() @ b.double().t()
+    for ak in (True, False):
+        for bk in (True, False):
+            c = ops.gemm(_layout_operand(a, ak), _layout_operand(b, bk), ak, bk, out_dtype=torch.float32).cpu()
+            assert torch.allclose(c.double(), ref, rtol=1e-5, atol=1e-3), (ak, bk)
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm
 # ---------------------------------------------------------------------------
