@@ -18,7 +18,7 @@ Modules and the reference code each follows:
   engine.py zero/stage{0,1,2,3}*.py step semantics at world_size=1.
   data.py   data/fineweb.py:100-139 and train.py:139-145 (synthetic data).
 
-How each part is pinned (see tests/test_oracle_*.py):
+How each part is pinned (tests/test_oracle.py):
   - the reference's golden loss 4.901787757873535 (tests/test_model.py:46-64)
     pins init order, RMSNorm, RoPE, attention, SwiGLU and the chunked loss;
   - library routines: F.scaled_dot_product_attention, F.cross_entropy,
