@@ -54,12 +54,20 @@ struct AttnArgs {
   float scale;
 };
 
-__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
-  uint4 w;
-  w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-  w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-  w.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-  w.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 (round to nearest even) packed low/high, one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
+// Elements e0..e0+7 of an accumulator -> an 8 x bf16 MFMA operand.
+__device__ __forceinline__ bf16x8_t pack8(const f32x16_t& v, int e0) {
+  const uint4 w = make_uint4(pack_bf16x2(v[e0], v[e0 + 1]), pack_bf16x2(v[e0 + 2], v[e0 + 3]),
+                             pack_bf16x2(v[e0 + 4], v[e0 + 5]), pack_bf16x2(v[e0 + 6], v[e0 + 7]));
   return __builtin_bit_cast(bf16x8_t, w);
 }
 
@@ -130,16 +138,22 @@ __device__ __forceinline__ void load_trows(char* dst, int rb, const uint16_t* sr
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  256 threads; 128 queries per workgroup (32 per wave); 64-key steps.
+// Forward.  256 threads; 128 queries per workgroup (32 per wave); 64-key
+// steps.  The K and V^T tiles of step i+1 are loaded into registers while step
+// i computes from the other LDS buffer, so global latency overlaps the MFMAs.
+// Softmax in log2 space: p = exp2(s*c - m) with c = scale*log2(e) folded into
+// one FMA; O and l are rescaled only when some lane's running max moved.
 // ---------------------------------------------------------------------------
 template <int HD>
-__global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_kernel(AttnArgs a) {
   constexpr int BQ = 128, BKV = 64, NT = 256;
   constexpr int KROW = HD * 2 + 16;
   constexpr int VROW = BKV * 2 + 8;
-  __shared__ __attribute__((aligned(16))) char smem[BKV * KROW + HD * VROW];
-  char* Ks = smem;
-  char* Vts = smem + BKV * KROW;
+  constexpr int kBuf = BKV * KROW + HD * VROW;
+  constexpr int kKC = BKV * HD / 8 / NT;  // 16-byte K chunks per thread per step
+  constexpr int kVC = HD * BKV / 8 / NT;  // 16-byte V^T chunks per thread per step
+  static_assert(kKC * NT * 8 == BKV * HD && kVC * NT * 8 == HD * BKV, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) char smem[2 * kBuf];
 
   const int S = a.S, H = a.H, KV = a.KV;
   const int nqb = (S + BQ - 1) / BQ;
@@ -172,10 +186,46 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
   const uint16_t* vtbase = a.vt + (int64_t)(b * KV + g) * HD * S;
 
-  for (int k0 = 0; k0 < kv_end; k0 += BKV) {
-    load_rows<HD, BKV, NT>(Ks, KROW, kbase, a.ldk, k0, S, tid);
-    load_trows<HD, BKV, NT>(Vts, VROW, vtbase, S, k0, tid);
-    __syncthreads();
+  uint4 kreg[kKC], vreg[kVC];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kKC; ++i) {
+      const int cidx = tid + i * NT, row = cidx / (HD / 8), ch = cidx % (HD / 8);
+      const int r = k0 + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(kbase + (int64_t)min(r, S - 1) * a.ldk + ch * 8);
+      const uint32_t msk = r < S ? ~0u : 0u;
+      kreg[i] = make_uint4(v.x & msk, v.y & msk, v.z & msk, v.w & msk);
+    }
+#pragma unroll
+    for (int i = 0; i < kVC; ++i) {
+      const int cidx = tid + i * NT, row = cidx / (BKV / 8), ch = cidx % (BKV / 8);
+      vreg[i] = load8(vtbase + (int64_t)row * S, k0 + ch * 8, S);
+    }
+  };
+  auto lstore = [&](char* buf) {
+#pragma unroll
+    for (int i = 0; i < kKC; ++i) {
+      const int cidx = tid + i * NT, row = cidx / (HD / 8), ch = cidx % (HD / 8);
+      *reinterpret_cast<uint4*>(buf + row * KROW + ch * 16) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kVC; ++i) {
+      const int cidx = tid + i * NT, row = cidx / (BKV / 8), ch = cidx % (BKV / 8);
+      uint2* d = reinterpret_cast<uint2*>(buf + BKV * KROW + row * VROW + ch * 16);
+      d[0] = make_uint2(vreg[i].x, vreg[i].y);
+      d[1] = make_uint2(vreg[i].z, vreg[i].w);
+    }
+  };
+
+  const int nsteps = (kv_end + BKV - 1) / BKV;
+  gload(0);
+  lstore(smem);
+  __syncthreads();
+  for (int it = 0; it < nsteps; ++it) {
+    const int k0 = it * BKV;
+    if (it + 1 < nsteps) gload(k0 + BKV);
+    const char* Ks = smem + (it & 1) * kBuf;
+    const char* Vts = Ks + BKV * KROW;
     if (k0 < kv_end_w) {
       f32x16_t s[2];
 #pragma unroll
@@ -194,39 +244,38 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float x = s[t][r] * c;
           if (need_mask) {
             const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (kv > qrow || kv >= S) x = -INFINITY;
+            if (kv > qrow || kv >= S) s[t][r] = -INFINITY;
           }
-          s[t][r] = x;
-          mx = fmaxf(mx, x);
+          mx = fmaxf(mx, s[t][r]);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx);
-      const float alpha = exp2f(m - m_new);
+      const float m_new = fmaxf(m, mx * c);
+      const float nm = -m_new;
       float rs = 0.f;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(s[t][r] - m_new);
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
           s[t][r] = p;
           rs += p;
         }
       rs += __shfl_xor(rs, 32, 64);
-      l = l * alpha + rs;
+      if (__builtin_amdgcn_read_exec() & __ballot(m_new != m)) {  // some lane's max moved
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      }
+      l += rs;
       m = m_new;
 #pragma unroll
-      for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-#pragma unroll
       for (int ks = 0; ks < BKV / 16; ++ks) {
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = s[ks >> 1][8 * (ks & 1) + e];
-        const bf16x8_t pb = pack_bf16x8(pv);
+        const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
 #pragma unroll
         for (int i = 0; i < HD / 32; ++i) {
           const char* row = Vts + (i * 32 + l32) * VROW;
@@ -235,6 +284,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
         }
       }
     }
+    if (it + 1 < nsteps) lstore(smem + ((it + 1) & 1) * kBuf);
     __syncthreads();
   }
   if (qrow < S) {
@@ -352,21 +402,15 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(AttnArgs a) {
               const int r = 4 * r4 + e;
               const int q = q0 + qlb + e;
               const bool ok = q < S && kvrow <= q && kvrow < S;
-              const float p = ok ? exp2f(s[t][r] * c - lv[e]) : 0.f;
+              const float p = ok ? __builtin_amdgcn_exp2f(fmaf(s[t][r], c, -lv[e])) : 0.f;
               dp[t][r] = p * (dp[t][r] - dvv[e]);
               s[t][r] = p;
             }
           }
 #pragma unroll
         for (int ks = 0; ks < BQ / 16; ++ks) {
-          float pv[8], dsv[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            pv[e] = s[ks >> 1][8 * (ks & 1) + e];
-            dsv[e] = dp[ks >> 1][8 * (ks & 1) + e];
-          }
-          const bf16x8_t pb = pack_bf16x8(pv);
-          const bf16x8_t dsb = pack_bf16x8(dsv);
+          const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
+          const bf16x8_t dsb = pack8(dp[ks >> 1], 8 * (ks & 1));
 #pragma unroll
           for (int i = 0; i < HD / 32; ++i) {
             const char* dorow = dOts + (i * 32 + l32) * TROW;
@@ -475,15 +519,12 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
         for (int r = 0; r < 16; ++r) {
           const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           const bool ok = kv <= qrow && kv < S && qrow < S;
-          const float p = ok ? exp2f(st[t][r] * c - lse2) : 0.f;
+          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(st[t][r], c, -lse2)) : 0.f;
           dpt[t][r] = p * (dpt[t][r] - Dq);
         }
 #pragma unroll
       for (int ks = 0; ks < BKV / 16; ++ks) {
-        float dsv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dsv[e] = dpt[ks >> 1][8 * (ks & 1) + e];
-        const bf16x8_t dsb = pack_bf16x8(dsv);
+        const bf16x8_t dsb = pack8(dpt[ks >> 1], 8 * (ks & 1));
 #pragma unroll
         for (int i = 0; i < HD / 32; ++i) {
           const char* row = Kts + (i * 32 + l32) * TROW;
