@@ -548,6 +548,472 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tile path (S a multiple of 64).  Every operand tile is a [64][HD] bf16 block
+// of a row-major source (Q, dO, K or V rows), copied into LDS by
+// global_load_lds_dwordx4 with no staging registers, in unpadded rows whose
+// 16-byte chunks are XOR-swizzled by tswz().  Operands that the MFMAs need
+// with the other dimension innermost (V^T, K^T, Q^T, dO^T) are read from the
+// same tiles with ds_read_b64_tr_b16: within each 16-lane group, lane 4j+q
+// points at row k0+j, columns n0+4q..n0+4q+3, and lane i receives column
+// n0+i, rows k0..k0+3.  So no transposed copy of any operand exists in HBM.
+// Two LDS stages: the tiles of step i+1 are issued right after the barrier
+// that opens step i (the barrier's fence waits for the loads of step i).
+// ---------------------------------------------------------------------------
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
+
+// Chunk swizzle of a tile row r: keeps the 16-byte reads of 16 consecutive
+// rows (row fragments) and the 8-byte transposed reads of 4 consecutive rows
+// x 64 bytes (one half-wave of ds_read_b64_tr_b16) on distinct banks of the
+// 64-bank LDS.
+template <int HD>
+__device__ __forceinline__ int tswz(int r) {
+  if constexpr (HD == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+}
+
+template <int HD>
+__device__ __forceinline__ int toff(int r, int chunk) {
+  return r * (HD * 2) + ((chunk ^ tswz<HD>(r)) << 4);
+}
+
+// A [64][HD] tile of rows `src` (stride ld elements) into LDS at `dst` by DMA:
+// 64*HD*2/1024 wave loads split over the 4 waves.
+template <int HD>
+__device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, char* dst, int wave, int lane) {
+  constexpr int kRowsPerLoad = 1024 / (HD * 2), kChunks = HD / 8;
+  constexpr int kPer = 64 / kRowsPerLoad / 4;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int r = (wave * kPer + q) * kRowsPerLoad + lane / kChunks;
+    const int c = (lane % kChunks) ^ tswz<HD>(r);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)r * ld + c * 8, dst + (wave * kPer + q) * 1024, 16, 0, 0);
+  }
+}
+
+// 16 floats at src into LDS at dst by lanes 0-15 of the calling wave, and 16
+// floats at src2 into dst + 256 by lanes 16-31 (dst uniform).
+__device__ __forceinline__ void dma_rows64(const float* src, const float* src2, char* dst, int lane) {
+  if (lane < 32) {
+    const float* p = lane < 16 ? src + 4 * lane : src2 + 4 * (lane - 16);
+    __builtin_amdgcn_global_load_lds(p, dst, 16, 0, 0);
+  }
+}
+
+// Per-lane LDS offsets of the fragment reads of a tile.  tswz() depends only
+// on the row modulo 16, so every offset splits into a per-lane part and a
+// part that only depends on the 16-row block and the 32-column block.
+template <int HD>
+struct TileOffsets {
+  static constexpr int RB = HD * 2;
+  int row;              // row fragments: (lane % 32) * RB
+  int chunk[HD / 16];   // row fragments: ((2*kk + lane/32) ^ tswz) * 16
+  int tbase[2];         // transposed reads 1 and 2 (rows +0 and +8)
+  int tcol[HD / 32];    // transposed reads: 32-column block i
+
+  __device__ __forceinline__ void init(int lane) {
+    const int l32 = lane & 31, half = lane >> 5;
+    row = l32 * RB;
+    const int sw = tswz<HD>(l32);
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) chunk[kk] = ((2 * kk + half) ^ sw) << 4;
+    // lane 4j+q of each 16-lane group points at row r0 + j (+8), columns
+    // c0 + 16*(group % 2) + 4q .. +3
+    const int p = lane & 15;
+    const int col = ((lane >> 4) & 1) * 16 + 4 * (p & 3);
+    const int cl = col >> 3;
+    int swh = 0;
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const int r = 4 * half + (p >> 2) + 8 * rd;  // row within a 16-row block
+      const int swr = tswz<HD>(r);
+      tbase[rd] = r * RB + ((cl ^ (swr & 3)) << 4) + (col & 7) * 2;
+      swh = swr >> 2;  // the same for both reads
+    }
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) tcol[i] = (i ^ swh) << 6;
+  }
+
+  // Row fragment: row 32*t + lane%32, columns 16*kk + 8*(lane/32) .. +7.
+  __device__ __forceinline__ bf16x8_t frag(const char* tile, int t, int kk) const {
+    return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tile + t * 32 * RB + row + chunk[kk]));
+  }
+
+  // Transposed fragment for an MFMA operand whose k index runs over tile rows:
+  // lane l gets column 32*i + l%32 at rows 16*ks + 8*(e/4) + 4*(l/32) + e%4
+  // for k-slots e = 0..7 (the slot order of the accumulator layout).
+  __device__ __forceinline__ bf16x8_t frag_t(const char* tile, int ks, int i) const {
+    const char* blk = tile + ks * 16 * RB + tcol[i];
+    const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + tbase[0]));
+    const v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + tbase[1]));
+    const uint2 xw = __builtin_bit_cast(uint2, x), yw = __builtin_bit_cast(uint2, y);
+    return __builtin_bit_cast(bf16x8_t, make_uint4(xw.x, xw.y, yw.x, yw.y));
+  }
+};
+
+// Forward on tiles: 128 queries per workgroup (32 per wave), 64-key steps.
+template <int HD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_tile_kernel(AttnArgs a) {
+  constexpr int BQ = 128, BKV = 64;
+  constexpr int kTile = BKV * HD * 2;
+  constexpr int kStage = 2 * kTile;  // K, V
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+
+  const int S = a.S, H = a.H, KV = a.KV;
+  const int nqb = (S + BQ - 1) / BQ;
+  const int bh = a.B * H;
+  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
+  const int rem = blockIdx.x % bh;
+  const int b = rem / H, h = rem % H;
+  const int g = h / (H / KV);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  TileOffsets<HD> to;
+  to.init(lane);
+  const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
+  const int qrow = qw0 + l32;
+
+  bf16x8_t qf[HD / 16];
+  {
+    const uint16_t* qp = a.q + ((int64_t)b * S + min(qrow, S - 1)) * a.ldq + (int64_t)h * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qp + kk * 16));
+  }
+  f32x16_t o[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float c = a.scale * kLog2e;
+
+  const int kv_end = min(S, q0 + BQ);  // a multiple of 64
+  const int kv_end_w = min(S, qw0 + 32);
+  const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
+  const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
+  const int nsteps = kv_end / BKV;
+
+  dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
+  dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
+  for (int it = 0; it < nsteps; ++it) {
+    __syncthreads();  // this step's tiles landed (every wave's loads), last step's reads retired
+    if (it + 1 < nsteps) {
+      char* nxt = smem + ((it + 1) & 1) * kStage;
+      dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, nxt, wave, lane);
+      dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, nxt + kTile, wave, lane);
+    }
+    const int k0 = it * BKV;
+    const char* Kt = smem + (it & 1) * kStage;
+    const char* Vt = Kt + kTile;
+    if (k0 < kv_end_w) {
+      f32x16_t s[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; ++kk)
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], s[t], 0,
+                                                         0, 0);
+      }
+      const bool need_mask = k0 + BKV - 1 > qw0;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          if (need_mask) {
+            const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (kv > qrow) s[t][r] = -INFINITY;
+          }
+          mx = fmaxf(mx, s[t][r]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m, mx * c);
+      const float nm = -m_new;
+      float rs = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
+          s[t][r] = p;
+          rs += p;
+        }
+      rs += __shfl_xor(rs, 32, 64);
+      if (__builtin_amdgcn_read_exec() & __ballot(m_new != m)) {  // some lane's max moved
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      }
+      l += rs;
+      m = m_new;
+#pragma unroll
+      for (int ks = 0; ks < BKV / 16; ++ks) {
+        const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i)
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Vt, ks, i), pb, o[i], 0, 0, 0);
+      }
+    }
+  }
+  if (qrow < S) {
+    const float inv_l = 1.0f / l;
+    uint16_t* op = a.o + ((int64_t)b * S + qrow) * a.ldo + (int64_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(op + hd, o[i][4 * q4] * inv_l, o[i][4 * q4 + 1] * inv_l, o[i][4 * q4 + 2] * inv_l,
+                     o[i][4 * q4 + 3] * inv_l);
+      }
+    if (half == 0) a.lse[((int64_t)b * H + h) * S + qrow] = (m + log2f(l)) * kLn2;
+  }
+}
+
+// Issues the tiles of dK/dV step `step` (query head step/nqs, query block
+// step%nqs from qstart) into the stage at `st`: Q, dO, then lse and delta.
+template <int HD>
+__device__ __forceinline__ void dkdv_issue(const AttnArgs& a, int step, int nqs, int qstart, int b, int g, int rep,
+                                           char* st, int wave, int lane) {
+  constexpr int kTile = 64 * HD * 2;
+  const int S = a.S;
+  const int hq = step / nqs, q0 = qstart + (step - hq * nqs) * 64;
+  const int h = g * rep + hq;
+  dma_tile<HD>(a.q + ((int64_t)b * S + q0) * a.ldq + (int64_t)h * HD, a.ldq, st, wave, lane);
+  dma_tile<HD>(a.dout + ((int64_t)b * S + q0) * a.lddo + (int64_t)h * HD, a.lddo, st + kTile, wave, lane);
+  if (wave == 0) {
+    const int64_t off = ((int64_t)b * a.H + h) * S + q0;
+    dma_rows64(a.lse + off, a.delta + off, st + 2 * kTile, lane);
+  }
+}
+
+// dK/dV on tiles: 128 keys per workgroup (32 per wave), 64-query steps over
+// every query head of the kv head's group, from the diagonal on.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_bwd_dkdv_tile_kernel(AttnArgs a) {
+  constexpr int BKV = 128, BQ = 64;
+  constexpr int kTile = BQ * HD * 2;
+  constexpr int kStage = 2 * kTile + 512;  // Q, dO, lse[64], delta[64]
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+
+  const int S = a.S, H = a.H, KV = a.KV, rep = H / KV;
+  const int bkv = a.B * KV;
+  const int kvb = blockIdx.x / bkv;
+  const int rem = blockIdx.x % bkv;
+  const int b = rem / KV, g = rem % KV;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  TileOffsets<HD> to;
+  to.init(lane);
+  const int k0 = kvb * BKV, kw0 = k0 + 32 * wave;
+  const int kvrow = kw0 + l32;
+  const float c = a.scale * kLog2e;
+
+  bf16x8_t kf[HD / 16], vf[HD / 16];
+  {
+    const int64_t r = (int64_t)b * S + min(kvrow, S - 1);
+    const uint16_t* kp = a.k + r * a.ldk + (int64_t)g * HD + 8 * half;
+    const uint16_t* vp = a.v + r * a.ldv + (int64_t)g * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      kf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kp + kk * 16));
+      vf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(vp + kk * 16));
+    }
+  }
+  f32x16_t dk[HD / 32], dv[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[i][r] = 0.f;
+      dv[i][r] = 0.f;
+    }
+
+  const int qstart = (k0 / BQ) * BQ;
+  const int nqs = (S - qstart) / BQ;
+  const int nsteps = rep * nqs;
+  dkdv_issue<HD>(a, 0, nqs, qstart, b, g, rep, smem, wave, lane);
+  for (int step = 0; step < nsteps; ++step) {
+    __syncthreads();  // this step's tiles landed (every wave's loads), last step's reads retired
+    if (step + 1 < nsteps) dkdv_issue<HD>(a, step + 1, nqs, qstart, b, g, rep, smem + ((step + 1) & 1) * kStage, wave, lane);
+    const int hq = step / nqs, q0 = qstart + (step - hq * nqs) * BQ;
+    const char* Qt = smem + (step & 1) * kStage;
+    const char* dOt = Qt + kTile;
+    const float* lse_s = reinterpret_cast<const float*>(Qt + 2 * kTile);
+    const float* D_s = lse_s + BQ;
+    if (q0 + BQ - 1 >= kw0 && kw0 < S) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x16_t sc, dp;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sc[r] = 0.f;
+          dp[r] = 0.f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; ++kk) {
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Qt, t, kk), kf[kk], sc, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(dOt, t, kk), vf[kk], dp, 0,
+                                                       0, 0);
+        }
+        // lane holds key column kvrow; query rows t*32 + 8*(r/4) + 4*half + r%4
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int qlb = t * 32 + 8 * r4 + 4 * half;
+          const float4 l4 = *reinterpret_cast<const float4*>(lse_s + qlb);
+          const float4 d4 = *reinterpret_cast<const float4*>(D_s + qlb);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+          const float dvv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            const bool ok = kvrow <= q0 + qlb + e && kvrow < S;
+            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lv[e] * kLog2e)) : 0.f;
+            dp[r] = p * (dp[r] - dvv[e]);
+            sc[r] = p;
+          }
+        }
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const int ks = 2 * t + kh;
+          const bf16x8_t pb = pack8(sc, 8 * kh);
+          const bf16x8_t dsb = pack8(dp, 8 * kh);
+#pragma unroll
+          for (int i = 0; i < HD / 32; ++i) {
+            dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(dOt, ks, i), pb, dv[i], 0, 0, 0);
+            dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Qt, ks, i), dsb, dk[i], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+  if (kvrow < S) {
+    uint16_t* dkp = a.dk + ((int64_t)b * S + kvrow) * a.lddk + (int64_t)g * HD;
+    uint16_t* dvp = a.dv + ((int64_t)b * S + kvrow) * a.lddv + (int64_t)g * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(dkp + hd, dk[i][4 * q4] * a.scale, dk[i][4 * q4 + 1] * a.scale, dk[i][4 * q4 + 2] * a.scale,
+                     dk[i][4 * q4 + 3] * a.scale);
+        store_bf16x4(dvp + hd, dv[i][4 * q4], dv[i][4 * q4 + 1], dv[i][4 * q4 + 2], dv[i][4 * q4 + 3]);
+      }
+  }
+}
+
+// dQ on tiles: 128 queries per workgroup, 64-key steps up to the diagonal.
+template <int HD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_bwd_dq_tile_kernel(AttnArgs a) {
+  constexpr int BQ = 128, BKV = 64;
+  constexpr int kTile = BKV * HD * 2;
+  constexpr int kStage = 2 * kTile;  // K, V
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+
+  const int S = a.S, H = a.H, KV = a.KV;
+  const int nqb = (S + BQ - 1) / BQ;
+  const int bh = a.B * H;
+  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
+  const int rem = blockIdx.x % bh;
+  const int b = rem / H, h = rem % H;
+  const int g = h / (H / KV);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  TileOffsets<HD> to;
+  to.init(lane);
+  const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
+  const int qrow = qw0 + l32;
+  const int qc = min(qrow, S - 1);
+  const float c = a.scale * kLog2e;
+
+  bf16x8_t qf[HD / 16], df[HD / 16];
+  {
+    const uint16_t* qp = a.q + ((int64_t)b * S + qc) * a.ldq + (int64_t)h * HD + 8 * half;
+    const uint16_t* dp_ = a.dout + ((int64_t)b * S + qc) * a.lddo + (int64_t)h * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qp + kk * 16));
+      df[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(dp_ + kk * 16));
+    }
+  }
+  const float nl2 = -a.lse[((int64_t)b * H + h) * S + qc] * kLog2e;
+  const float Dq = a.delta[((int64_t)b * H + h) * S + qc];
+  f32x16_t dq[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+
+  const int kv_end = min(S, q0 + BQ);
+  const int kv_end_w = min(S, qw0 + 32);
+  const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
+  const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
+  const int nsteps = kv_end / BKV;
+
+  dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
+  dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
+  for (int it = 0; it < nsteps; ++it) {
+    __syncthreads();  // this step's tiles landed (every wave's loads), last step's reads retired
+    if (it + 1 < nsteps) {
+      char* nxt = smem + ((it + 1) & 1) * kStage;
+      dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, nxt, wave, lane);
+      dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, nxt + kTile, wave, lane);
+    }
+    const int k0 = it * BKV;
+    const char* Kt = smem + (it & 1) * kStage;
+    const char* Vt = Kt + kTile;
+    if (k0 < kv_end_w) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x16_t st, dpt;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          st[r] = 0.f;
+          dpt[r] = 0.f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; ++kk) {
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], st, 0, 0, 0);
+          dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Vt, t, kk), df[kk], dpt, 0,
+                                                        0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool ok = kv <= qrow && qrow < S;
+          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, nl2)) : 0.f;
+          dpt[r] = p * (dpt[r] - Dq);
+        }
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const int ks = 2 * t + kh;
+          const bf16x8_t dsb = pack8(dpt, 8 * kh);
+#pragma unroll
+          for (int i = 0; i < HD / 32; ++i)
+            dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Kt, ks, i), dsb, dq[i], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (qrow < S) {
+    uint16_t* dqp = a.dq + ((int64_t)b * S + qrow) * a.lddq + (int64_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(dqp + hd, dq[i][4 * q4] * a.scale, dq[i][4 * q4 + 1] * a.scale, dq[i][4 * q4 + 2] * a.scale,
+                     dq[i][4 * q4 + 3] * a.scale);
+      }
+  }
+}
+
 // delta[b,h,s] = sum_d dO[b,s,h,d] * O[b,s,h,d]; one wave per (b, s, h) row.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_delta_kernel(const T* __restrict__ o, int64_t ldo, const T* __restrict__ dout,
@@ -771,10 +1237,14 @@ int check_shape(int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd) {
 
 }  // namespace
 
-// Which path lz_attn_fwd/bwd take for these arguments: 1 = MFMA tiles (needs
-// the transposed operand buffers), 0 = generic.
-LZ_EXPORT int lz_attn_uses_mfma(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
-  return dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0;
+// Which path lz_attn_fwd/bwd take for these arguments: 2 = MFMA on LDS tiles
+// (S a multiple of 64; no transposed buffers), 1 = MFMA with the transposed
+// operand buffers (V^T for the forward; Q^T, K^T, dO^T for the backward),
+// 0 = generic.
+LZ_EXPORT int lz_attn_path(int dtype, int64_t S, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
+  const bool mfma =
+      dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0;
+  return mfma ? (S % 64 == 0 ? 2 : 1) : 0;
 }
 
 // Forward.  vt: V^T [B,KV,hd,S] (needed on the MFMA path only).
@@ -785,6 +1255,17 @@ LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk
   if (rc) return rc;
   LZ_REQUIRE(q && k && v && o && lse, "lz_attn_fwd: null pointer");
   hipStream_t s = lz_stream(stream);
+  if (mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o) && S % 64 == 0) {
+    AttnArgs a{};
+    a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv;
+    a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
+    const unsigned grid = (unsigned)(lz_cdiv(S, 128) * B * H);
+    if (hd == 128) attn_fwd_tile_kernel<128><<<grid, 256, 0, s>>>(a);
+    else attn_fwd_tile_kernel<64><<<grid, 256, 0, s>>>(a);
+    return lz_check_launch("lz_attn_fwd");
+  }
   if (mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o)) {
     LZ_REQUIRE(vt && lz_aligned16(vt), "lz_attn_fwd: MFMA path needs an aligned V^T buffer");
     AttnArgs a{};
@@ -842,7 +1323,29 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
   if (rc) return rc;
   LZ_REQUIRE(q && k && v && dout && lse && delta && dq && dk && dv, "lz_attn_bwd: null pointer");
   hipStream_t s = lz_stream(stream);
-  if (mfma_ok(dtype, hd, ldq, ldk, ldv, lddo, q, k, v, dout) && lddq % 4 == 0 && lddk % 4 == 0 && lddv % 4 == 0) {
+  const bool mfma = mfma_ok(dtype, hd, ldq, ldk, ldv, lddo, q, k, v, dout) && lddq % 4 == 0 && lddk % 4 == 0 &&
+                    lddv % 4 == 0;
+  if (mfma && S % 64 == 0) {
+    AttnArgs a{};
+    a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv;
+    a.lse = const_cast<float*>(lse);
+    a.dout = (const uint16_t*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
+    a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
+    const unsigned grid_kv = (unsigned)(lz_cdiv(S, 128) * B * KV);
+    const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
+    if (hd == 128) {
+      attn_bwd_dkdv_tile_kernel<128><<<grid_kv, 256, 0, s>>>(a);
+      attn_bwd_dq_tile_kernel<128><<<grid_q, 256, 0, s>>>(a);
+    } else {
+      attn_bwd_dkdv_tile_kernel<64><<<grid_kv, 256, 0, s>>>(a);
+      attn_bwd_dq_tile_kernel<64><<<grid_q, 256, 0, s>>>(a);
+    }
+    return lz_check_launch("lz_attn_bwd");
+  }
+  if (mfma) {
     LZ_REQUIRE(qt && kt && dot, "lz_attn_bwd: MFMA path needs the transposed Q, K and dO buffers");
     AttnArgs a{};
     a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;

@@ -406,10 +406,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 // Global data goes straight into LDS with global_load_lds_dwordx4 (each lane's
 // 16 bytes land at the wave-uniform destination + 16*lane), so staging takes
 // no registers and no LDS-write instructions.  K advances DBK per stage over
-// NST LDS stages: the loads for stage k+NST-1 are issued right after the
-// barrier that opens stage k, and each wave waits only for its own loads of
-// the stage it is about to read (explicit vmcnt, then a bare s_barrier: a
-// __syncthreads() fence would wait for every load in flight).  LDS rows are
+// two LDS stages: the loads for stage k+1 are issued right after the barrier
+// that opens stage k (whose fence waits for stage k's loads).  LDS rows are
 // DBK*2 bytes without padding, XOR-swizzled by swz().  Rows past M or N are
 // clamped to the last row (they only feed outputs that are not stored); K
 // must be a multiple of DBK in every split.
@@ -422,11 +420,6 @@ __device__ __forceinline__ int swz(int r) {
   if constexpr (kChunks == 4) return ((r >> 1) ^ (r >> 3)) & 3;
   else return ((r >> 1) ^ ((r & 1) << 2)) & 7;
 }
-
-// s_waitcnt immediate that waits until at most n vector-memory operations are
-// outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
-// left at their maxima).
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
 // Issues one stage's loads for this wave: kPerWave 1 KB wave loads of A rows
 // then of B rows into the stage at `base`, K offset `k0` of the split.
@@ -443,8 +436,9 @@ __device__ __forceinline__ void dma_stage(const uint16_t* const (&pa)[kPerWave],
                                      0, 0);
 }
 
-template <int WM, int WN, int DBK, int NST>
+template <int WM, int WN, int DBK>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
+  constexpr int NST = 2;  // LDS stages
   constexpr int BM = 256, BN = 256;
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -454,10 +448,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   constexpr int kOpBytes = BM * kRowB;           // one operand, one stage
   constexpr int kStage = 2 * kOpBytes;
   constexpr int kPerWave = kOpBytes / 1024 / kWaves;  // wave loads per operand per stage
-  constexpr int kDmaPerStage = 2 * kPerWave;          // per wave
   static_assert(kPerWave * kWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
   static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
-  static_assert(NST >= 2 && NST * kStage <= 160 * 1024, "LDS stages do not fit");
+  static_assert(NST * kStage <= 160 * 1024, "LDS stages do not fit");
 
   __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
 
@@ -515,17 +508,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
     if (s < ktiles) dma_stage<kPerWave, kOpBytes, kRowB>(pa, pb, smem + s * kStage, wave, (int64_t)s * DBK);
 
   for (int kt = 0; kt < ktiles; ++kt) {
-    // this wave's loads of stage kt are done once at most the loads of the
-    // stages issued after it are outstanding; the barrier then publishes every
-    // wave's part and retires the reads of stage kt-1, whose slot is refilled
-    const int later = min(ktiles - 1 - kt, NST - 2);
-    if (later >= 2)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kDmaPerStage));
-    else if (later == 1)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaPerStage));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    __builtin_amdgcn_s_barrier();
+    // with two stages only stage kt's loads are in flight here: the barrier's
+    // fence waits for them, publishes every wave's part and retires the reads
+    // of stage kt-1, whose slot is refilled next
+    __syncthreads();
     if (kt + NST - 1 < ktiles)
       dma_stage<kPerWave, kOpBytes, kRowB>(pa, pb, smem + ((kt + NST - 1) % NST) * kStage, wave,
                                           (int64_t)(kt + NST - 1) * DBK);
@@ -627,18 +613,18 @@ int launch(const GemmArgs& g, int splits, hipStream_t s) {
   return lz_check_launch("lz_gemm");
 }
 
-template <int WM, int WN, int DBK, int NST>
+template <int WM, int WN, int DBK>
 int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
   const int64_t tiles = lz_cdiv(g.M, 256) * lz_cdiv(g.N, 256);
   LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
-  gemm_dma_kernel<WM, WN, DBK, NST><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  gemm_dma_kernel<WM, WN, DBK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
   return lz_check_launch("lz_gemm");
 }
 
 template <bool AK, bool BK>
 int dispatch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   if constexpr (AK && BK) {
-    if (cfg == 5) return launch_dma<2, 4, 64, 2>(g, splits, s);
+    if (cfg == 5) return launch_dma<2, 4, 64>(g, splits, s);
   }
   switch (cfg) {
     case 0:

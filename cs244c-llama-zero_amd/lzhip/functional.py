@@ -191,7 +191,7 @@ class AttnProjFn(Function):
         v2 = qkv[:, (H + KV) * hd :]
         ld = qkv.shape[1]
         vt = None
-        if ops.attn_uses_mfma(qkv.dtype, hd, ld, ld, ld, H * hd):
+        if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, H * hd) == 1:
             vt = ops.transpose_heads(qkv, B, S, KV, hd, col0=(H + KV) * hd)
         o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
         ctx.save_for_backward(h2, wq, wk, wv, qkv, o, lse, cos, sin)
@@ -206,7 +206,7 @@ class AttnProjFn(Function):
         ld = qkv.shape[1]
         dqkv = torch.empty_like(qkv)
         qt = kt = dot = None
-        if ops.attn_uses_mfma(qkv.dtype, hd, ld, ld, ld, do2.stride(0)):
+        if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, do2.stride(0)) == 1:
             qt = ops.transpose_heads(qkv, B, S, H, hd, col0=0)
             kt = ops.transpose_heads(qkv, B, S, KV, hd, col0=H * hd)
             dot = ops.transpose_heads(do2, B, S, H, hd, col0=0)

@@ -553,10 +553,12 @@ def ce_bwd(logits2: torch.Tensor, labels: torch.Tensor, seq: int, lse: torch.Ten
     return out
 
 
-def attn_uses_mfma(dtype: torch.dtype, hd: int, ldq: int, ldk: int, ldv: int, ldo: int) -> bool:
+def attn_path(dtype: torch.dtype, S: int, hd: int, ldq: int, ldk: int, ldv: int, ldo: int) -> int:
+    """2: MFMA on LDS tiles (no transposed operands), 1: MFMA with transposed
+    operand buffers (V^T forward; Q^T, K^T, dO^T backward), 0: generic."""
     if dtype not in _DTYPES:
-        return False
-    return bool(_lib.load().lz_attn_uses_mfma(_DTYPES[dtype], hd, ldq, ldk, ldv, ldo))
+        return 0
+    return int(_lib.load().lz_attn_path(_DTYPES[dtype], S, hd, ldq, ldk, ldv, ldo))
 
 
 def attn_fwd(q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, B: int, S: int, H: int, KV: int, hd: int,

@@ -183,9 +183,12 @@ int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, 
                int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* stream);
 
 /* Causal GQA flash attention (model/llama.py:88-117: repeat_kv +
- * F.scaled_dot_product_attention(is_causal=True)).  1 if the MFMA path applies
- * (bf16, hd 64 or 128), which needs the transposed operand buffers. */
-int lz_attn_uses_mfma(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo);
+ * F.scaled_dot_product_attention(is_causal=True)).  lz_attn_path reports the
+ * path lz_attn_fwd/bwd take: 2 = MFMA on LDS tiles (bf16, hd 64 or 128, S a
+ * multiple of 64; the transposed-operand arguments may be NULL), 1 = MFMA
+ * with the transposed operand buffers (vt for the forward; qt, kt, dot for the
+ * backward, each [B, heads, hd, S]), 0 = generic. */
+int lz_attn_path(int dtype, int64_t S, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo);
 int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* vt,
                 void* o, int64_t ldo, float* lse, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
                 int dtype, void* stream);

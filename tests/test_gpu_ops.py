@@ -268,7 +268,9 @@ def test_attention_fwd_bwd(B, S, H, KV, hd):
     d = qkv.to(DEV)
     q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
     scale = hd**-0.5
-    mfma = ops.attn_uses_mfma(torch.bfloat16, hd, ld, ld, ld, H * hd)
+    path = ops.attn_path(torch.bfloat16, S, hd, ld, ld, ld, H * hd)
+    assert path == (2 if hd in (64, 128) and S % 64 == 0 else 1 if hd in (64, 128) else 0)
+    mfma = path == 1  # the transposed-operand path needs V^T, Q^T, K^T, dO^T
     vt = ops.transpose_heads(d, B, S, KV, hd, col0=(H + KV) * hd) if mfma else None
     o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
 
