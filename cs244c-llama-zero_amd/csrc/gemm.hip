@@ -401,16 +401,19 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS kernel for two K-major operands (the forward product).
+// ---------------------------------------------------------------------------
+// Direct-to-LDS kernel.
 //
 // Global data goes straight into LDS with global_load_lds_dwordx4 (each lane's
 // 16 bytes land at the wave-uniform destination + 16*lane), so staging takes
-// no registers and no LDS-write instructions.  K advances DBK per stage over
-// two LDS stages: the loads for stage k+1 are issued right after the barrier
-// that opens stage k (whose fence waits for stage k's loads).  LDS rows are
-// DBK*2 bytes without padding, XOR-swizzled by swz().  Rows past M or N are
-// clamped to the last row (they only feed outputs that are not stored); K
-// must be a multiple of DBK in every split.
+// no registers and no LDS-write instructions.  K advances 64 per stage over two
+// LDS stages: the loads for stage k+1 are issued right after the barrier that
+// opens stage k (whose fence waits for stage k's loads).  Stages are stored as
+// they lie in memory (K-major rows or M/N-major rows, unpadded, XOR-swizzled);
+// an M/N-major operand's fragments come from ds_read_b64_tr_b16, which
+// transposes 4x4 blocks of 16-bit values across each 16-lane group.  Rows
+// (K-major) or columns (M/N-major) past M or N are clamped to valid memory;
+// they only feed outputs that are not stored.
 // ---------------------------------------------------------------------------
 // LDS row swizzle: chunk c (8 K values) of row r sits in slot c ^ swz(r).
 // For 4-chunk (64-byte) and 8-chunk (128-byte) rows this keeps the 16-byte
@@ -421,38 +424,109 @@ __device__ __forceinline__ int swz(int r) {
   else return ((r >> 1) ^ ((r & 1) << 2)) & 7;
 }
 
-// Issues one stage's loads for this wave: kPerWave 1 KB wave loads of A rows
-// then of B rows into the stage at `base`, K offset `k0` of the split.
-template <int kPerWave, int kOpBytes, int kRowB>
-__device__ __forceinline__ void dma_stage(const uint16_t* const (&pa)[kPerWave], const uint16_t* const (&pb)[kPerWave],
-                                          char* base, int wave, int64_t k0) {
-  constexpr int kRowsPerLoad = 1024 / kRowB;
-#pragma unroll
-  for (int q = 0; q < kPerWave; ++q)
-    __builtin_amdgcn_global_load_lds(pa[q] + k0, base + (wave * kPerWave + q) * kRowsPerLoad * kRowB, 16, 0, 0);
-#pragma unroll
-  for (int q = 0; q < kPerWave; ++q)
-    __builtin_amdgcn_global_load_lds(pb[q] + k0, base + kOpBytes + (wave * kPerWave + q) * kRowsPerLoad * kRowB, 16,
-                                     0, 0);
-}
+// Swizzle of the 16-byte chunks of an M/N-major stage row (64 K rows of 256
+// M/N values, 512 bytes): keeps each half-wave of ds_read_b64_tr_b16 (4
+// consecutive rows x 64 bytes) on distinct banks.
+__device__ __forceinline__ int swz_mn(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-template <int WM, int WN, int DBK>
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
+
+// One operand of the direct-to-LDS kernel: a 256 (M or N) x 64 (K) stage,
+// 32 KB, filled by 32 wave loads of 1 KB.
+//   K-major: 256 rows of 64 K (128 bytes, 8 chunks, swizzled by swz<8>);
+//            fragments are plain 16-byte reads.
+//   M/N-major: 64 rows of 256 M/N values (512 bytes, 32 chunks, swizzled by
+//            swz_mn); fragments are two ds_read_b64_tr_b16 (k-slots 0-3 and
+//            4-7 of the 32x32x16 operand: rows 16*kk + 8*(lane/32) + 0..3 and
+//            + 4..7).
+template <bool KMAJOR, int kPerWave>
+struct DmaOperand {
+  const uint16_t* src[kPerWave];
+  int64_t kadv;  // elements to advance per 64-deep K step
+
+  __device__ __forceinline__ void init(const uint16_t* p, int64_t ld, int64_t row0, int64_t nrows, int64_t kbeg,
+                                       int wave, int lane) {
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      if constexpr (KMAJOR) {
+        const int r = (wave * kPerWave + q) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ swz<8>(r);
+        src[q] = p + min(row0 + r, nrows - 1) * ld + kbeg + c * 8;
+      } else {
+        const int r = (wave * kPerWave + q) * 2 + (lane >> 5);
+        const int c = (lane & 31) ^ swz_mn(r);
+        src[q] = p + (kbeg + r) * ld + min(row0 + c * 8, nrows - 8);
+      }
+    }
+    kadv = KMAJOR ? 64 : 64 * ld;
+  }
+
+  __device__ __forceinline__ void issue(char* dst, int wave, int kt) const {
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q)
+      __builtin_amdgcn_global_load_lds(src[q] + kt * kadv, dst + (wave * kPerWave + q) * 1024, 16, 0, 0);
+  }
+};
+
+// Per-lane LDS offsets of this wave's NF fragments (32-row blocks blk0 ..
+// blk0+NF-1 of the operand) for the four 16-deep sub-steps of a stage.
+template <bool KMAJOR, int NF>
+struct DmaFrags {
+  int off[KMAJOR ? NF : 1][4];       // K-major
+  int base[2], ioff[KMAJOR ? 1 : NF];  // M/N-major
+
+  __device__ __forceinline__ void init(int blk0, int lane) {
+    if constexpr (KMAJOR) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int r = (blk0 + f) * 32 + (lane & 31);
+          off[f][kk] = r * 128 + (((2 * kk + (lane >> 5)) ^ swz<8>(r)) << 4);
+        }
+    } else {
+      // lane 4j+q of 16-lane group G reads row 8*(G/2) + j (+4), columns
+      // 16*(G%2) + 4q .. +3 of the 32-column block, and receives column
+      // 16*(G%2) + (lane%16) at 4 consecutive rows
+      const int p = lane & 15, h = lane >> 5, cg = (lane >> 4) & 1;
+      const int x = 2 * cg + ((p & 3) >> 1);
+#pragma unroll
+      for (int rd = 0; rd < 2; ++rd)
+        base[rd] = (8 * h + (p >> 2) + 4 * rd) * 512 + ((x ^ ((2 * h + rd) & 3)) << 4) + (p & 1) * 8;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) ioff[f] = ((blk0 + f) ^ (p >> 2)) << 6;
+    }
+  }
+
+  __device__ __forceinline__ bf16x8_t frag(const char* op, int f, int kk) const {
+    if constexpr (KMAJOR) {
+      return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(op + off[f][kk]));
+    } else {
+      const char* blk = op + kk * 16 * 512 + ioff[f];
+      const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[0]));
+      const v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[1]));
+      const uint2 xw = __builtin_bit_cast(uint2, x), yw = __builtin_bit_cast(uint2, y);
+      return __builtin_bit_cast(bf16x8_t, make_uint4(xw.x, xw.y, yw.x, yw.y));
+    }
+  }
+};
+
+// Direct-to-LDS kernel, any operand layouts: 256x256 tile, 64-deep K steps
+// over two 64 KB LDS stages.  K must be a multiple of 64 in every split; an
+// M-major A needs M % 8 == 0 (N-major B: N % 8 == 0).
+template <int WM, int WN, bool AK, bool BK>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
-  constexpr int NST = 2;  // LDS stages
-  constexpr int BM = 256, BN = 256;
+  constexpr int BM = 256, BN = 256, DBK = 64;
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-  constexpr int kRowB = DBK * 2;                 // bytes per LDS row
-  constexpr int kChunks = DBK / 8;               // 16-byte chunks per row
-  constexpr int kRowsPerLoad = 1024 / kRowB;     // rows covered by one wave load
-  constexpr int kOpBytes = BM * kRowB;           // one operand, one stage
+  constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage (32 KB)
   constexpr int kStage = 2 * kOpBytes;
   constexpr int kPerWave = kOpBytes / 1024 / kWaves;  // wave loads per operand per stage
   static_assert(kPerWave * kWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
-  static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
-  static_assert(NST * kStage <= 160 * 1024, "LDS stages do not fit");
+  static_assert(kWaves * 32 * (TN + 4) * 4 <= 2 * kStage, "epilogue staging does not fit");
 
-  __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -463,37 +537,14 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   const int64_t kbeg = (int64_t)blockIdx.y * g.kper, kend = min(g.K, kbeg + g.kper);
   const int ktiles = kend > kbeg ? (int)((kend - kbeg) / DBK) : 0;
 
-  // This lane's source rows: wave load q covers LDS rows
-  // (wave*kPerWave+q)*kRowsPerLoad + lane/kChunks, slot lane%kChunks holding
-  // chunk slot ^ swz(row).
-  const uint16_t* pa[kPerWave];
-  const uint16_t* pb[kPerWave];
-#pragma unroll
-  for (int q = 0; q < kPerWave; ++q) {
-    const int r = (wave * kPerWave + q) * kRowsPerLoad + lane / kChunks;
-    const int c = (lane % kChunks) ^ swz<kChunks>(r);
-    pa[q] = g.A + min(m0 + r, g.M - 1) * g.lda + kbeg + c * 8;
-    pb[q] = g.B + min(n0 + r, g.N - 1) * g.ldb + kbeg + c * 8;
-  }
-
-  // fragment byte offsets within a stage, per 16-deep sub-step
-  constexpr int kSub = DBK / 16;
-  const int frag_row = lane & 31, frag_half = lane >> 5;
-  int offa[FM][kSub], offb[FN][kSub];
-#pragma unroll
-  for (int kk = 0; kk < kSub; ++kk) {
-    const int c = kk * 2 + frag_half;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int r = wm * TM + i * 32 + frag_row;
-      offa[i][kk] = r * kRowB + ((c ^ swz<kChunks>(r)) << 4);
-    }
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int r = wn * TN + j * 32 + frag_row;
-      offb[j][kk] = kOpBytes + r * kRowB + ((c ^ swz<kChunks>(r)) << 4);
-    }
-  }
+  DmaOperand<AK, kPerWave> la;
+  DmaOperand<BK, kPerWave> lb;
+  la.init(g.A, g.lda, m0, g.M, kbeg, wave, lane);
+  lb.init(g.B, g.ldb, n0, g.N, kbeg, wave, lane);
+  DmaFrags<AK, FM> fra;
+  DmaFrags<BK, FN> frb;
+  fra.init(wm * FM, lane);
+  frb.init(wn * FN, lane);
 
   f32x16_t acc[FM][FN];
 #pragma unroll
@@ -503,26 +554,29 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-#pragma unroll
-  for (int s = 0; s < NST - 1; ++s)
-    if (s < ktiles) dma_stage<kPerWave, kOpBytes, kRowB>(pa, pb, smem + s * kStage, wave, (int64_t)s * DBK);
-
+  if (ktiles > 0) {
+    la.issue(smem, wave, 0);
+    lb.issue(smem + kOpBytes, wave, 0);
+  }
   for (int kt = 0; kt < ktiles; ++kt) {
-    // with two stages only stage kt's loads are in flight here: the barrier's
-    // fence waits for them, publishes every wave's part and retires the reads
-    // of stage kt-1, whose slot is refilled next
+    // only stage kt's loads are in flight here: the barrier's fence waits for
+    // them, publishes every wave's part and retires the reads of stage kt-1,
+    // whose slot is refilled next
     __syncthreads();
-    if (kt + NST - 1 < ktiles)
-      dma_stage<kPerWave, kOpBytes, kRowB>(pa, pb, smem + ((kt + NST - 1) % NST) * kStage, wave,
-                                          (int64_t)(kt + NST - 1) * DBK);
-    const char* st = smem + (kt % NST) * kStage;
+    if (kt + 1 < ktiles) {
+      char* nxt = smem + ((kt + 1) & 1) * kStage;
+      la.issue(nxt, wave, kt + 1);
+      lb.issue(nxt + kOpBytes, wave, kt + 1);
+    }
+    const char* sa = smem + (kt & 1) * kStage;
+    const char* sb = sa + kOpBytes;
 #pragma unroll
-    for (int kk = 0; kk < kSub; ++kk) {
+    for (int kk = 0; kk < DBK / 16; ++kk) {
       bf16x8_t fa[FN], fb[FM];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) fa[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + offb[j][kk]));
+      for (int j = 0; j < FN; ++j) fa[j] = frb.frag(sb, j, kk);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) fb[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + offa[i][kk]));
+      for (int i = 0; i < FM; ++i) fb[i] = fra.frag(sa, i, kk);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -558,8 +612,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
 
 // Tile configurations: 0 = 256x256 with 8 waves (128x64 per wave),
 // 1 = 256x256 with 4 waves (128x128 per wave, accumulators in AGPRs),
-// 2 = 128x128 with 4 waves; 5 = the direct-to-LDS kernel (both operands
-// K-major, 8 waves, 2 stages of 64 K).
+// 2 = 128x128 with 4 waves; 5 and 6 = the direct-to-LDS kernel (any
+// layouts, 8 or 4 waves, two stages of 64 K).
 struct Plan {
   int cfg;
   int splits;
@@ -570,23 +624,23 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
   const int cus = lz_num_cus();
   const int64_t big = lz_cdiv(M, 256) * lz_cdiv(N, 256);
   const int64_t small = lz_cdiv(M, 128) * lz_cdiv(N, 128);
-  // K-major A: the 8-wave tile; M-major A (weight gradients): the 4-wave
-  // tile, whose larger per-wave sub-tile holds up better with the in-register
-  // transposes of both operands.
-  Plan p{ak ? 0 : 1, 1, K};
+  // 256x256 tiles: the direct-to-LDS kernel whenever every split is a whole
+  // number of 64-deep K steps; otherwise the register-staged kernel (8 waves
+  // for a K-major A, 4 waves when both operands are transposed in registers).
+  const int big_cfg = K % 64 == 0 ? 5 : (ak ? 0 : 1);
+  Plan p{big_cfg, 1, K};
   if (ak && bk) {
-    // Both K-major: the 8-wave 256x256 tile (one per CU) is the faster tile;
     // 128x128 tiles (two per CU) win when they fill the chip in fewer rounds.
     // Relative speeds measured on MI355X: 0.85 and 0.75.
     const double c256 = (double)lz_cdiv(big, cus) * 4.0 / 0.85;
     const double c128 = (double)lz_cdiv(small, 2 * cus) * 2.0 / 0.75;
-    // the direct-to-LDS kernel needs whole 64-deep K steps
-    p.cfg = c128 < c256 ? 2 : (K % 64 == 0 ? 5 : 0);
+    if (c128 < c256) p.cfg = 2;
   }
   if (p.cfg != 2 && big < 2 * cus && K >= 2048) {
     // Long K over few output tiles: split K so the grid covers the chip.
     // Cost in units of one un-split tile: rounds of the grid over the CUs,
     // each 1/S as long, plus a small charge per split for the slab traffic.
+    // Splits are whole multiples of 64 in K.
     double best = 1e30;
     for (int sp = 1; sp <= 8; ++sp) {
       const int64_t kper = lz_cdiv(lz_cdiv(K, sp), 64) * 64;
@@ -613,19 +667,30 @@ int launch(const GemmArgs& g, int splits, hipStream_t s) {
   return lz_check_launch("lz_gemm");
 }
 
-template <int WM, int WN, int DBK>
+// Explicit instantiations: when the host pass only meets these kernels through
+// the dispatch templates it does not emit the launch stubs of the variants
+// that use ds_read_b64_tr_b16.
+template __global__ void gemm_dma_kernel<2, 4, true, true>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, true, false>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, false, true>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, false, false>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 2, true, true>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 2, true, false>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 2, false, true>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 2, false, false>(GemmArgs);
+
+template <int WM, int WN, bool AK, bool BK>
 int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
   const int64_t tiles = lz_cdiv(g.M, 256) * lz_cdiv(g.N, 256);
   LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
-  gemm_dma_kernel<WM, WN, DBK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  gemm_dma_kernel<WM, WN, AK, BK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
   return lz_check_launch("lz_gemm");
 }
 
 template <bool AK, bool BK>
 int dispatch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
-  if constexpr (AK && BK) {
-    if (cfg == 5) return launch_dma<2, 4, 64>(g, splits, s);
-  }
+  if (cfg == 5) return launch_dma<2, 4, AK, BK>(g, splits, s);
+  if (cfg == 6) return launch_dma<2, 2, AK, BK>(g, splits, s);
   switch (cfg) {
     case 0:
       return launch<256, 256, 2, 4, AK, BK>(g, splits, s);

@@ -107,7 +107,7 @@ def _layout_operand(t, kmajor):
 @pytest.mark.parametrize("a_kmajor,b_kmajor", [(True, True), (True, False), (False, True), (False, False)])
 @pytest.mark.parametrize(
     "M,N,K",
-    [(64, 64, 64), (520, 264, 200), (1000, 1000, 520), (2048, 1024, 1536),
+    [(64, 64, 64), (520, 264, 200), (1000, 1000, 520), (1000, 1000, 512), (2048, 1024, 1536),
      # few output tiles, long K: split along K (K not a multiple of 64 in the last case)
      (512, 384, 8192), (1024, 768, 8200)],
 )

@@ -307,3 +307,21 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     assert set(declared) == set(L.SIGNATURES)
     assert lib.lz_version() == 1
+
+
+def test_library_defines_every_kernel_launch_stub():
+    """Every kernel the library launches has its host launch stub: an undefined
+    __device_stub__ symbol would only fail when the library is loaded."""
+    import shutil
+    import subprocess
+
+    import lzhip._lib as L
+
+    if not L.LIB_PATH.exists():
+        pytest.skip("libllamazero_hip.so not built (run __graft_entry__.build())")
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-C", "--undefined-only", str(L.LIB_PATH)], capture_output=True, text=True, check=True)
+    stubs = [line for line in out.stdout.splitlines() if "__device_stub__" in line]
+    assert not stubs, stubs[:5]
