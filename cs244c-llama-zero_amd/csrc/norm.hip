@@ -5,14 +5,24 @@
 // One 64-lane wavefront per row; each lane keeps its slice of the row in
 // registers (8 elements per 16-byte access), so x is read once and y written
 // once: 4 B/element in bf16.  The backward reads x and dy, writes dx (and an
-// optional residual-gradient add), 6 B/element, and reduces dw through per-wave
-// fp32 partials and a second column-sum kernel.
+// optional residual-gradient add), 6 B/element, and reduces dw through fp32
+// partial rows (one per workgroup for bf16, per wave otherwise) and a
+// two-level column sum.
 #include "lz_common.h"
 
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave per row
 constexpr int kThreads = 64 * kRowsPerBlock;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 (round to nearest even, one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
 
 template <typename T>
 struct Pack8;
@@ -27,12 +37,14 @@ struct Pack8<uint16_t> {
     r[6] = bf2f(v.w & 0xffff); r[7] = bf2f(v.w >> 16);
   }
   static __device__ __forceinline__ void store(uint16_t* p, const float (&r)[8]) {
-    uint4 v;
-    v.x = (uint32_t)f2bf(r[0]) | ((uint32_t)f2bf(r[1]) << 16);
-    v.y = (uint32_t)f2bf(r[2]) | ((uint32_t)f2bf(r[3]) << 16);
-    v.z = (uint32_t)f2bf(r[4]) | ((uint32_t)f2bf(r[5]) << 16);
-    v.w = (uint32_t)f2bf(r[6]) | ((uint32_t)f2bf(r[7]) << 16);
-    *reinterpret_cast<uint4*>(p) = v;
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]),
+                                              pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7]));
+  }
+  static __device__ __forceinline__ void unpack(const uint4& v, float (&r)[8]) {
+    r[0] = bf2f(v.x & 0xffff); r[1] = bf2f(v.x >> 16);
+    r[2] = bf2f(v.y & 0xffff); r[3] = bf2f(v.y >> 16);
+    r[4] = bf2f(v.z & 0xffff); r[5] = bf2f(v.z >> 16);
+    r[6] = bf2f(v.w & 0xffff); r[7] = bf2f(v.w >> 16);
   }
 };
 
@@ -86,6 +98,128 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(const T* __restri
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (v[j][e] * r) * wv[e];
       Pack8<T>::store(yr + 8 * c, o);
+    }
+  }
+}
+
+// bf16 backward: workgroup b owns rows [b*rpb, (b+1)*rpb), its wave w takes
+// rows w, w+4, ... of that range and loads the next one while it computes the
+// current one.  The 4 waves' dw contributions are summed in LDS (in a fixed
+// order) into one fp32 partial row per workgroup: dw_part[b][cols].
+template <int NC>
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ rstd,
+    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ dres, uint16_t* __restrict__ dx,
+    float* __restrict__ dw_part, int64_t rows, int64_t rpb, int cols, int64_t ldx, int64_t lddy, int64_t lddx) {
+  __shared__ float red[2][NC * 512];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nchunk = cols >> 3;
+  const int64_t r0 = (int64_t)blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
+  float wv[NC][8], dwacc[NC][8];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      dwacc[j][e] = 0.f;
+      wv[j][e] = 0.f;
+    }
+    if (c < nchunk) Pack8<uint16_t>::load(w + 8 * c, wv[j]);
+  }
+  const float inv_n = 1.0f / (float)cols;
+  uint4 xn[NC], gn[NC];
+  auto fetch = [&](int64_t row) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk) {
+        xn[j] = *reinterpret_cast<const uint4*>(x + row * ldx + 8 * c);
+        gn[j] = *reinterpret_cast<const uint4*>(dy + row * lddy + 8 * c);
+      }
+    }
+  };
+  int64_t row = r0 + wave;
+  if (row < r1) fetch(row);
+  for (; row < r1; row += kRowsPerBlock) {
+    uint4 xc[NC], gc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      xc[j] = xn[j];
+      gc[j] = gn[j];
+    }
+    if (row + kRowsPerBlock < r1) fetch(row + kRowsPerBlock);
+    const float r = rstd[row];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      if (lane + 64 * j < nchunk) {
+        float xv[8], gv[8];
+        Pack8<uint16_t>::unpack(xc[j], xv);
+        Pack8<uint16_t>::unpack(gc[j], gv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dot = fmaf(gv[e] * wv[j][e], xv[e], dot);
+          dwacc[j][e] = fmaf(gv[e], xv[e] * r, dwacc[j][e]);
+        }
+      }
+    }
+    dot = wave_sum(dot);
+    const float coef = dot * r * r * r * inv_n;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk) {
+        float xv[8], gv[8], o[8];
+        Pack8<uint16_t>::unpack(xc[j], xv);
+        Pack8<uint16_t>::unpack(gc[j], gv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = r * wv[j][e] * gv[e] - coef * xv[e];
+        if (dres) {
+          float rv[8];
+          Pack8<uint16_t>::load(dres + row * lddx + 8 * c, rv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] += rv[e];
+        }
+        Pack8<uint16_t>::store(dx + row * lddx + 8 * c, o);
+      }
+    }
+  }
+  // dw: waves 2,3 park their sums, waves 0,1 add them; wave 1 parks, wave 0
+  // adds and writes the workgroup's partial row.
+  auto park = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[slot][8 * c + e] = dwacc[j][e];
+    }
+  };
+  auto take = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dwacc[j][e] += red[slot][8 * c + e];
+    }
+  };
+  if (wave >= 2) park(wave - 2);
+  __syncthreads();
+  if (wave < 2) take(wave);
+  __syncthreads();
+  if (wave == 1) park(0);
+  __syncthreads();
+  if (wave == 0) {
+    take(0);
+    float* part = dw_part + (int64_t)blockIdx.x * cols;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk) {
+        reinterpret_cast<float4*>(part + 8 * c)[0] = make_float4(dwacc[j][0], dwacc[j][1], dwacc[j][2], dwacc[j][3]);
+        reinterpret_cast<float4*>(part + 8 * c)[1] = make_float4(dwacc[j][4], dwacc[j][5], dwacc[j][6], dwacc[j][7]);
+      }
     }
   }
 }
@@ -242,6 +376,14 @@ __global__ void dw_final_kernel(const float* __restrict__ slices, int cols, T* _
   Elem<T>::store(dw, c, s);
 }
 
+// bf16 vector backward: number of workgroups (one dw partial row each), one
+// resident round of them (the register footprint grows with cols: 8, 4, 2, 1
+// workgroups per CU for cols <= 512, 1024, 2048, 4096).
+inline int64_t bwd_blocks(int64_t rows, int64_t cols) {
+  const int per_cu = cols <= 512 ? 8 : cols <= 1024 ? 4 : cols <= 2048 ? 2 : 1;
+  return std::max<int64_t>(1, std::min<int64_t>((int64_t)lz_num_cus() * per_cu, lz_cdiv(rows, kRowsPerBlock)));
+}
+
 inline int64_t bwd_waves(int64_t rows) {
   // two workgroups (8 waves) per compute unit, at most one wave per row
   int64_t n = std::min<int64_t>((int64_t)lz_num_cus() * 2 * kRowsPerBlock, std::max<int64_t>(rows, kRowsPerBlock));
@@ -269,16 +411,41 @@ template <typename T>
 int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
                  int dw_accumulate, float* ws, int64_t ws_bytes, int64_t rows, int cols, int64_t ldx, int64_t lddy,
                  int64_t lddx, hipStream_t s) {
-  // workspace: one fp32 partial row per wave, then kSlices rows of slice sums
-  const int64_t nwaves = bwd_waves(rows);
-  LZ_REQUIRE(ws_bytes >= (nwaves + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
-             (long long)ws_bytes);
-  const int grid = (int)(nwaves / kRowsPerBlock);
+  // workspace: one fp32 partial row per wave (per workgroup on the bf16
+  // vector path), then kSlices rows of slice sums
   const bool vec = cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(dy) && lz_aligned16(dx) &&
                    (dres == nullptr || lz_aligned16(dres)) && (ldx * (int64_t)sizeof(T)) % 16 == 0 &&
                    (lddy * (int64_t)sizeof(T)) % 16 == 0 && (lddx * (int64_t)sizeof(T)) % 16 == 0;
   const T *xp = (const T*)x, *wp = (const T*)w, *gp = (const T*)dy, *rp = (const T*)dres;
   T* dxp = (T*)dx;
+  if constexpr (sizeof(T) == 2) {
+    if (vec && cols <= 4096) {
+      const int64_t nblk = bwd_blocks(rows, cols), rpb = lz_cdiv(rows, nblk);
+      LZ_REQUIRE(ws_bytes >= (nblk + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
+                 (long long)ws_bytes);
+      const uint16_t *x16 = (const uint16_t*)x, *w16 = (const uint16_t*)w, *g16 = (const uint16_t*)dy,
+                     *r16 = (const uint16_t*)dres;
+      uint16_t* dx16 = (uint16_t*)dx;
+      const unsigned grid = (unsigned)nblk;
+      if (cols <= 512) rmsnorm_bwd_bf16_kernel<1><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else if (cols <= 1024) rmsnorm_bwd_bf16_kernel<2><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else if (cols <= 2048) rmsnorm_bwd_bf16_kernel<4><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else rmsnorm_bwd_bf16_kernel<8><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      int rc = lz_check_launch("lz_rmsnorm_bwd");
+      if (rc) return rc;
+      if (dw) {
+        float* slices = ws + nblk * (int64_t)cols;
+        dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(ws, nblk, cols, slices);
+        dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, (T*)dw, dw_accumulate);
+        rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
+      }
+      return rc;
+    }
+  }
+  const int64_t nwaves = bwd_waves(rows);
+  LZ_REQUIRE(ws_bytes >= (nwaves + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
+             (long long)ws_bytes);
+  const int grid = (int)(nwaves / kRowsPerBlock);
   if (vec && cols <= 512) rmsnorm_bwd_kernel<T, 1><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
   else if (vec && cols <= 1024) rmsnorm_bwd_kernel<T, 2><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
   else if (vec && cols <= 2048) rmsnorm_bwd_kernel<T, 4><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
@@ -309,7 +476,7 @@ LZ_EXPORT int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,
 
 // Workspace bytes the backward wants for its dw partials.
 LZ_EXPORT int64_t lz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
-  return (bwd_waves(rows) + kSlices) * cols * 4;
+  return (std::max(bwd_waves(rows), bwd_blocks(rows, cols)) + kSlices) * cols * 4;
 }
 
 LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,

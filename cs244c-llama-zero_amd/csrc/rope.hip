@@ -73,6 +73,56 @@ __global__ void rope_kernel(T* __restrict__ x, int64_t ld, int64_t rows, int64_t
   }
 }
 
+// Vectorized rotation: one thread per (row, head, group of V consecutive
+// i < hd/2), V = 16 bytes of elements; the two halves of the head, cos and sin
+// are read as 16-byte vectors.  Same per-element arithmetic as rope_kernel.
+template <typename T, bool kBwd>
+__global__ void __launch_bounds__(256) rope_vec_kernel(T* __restrict__ x, int64_t ld, int64_t rows, int64_t seq,
+                                                       int nheads, int hd, const T* __restrict__ cos_t,
+                                                       const T* __restrict__ sin_t, int64_t pos_offset) {
+  constexpr int V = 16 / sizeof(T);
+  const int half = hd / 2, groups = half / V;
+  const int64_t per_row = (int64_t)nheads * groups;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * per_row) return;
+  const int64_t row = idx / per_row;
+  const int rem = (int)(idx - row * per_row);
+  const int head = rem / groups;
+  const int i = (rem - head * groups) * V;
+  const int64_t pos = row % seq + pos_offset;
+  T* p = x + row * ld + (int64_t)head * hd;
+  const T* cp = cos_t + pos * hd;
+  const T* sp = sin_t + pos * hd;
+  const uint4 av = *reinterpret_cast<const uint4*>(p + i), bv = *reinterpret_cast<const uint4*>(p + i + half);
+  const uint4 c1v = *reinterpret_cast<const uint4*>(cp + i), c2v = *reinterpret_cast<const uint4*>(cp + i + half);
+  const uint4 s1v = *reinterpret_cast<const uint4*>(sp + i), s2v = *reinterpret_cast<const uint4*>(sp + i + half);
+  const T* a = reinterpret_cast<const T*>(&av);
+  const T* b = reinterpret_cast<const T*>(&bv);
+  const T* c1 = reinterpret_cast<const T*>(&c1v);
+  const T* c2 = reinterpret_cast<const T*>(&c2v);
+  const T* s1 = reinterpret_cast<const T*>(&s1v);
+  const T* s2 = reinterpret_cast<const T*>(&s2v);
+  uint4 o1v, o2v;
+  T* o1 = reinterpret_cast<T*>(&o1v);
+  T* o2 = reinterpret_cast<T*>(&o2v);
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const float ae = Elem<T>::load(a, e), be = Elem<T>::load(b, e);
+    float r1, r2;
+    if (!kBwd) {
+      r1 = Elem<T>::round(add_r(Elem<T>::round(mul_r(ae, Elem<T>::load(c1, e))), Elem<T>::round(mul_r(-be, Elem<T>::load(s1, e)))));
+      r2 = Elem<T>::round(add_r(Elem<T>::round(mul_r(be, Elem<T>::load(c2, e))), Elem<T>::round(mul_r(ae, Elem<T>::load(s2, e)))));
+    } else {
+      r1 = Elem<T>::round(add_r(Elem<T>::round(mul_r(ae, Elem<T>::load(c1, e))), Elem<T>::round(mul_r(be, Elem<T>::load(s2, e)))));
+      r2 = Elem<T>::round(add_r(Elem<T>::round(mul_r(be, Elem<T>::load(c2, e))), -Elem<T>::round(mul_r(ae, Elem<T>::load(s1, e)))));
+    }
+    Elem<T>::store(o1, e, r1);
+    Elem<T>::store(o2, e, r2);
+  }
+  *reinterpret_cast<uint4*>(p + i) = o1v;
+  *reinterpret_cast<uint4*>(p + i + half) = o2v;
+}
+
 inline int grid_for(int64_t n) {
   int64_t b = lz_cdiv(n, 256);
   int64_t cap = (int64_t)lz_num_cus() * 16;
@@ -116,6 +166,21 @@ LZ_EXPORT int lz_rope(void* x, int dtype, int64_t ld, int64_t rows, int64_t seq,
   LZ_REQUIRE(ld >= nheads * hd, "lz_rope: leading dimension %lld < %lld", (long long)ld, (long long)(nheads * hd));
   if (rows == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
+  const int esz = dtype == LZ_BF16 ? 2 : 4, vec = 16 / esz;
+  if ((dtype == LZ_BF16 || dtype == LZ_F32) && (hd / 2) % vec == 0 && (ld * esz) % 16 == 0 && lz_aligned16(x) &&
+      lz_aligned16(cos_t) && lz_aligned16(sin_t)) {
+    const int64_t work = rows * nheads * (hd / 2 / vec);
+    LZ_REQUIRE(lz_cdiv(work, 256) < (1ll << 31), "lz_rope: too many rows");
+    const unsigned grid = (unsigned)lz_cdiv(work, 256);
+    if (dtype == LZ_BF16) {
+      if (backward) rope_vec_kernel<uint16_t, true><<<grid, 256, 0, s>>>((uint16_t*)x, ld, rows, seq, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);
+      else rope_vec_kernel<uint16_t, false><<<grid, 256, 0, s>>>((uint16_t*)x, ld, rows, seq, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);
+    } else {
+      if (backward) rope_vec_kernel<float, true><<<grid, 256, 0, s>>>((float*)x, ld, rows, seq, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
+      else rope_vec_kernel<float, false><<<grid, 256, 0, s>>>((float*)x, ld, rows, seq, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
+    }
+    return lz_check_launch("lz_rope");
+  }
   const int g = grid_for(rows * nheads * hd / 2);
   if (dtype == LZ_BF16) {
     if (backward) rope_kernel<uint16_t, true><<<g, 256, 0, s>>>((uint16_t*)x, ld, rows, seq, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);

@@ -7,6 +7,8 @@
 //   dg = r(ds * sig * (1 + g * (1 - sig))).
 // Gate and up may be two column ranges of one fused [T, 2*ffn] projection.
 // HBM-bound: forward 6 B/element (read g,u; write h), backward 10 B/element.
+// The bf16 vector kernels evaluate sigmoid with the hardware exp2/reciprocal
+// (about 1 ulp in fp32, below the bf16 rounding of every output).
 #include "lz_common.h"
 
 namespace {
@@ -26,13 +28,30 @@ __global__ void swiglu_fwd_kernel(const T* __restrict__ g, int64_t ldg, const T*
   }
 }
 
-// Vector path: 8 bf16 per thread (16-byte accesses).
-__global__ void swiglu_fwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t ldg, const uint16_t* __restrict__ u,
-                                         int64_t ldu, uint16_t* __restrict__ h, int64_t ldh, int64_t rows, int64_t cols) {
-  const int64_t cpr = cols >> 3;
-  const int64_t total = rows * cpr;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = idx / cpr, c = (idx - r * cpr) << 3;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+// bf16 round trip through the hardware converter (round to nearest even).
+__device__ __forceinline__ float hw_round_bf(float x) { return bf2f((uint16_t)(pack_bf16x2(x, 0.f) & 0xffff)); }
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal.
+__device__ __forceinline__ float sigmoid_hw(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+}
+
+// Vector path: 8 bf16 per thread (16-byte accesses).  blockIdx.x covers a
+// row's 16-byte chunks, blockIdx.y strides over rows, so no index division.
+__global__ void __launch_bounds__(256) swiglu_fwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t ldg,
+                                                                const uint16_t* __restrict__ u, int64_t ldu,
+                                                                uint16_t* __restrict__ h, int64_t ldh, int64_t rows,
+                                                                int cpr) {
+  const int cc = blockIdx.x * blockDim.x + threadIdx.x;
+  if (cc >= cpr) return;
+  const int64_t c = (int64_t)cc << 3;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
     const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
     const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
     const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
@@ -42,8 +61,8 @@ __global__ void swiglu_fwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t
     for (int k = 0; k < 4; ++k) {
       const float g0 = bf2f(gw[k] & 0xffff), g1 = bf2f(gw[k] >> 16);
       const float u0 = bf2f(uw[k] & 0xffff), u1 = bf2f(uw[k] >> 16);
-      const float h0 = round_bf(silu_f(g0)) * u0, h1 = round_bf(silu_f(g1)) * u1;
-      ow[k] = (uint32_t)f2bf(h0) | ((uint32_t)f2bf(h1) << 16);
+      const float h0 = hw_round_bf(g0 * sigmoid_hw(g0)) * u0, h1 = hw_round_bf(g1 * sigmoid_hw(g1)) * u1;
+      ow[k] = pack_bf16x2(h0, h1);
     }
     *reinterpret_cast<uint4*>(h + r * ldh + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
   }
@@ -72,14 +91,14 @@ __global__ void swiglu_bwd_kernel(const T* __restrict__ g, int64_t ldg, const T*
   }
 }
 
-__global__ void swiglu_bwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t ldg, const uint16_t* __restrict__ u,
-                                         int64_t ldu, const uint16_t* __restrict__ dh, int64_t lddh,
-                                         uint16_t* __restrict__ dg, int64_t lddg, uint16_t* __restrict__ du,
-                                         int64_t lddu, int64_t rows, int64_t cols) {
-  const int64_t cpr = cols >> 3;
-  const int64_t total = rows * cpr;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = idx / cpr, c = (idx - r * cpr) << 3;
+__global__ void __launch_bounds__(256) swiglu_bwd_bf16x8_kernel(
+    const uint16_t* __restrict__ g, int64_t ldg, const uint16_t* __restrict__ u, int64_t ldu,
+    const uint16_t* __restrict__ dh, int64_t lddh, uint16_t* __restrict__ dg, int64_t lddg, uint16_t* __restrict__ du,
+    int64_t lddu, int64_t rows, int cpr) {
+  const int cc = blockIdx.x * blockDim.x + threadIdx.x;
+  if (cc >= cpr) return;
+  const int64_t c = (int64_t)cc << 3;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
     const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
     const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
     const uint4 hv = *reinterpret_cast<const uint4*>(dh + r * lddh + c);
@@ -89,15 +108,30 @@ __global__ void swiglu_bwd_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t
     uint32_t ga[4], ua[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float dg0, du0, dg1, du1;
-      swiglu_bwd_elem<uint16_t>(bf2f(gw[k] & 0xffff), bf2f(uw[k] & 0xffff), bf2f(hw[k] & 0xffff), dg0, du0);
-      swiglu_bwd_elem<uint16_t>(bf2f(gw[k] >> 16), bf2f(uw[k] >> 16), bf2f(hw[k] >> 16), dg1, du1);
-      ga[k] = (uint32_t)f2bf(dg0) | ((uint32_t)f2bf(dg1) << 16);
-      ua[k] = (uint32_t)f2bf(du0) | ((uint32_t)f2bf(du1) << 16);
+      float dgv[2], duv[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float gx = bf2f((uint16_t)(gw[k] >> (16 * e))), ux = bf2f((uint16_t)(uw[k] >> (16 * e)));
+        const float dx = bf2f((uint16_t)(hw[k] >> (16 * e)));
+        const float sig = sigmoid_hw(gx);
+        const float sl = hw_round_bf(gx * sig);
+        const float ds = hw_round_bf(dx * ux);
+        duv[e] = dx * sl;
+        dgv[e] = ds * sig * (1.0f + gx * (1.0f - sig));
+      }
+      ga[k] = pack_bf16x2(dgv[0], dgv[1]);
+      ua[k] = pack_bf16x2(duv[0], duv[1]);
     }
     *reinterpret_cast<uint4*>(dg + r * lddg + c) = make_uint4(ga[0], ga[1], ga[2], ga[3]);
     *reinterpret_cast<uint4*>(du + r * lddu + c) = make_uint4(ua[0], ua[1], ua[2], ua[3]);
   }
+}
+
+// 2-D grid of the vector kernels: enough workgroups for ~16 per CU.
+inline dim3 vec_grid(int64_t rows, int cpr) {
+  const int bx = (int)lz_cdiv(cpr, 256);
+  const int64_t by = std::min<int64_t>(rows, std::max<int64_t>(1, (int64_t)lz_num_cus() * 16 / bx));
+  return dim3((unsigned)bx, (unsigned)std::min<int64_t>(by, 65535));
 }
 
 inline int grid_for(int64_t n) {
@@ -112,12 +146,13 @@ inline bool vec_ok(const void* p, int64_t ld) { return lz_aligned16(p) && (ld % 
 
 LZ_EXPORT int lz_swiglu_fwd(const void* g, int64_t ldg, const void* u, int64_t ldu, void* h, int64_t ldh, int64_t rows,
                             int64_t cols, int dtype, void* stream) {
-  LZ_REQUIRE(rows >= 0 && cols >= 0 && ldg >= cols && ldu >= cols && ldh >= cols, "lz_swiglu_fwd: bad shape");
+  LZ_REQUIRE(rows >= 0 && cols >= 0 && cols < ((int64_t)1 << 31) && ldg >= cols && ldu >= cols && ldh >= cols,
+             "lz_swiglu_fwd: bad shape");
   if (rows == 0 || cols == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   if (dtype == LZ_BF16) {
     if (cols % 8 == 0 && vec_ok(g, ldg) && vec_ok(u, ldu) && vec_ok(h, ldh))
-      swiglu_fwd_bf16x8_kernel<<<grid_for(rows * cols / 8), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)h, ldh, rows, cols);
+      swiglu_fwd_bf16x8_kernel<<<vec_grid(rows, (int)(cols / 8)), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)h, ldh, rows, (int)(cols / 8));
     else
       swiglu_fwd_kernel<uint16_t><<<grid_for(rows * cols), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)h, ldh, rows, cols);
   } else if (dtype == LZ_F32) {
@@ -131,13 +166,14 @@ LZ_EXPORT int lz_swiglu_fwd(const void* g, int64_t ldg, const void* u, int64_t l
 LZ_EXPORT int lz_swiglu_bwd(const void* g, int64_t ldg, const void* u, int64_t ldu, const void* dh, int64_t lddh,
                             void* dg, int64_t lddg, void* du, int64_t lddu, int64_t rows, int64_t cols, int dtype,
                             void* stream) {
-  LZ_REQUIRE(rows >= 0 && cols >= 0 && ldg >= cols && ldu >= cols && lddh >= cols && lddg >= cols && lddu >= cols,
+  LZ_REQUIRE(rows >= 0 && cols >= 0 && cols < ((int64_t)1 << 31) && ldg >= cols && ldu >= cols && lddh >= cols &&
+                 lddg >= cols && lddu >= cols,
              "lz_swiglu_bwd: bad shape");
   if (rows == 0 || cols == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   if (dtype == LZ_BF16) {
     if (cols % 8 == 0 && vec_ok(g, ldg) && vec_ok(u, ldu) && vec_ok(dh, lddh) && vec_ok(dg, lddg) && vec_ok(du, lddu))
-      swiglu_bwd_bf16x8_kernel<<<grid_for(rows * cols / 8), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (const uint16_t*)dh, lddh, (uint16_t*)dg, lddg, (uint16_t*)du, lddu, rows, cols);
+      swiglu_bwd_bf16x8_kernel<<<vec_grid(rows, (int)(cols / 8)), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (const uint16_t*)dh, lddh, (uint16_t*)dg, lddg, (uint16_t*)du, lddu, rows, (int)(cols / 8));
     else
       swiglu_bwd_kernel<uint16_t><<<grid_for(rows * cols), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (const uint16_t*)dh, lddh, (uint16_t*)dg, lddg, (uint16_t*)du, lddu, rows, cols);
   } else if (dtype == LZ_F32) {
