@@ -10,9 +10,10 @@ gradient buckets), step_with_stats (norm + fused AdamW).
 
 Also reported: MFMA utilisation of that step (model FLOPs, 3x forward, over
 2.5 PFLOP/s), the 125M-class ZeRO-1 step (B=16, S=1024), fused AdamW HBM
-bandwidth on a 124M-element flat fp32 buffer, the GEMM kernel's roofline
-measured with HIP events inside the timed steps, and the CPU oracle's
-throughput on a bounded sample of the same workload.
+bandwidth on a 124M-element flat fp32 buffer, the other HBM-bound kernels at
+the step's shapes, the dominant GEMM kernel's roofline measured with HIP
+events inside the timed steps (every GEMM kernel's share is listed too), and
+the CPU oracle's throughput on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 """
@@ -96,6 +97,63 @@ def bench_adamw(dev: torch.device, n: int = 124_000_000, iters: int = 10):
     return {"elements": n, "bytes_per_elem": 28, "ms": ms, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
 
 
+def _time_ms(fn, iters: int = 20) -> float:
+    for _ in range(3):
+        fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def bench_pointwise(dev: torch.device, rows: int = 16384, dim: int = 2048, ffn: int = 5632, heads: int = 16):
+    """The step's HBM-bound kernels at the 1B step's shapes (bf16, 8x2048
+    tokens): bytes moved (each input read once, each output written once) per
+    launch time.  A plain 1 GiB device copy is timed beside them as the
+    achievable-bandwidth reference.  Tensors under ~256 MB can be partly
+    served from the 256 MB Infinity Cache, so those rates may exceed HBM's."""
+    from lzhip import ops
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    out = {}
+
+    def rec(name, ms, nbytes):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
+
+    # plain copy of 1 GiB with this library's copy2d_kernel (also the known-size
+    # kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters)
+    a = torch.ones(1 << 14, 1 << 15, dtype=bf, device=dev)
+    b = torch.empty_like(a)
+    rec("device copy 1 GiB (copy2d_kernel)", _time_ms(lambda: ops.copy2d(a, b), 10), 2 * 2 * a.numel())
+    del a, b
+    x = torch.randn(rows, dim, device=dev, generator=g).to(bf)
+    w = (1 + 0.02 * torch.randn(dim, device=dev, generator=g)).to(bf)
+    dy = torch.randn(rows, dim, device=dev, generator=g).to(bf)
+    n = rows * dim
+    rec(f"rmsnorm fwd [{rows},{dim}]", _time_ms(lambda: ops.rmsnorm_fwd(x, w, 1e-5)), 4 * n)
+    _, rstd = ops.rmsnorm_fwd(x, w, 1e-5)
+    rec(f"rmsnorm bwd [{rows},{dim}]", _time_ms(lambda: ops.rmsnorm_bwd(x, w, rstd, dy)), 6 * n)
+    hd = dim // heads
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32, device=dev) / hd))
+    cos, sin = ops.rope_table(2048, hd, inv, bf)
+    rec(f"rope fwd [{rows},{heads}x{hd}] in place", _time_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin)), 4 * n)
+    del x, dy
+    gu = torch.randn(rows, 2 * ffn, device=dev, generator=g).to(bf)
+    gate, up = gu[:, :ffn], gu[:, ffn:]
+    rec(f"swiglu fwd [{rows},{ffn}]", _time_ms(lambda: ops.swiglu_fwd(gate, up)), 6 * rows * ffn)
+    dh = torch.randn(rows, ffn, device=dev, generator=g).to(bf)
+    dgu = torch.empty_like(gu)
+    rec(f"swiglu bwd [{rows},{ffn}]",
+        _time_ms(lambda: ops.swiglu_bwd(gate, up, dh, dgu[:, :ffn], dgu[:, ffn:])), 10 * rows * ffn)
+    return out
+
+
 def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
     """The CPU oracle (a port of the reference math) on a bounded sample of the
     same workload: one forward+backward over `tokens` tokens of the 1B model
@@ -172,6 +230,15 @@ def main() -> int:
     hw_flops = estimate_transformer_train_flops(cfg, B, S, stage=3)
     n_launch, gemm_flops, gemm_ms = probe.summary()
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    # the dominant GEMM kernel: the one with the most launch time in the steps
+    per_kernel = probe.by_key()
+    top_key = max(per_kernel, key=lambda k: per_kernel[k][2])
+    top_n, top_flops, top_ms = per_kernel[top_key]
+    top_tflops = top_flops / (top_ms * 1e-3) / 1e12
+    gemm_kernels = sorted(
+        ({"kernel": ops.gemm_kernel_name(k), "launches": v[0], "ms_per_step": v[2] / args.steps,
+          "TFLOP/s": v[1] / (v[2] * 1e-3) / 1e12} for k, v in per_kernel.items()),
+        key=lambda d: -d["ms_per_step"])
     log(f"1B ZeRO-3: {ms:.1f} ms/step, {value:,.0f} tok/s, loss {losses[0]:.3f}->{losses[-1]:.3f}")
     peak_mem = torch.cuda.max_memory_allocated(dev) / 2**30
 
@@ -192,6 +259,8 @@ def main() -> int:
         torch.cuda.empty_cache()
     log("AdamW 124M")
     adamw = bench_adamw(dev)
+    log("pointwise kernels")
+    pointwise = bench_pointwise(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -225,17 +294,21 @@ def main() -> int:
         "loss_first_last": [losses[0], losses[-1]],
         "llama_125m_zero1": res_125m,
         "adamw_124m": adamw,
+        "pointwise": pointwise,
+        "gemm_all_launches": {"launches": n_launch, "ms_per_step": gemm_ms / args.steps, "TFLOP/s": gemm_tflops,
+                              "frac": gemm_tflops / PEAK_BF16_TFLOPS},
+        "gemm_kernels": gemm_kernels,
         "roofline": {
-            "kernel": "gemm_kernel (bf16 MFMA GEMM, all launches of the timed steps)",
+            "kernel": ops.gemm_kernel_name(top_key),
             "bound": "mfma",
-            "achieved": gemm_tflops,
+            "achieved": top_tflops,
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": gemm_tflops / PEAK_BF16_TFLOPS,
+            "frac": top_tflops / PEAK_BF16_TFLOPS,
             "traffic": None,
-            "launches": n_launch,
-            "avg_launch_ms": gemm_ms / max(n_launch, 1),
-            "flop_per_launch": gemm_flops / max(n_launch, 1),
+            "launches": top_n,
+            "avg_launch_ms": top_ms / max(top_n, 1),
+            "flop_per_launch": top_flops / max(top_n, 1),
         },
         "cpu_baseline": cpu,
     }

@@ -44,6 +44,7 @@ struct GemmArgs {
   float alpha, beta;
   int c_f32;      // output dtype fp32 (else bf16)
   int vec_store;  // N, ldc, ldr multiples of 4 and pointers aligned
+  int vec16;      // C rows (and R rows) start 16-byte aligned: row-contiguous 16-byte epilogue
   int64_t kper;   // K range of one split (multiple of 64); blockIdx.y is the split
   int64_t slab;   // elements between the fp32 partial slabs of consecutive splits
 };
@@ -216,20 +217,144 @@ struct TileLoader {
   }
 };
 
+// fp32 output of 4 staged values (already scaled by alpha) of row m, columns
+// n..n+3, after beta*C and the residual R.
+__device__ __forceinline__ uint4 finish16(const GemmArgs& go, uint4 v, int64_t m, int64_t n) {
+  {
+    float o[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+    if (go.beta != 0.f) {
+      const float4 c = *reinterpret_cast<const float4*>(static_cast<const float*>(go.C) + m * go.ldc + n);
+      o[0] = fmaf(go.beta, c.x, o[0]); o[1] = fmaf(go.beta, c.y, o[1]);
+      o[2] = fmaf(go.beta, c.z, o[2]); o[3] = fmaf(go.beta, c.w, o[3]);
+    }
+    if (go.R) {
+      const uint2 r = *reinterpret_cast<const uint2*>(go.R + m * go.ldr + n);
+      o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+    }
+    return make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
+  }
+}
+
+// Chunk swizzle of a staged epilogue row of kRow bytes: rows that share a
+// 256-byte bank window are told apart by the XOR, so 16 lanes writing one
+// chunk of 16 consecutive rows (or reading 16 chunks of a row) hit 16
+// distinct 16-byte bank groups.
+template <int kRow>
+__device__ __forceinline__ int epi_swz(int row) {
+  constexpr int kPer256 = kRow >= 256 ? 1 : 256 / kRow;
+  constexpr int kMask = (kRow / 16 - 1) < 15 ? (kRow / 16 - 1) : 15;
+  return (row / kPer256) & kMask;
+}
+
+// Interior tiles, 16-byte path: each wave parks its TM x TN sub-tile in a
+// private LDS region (rows of TN values, 16-byte chunks XOR-swizzled so that
+// both the accumulator-layout writes and the row-wise reads are free of bank
+// conflicts), then writes whole 16-byte pieces of consecutive row bytes, so a
+// store instruction covers full cache lines.  fp32 output goes in two passes
+// of TM/2 rows.  Needs BM*BN*2 bytes of LDS.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
+                                             int64_t m0, int64_t n0, char* smem, int lane, int wave) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static_assert(FM % 2 == 0, "fp32 output is staged in two halves");
+  const int wm = wave / WN, wn = wave % WN;
+  const int frag_row = lane & 31, half = lane >> 5;
+  const int64_t mrow0 = m0 + wm * TM, ncol0 = n0 + wn * TN;
+  char* st = smem + wave * (TM * TN * 2);
+  if (!go.c_f32) {
+    constexpr int kRow = TN * 2, kChunks = kRow / 16;  // bytes and 16-byte chunks per row
+    static_assert(kChunks >= 4 && kChunks <= 64, "bf16 rows of 32 to 512 values");
+    const bool plain = go.beta == 0.f && go.R == nullptr;
+    if (plain) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int row = i * 32 + frag_row, chunk = j * 4 + q;
+            *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
+                make_uint2(pack_bf16x2(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha),
+                           pack_bf16x2(acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha));
+          }
+      asm volatile("" ::: "memory");
+      // 64 lanes x 16 bytes per store: whole rows (or 64-chunk row pieces)
+#pragma unroll
+      for (int t = 0; t < TM * kChunks / 64; ++t) {
+        const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+        const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) = v;
+      }
+      return;
+    }
+  }
+  // fp32 values staged (fp32 output, or bf16 output with beta / residual,
+  // which are applied before the single rounding): two passes of TM/2 rows
+  constexpr int kRow = TN * 4, kChunks = kRow / 16;
+  static_assert(kChunks >= 4 && kChunks <= 64, "fp32 rows of 16 to 256 values");
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+#pragma unroll
+    for (int ii = 0; ii < FM / 2; ++ii) {
+      const int i = p * (FM / 2) + ii;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = ii * 32 + frag_row, chunk = j * 8 + q * 2 + half;
+          *reinterpret_cast<float4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4)) =
+              make_float4(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
+                          acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha);
+        }
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
+      const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+      const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+      const int64_t m = mrow0 + p * (TM / 2) + row, n = ncol0 + chunk * 4;
+      if (go.c_f32) {
+        *reinterpret_cast<uint4*>(static_cast<float*>(go.C) + m * go.ldc + n) = finish16(go, v, m, n);
+      } else {
+        float o[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+        uint16_t* cp = static_cast<uint16_t*>(go.C) + m * go.ldc + n;
+        if (go.beta != 0.f) {
+          const uint2 c = *reinterpret_cast<const uint2*>(cp);
+          o[0] = fmaf(go.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, bf2f(c.x >> 16), o[1]);
+          o[2] = fmaf(go.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, bf2f(c.y >> 16), o[3]);
+        }
+        if (go.R) {
+          const uint2 r = *reinterpret_cast<const uint2*>(go.R + m * go.ldr + n);
+          o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+        }
+        *reinterpret_cast<uint2*>(cp) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+      }
+    }
+    asm volatile("" ::: "memory");
+  }
+}
+
 // Writes a workgroup's BM x BN accumulator tile.  Lane layout of the
 // accumulators: output row m = lane % 32 of each 32x32 tile, columns
-// n = 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Interior tiles store each
-// lane's 4-column groups straight from the accumulators (8 or 16 bytes) with
-// the row address formed once per 32-row band; edge tiles go through LDS one
-// 32-row band at a time and are written as whole rows with bounds checks, so
-// the accumulators are never indexed dynamically.  `smem` must be free and at
-// least WM*WN*32*(BN/WN+4)*4 bytes.
+// n = 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Interior tiles with 16-byte
+// aligned rows and wave tiles up to 64 wide take store_tile16; other interior
+// tiles store each lane's 4-column groups straight from the accumulators (8
+// or 16 bytes) with the row address formed once per 32-row band; edge tiles
+// go through LDS one 32-row band at a time and are written as whole rows with
+// bounds checks, so the accumulators are never indexed dynamically.  `smem` must be free and at
+// least max(WM*WN*32*(BN/WN+4)*4, BM*BN*2) bytes.
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0,
                                            int64_t n0, char* smem, int lane, int wave) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   const int wm = wave / WN, wn = wave % WN;
   const int frag_row = lane & 31, half = lane >> 5;
+  if constexpr (TN <= 64) {  // (wider wave tiles run out of registers in the staged path)
+    if (m0 + BM <= go.M && n0 + BN <= go.N && go.vec16) {
+      store_tile16<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+      return;
+    }
+  }
   if (m0 + BM <= go.M && n0 + BN <= go.N && go.vec_store) {
     const int64_t ncol0 = n0 + wn * TN + half * 4;
     if (go.c_f32) {
@@ -432,26 +557,34 @@ __device__ __forceinline__ int swz_mn(int r) { return ((r & 3) << 2) | ((r >> 2)
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
 
-// One operand of the direct-to-LDS kernel: a 256 (M or N) x 64 (K) stage,
-// 32 KB, filled by 32 wave loads of 1 KB.
-//   K-major: 256 rows of 64 K (128 bytes, 8 chunks, swizzled by swz<8>);
+// Swizzle of the 16-byte chunks of a K-major stage row of 32 K (64 bytes,
+// 4 chunks): the 16 lanes of a ds_read_b128 quarter-wave (16 consecutive rows,
+// one logical chunk) land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz_k4(int r) { return (r >> 2) & 3; }
+
+// One operand of the direct-to-LDS kernel: a 256 (M or N) x DBK (K) stage,
+// 512 * DBK bytes, filled by wave loads of 1 KB (64 lanes x 16 bytes).
+//   K-major: 256 rows of DBK K values (2*DBK bytes: 8 chunks swizzled by
+//            swz<8> for DBK 64, 4 chunks swizzled by swz_k4 for DBK 32);
 //            fragments are plain 16-byte reads.
-//   M/N-major: 64 rows of 256 M/N values (512 bytes, 32 chunks, swizzled by
+//   M/N-major: DBK rows of 256 M/N values (512 bytes, 32 chunks, swizzled by
 //            swz_mn); fragments are two ds_read_b64_tr_b16 (k-slots 0-3 and
 //            4-7 of the 32x32x16 operand: rows 16*kk + 8*(lane/32) + 0..3 and
 //            + 4..7).
-template <bool KMAJOR, int kPerWave>
+template <bool KMAJOR, int kPerWave, int DBK>
 struct DmaOperand {
+  static constexpr int kChunksK = DBK / 8;        // 16-byte chunks per K-major row
+  static constexpr int kRowsK = 64 / kChunksK;    // K-major rows per wave load
   const uint16_t* src[kPerWave];
-  int64_t kadv;  // elements to advance per 64-deep K step
+  int64_t kadv;  // elements to advance per DBK-deep K step
 
   __device__ __forceinline__ void init(const uint16_t* p, int64_t ld, int64_t row0, int64_t nrows, int64_t kbeg,
                                        int wave, int lane) {
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
       if constexpr (KMAJOR) {
-        const int r = (wave * kPerWave + q) * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ swz<8>(r);
+        const int r = (wave * kPerWave + q) * kRowsK + lane / kChunksK;
+        const int c = (lane % kChunksK) ^ (DBK == 64 ? swz<8>(r) : swz_k4(r));
         src[q] = p + min(row0 + r, nrows - 1) * ld + kbeg + c * 8;
       } else {
         const int r = (wave * kPerWave + q) * 2 + (lane >> 5);
@@ -459,7 +592,7 @@ struct DmaOperand {
         src[q] = p + (kbeg + r) * ld + min(row0 + c * 8, nrows - 8);
       }
     }
-    kadv = KMAJOR ? 64 : 64 * ld;
+    kadv = KMAJOR ? DBK : DBK * ld;
   }
 
   __device__ __forceinline__ void issue(char* dst, int wave, int kt) const {
@@ -470,10 +603,10 @@ struct DmaOperand {
 };
 
 // Per-lane LDS offsets of this wave's NF fragments (32-row blocks blk0 ..
-// blk0+NF-1 of the operand) for the four 16-deep sub-steps of a stage.
-template <bool KMAJOR, int NF>
+// blk0+NF-1 of the operand) for the DBK/16 16-deep slices of a stage.
+template <bool KMAJOR, int NF, int DBK>
 struct DmaFrags {
-  int off[KMAJOR ? NF : 1][4];       // K-major
+  int off[KMAJOR ? NF : 1][DBK / 16];  // K-major
   int base[2], ioff[KMAJOR ? 1 : NF];  // M/N-major
 
   __device__ __forceinline__ void init(int blk0, int lane) {
@@ -481,9 +614,9 @@ struct DmaFrags {
 #pragma unroll
       for (int f = 0; f < NF; ++f)
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
+        for (int kk = 0; kk < DBK / 16; ++kk) {
           const int r = (blk0 + f) * 32 + (lane & 31);
-          off[f][kk] = r * 128 + (((2 * kk + (lane >> 5)) ^ swz<8>(r)) << 4);
+          off[f][kk] = r * (2 * DBK) + (((2 * kk + (lane >> 5)) ^ (DBK == 64 ? swz<8>(r) : swz_k4(r))) << 4);
         }
     } else {
       // lane 4j+q of 16-lane group G reads row 8*(G/2) + j (+4), columns
@@ -512,21 +645,68 @@ struct DmaFrags {
   }
 };
 
-// Direct-to-LDS kernel, any operand layouts: 256x256 tile, 64-deep K steps
-// over two 64 KB LDS stages.  K must be a multiple of 64 in every split; an
-// M-major A needs M % 8 == 0 (N-major B: N % 8 == 0).
-template <int WM, int WN, bool AK, bool BK>
+// Fragments of one 16-deep K slice: fa (B operand, FN of them) and fb (A
+// operand, FM), read from the LDS stage at (sa, sb).
+template <bool AK, bool BK, int FM, int FN, int DBK>
+__device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM, DBK>& fra, const DmaFrags<BK, FN, DBK>& frb, const char* sa,
+                                               const char* sb, int kk, bf16x8_t (&fa)[FN], bf16x8_t (&fb)[FM]) {
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fa[j] = frb.frag(sb, j, kk);
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fb[i] = fra.frag(sa, i, kk);
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void dma_mfma(f32x16_t (&acc)[FM][FN], const bf16x8_t (&fa)[FN], const bf16x8_t (&fb)[FM]) {
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
+}
+
+// Scheduling of one K slice: NM MFMAs, each followed by up to ceil(R/NM) of
+// the R LDS reads of the next slice (instruction-group barriers: 0x008 =
+// MFMA, 0x100 = LDS read).
+template <int R, int NM, int Q = 0>
+__device__ __forceinline__ void sched_slice() {
+  if constexpr (Q < NM) {
+    constexpr int rpm = (R + NM - 1) / NM;
+    constexpr int left = R - Q * rpm;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (left > 0) __builtin_amdgcn_sched_group_barrier(0x100, left < rpm ? left : rpm, 0);
+    sched_slice<R, NM, Q + 1>();
+  }
+}
+
+// s_waitcnt with only the vector-memory counter limited to N (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Direct-to-LDS kernel, any operand layouts: 256x256 tile, DBK-deep K steps
+// over NST LDS stages of 2 x 512 x DBK bytes.  NST == 2: one stage loads while
+// the other is read, and the barrier's fence waits for all loads.  NST > 2:
+// NST-1 stages are in flight; each step waits (vmcnt) only for the oldest
+// stage's loads and then syncs the workgroup with a bare barrier.  K must be
+// a multiple of DBK in every split; an M-major A needs M % 8 == 0 (N-major B:
+// N % 8 == 0).
+template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
-  constexpr int BM = 256, BN = 256, DBK = 64;
+  constexpr int BM = 256, BN = 256;
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-  constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage (32 KB)
+  constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage
   constexpr int kStage = 2 * kOpBytes;
   constexpr int kPerWave = kOpBytes / 1024 / kWaves;  // wave loads per operand per stage
+  constexpr int kSlices = DBK / 16;
   static_assert(kPerWave * kWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
-  static_assert(kWaves * 32 * (TN + 4) * 4 <= 2 * kStage, "epilogue staging does not fit");
+  static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
+  static_assert(kSlices == 2 || kSlices == 4, "stages hold 2 or 4 K slices");
 
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -537,12 +717,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   const int64_t kbeg = (int64_t)blockIdx.y * g.kper, kend = min(g.K, kbeg + g.kper);
   const int ktiles = kend > kbeg ? (int)((kend - kbeg) / DBK) : 0;
 
-  DmaOperand<AK, kPerWave> la;
-  DmaOperand<BK, kPerWave> lb;
+  DmaOperand<AK, kPerWave, DBK> la;
+  DmaOperand<BK, kPerWave, DBK> lb;
   la.init(g.A, g.lda, m0, g.M, kbeg, wave, lane);
   lb.init(g.B, g.ldb, n0, g.N, kbeg, wave, lane);
-  DmaFrags<AK, FM> fra;
-  DmaFrags<BK, FN> frb;
+  DmaFrags<AK, FM, DBK> fra;
+  DmaFrags<BK, FN, DBK> frb;
   fra.init(wm * FM, lane);
   frb.init(wn * FN, lane);
 
@@ -554,35 +734,57 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  if (ktiles > 0) {
-    la.issue(smem, wave, 0);
-    lb.issue(smem + kOpBytes, wave, 0);
-  }
+#pragma unroll
+  for (int st = 0; st < NST - 1; ++st)
+    if (st < ktiles) {
+      la.issue(smem + st * kStage, wave, st);
+      lb.issue(smem + st * kStage + kOpBytes, wave, st);
+    }
   for (int kt = 0; kt < ktiles; ++kt) {
-    // only stage kt's loads are in flight here: the barrier's fence waits for
-    // them, publishes every wave's part and retires the reads of stage kt-1,
-    // whose slot is refilled next
-    __syncthreads();
-    if (kt + 1 < ktiles) {
-      char* nxt = smem + ((kt + 1) & 1) * kStage;
-      la.issue(nxt, wave, kt + 1);
-      lb.issue(nxt + kOpBytes, wave, kt + 1);
+    if constexpr (NST == 2) {
+      // only stage kt's loads are in flight here: the barrier's fence waits
+      // for them, publishes every wave's part and retires the reads of stage
+      // kt-1, whose slot is refilled next
+      __syncthreads();
+    } else {
+      // stage kt's loads are this wave's oldest: let the (up to NST-2) later
+      // stages stay in flight, then the barrier publishes every wave's part
+      // and retires the reads of stage kt-1, whose slot is refilled next
+      static_assert(NST == 4, "the wait ladder below covers four stages");
+      constexpr int kLoads = 2 * kPerWave;  // DMA instructions per wave per stage
+      const int ahead = ktiles - 1 - kt;
+      asm volatile("" ::: "memory");
+      if (ahead >= 2) wait_vmcnt<2 * kLoads>();
+      else if (ahead == 1) wait_vmcnt<kLoads>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
     }
-    const char* sa = smem + (kt & 1) * kStage;
+    if (kt + NST - 1 < ktiles) {
+      char* nxt = smem + ((kt + NST - 1) % NST) * kStage;
+      la.issue(nxt, wave, kt + NST - 1);
+      lb.issue(nxt + kOpBytes, wave, kt + NST - 1);
+    }
+    const char* sa = smem + (kt % NST) * kStage;
     const char* sb = sa + kOpBytes;
-#pragma unroll
-    for (int kk = 0; kk < DBK / 16; ++kk) {
-      bf16x8_t fa[FN], fb[FM];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) fa[j] = frb.frag(sb, j, kk);
-#pragma unroll
-      for (int i = 0; i < FM; ++i) fb[i] = fra.frag(sa, i, kk);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
+    // fragments double-buffered in registers: slice kk+1 is read while the
+    // MFMAs of slice kk run
+    bf16x8_t fa0[FN], fb0[FM], fa1[FN], fb1[FM];
+    constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);
+    dma_load_frags(fra, frb, sa, sb, 0, fa0, fb0);
+    dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
+    dma_mfma(acc, fa0, fb0);
+    if constexpr (kSlices == 4) {
+      dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
+      dma_mfma(acc, fa1, fb1);
+      dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
+      dma_mfma(acc, fa0, fb0);
     }
+    dma_mfma(acc, fa1, fb1);
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+#pragma unroll
+    for (int q = 0; q < kSlices - 1; ++q) sched_slice<kReads, FM * FN>();
+    sched_slice<0, FM * FN>();
   }
   __syncthreads();  // every wave is done with the stages before the epilogue may reuse LDS
 
@@ -612,8 +814,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
 
 // Tile configurations: 0 = 256x256 with 8 waves (128x64 per wave),
 // 1 = 256x256 with 4 waves (128x128 per wave, accumulators in AGPRs),
-// 2 = 128x128 with 4 waves; 5 and 6 = the direct-to-LDS kernel (any
-// layouts, 8 or 4 waves, two stages of 64 K).
+// 2 = 128x128 with 4 waves; 5 = the direct-to-LDS kernel (any layouts,
+// 8 waves, two stages of 64 K).
 struct Plan {
   int cfg;
   int splits;
@@ -670,27 +872,22 @@ int launch(const GemmArgs& g, int splits, hipStream_t s) {
 // Explicit instantiations: when the host pass only meets these kernels through
 // the dispatch templates it does not emit the launch stubs of the variants
 // that use ds_read_b64_tr_b16.
-template __global__ void gemm_dma_kernel<2, 4, true, true>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 4, true, false>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 4, false, true>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 4, false, false>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 2, true, true>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 2, true, false>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 2, false, true>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 2, false, false>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, true, true, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, true, false, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, false, true, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<2, 4, false, false, 64, 2>(GemmArgs);
 
-template <int WM, int WN, bool AK, bool BK>
+template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
 int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
   const int64_t tiles = lz_cdiv(g.M, 256) * lz_cdiv(g.N, 256);
   LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
-  gemm_dma_kernel<WM, WN, AK, BK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  gemm_dma_kernel<WM, WN, AK, BK, DBK, NST><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
   return lz_check_launch("lz_gemm");
 }
 
 template <bool AK, bool BK>
 int dispatch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
-  if (cfg == 5) return launch_dma<2, 4, AK, BK>(g, splits, s);
-  if (cfg == 6) return launch_dma<2, 2, AK, BK>(g, splits, s);
+  if (cfg == 5) return launch_dma<2, 4, AK, BK, 64, 2>(g, splits, s);
   switch (cfg) {
     case 0:
       return launch<256, 256, 2, 4, AK, BK>(g, splits, s);
@@ -715,6 +912,16 @@ int dispatch_layout(const GemmArgs& g, bool ak, bool bk, int cfg, int splits, hi
 LZ_EXPORT int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   return plan_workspace(make_plan(M, N, K, a_kmajor != 0, b_kmajor != 0), M, N);
+}
+
+// The kernel lz_gemm launches for this shape and layout, encoded as
+// 16 * cfg + splits: cfg 5 = direct-to-LDS 256x256 tile with 8 waves,
+// 0 / 1 = register-staged 256x256 with 8 / 4 waves, 2 = 128x128 with 4 waves;
+// splits = number of K slices (1 = unsplit; more need the workspace).
+LZ_EXPORT int lz_gemm_plan(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const Plan p = make_plan(M, N, K, a_kmajor != 0, b_kmajor != 0);
+  return 16 * p.cfg + p.splits;
 }
 
 // C = alpha * sum_k A(m,k) B(n,k) (+ beta*C) (+ R), see the top of this file
@@ -756,6 +963,8 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
   g.beta = beta;
   g.c_f32 = c_dtype == LZ_F32;
   const int esz = g.c_f32 ? 4 : 2;
+  g.vec16 = ((ldc * esz) % 16 == 0) && lz_aligned16(C) &&
+            (R == nullptr || ((ldr * 2) % 8 == 0 && (reinterpret_cast<uintptr_t>(R) & 7) == 0));
   g.vec_store = (N % 4 == 0) && (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & (4 * esz - 1)) == 0) &&
                 (R == nullptr || ((ldr % 4 == 0) && (reinterpret_cast<uintptr_t>(R) & 7) == 0));
   g.kper = K > 0 ? K : 1;
@@ -776,6 +985,7 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
   gs.beta = 0.f;
   gs.R = nullptr;
   gs.vec_store = N % 4 == 0;
+  gs.vec16 = N % 4 == 0 && lz_aligned16(ws);
   gs.kper = p.kper;
   gs.slab = M * N;
   int rc = dispatch_layout(gs, ak, bk, p.cfg, p.splits, s);

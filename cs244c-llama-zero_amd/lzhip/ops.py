@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional, Sequence, Tuple
+from typing import Dict, Optional, Sequence, Tuple
 
 import torch
 
@@ -428,19 +428,39 @@ def transpose_padded(src2: torch.Tensor) -> torch.Tensor:
 
 class LaunchProbe:
     """Opt-in timing of GEMM launches with HIP events recorded on the launch
-    stream: (flops, start, end) per launch.  Used by the benchmark to measure
+    stream: (flops, start, end, kernel key) per launch, the key being
+    (a_kmajor, b_kmajor, lz_gemm_plan code).  Used by the benchmark to measure
     the MFMA kernel inside a timed training step."""
 
     def __init__(self) -> None:
         self.records = []
 
-    def add(self, flops: float, start, end) -> None:
-        self.records.append((flops, start, end))
+    def add(self, flops: float, start, end, key=None) -> None:
+        self.records.append((flops, start, end, key))
 
-    def summary(self) -> Tuple[int, float, float]:
-        """(launches, total flops, total milliseconds) — call after a sync."""
-        ms = sum(s.elapsed_time(e) for _, s, e in self.records)
-        return len(self.records), sum(f for f, _, _ in self.records), ms
+    def summary(self, key=None) -> Tuple[int, float, float]:
+        """(launches, total flops, total milliseconds) over every launch, or
+        over the launches of one kernel key — call after a sync."""
+        rec = [r for r in self.records if key is None or r[3] == key]
+        ms = sum(s.elapsed_time(e) for _, s, e, _ in rec)
+        return len(rec), sum(f for f, _, _, _ in rec), ms
+
+    def by_key(self) -> Dict[tuple, Tuple[int, float, float]]:
+        """{kernel key: (launches, flops, milliseconds)} — call after a sync."""
+        return {k: self.summary(k) for k in {r[3] for r in self.records}}
+
+
+def gemm_kernel_name(key) -> str:
+    """Kernel name (as profilers print it) of a LaunchProbe key."""
+    ak, bk, code = key
+    cfg, splits = code // 16, code % 16
+    tf = lambda b: "true" if b else "false"
+    if cfg == 5:
+        name = f"gemm_dma_kernel<2, 4, {tf(ak)}, {tf(bk)}, 64, 2>"
+    else:
+        bm, wn = (128, 2) if cfg == 2 else (256, 4 if cfg == 0 else 2)
+        name = f"gemm_kernel<{bm}, {bm}, 2, {wn}, {tf(ak)}, {tf(bk)}>"
+    return name + (f" split-K x{splits} (+ splitk_reduce_kernel)" if splits > 1 else "")
 
 
 _gemm_probe: Optional[LaunchProbe] = None
@@ -515,7 +535,8 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
               ws_bytes if ws is not None else 0, stream_ptr(a.device))
     if probe is not None:
         end.record()
-        probe.add(2.0 * M * N * K, start, end)
+        probe.add(2.0 * M * N * K, start, end, (bool(a_kmajor), bool(b_kmajor),
+                                                int(lib.lz_gemm_plan(M, N, Kp, int(a_kmajor), int(b_kmajor)))))
     return out
 
 
