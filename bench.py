@@ -42,7 +42,7 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_engine(size: str, stage: int, batch: int, seq: int, dev: torch.device):
+def make_engine(size: str, stage: int, batch: int, seq: int, dev: torch.device, recompute: bool = True):
     from model import LlamaForCausalLM, build_config
     from zero import ZeROStage1Optimizer, ZeROStage3Optimizer
 
@@ -51,7 +51,8 @@ def make_engine(size: str, stage: int, batch: int, seq: int, dev: torch.device):
     model = LlamaForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16)
     model.set_loss_chunk_size(128)
     cls = ZeROStage3Optimizer if stage == 3 else ZeROStage1Optimizer
-    engine = cls(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    kw = {} if stage != 3 else {"recompute": recompute}
+    engine = cls(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, **kw)
     return cfg, model, engine
 
 
@@ -242,10 +243,23 @@ def main() -> int:
     log(f"1B ZeRO-3: {ms:.1f} ms/step, {value:,.0f} tok/s, loss {losses[0]:.3f}->{losses[-1]:.3f}")
     peak_mem = torch.cuda.max_memory_allocated(dev) / 2**30
 
+    del model, engine
+    torch.cuda.empty_cache()
+    log("1B ZeRO-3 with recompute=False")
+    cfg_nr, m_nr, e_nr = make_engine("1b", 3, B, S, dev, recompute=False)
+    el_nr, l_nr = run_steps(m_nr, e_nr, batches, steps=args.steps, warmup=args.warmup)
+    res_norecompute = {
+        "tokens_per_s": tokens * args.steps / el_nr, "ms_per_step": el_nr * 1000.0 / args.steps,
+        "mfma_util": model_flops * args.steps / el_nr / 1e12 / PEAK_BF16_TFLOPS, "loss_first_last": [l_nr[0], l_nr[-1]],
+        "workload": "same 1B ZeRO-3 step with the engine's recompute=False (each module's forward graph kept; "
+                    "same gradients, one forward per step)",
+    }
+    log(f"1B ZeRO-3 recompute=False: {res_norecompute['ms_per_step']:.1f} ms/step")
+    del m_nr, e_nr
+    torch.cuda.empty_cache()
+
     res_125m = None
     if not args.skip_125m:
-        del model, engine
-        torch.cuda.empty_cache()
         log("125M ZeRO-1")
         cfg2, m2, e2 = make_engine("125m", 1, 16, 1024, dev)
         b2 = [torch.randint(0, 32000, (16, 1024), device=dev, generator=gen) for _ in range(4)]
@@ -292,6 +306,7 @@ def main() -> int:
         "hardware_tflop_per_step_with_recompute": hw_flops / 1e12,
         "peak_hbm_gib": peak_mem,
         "loss_first_last": [losses[0], losses[-1]],
+        "llama_1b_zero3_recompute_off": res_norecompute,
         "llama_125m_zero1": res_125m,
         "adamw_124m": adamw,
         "pointwise": pointwise,

@@ -2,8 +2,10 @@
 
 Flags, defaults, stdout step lines (the experiment harness's contract), the
 --profile-json payload and checkpoints follow the reference.  Additions: the
-`plumbing`/`125m`/`1b`/`7b` presets, the `synthetic-uniform` data mode and
---grad-bucket-numel (the gradient bucket size of stages 0, 1 and 3).  The
+`plumbing`/`125m`/`1b`/`7b` presets, the `synthetic-uniform` data mode,
+--grad-bucket-numel (the gradient bucket size of stages 0, 1 and 3) and
+--zero3-recompute off (stage 3 keeps each module's forward graph instead of
+recomputing it in backward; same gradients, one forward per step).  The
 engines run at world_size 1 with LocalCollectives; launching with
 WORLD_SIZE > 1 is rejected.
 """
@@ -71,6 +73,8 @@ def build_parser() -> argparse.ArgumentParser:
                    help="Compatibility knob only; stage 2 uses one contiguous gradient buffer per backward pass.")
     p.add_argument("--grad-bucket-numel", type=int, default=GRAD_BUCKET_NUMEL,
                    help="Elements per gradient bucket of the stage 0/1/3 flatten (reduce-scatter/all-reduce unit).")
+    p.add_argument("--zero3-recompute", type=str, default="on", choices=["on", "off"],
+                   help="Stage 3: recompute each module in backward (reference behaviour) or keep its forward graph.")
     p.add_argument("--dtype", type=str, default="float32", choices=["float32", "bfloat16"])
     p.add_argument("--seed", type=int, default=1337)
     p.add_argument("--loss-chunk-size", type=int, default=128,
@@ -170,7 +174,8 @@ def build_engine(args: argparse.Namespace, model: LlamaForCausalLM, collectives)
         numel = max(1, int((args.stage2_grad_bucket_mb * 1024.0 * 1024.0) / 4.0))
         return ZeROStage2Optimizer(**kw, grad_bucket_numel=numel)
     if args.zero_stage == 3:
-        return ZeROStage3Optimizer(**kw, grad_bucket_numel=bucket)
+        return ZeROStage3Optimizer(**kw, grad_bucket_numel=bucket,
+                                   recompute=getattr(args, "zero3_recompute", "on") == "on")
     raise ValueError(f"Unsupported stage: {args.zero_stage}")
 
 

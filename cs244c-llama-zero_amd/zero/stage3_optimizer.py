@@ -19,6 +19,15 @@ MI355X data path:
     reduce-scatter unit), each bucket accumulated into the fp32 shard.
 At world_size 1 the all-gather and reduce-scatter are the identity and are
 elided unless a tracing wrapper needs to observe them.
+
+`recompute=False` (world_size 1 only; default True = reference behaviour)
+keeps every module's forward autograd graph instead of recomputing it in
+backward.  The gradients are the same (the backward of each module call is
+taken with autograd.grad over the module's inputs and parameters and
+flattened into the fp32 shard per call, exactly as after a recompute), the
+forward runs once, and the parameters stay materialised: they live in one
+engine-wide bf16 buffer that the fused AdamW rewrites in place, so the
+per-module materialise casts and reshards disappear too.
 """
 from __future__ import annotations
 
@@ -102,6 +111,7 @@ class _Stage3ParamHandle:
     def __post_init__(self) -> None:
         self.param_dtype = model_param_dtype(self.meta)
         self.materialized = True
+        self.pinned = False  # parameters kept materialised (recompute=False)
         # engine-owned flat state; bound by the engine right after creation
         self.local_master_param_shard: Optional[torch.Tensor] = None
         self.exp_avg: Optional[torch.Tensor] = None
@@ -128,7 +138,7 @@ class _Stage3ParamHandle:
         return (time.perf_counter() - t0) * 1000.0
 
     def reshard(self) -> None:
-        if not self.materialized:
+        if not self.materialized or self.pinned:
             return
         for p in self.meta.params:
             p.grad = None
@@ -186,6 +196,27 @@ class _ShardedModuleFunction(torch.autograd.Function):
             else:
                 ctx.arg_requires_grad.append(False)
                 ctx.non_tensor_args.append(a)
+        eng, h = runner.engine, runner.handle
+        if not eng.recompute:
+            # keep the module's own graph: inputs detached (grad-requiring
+            # ones marked), parameters already materialised
+            rebuilt: List[object] = []
+            grad_inputs: List[torch.Tensor] = []
+            it = iter(tensor_args)
+            with torch.enable_grad():
+                for is_t, rg, nt in zip(ctx.arg_is_tensor, ctx.arg_requires_grad, ctx.non_tensor_args):
+                    if not is_t:
+                        rebuilt.append(nt)
+                        continue
+                    t = next(it)
+                    if rg:
+                        t = t.detach().requires_grad_(True)
+                        grad_inputs.append(t)
+                    rebuilt.append(t)
+                out = runner.module(*rebuilt)
+            ctx.inner = (out, grad_inputs)
+            eng._record_forward_allgather_ms(0.0, num_bytes=0)
+            return out.detach()
         ctx.save_for_backward(*tensor_args)
         ctx.cpu_rng_state = torch.get_rng_state()
         dev = runner.device
@@ -193,13 +224,12 @@ class _ShardedModuleFunction(torch.autograd.Function):
             idx = dev.index if dev.index is not None else torch.cuda.current_device()
             ctx.cuda_rng_state = torch.cuda.get_rng_state(idx)
             ctx.autocast_enabled = torch.is_autocast_enabled()
-            ctx.autocast_dtype = torch.get_autocast_gpu_dtype()
+            ctx.autocast_dtype = torch.get_autocast_dtype("cuda")
         else:
             ctx.cuda_rng_state = None
             ctx.autocast_enabled = torch.is_autocast_cpu_enabled() if dev.type == "cpu" else False
-            ctx.autocast_dtype = torch.get_autocast_cpu_dtype() if dev.type == "cpu" else torch.float32
+            ctx.autocast_dtype = torch.get_autocast_dtype("cpu") if dev.type == "cpu" else torch.float32
 
-        eng, h = runner.engine, runner.handle
         nbytes = h.meta.total_numel * _elem_size(h.param_dtype)
         eng._record_memory_event(f"measured_step_stage3_{runner.name}_pre_allgather_forward")
         eng._record_forward_allgather_ms(h.materialize("forward"), num_bytes=nbytes)
@@ -215,6 +245,20 @@ class _ShardedModuleFunction(torch.autograd.Function):
     def backward(ctx, grad_output: torch.Tensor):
         runner = ctx.runner
         eng, h = runner.engine, runner.handle
+        if not eng.recompute:
+            out, grad_inputs = ctx.inner
+            del ctx.inner
+            params = list(h.meta.params)
+            grads = torch.autograd.grad(outputs=out, inputs=grad_inputs + params, grad_outputs=grad_output,
+                                        allow_unused=True)
+            del out
+            nbytes = h.meta.total_numel * _elem_size(h.param_dtype)
+            eng._record_backward_allgather_ms(0.0, num_bytes=0)
+            eng._record_backward_reduce_scatter_ms(h.accumulate_grad_shard(grads[len(grad_inputs):]),
+                                                   num_bytes=nbytes)
+            it = iter(grads[: len(grad_inputs)])
+            return (None, None, *[next(it) if (is_t and rg) else None
+                                  for is_t, rg in zip(ctx.arg_is_tensor, ctx.arg_requires_grad)])
         saved = iter(ctx.saved_tensors)
         rebuilt: List[object] = []
         grad_inputs: List[torch.Tensor] = []
@@ -288,6 +332,7 @@ class ZeROStage3Optimizer:
     memory_trace_active: bool = False
     memory_state_timeline: Optional[List[Dict[str, object]]] = None
     grad_bucket_numel: int = GRAD_BUCKET_NUMEL
+    recompute: bool = True
 
     def __post_init__(self) -> None:
         self.rank, self.world_size = get_rank_world_size()
@@ -303,9 +348,33 @@ class ZeROStage3Optimizer:
         self._bucket: Optional[torch.Tensor] = None
         self._build_module_runners()
         self._bind_flat_state()
+        self._param_flat: Optional[torch.Tensor] = None
+        if not self.recompute:
+            self._pin_params()
         self._fused = FusedStep(self._device)
         self.model._zero3_executor = self
         self._reshard_all_params()
+
+    def _pin_params(self) -> None:
+        """recompute=False: every parameter becomes a view of one bf16 buffer in
+        handle order (the master's order), filled from the master once and
+        afterwards rewritten by the fused AdamW."""
+        if not self.collectives.is_identity:
+            raise ValueError("recompute=False keeps parameters materialised and needs world_size 1")
+        dtypes = {h.param_dtype for h in self._handle_order}
+        if len(dtypes) != 1:
+            raise ValueError(f"recompute=False needs one parameter dtype across modules, got {sorted(map(str, dtypes))}")
+        for h in self._handle_order:
+            if h.shard.shard_numel != h.meta.total_numel:
+                raise ValueError("recompute=False needs unpadded shards (world_size 1)")
+        self._param_flat = ops.cast(self._master_all, dtypes.pop())
+        off = 0
+        for h in self._handle_order:
+            n = h.meta.total_numel
+            views_into(h.meta, self._param_flat[off : off + n])
+            h.materialized = True
+            h.pinned = True
+            off += n
 
     def _reset_comm_stats(self) -> None:
         self._forward_comm_ms = 0.0
@@ -437,7 +506,7 @@ class ZeROStage3Optimizer:
         t_opt0 = time.perf_counter()
         self._fused.adamw(self._master_all, self._exp_avg_all, self._exp_avg_sq_all, self._grad_all, lr=self.lr,
                           betas=self.betas, eps=self.eps, weight_decay=self.weight_decay, step=self.step_count,
-                          max_grad_norm=max_grad_norm)
+                          max_grad_norm=max_grad_norm, p_out=self._param_flat)
         optim_ms = (time.perf_counter() - t_opt0) * 1000.0
         self._reshard_all_params()
         grad_norm = self._fused.read_norm()
@@ -521,4 +590,6 @@ class ZeROStage3Optimizer:
                     raise ValueError(f"stage3 handle '{h.name}' {key}: {src.numel()} != {dst.numel()} elements")
                 dst.copy_(src.to(dtype=torch.float32).view(-1))
             h.reset_grad()
+        if self._param_flat is not None:
+            ops.cast(self._master_all, self._param_flat.dtype, out=self._param_flat)
         self._reshard_all_params()

@@ -132,6 +132,52 @@ def test_stage3_matches_stage0_training():
         assert rel < 2e-2, (n, rel)
 
 
+def test_stage3_recompute_off_matches_recompute_on():
+    """Keeping each module's forward graph gives the recompute path's
+    gradients: same loss bits, same fp32 gradient flatten (up to the order of
+    the embedding gradient's fp32 atomics), and the same training."""
+    kw = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01)
+    ma, mb = _model(55), _model(55)
+    ea = ZeROStage3Optimizer(model=ma, **kw)
+    eb = ZeROStage3Optimizer(model=mb, recompute=False, **kw)
+    assert all(p.numel() > 0 for p in mb.parameters())
+    for e, m in ((ea, ma), (eb, mb)):
+        e.zero_grad()
+        e.prepare_forward()
+        for s in range(2):  # two micro-batches accumulate into the fp32 shard
+            loss = m(input_ids=_batch(s), labels=_batch(s)).loss
+            e.backward(loss)
+        e._last_loss = float(loss)
+    assert ea._last_loss == eb._last_loss
+    ga, gb = ea._grad_all.double(), eb._grad_all.double()
+    assert float((ga - gb).norm() / ga.norm()) < 1e-5
+    ea.step(max_grad_norm=0.5)
+    eb.step(max_grad_norm=0.5)
+    la, lb = _train(ea, ma, 3, max_norm=0.5), _train(eb, mb, 3, max_norm=0.5)
+    for a, b in zip(la, lb):
+        assert abs(a - b) <= 1e-4 * abs(a)
+    pa, pb = _full_params(ea, ma), _full_params(eb, mb)
+    for n in pa:
+        assert torch.allclose(pa[n], pb[n], rtol=1e-3, atol=1e-5), n
+    # parameters stay materialised and equal the bf16 rounding of the master
+    assert all(p.numel() > 0 for p in mb.parameters())
+    assert torch.equal(eb._param_flat, eb._master_all.to(torch.bfloat16))
+    assert eb._forward_allgather_ms == 0.0
+
+
+def test_stage3_recompute_off_checkpoint_restore():
+    kw = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01, recompute=False)
+    m_src = _model(31)
+    e_src = ZeROStage3Optimizer(model=m_src, **kw)
+    _train(e_src, m_src, 2, max_norm=0.25)
+    m_dst = _model(32)
+    e_dst = ZeROStage3Optimizer(model=m_dst, **kw)
+    e_dst.load_state_dict(e_src.state_dict())
+    a, b = _full_params(e_src, m_src), _full_params(e_dst, m_dst)
+    for n in a:
+        assert torch.equal(a[n], b[n]), n
+
+
 def test_stage3_reshards_and_summons():
     model = _model(7)
     eng = ZeROStage3Optimizer(model=model, lr=1e-3, weight_decay=0.0)
