@@ -98,6 +98,39 @@ def bench_adamw(dev: torch.device, n: int = 124_000_000, iters: int = 10):
     return {"elements": n, "bytes_per_elem": 28, "ms": ms, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
 
 
+def run_no_recompute(args, B, S, dev, batches, tokens, model_flops):
+    """The 1B ZeRO-3 step with the engine's recompute=False."""
+    log("1B ZeRO-3 with recompute=False")
+    _, m_nr, e_nr = make_engine("1b", 3, B, S, dev, recompute=False)
+    el_nr, l_nr = run_steps(m_nr, e_nr, batches, steps=args.steps, warmup=args.warmup)
+    res = {
+        "tokens_per_s": tokens * args.steps / el_nr, "ms_per_step": el_nr * 1000.0 / args.steps,
+        "mfma_util": model_flops * args.steps / el_nr / 1e12 / PEAK_BF16_TFLOPS, "loss_first_last": [l_nr[0], l_nr[-1]],
+        "workload": "same 1B ZeRO-3 step with the engine's recompute=False (each module's forward graph kept; "
+                    "same gradients, one forward per step)",
+    }
+    log(f"1B ZeRO-3 recompute=False: {res['ms_per_step']:.1f} ms/step")
+    del m_nr, e_nr
+    torch.cuda.empty_cache()
+    return res
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_dma_kernel_nt_1b_zero3_traffic.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE/WRITE_SIZE
+    profile (a line `traffic_bytes_per_launch <kernel> = N`), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch") and kernel in line:
+                    return float(line.rsplit("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def _time_ms(fn, iters: int = 20) -> float:
     for _ in range(3):
         fn()
@@ -194,6 +227,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-125m", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the 1B ZeRO-3 step (no recompute=False, 125M, AdamW or pointwise legs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's engines run at world_size 1 (got --gpus {args.gpus})",
@@ -245,19 +280,11 @@ def main() -> int:
 
     del model, engine
     torch.cuda.empty_cache()
-    log("1B ZeRO-3 with recompute=False")
-    cfg_nr, m_nr, e_nr = make_engine("1b", 3, B, S, dev, recompute=False)
-    el_nr, l_nr = run_steps(m_nr, e_nr, batches, steps=args.steps, warmup=args.warmup)
-    res_norecompute = {
-        "tokens_per_s": tokens * args.steps / el_nr, "ms_per_step": el_nr * 1000.0 / args.steps,
-        "mfma_util": model_flops * args.steps / el_nr / 1e12 / PEAK_BF16_TFLOPS, "loss_first_last": [l_nr[0], l_nr[-1]],
-        "workload": "same 1B ZeRO-3 step with the engine's recompute=False (each module's forward graph kept; "
-                    "same gradients, one forward per step)",
-    }
-    log(f"1B ZeRO-3 recompute=False: {res_norecompute['ms_per_step']:.1f} ms/step")
-    del m_nr, e_nr
-    torch.cuda.empty_cache()
-
+    if args.headline_only:
+        args.skip_125m = True
+    res_norecompute = adamw = pointwise = None
+    if not args.headline_only:
+        res_norecompute = run_no_recompute(args, B, S, dev, batches, tokens, model_flops)
     res_125m = None
     if not args.skip_125m:
         log("125M ZeRO-1")
@@ -271,10 +298,11 @@ def main() -> int:
                     "workload": "125m ZeRO-1 (d768 L12 12q/4kv ffn2048 V32000), B=16 S=1024"}
         del m2, e2
         torch.cuda.empty_cache()
-    log("AdamW 124M")
-    adamw = bench_adamw(dev)
-    log("pointwise kernels")
-    pointwise = bench_pointwise(dev)
+    if not args.headline_only:
+        log("AdamW 124M")
+        adamw = bench_adamw(dev)
+        log("pointwise kernels")
+        pointwise = bench_pointwise(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -320,7 +348,8 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": top_tflops / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic(ops.gemm_kernel_name(top_key)),
+            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
             "launches": top_n,
             "avg_launch_ms": top_ms / max(top_n, 1),
             "flop_per_launch": top_flops / max(top_n, 1),
