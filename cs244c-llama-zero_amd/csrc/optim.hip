@@ -224,6 +224,67 @@ __global__ void cast_kernel(const S* __restrict__ src, D* __restrict__ dst, int6
     Elem<D>::store(dst, i, Elem<S>::load(src, i));
 }
 
+// Eight consecutive elements as floats (16-byte accesses; fp32 takes two).
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&r)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w; r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&r)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(r[0], r[1], r[2], r[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(r[4], r[5], r[6], r[7]);
+  }
+};
+template <>
+struct Vec8<uint16_t> {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {  // round to nearest even
+    const f32x2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+  }
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&r)[8]) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r[2 * k] = __uint_as_float(w[k] << 16);
+      r[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float (&r)[8]) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack(r[0], r[1]), pack(r[2], r[3]), pack(r[4], r[5]), pack(r[6], r[7]));
+  }
+};
+
+// Vector paths: one 8-element group per thread over a full grid.
+template <typename S, typename D>
+__global__ void __launch_bounds__(kThreads) cast_vec8_kernel(const S* __restrict__ src, D* __restrict__ dst, int64_t n8) {
+  const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (q >= n8) return;
+  float r[8];
+  Vec8<S>::load(src + 8 * q, r);
+  Vec8<D>::store(dst + 8 * q, r);
+}
+
+template <typename S>
+__global__ void __launch_bounds__(kThreads) axpy_vec8_kernel(float* __restrict__ dst, const S* __restrict__ src,
+                                                             int64_t n8, float alpha, int unit_alpha) {
+  const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (q >= n8) return;
+  float a[8], d[8];
+  Vec8<S>::load(src + 8 * q, a);
+  Vec8<float>::load(dst + 8 * q, d);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) d[e] = unit_alpha ? d[e] + a[e] : fmaf(alpha, a[e], d[e]);
+  Vec8<float>::store(dst + 8 * q, d);
+}
+
+inline unsigned vec_grid(int64_t n8) { return (unsigned)std::max<int64_t>(1, lz_cdiv(n8, kThreads)); }
+
 // dst(f32) += alpha * src
 template <typename S>
 __global__ void axpy_f32_kernel(float* __restrict__ dst, const S* __restrict__ src, int64_t n, float alpha, int unit_alpha) {
@@ -341,7 +402,29 @@ __global__ void __launch_bounds__(kThreads) mt_gather_args_kernel(const SegArgs 
       const int64_t numel = t.numel[s], off = t.off[s];
       if (off >= c1) break;
       const int64_t lo = max(c0, off), hi = min(c1, off + numel);
-      for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+      int64_t i0 = lo;
+      // 8 elements per thread where source and destination are 16-byte aligned
+      // at the same element
+      if (ptr && ((lo - off) & 7) == 0 && ((lo - dst_base) & 7) == 0 &&
+          ((reinterpret_cast<uintptr_t>(ptr) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
+        const int64_t nv = (hi - lo) >> 3;
+        for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
+          float r[8];
+          Vec8<S>::load(ptr + (lo - off) + 8 * v, r);
+          if (mode == 1) {
+            float d[8];
+            float* dp = reinterpret_cast<float*>(dst) + (lo - dst_base) + 8 * v;
+            Vec8<float>::load(dp, d);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d[e] += r[e];
+            Vec8<float>::store(dp, d);
+          } else {
+            Vec8<D>::store(dst + (lo - dst_base) + 8 * v, r);
+          }
+        }
+        i0 = lo + 8 * nv;
+      }
+      for (int64_t i = i0 + threadIdx.x; i < hi; i += blockDim.x) {
         const float val = ptr ? Elem<S>::load(ptr, i - off) : 0.0f;
         if (mode == 1) reinterpret_cast<float*>(dst)[i - dst_base] += val;
         else Elem<D>::store(dst, i - dst_base, val);
@@ -500,6 +583,20 @@ LZ_EXPORT int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, 
   LZ_REQUIRE(n >= 0, "lz_cast: negative n");
   if (n == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
+  if ((src_dtype == LZ_F32 || src_dtype == LZ_BF16) && (dst_dtype == LZ_F32 || dst_dtype == LZ_BF16) &&
+      lz_aligned16(src) && lz_aligned16(dst) && n >= 8) {
+    const int64_t n8 = n / 8, done = 8 * n8;
+    const unsigned g8 = vec_grid(n8);
+    if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) cast_vec8_kernel<float, uint16_t><<<g8, kThreads, 0, s>>>((const float*)src, (uint16_t*)dst, n8);
+    else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) cast_vec8_kernel<uint16_t, float><<<g8, kThreads, 0, s>>>((const uint16_t*)src, (float*)dst, n8);
+    else if (src_dtype == LZ_F32) cast_vec8_kernel<float, float><<<g8, kThreads, 0, s>>>((const float*)src, (float*)dst, n8);
+    else cast_vec8_kernel<uint16_t, uint16_t><<<g8, kThreads, 0, s>>>((const uint16_t*)src, (uint16_t*)dst, n8);
+    int rc = lz_check_launch("lz_cast");
+    if (rc || done == n) return rc;
+    const size_t ss = src_dtype == LZ_F32 ? 4 : 2, ds = dst_dtype == LZ_F32 ? 4 : 2;
+    return lz_cast(static_cast<const char*>(src) + done * ss, src_dtype, static_cast<char*>(dst) + done * ds, dst_dtype,
+                   n - done, stream);
+  }
   const int g = stream_grid(n);
   if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) cast_kernel<float, uint16_t><<<g, kThreads, 0, s>>>((const float*)src, (uint16_t*)dst, n);
   else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) cast_kernel<uint16_t, float><<<g, kThreads, 0, s>>>((const uint16_t*)src, (float*)dst, n);
@@ -514,6 +611,15 @@ LZ_EXPORT int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n,
   if (n == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   const int unit = alpha == 1.0f;
+  if ((src_dtype == LZ_BF16 || src_dtype == LZ_F32) && lz_aligned16(dst) && lz_aligned16(src) && n >= 8) {
+    const int64_t n8 = n / 8, done = 8 * n8;
+    if (src_dtype == LZ_BF16) axpy_vec8_kernel<uint16_t><<<vec_grid(n8), kThreads, 0, s>>>(dst, (const uint16_t*)src, n8, alpha, unit);
+    else axpy_vec8_kernel<float><<<vec_grid(n8), kThreads, 0, s>>>(dst, (const float*)src, n8, alpha, unit);
+    int rc = lz_check_launch("lz_axpy_f32");
+    if (rc || done == n) return rc;
+    return lz_axpy_f32(dst + done, static_cast<const char*>(src) + done * (src_dtype == LZ_F32 ? 4 : 2), src_dtype,
+                       n - done, alpha, stream);
+  }
   if (src_dtype == LZ_BF16) axpy_f32_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>(dst, (const uint16_t*)src, n, alpha, unit);
   else if (src_dtype == LZ_F32) axpy_f32_kernel<float><<<stream_grid(n), kThreads, 0, s>>>(dst, (const float*)src, n, alpha, unit);
   else return lz_set_error(LZ_EINVAL, "lz_axpy_f32: bad dtype %d", src_dtype);

@@ -117,6 +117,9 @@ class _Stage3ParamHandle:
         self.exp_avg: Optional[torch.Tensor] = None
         self.exp_avg_sq: Optional[torch.Tensor] = None
         self.grad_shard: Optional[torch.Tensor] = None
+        # the shard holds no gradient of this step yet: the first accumulation
+        # writes instead of adding (the engine's zero_grad fill is deferred)
+        self.grad_fresh = False
 
     @property
     def world_size(self) -> int:
@@ -147,6 +150,7 @@ class _Stage3ParamHandle:
 
     def reset_grad(self) -> None:
         ops.fill_(self.grad_shard, 0.0)
+        self.grad_fresh = False
 
     def accumulate_grad_shard(self, param_grads: Sequence[Optional[torch.Tensor]]) -> float:
         """Flatten the gradients (zeros for None) bucket by bucket, reduce-scatter
@@ -171,7 +175,11 @@ class _Stage3ParamHandle:
                 if reduced.numel() < b1 - b0:
                     raise ValueError(f"reduce_scatter returned too few elements: {reduced.numel()} < {b1 - b0}")
             comm_ms += (time.perf_counter() - t0) * 1000.0
-            ops.axpy_f32_(self.grad_shard[b0:b1], reduced[: b1 - b0], 1.0 / self.world_size)
+            if self.grad_fresh and self.world_size == 1:
+                ops.cast(reduced[: b1 - b0], torch.float32, out=self.grad_shard[b0:b1])
+            else:
+                ops.axpy_f32_(self.grad_shard[b0:b1], reduced[: b1 - b0], 1.0 / self.world_size)
+        self.grad_fresh = False
         return comm_ms
 
 
@@ -494,13 +502,18 @@ class ZeROStage3Optimizer:
 
     def zero_grad(self) -> None:
         self._reset_comm_stats()
-        ops.fill_(self._grad_all, 0.0)
+        # zeroing is deferred: each handle's first gradient of the step is
+        # written over its shard, and shards that receive none are zeroed
+        # before the norm (_finish_grads)
+        for h in self._handle_order:
+            h.grad_fresh = True
         for p in self.model.parameters():
             p.grad = None
         self._reshard_all_params()
 
     def step_with_stats(self, max_grad_norm: float = 0.0) -> Dict[str, float]:
         t0 = time.perf_counter()
+        self._finish_grads()
         self._fused.grad_norm_and_scale([self._grad_all], max_grad_norm)
         self.step_count += 1
         t_opt0 = time.perf_counter()
@@ -525,6 +538,11 @@ class ZeROStage3Optimizer:
             "optim_ms": optim_ms,
             "total_ms": (time.perf_counter() - t0) * 1000.0,
         }
+
+    def _finish_grads(self) -> None:
+        for h in self._handle_order:
+            if h.grad_fresh:
+                h.reset_grad()
 
     def step(self, max_grad_norm: float = 0.0) -> float:
         return float(self.step_with_stats(max_grad_norm=max_grad_norm)["grad_norm"])

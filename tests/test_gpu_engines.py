@@ -149,6 +149,8 @@ def test_stage3_recompute_off_matches_recompute_on():
             e.backward(loss)
         e._last_loss = float(loss)
     assert ea._last_loss == eb._last_loss
+    ea._finish_grads()
+    eb._finish_grads()
     ga, gb = ea._grad_all.double(), eb._grad_all.double()
     assert float((ga - gb).norm() / ga.norm()) < 1e-5
     ea.step(max_grad_norm=0.5)
