@@ -115,6 +115,53 @@ def run_no_recompute(args, B, S, dev, batches, tokens, model_flops):
     return res
 
 
+def fit_sweep(dev: torch.device, max_batch: int, seq: int = 2048, steps: int = 2, warmup: int = 1):
+    """The 7B workload (d4096, 32 layers, 32 q / 8 kv heads, ffn 11008, vocab
+    32000, tied) through the ZeRO-3 engine at world size 1, micro-batch 1, 2,
+    4, ... until the device runs out of memory (or max_batch): tokens/s and
+    peak HBM per size.  Parameters are created on the device."""
+    from model import LlamaForCausalLM, build_config
+    from profiler import estimate_transformer_train_flops
+    from zero import ZeROStage3Optimizer
+
+    cfg = build_config("7b", vocab_size=32000, max_seq_len=seq)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    engine = ZeROStage3Optimizer(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    n_params = sum(h.meta.total_numel for h in engine._handle_order)
+    total = torch.cuda.get_device_properties(dev).total_memory
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rows = []
+    b = 1
+    while b <= max_batch:
+        log(f"7B fit sweep: micro-batch {b}")
+        try:
+            torch.cuda.reset_peak_memory_stats(dev)
+            batches = [torch.randint(0, cfg.vocab_size, (b, seq), device=dev, generator=gen)]
+            el, losses = run_steps(model, engine, batches, steps=steps, warmup=warmup)
+            peak = torch.cuda.max_memory_allocated(dev)
+            flops = estimate_transformer_train_flops(cfg, b, seq, stage=0)
+            rows.append({"micro_batch": b, "tokens_per_s": b * seq * steps / el, "ms_per_step": el * 1000 / steps,
+                         "mfma_util": flops * steps / el / 1e12 / PEAK_BF16_TFLOPS,
+                         "peak_hbm_gib": peak / 2**30, "loss": losses[-1]})
+            log(f"  {rows[-1]['ms_per_step']:.0f} ms/step, {rows[-1]['tokens_per_s']:,.0f} tok/s, "
+                f"peak {rows[-1]['peak_hbm_gib']:.1f} GiB")
+        except torch.cuda.OutOfMemoryError:
+            rows.append({"micro_batch": b, "oom": True})
+            log("  out of memory")
+            break
+        finally:
+            batches = None
+            engine.zero_grad()
+            torch.cuda.empty_cache()
+        b *= 2
+    return {"metric": "7B ZeRO-3 fit-to-memory sweep (world size 1, S=2048, bf16 + fp32 master)",
+            "params": n_params, "device_memory_gib": total / 2**30, "sweep": rows}
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_dma_kernel_nt_1b_zero3_traffic.md")
 
 
@@ -227,6 +274,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-125m", action="store_true")
+    ap.add_argument("--fit-sweep", action="store_true",
+                    help="7B ZeRO-3 fit-to-memory sweep: micro-batch 1, 2, 4, ... (S=2048) until the device is "
+                         "out of memory or --fit-max-batch; prints one JSON line and exits")
+    ap.add_argument("--fit-max-batch", type=int, default=64)
     ap.add_argument("--headline-only", action="store_true",
                     help="only the 1B ZeRO-3 step (no recompute=False, 125M, AdamW or pointwise legs)")
     args = ap.parse_args()
@@ -245,6 +296,9 @@ def main() -> int:
     lzhip.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.fit_sweep:
+        print(json.dumps(fit_sweep(dev, args.fit_max_batch)), flush=True)
+        return 0
     B, S = 8, 2048
     log("building 1B model + ZeRO-3 engine")
     cfg, model, engine = make_engine("1b", 3, B, S, dev)
