@@ -308,6 +308,14 @@ __global__ void scale_kernel(T* __restrict__ x, int64_t n, float alpha) {
     Elem<T>::store(x, i, Elem<T>::load(x, i) * alpha);
 }
 
+// x *= *scale (a device scalar, e.g. an upstream loss gradient).
+template <typename T>
+__global__ void scale_dev_kernel(T* __restrict__ x, int64_t n, const float* __restrict__ scale) {
+  const float a = *scale;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(x, i, Elem<T>::load(x, i) * a);
+}
+
 // ---------------------------------------------------------------------------
 // Multi-tensor gather/scatter.  `table` is a device int64 array of nseg
 // records {ptr, numel, flat_offset}, sorted by flat_offset.  A record with a
@@ -624,6 +632,16 @@ LZ_EXPORT int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n,
   else if (src_dtype == LZ_F32) axpy_f32_kernel<float><<<stream_grid(n), kThreads, 0, s>>>(dst, (const float*)src, n, alpha, unit);
   else return lz_set_error(LZ_EINVAL, "lz_axpy_f32: bad dtype %d", src_dtype);
   return lz_check_launch("lz_axpy_f32");
+}
+
+LZ_EXPORT int lz_scale_dev(void* x, int dtype, int64_t n, const float* scale, void* stream) {
+  LZ_REQUIRE(n >= 0 && scale, "lz_scale_dev: bad arguments");
+  if (n == 0) return LZ_OK;
+  hipStream_t s = lz_stream(stream);
+  if (dtype == LZ_BF16) scale_dev_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, scale);
+  else if (dtype == LZ_F32) scale_dev_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)x, n, scale);
+  else return lz_set_error(LZ_EINVAL, "lz_scale_dev: bad dtype %d", dtype);
+  return lz_check_launch("lz_scale_dev");
 }
 
 LZ_EXPORT int lz_add_inplace(void* dst, const void* src, int dtype, int64_t n, void* stream) {

@@ -41,6 +41,7 @@ SIGNATURES = {
     "lz_axpy_f32": (_i32, [_vp, _vp, _i32, _i64, _f32, _vp]),
     "lz_add_inplace": (_i32, [_vp, _vp, _i32, _i64, _vp]),
     "lz_scale_inplace": (_i32, [_vp, _i32, _i64, _f32, _vp]),
+    "lz_scale_dev": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "lz_fill": (_i32, [_vp, _i32, _i64, _f64, _vp]),
     "lz_cast": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp]),
     "lz_rmsnorm_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _f32, _vp]),

@@ -334,3 +334,76 @@ class CrossEntropyFn(Function):
 
 def cross_entropy(logits: torch.Tensor, labels: torch.Tensor, clamp: bool, inplace: bool = False) -> torch.Tensor:
     return CrossEntropyFn.apply(logits, labels, clamp, inplace)
+
+
+class LMHeadCEFn(Function):
+    """Fused LM head + shifted cross entropy: the tied lm_head product
+    (model/llama.py:178) and the loss of model/llama.py:273-302 without ever
+    holding the [B*S, V] logits.  Logits are formed for whole sequences, as
+    many as fit in `chunk_bytes`, in one reused buffer.  When gradients are
+    wanted, each chunk's logit gradient (softmax - onehot) / count for a unit
+    loss gradient is written over the chunk right after its loss and
+    contracted at once into dx (bf16) and an fp32 dW accumulator, so the
+    logits are read from HBM once more instead of being stored.  Backward
+    scales both by the incoming loss gradient (a device scalar)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, labels, clamp: bool, chunk_bytes: int, grad_wanted: bool):
+        B, S, d = x.shape
+        V = weight.shape[0]
+        T = B * S
+        dev = x.device
+        x2 = _rows(x)
+        lab = labels.contiguous()
+        lab_flat = lab.view(-1)
+        # gradients only when the caller records them (a no-grad forward, such
+        # as ZeRO-3's first pass, skips the backward products)
+        need_x = grad_wanted and ctx.needs_input_grad[0]
+        need_w = grad_wanted and ctx.needs_input_grad[1]
+        seqs = max(1, chunk_bytes // (max(S, 1) * V * x.element_size()))
+        rows_per = min(T, seqs * max(S, 1))
+        buf = torch.empty((rows_per, V), dtype=x.dtype, device=dev)
+        lse = torch.empty((T,), dtype=torch.float32, device=dev)
+        row_loss = torch.empty((T,), dtype=torch.float32, device=dev)
+        # the number of scored positions (the gradient's divisor) before any chunk
+        _, count = ops.ce_reduce(ops.zeros((T,), torch.float32, dev), lab, T, S, V, clamp)
+        dx = dw32 = unit = None
+        if need_x or need_w:
+            unit = ops.fill_(torch.empty((1,), dtype=torch.float32, device=dev), 1.0)
+            if need_x:
+                dx = torch.empty((T, d), dtype=x.dtype, device=dev)
+            if need_w:
+                dw32 = ops.zeros((V, d), torch.float32, dev)
+        for r0 in range(0, T, rows_per):
+            r1 = min(T, r0 + rows_per)
+            lg = buf[: r1 - r0]
+            ops.gemm(x2[r0:r1], weight, out=lg)
+            ops.ce_fwd(lg, lab_flat[r0:r1], S, lse=lse[r0:r1], row_loss=row_loss[r0:r1])
+            if unit is not None:
+                ops.ce_bwd(lg, lab_flat[r0:r1], S, lse[r0:r1], unit, count, out=lg)
+                if need_x:
+                    ops.gemm(lg, weight, b_kmajor=False, out=dx[r0:r1])
+                if need_w:
+                    ops.gemm(lg, x2[r0:r1], a_kmajor=False, b_kmajor=False, out=dw32, beta=1.0)
+        loss, _ = ops.ce_reduce(row_loss, lab, T, S, V, clamp)
+        ctx.save_for_backward(dx, dw32)
+        ctx.x_shape, ctx.w_dtype = x.shape, weight.dtype
+        return loss
+
+    @staticmethod
+    def backward(ctx, gloss):
+        dx, dw32 = ctx.saved_tensors
+        g = gloss.reshape(1).to(torch.float32).contiguous()
+        gx = gw = None
+        if dx is not None and ctx.needs_input_grad[0]:
+            ops.scale_dev_(dx, g)
+            gx = dx.view(ctx.x_shape)
+        if dw32 is not None and ctx.needs_input_grad[1]:
+            ops.scale_dev_(dw32, g)
+            gw = ops.cast(dw32, ctx.w_dtype)
+        return gx, gw, None, None, None, None
+
+
+def lm_head_cross_entropy(x: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, clamp: bool,
+                          chunk_bytes: int = 1 << 30) -> torch.Tensor:
+    return LMHeadCEFn.apply(x, weight, labels, clamp, chunk_bytes, torch.is_grad_enabled())

@@ -166,6 +166,16 @@ def scale_(x: torch.Tensor, alpha: float) -> None:
     _lib.call("lz_scale_inplace", x.data_ptr(), dtype_code(x), x.numel(), float(alpha), stream_ptr(x.device))
 
 
+def scale_dev_(x: torch.Tensor, scale: torch.Tensor) -> None:
+    """x *= scale[0] with `scale` a one-element fp32 device tensor."""
+    require_gpu(x, scale)
+    if not x.is_contiguous():
+        raise ValueError("scale_dev_ needs a contiguous tensor")
+    if scale.dtype != torch.float32 or scale.numel() != 1:
+        raise ValueError("scale must be one fp32 element")
+    _lib.call("lz_scale_dev", x.data_ptr(), dtype_code(x), x.numel(), scale.data_ptr(), stream_ptr(x.device))
+
+
 class SegmentTable:
     """Device table of {ptr, numel, flat_offset} records for the multi-tensor
     gather/scatter kernels.  Built on the host, uploaded once per call site."""
@@ -540,12 +550,18 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
     return out
 
 
-def ce_fwd(logits2: torch.Tensor, labels: torch.Tensor, seq: int, ignore_index: int = -100
+def ce_fwd(logits2: torch.Tensor, labels: torch.Tensor, seq: int, ignore_index: int = -100,
+           lse: Optional[torch.Tensor] = None, row_loss: Optional[torch.Tensor] = None
            ) -> Tuple[torch.Tensor, torch.Tensor]:
-    require_gpu(logits2, labels)
+    require_gpu(logits2, labels, lse, row_loss)
     rows, vocab = logits2.shape
-    lse = torch.empty((rows,), dtype=torch.float32, device=logits2.device)
-    row_loss = torch.empty((rows,), dtype=torch.float32, device=logits2.device)
+    if lse is None:
+        lse = torch.empty((rows,), dtype=torch.float32, device=logits2.device)
+    if row_loss is None:
+        row_loss = torch.empty((rows,), dtype=torch.float32, device=logits2.device)
+    for t in (lse, row_loss):
+        if t.dtype != torch.float32 or t.numel() != rows or not t.is_contiguous():
+            raise ValueError("lse / row_loss must be contiguous fp32 with one element per row")
     _lib.call("lz_ce_fwd", logits2.data_ptr(), _row_stride(logits2), rows, vocab, dtype_code(logits2),
               labels.data_ptr(), seq, ignore_index, lse.data_ptr(), row_loss.data_ptr(), stream_ptr(logits2.device))
     return lse, row_loss

@@ -41,6 +41,21 @@ class HipLinear(nn.Linear):
         return LF.linear(x, self.weight, residual)
 
 
+class HipLMHead(HipLinear):
+    """The LM head (nn.Linear, tied to the embedding).  Called with labels it
+    returns the shifted cross-entropy loss instead of the logits, through the
+    fused LM-head + loss Function, which never holds the [B*S, V] logits."""
+
+    fused_chunk_bytes = 1 << 30  # logits buffer of the fused loss
+
+    def forward(self, x: torch.Tensor, labels: Optional[torch.Tensor] = None, clamp: bool = False) -> torch.Tensor:
+        if labels is None:
+            return super().forward(x)
+        if self.bias is not None:
+            raise NotImplementedError("the fused LM-head loss has no bias path")
+        return LF.lm_head_cross_entropy(x, self.weight, labels, clamp, self.fused_chunk_bytes)
+
+
 class HipEmbedding(nn.Embedding):
     """nn.Embedding (same parameters and initialisation) with the HIP gather."""
 
@@ -202,7 +217,7 @@ class LlamaForCausalLM(nn.Module):
         self.dropout = nn.Dropout(cfg.dropout)
         self.layers = nn.ModuleList([TransformerBlock(cfg) for _ in range(cfg.n_layers)])
         self.norm = RMSNorm(cfg.dim, eps=cfg.rms_norm_eps)
-        self.lm_head = HipLinear(cfg.dim, cfg.vocab_size, bias=False)
+        self.lm_head = HipLMHead(cfg.dim, cfg.vocab_size, bias=False)
 
         if cfg.tie_word_embeddings:
             self.lm_head.weight = self.tok_embeddings.weight
@@ -211,6 +226,8 @@ class LlamaForCausalLM(nn.Module):
         self._zero3_executor = None
         self.loss_chunk_size = 0
         self.activation_checkpointing = False
+        # training loss without returned logits: LM head and cross entropy fused
+        self.fused_lm_head_loss = True
 
     def _init_weights(self, module: nn.Module) -> None:
         if isinstance(module, (nn.Linear, nn.Embedding)):
@@ -252,6 +269,16 @@ class LlamaForCausalLM(nn.Module):
         x = self._call_parametrized_module("norm", self.norm, x)
         logits = None
         chunked = self._should_chunk_training_loss(input_ids)
+        if labels is not None and not return_logits and self.fused_lm_head_loss:
+            if labels.shape != input_ids.shape:
+                raise ValueError(
+                    f"labels should have same shape as input_ids; got {tuple(labels.shape)} vs {tuple(input_ids.shape)}"
+                )
+            # same divisor rule as the unfused paths: the chunked loss (and a
+            # length-1 sequence) clamps the target count at 1
+            clamp = chunked or input_ids.size(1) <= 1
+            loss = self._call_parametrized_module("lm_head", self.lm_head, x, labels, clamp)
+            return CausalLMOutput(logits=None, loss=loss)
         if labels is None or return_logits or not chunked:
             logits = self._call_parametrized_module("lm_head", self.lm_head, x)
 

@@ -92,6 +92,10 @@ int lz_add_inplace(void* dst, const void* src, int dtype, int64_t n, void* strea
 
 /* x *= alpha in the storage dtype (grad averaging / clipping in place). */
 int lz_scale_inplace(void* x, int dtype, int64_t n, float alpha, void* stream);
+/* x *= *scale with `scale` a device float: applies an upstream gradient that
+ * is only known on the device (the fused LM-head + cross-entropy gradients,
+ * computed in the forward for a unit loss gradient). */
+int lz_scale_dev(void* x, int dtype, int64_t n, const float* scale, void* stream);
 
 /* Fill / cast.  Replace torch.zeros(...) for gradient buffers
  * (zero/stage2_optimizer.py:88-89) and dtype casts (.to()).  lz_fill also

@@ -68,6 +68,43 @@ def test_forward_backward_vs_oracle(dim, H, KV, L, V, B, S, chunk):
     _compare(model, P, _ocfg(cfg), ids, chunk)
 
 
+@pytest.mark.parametrize("chunk", [0, 128])
+def test_fused_lm_head_loss_matches_unfused(chunk):
+    """The fused LM-head + loss (logits formed one sequence at a time here, so
+    several chunks) against the unfused LM head + cross entropy, with ignored
+    targets in the labels: same loss, same gradients up to the fp32
+    summation order of the chunked dW."""
+    cfg = ModelConfig(name="t", vocab_size=1000, dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=688,
+                      max_seq_len=128)
+    torch.manual_seed(3)
+    ma = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+    mb = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+    mb.load_state_dict(ma.state_dict())
+    for m in (ma, mb):
+        m.set_loss_chunk_size(chunk)
+    ma.fused_lm_head_loss = True
+    ma.lm_head.fused_chunk_bytes = 128 * 1000 * 2  # one sequence of logits per chunk
+    mb.fused_lm_head_loss = False
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, 1000, (3, 128), generator=g)
+    labels = ids.clone()
+    labels[0, 10:20] = -100
+    labels[2, 100:] = -100
+    out_a = ma(input_ids=ids.to(DEV), labels=labels.to(DEV), return_logits=False)
+    out_b = mb(input_ids=ids.to(DEV), labels=labels.to(DEV), return_logits=False)
+    assert out_a.logits is None
+    (0.5 * out_a.loss).backward()
+    (0.5 * out_b.loss).backward()
+    la, lb = float(out_a.loss), float(out_b.loss)
+    assert abs(la - lb) <= 1e-6 * abs(lb), (la, lb)
+    with torch.no_grad():  # the no-grad pass forms no gradients and gives the same loss
+        assert float(ma(input_ids=ids.to(DEV), labels=labels.to(DEV), return_logits=False).loss) == la
+    for (n, pa), (_, pb) in zip(ma.named_parameters(), mb.named_parameters()):
+        ga, gb = pa.grad.double().view(-1), pb.grad.double().view(-1)
+        assert float(F.cosine_similarity(ga, gb, dim=0)) >= 0.9999, n
+        assert float((ga - gb).norm() / gb.norm()) <= 1e-2, n
+
+
 def test_reference_golden_config_in_bf16():
     """The reference's golden case (seed 123, chunk 4) through the HIP path in
     bf16: within 1e-2 of 4.901787757873535."""
