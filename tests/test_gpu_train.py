@@ -30,6 +30,11 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
 ROOT = Path(__file__).resolve().parents[1]
 PKG = ROOT / "cs244c-llama-zero_amd"
+# state_dict keys of the reference model (model/llama.py:169-192), plumbing size
+MODEL_KEYS_PLUMBING = {"tok_embeddings.weight", "norm.weight", "lm_head.weight"} | {
+    f"layers.{i}.{n}" for i in range(4) for n in (
+        "input_norm.weight", "attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight", "attn.o_proj.weight",
+        "post_attn_norm.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")}
 STEP_RE = re.compile(r"\[step\s+(\d+)\]\s+loss=([0-9.]+).*tokens/s=([0-9,]+)")
 
 
@@ -162,7 +167,14 @@ def test_train_py_cli(tmp_path):
                 "--seed", "0", "--log-interval", "1", "--save-dir", str(tmp_path)])
     lines = [m for m in STEP_RE.finditer(out)]
     assert len(lines) == 3, out
-    assert (tmp_path / "step_000003.pt").exists()
+    ckpt = tmp_path / "step_000003.pt"
+    assert ckpt.exists()
+    # checkpoint payload of train.py:163-181
+    payload = torch.load(ckpt, map_location="cpu", weights_only=True)
+    assert set(payload) == {"step", "model_state_dict", "optimizer_state_dict", "train_args", "extra"}
+    assert payload["step"] == 3
+    assert set(payload["model_state_dict"]) == MODEL_KEYS_PLUMBING
+    assert set(payload["optimizer_state_dict"]) == {"state", "param_groups"}
 
 
 @pytest.mark.parametrize("stage", [1, 3])
@@ -171,12 +183,29 @@ def test_train_zero_cli(stage, tmp_path):
     out = _run(["train_zero.py", "--zero-stage", str(stage), "--model-size", "plumbing", "--dtype", "bfloat16",
                 "--data-mode", "synthetic-uniform", "--synthetic-vocab-size", "32000", "--seq-len", "128",
                 "--batch-size", "4", "--max-steps", "3", "--log-interval", "1", "--max-grad-norm", "1.0",
-                "--checkpoint-interval", "0", "--profile-json", str(prof), "--profile-collectives",
-                "--measure-memory-step", "--memory-warmup-steps", "1"])
+                "--checkpoint-interval", "3", "--save-dir", str(tmp_path), "--profile-json", str(prof),
+                "--profile-collectives", "--measure-memory-step", "--memory-warmup-steps", "1"])
     assert len(STEP_RE.findall(out)) == 3, out
     assert "fb_ms=" in out and "tflops=" in out
     import json
 
+    # profile JSON schema of train_zero.py:727-757
     payload = json.loads(prof.read_text())
+    assert set(payload) == {
+        "rank", "world_size", "stage", "collective_impl", "args", "model_config", "optimizer_config",
+        "global_batch_size", "microbatch_size_per_gpu", "overlap_enabled", "timers", "memory", "flops", "steps",
+        "collective_trace_summary", "state_memory_breakdown_mb", "overlap_summary", "measured_step_memory",
+        "measured_step_state_timeline"}
+    assert set(payload["optimizer_config"]) == {"lr", "betas", "eps", "weight_decay", "max_grad_norm"}
+    assert set(payload["flops"]) == {"measurements", "profiled_step_flops", "tflops_mode"}
     assert payload["stage"] == stage and len(payload["steps"]) == 3
     assert payload["measured_step_memory"]["peak_allocated_mb"] > 0
+    # checkpoint payload of train_zero.py:232-255 (full parameters summoned)
+    ckpt = tmp_path / f"zero_stage{stage}_step000003_rank000.pt"
+    assert ckpt.exists(), sorted(p.name for p in tmp_path.iterdir())
+    state = torch.load(ckpt, map_location="cpu", weights_only=True)
+    assert set(state) == {"step", "rank", "model_state_dict", "engine_state_dict", "train_args", "extra"}
+    assert state["step"] == 3 and state["rank"] == 0
+    assert set(state["model_state_dict"]) == MODEL_KEYS_PLUMBING
+    assert all(t.numel() > 0 for t in state["model_state_dict"].values())
+    assert state["engine_state_dict"]["step_count"] == 3
