@@ -9,7 +9,9 @@ forward + loss, backward (with ZeRO-3's recomputation and 25M-element
 gradient buckets), step_with_stats (norm + fused AdamW).
 
 Also reported: MFMA utilisation of that step (model FLOPs, 3x forward, over
-2.5 PFLOP/s), the 125M-class ZeRO-1 step (B=16, S=1024), fused AdamW HBM
+2.5 PFLOP/s), the same step with the engine's recompute=False, the
+CPU-runnable train.py workload on the HIP path beside the CPU oracle's loop,
+the 125M-class ZeRO-1 step (B=16, S=1024), fused AdamW HBM
 bandwidth on a 124M-element flat fp32 buffer, the other HBM-bound kernels at
 the step's shapes, the dominant GEMM kernel's roofline measured with HIP
 events inside the timed steps (every GEMM kernel's share is listed too), and
@@ -176,6 +178,63 @@ def measured_traffic(kernel: str):
     except OSError:
         pass
     return None
+
+
+def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: int = 3):
+    """The CPU-runnable train.py workload (d256, 4 layers, 8/4 heads, ffn 688,
+    vocab 32000, B=4, S=128, grad accumulation 2, AdamW lr 3e-4, clip 1.0,
+    uniform ids from torch.Generator seed 0) for `steps` steps on the HIP path
+    (bf16), and the CPU oracle's train.py loop (fp32, every host thread) on
+    `cpu_steps` steps of the same stream."""
+    from lzhip.optim import FusedAdamW
+    from model import LlamaForCausalLM, build_config
+
+    B, S, GA = 4, 128, 2
+    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg)
+    P = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
+    model = model.to(device=dev, dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    gen = torch.Generator().manual_seed(0)
+    chunks = [torch.randint(0, 32000, (B, S + 1), generator=gen) for _ in range(GA * (steps + 5))]
+    ids_all = [c[:, :-1].contiguous().to(dev) for c in chunks]
+
+    def one(step):
+        opt.zero_grad(set_to_none=True)
+        loss = None
+        for a in range(GA):
+            ids = ids_all[GA * step + a]
+            loss = model(input_ids=ids, labels=ids, return_logits=False).loss
+            (loss / GA).backward()
+        opt.clip_grad_norm_(1.0)
+        opt.step()
+        return loss
+
+    for i in range(5):
+        one(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        loss = one(5 + i)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    res = {"workload": "train.py plumbing (d256 L4 8/4 heads ffn688 V32000), B=4 S=128 GA=2, 100 steps",
+           "hip_tokens_per_s": B * S * GA * steps / el, "hip_ms_per_step": el * 1000 / steps,
+           "hip_final_loss": float(loss)}
+    if cpu:
+        from oracle import engine as OE
+        from oracle import model as OM
+
+        ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
+                      n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta)
+        out = OE.train_reference(ocfg, P, iter(chunks), steps=cpu_steps, grad_accum_steps=GA, lr=3e-4,
+                                 betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1.0, loss_chunk_size=128)
+        sec = sum(out["seconds"])
+        res.update({"cpu_oracle_tokens_per_s": B * S * GA * cpu_steps / sec, "cpu_cores": torch.get_num_threads(),
+                    "cpu_sample": f"{cpu_steps} steps of the same stream in fp32 ({sec:.1f} s)"})
+    return res
 
 
 def _time_ms(fn, iters: int = 20) -> float:
@@ -352,7 +411,10 @@ def main() -> int:
                     "workload": "125m ZeRO-1 (d768 L12 12q/4kv ffn2048 V32000), B=16 S=1024"}
         del m2, e2
         torch.cuda.empty_cache()
+    plumbing = None
     if not args.headline_only:
+        log("plumbing workload (train.py config)")
+        plumbing = bench_plumbing(dev, cpu=not args.no_cpu_baseline)
         log("AdamW 124M")
         adamw = bench_adamw(dev)
         log("pointwise kernels")
@@ -389,6 +451,7 @@ def main() -> int:
         "peak_hbm_gib": peak_mem,
         "loss_first_last": [losses[0], losses[-1]],
         "llama_1b_zero3_recompute_off": res_norecompute,
+        "plumbing_train_py": plumbing,
         "llama_125m_zero1": res_125m,
         "adamw_124m": adamw,
         "pointwise": pointwise,
