@@ -237,6 +237,49 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
     return res
 
 
+def cpu_ops_baseline(rows: int = 16384, dim: int = 2048, ffn: int = 5632, heads: int = 16, n_adam: int = 124_000_000):
+    """The CPU oracle's op restatements at the op-level shapes (fp32 on the
+    host, every thread), forward + backward through autograd, and its AdamW
+    over 124M elements: milliseconds per call."""
+    from oracle import ops as O
+
+    def t(fn, reps=2):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) * 1000.0 / reps
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(rows, dim, generator=g).requires_grad_(True)
+    w = (1 + 0.02 * torch.randn(dim, generator=g)).requires_grad_(True)
+    dy = torch.randn(rows, dim, generator=g)
+    out = {"cores": torch.get_num_threads()}
+    out["rmsnorm fwd+bwd ms"] = t(lambda: O.rmsnorm(x, w, 1e-5).backward(dy))
+    hd = dim // heads
+    cos, sin = O.rope_tables(2048, hd, 10000.0)
+    xr = torch.randn(rows // 2048, heads, 2048, hd, generator=g).requires_grad_(True)
+    dr = torch.randn(xr.shape, generator=g)
+    out["rope fwd+bwd ms"] = t(lambda: O.apply_rope(xr, cos, sin).backward(dr))
+    gg = torch.randn(rows, ffn, generator=g).requires_grad_(True)
+    uu = torch.randn(rows, ffn, generator=g).requires_grad_(True)
+    dh = torch.randn(rows, ffn, generator=g)
+    out["swiglu fwd+bwd ms"] = t(lambda: O.swiglu(gg, uu).backward(dh))
+    del x, dy, xr, dr, gg, uu, dh
+    p = 0.02 * torch.randn(n_adam, generator=g)
+    m, v = torch.zeros(n_adam), torch.zeros(n_adam)
+    gr = 1e-3 * torch.randn(n_adam, generator=g)
+    st = [0]
+
+    def adam():
+        st[0] += 1
+        O.adamw_update(p, m, v, gr, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=st[0])
+
+    out["adamw 124M ms"] = t(adam, reps=1)
+    out["sample"] = "[16384, 2048] RMSNorm, [8, 16, 2048, 128] RoPE, [16384, 5632] SwiGLU in fp32, AdamW over 124M"
+    return out
+
+
 def _time_ms(fn, iters: int = 20) -> float:
     for _ in range(3):
         fn()
@@ -283,6 +326,8 @@ def bench_pointwise(dev: torch.device, rows: int = 16384, dim: int = 2048, ffn: 
     inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32, device=dev) / hd))
     cos, sin = ops.rope_table(2048, hd, inv, bf)
     rec(f"rope fwd [{rows},{heads}x{hd}] in place", _time_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin)), 4 * n)
+    rec(f"rope bwd [{rows},{heads}x{hd}] in place",
+        _time_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin, backward=True)), 4 * n)
     del x, dy
     gu = torch.randn(rows, 2 * ffn, device=dev, generator=g).to(bf)
     gate, up = gu[:, :ffn], gu[:, ffn:]
@@ -420,10 +465,13 @@ def main() -> int:
         log("pointwise kernels")
         pointwise = bench_pointwise(dev)
 
-    cpu = None
+    cpu = cpu_ops = None
     if not args.no_cpu_baseline:
         log("CPU oracle baseline")
         cpu = cpu_baseline(cfg)
+        if not args.headline_only:
+            log("CPU oracle ops")
+            cpu_ops = cpu_ops_baseline()
 
     line = {
         "metric": METRIC,
@@ -472,6 +520,7 @@ def main() -> int:
             "flop_per_launch": top_flops / max(top_n, 1),
         },
         "cpu_baseline": cpu,
+        "cpu_ops_baseline": cpu_ops,
     }
     print(json.dumps(line), flush=True)
     return 0
