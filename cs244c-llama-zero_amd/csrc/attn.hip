@@ -776,31 +776,55 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
-// Issues the tiles of dK/dV step `step` (query head step/nqs, query block
-// step%nqs from qstart) into the stage at `st`: Q, dO, then lse and delta.
+// A [64][HD] tile like dma_tile, loaded by the four waves of group `wg4`
+// (wave index 0..3 within the group), rows past `nvalid` clamped to the last
+// valid row (their results are masked).
 template <int HD>
-__device__ __forceinline__ void dkdv_issue(const AttnArgs& a, int step, int nqs, int qstart, int b, int g, int rep,
-                                           char* st, int wave, int lane) {
+__device__ __forceinline__ void dma_tile_rows(const uint16_t* src, int64_t ld, int nvalid, char* dst, int wg4,
+                                              int lane) {
+  constexpr int kRowsPerLoad = 1024 / (HD * 2), kChunks = HD / 8;
+  constexpr int kPer = 64 / kRowsPerLoad / 4;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int r = (wg4 * kPer + q) * kRowsPerLoad + lane / kChunks;
+    const int c = (lane % kChunks) ^ tswz<HD>(r);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)min(r, nvalid - 1) * ld + c * 8, dst + (wg4 * kPer + q) * 1024,
+                                     16, 0, 0);
+  }
+}
+
+// Issues the tiles of dK/dV step `step` for the 8-wave kernel: Q by waves
+// 0-3, dO by waves 4-7, lse and delta by wave 0.
+template <int HD>
+__device__ __forceinline__ void dkdv8_issue(const AttnArgs& a, int step, int nqs, int qstart, int b, int g, int rep,
+                                            char* st, int wave, int lane) {
   constexpr int kTile = 64 * HD * 2;
   const int S = a.S;
   const int hq = step / nqs, q0 = qstart + (step - hq * nqs) * 64;
   const int h = g * rep + hq;
-  dma_tile<HD>(a.q + ((int64_t)b * S + q0) * a.ldq + (int64_t)h * HD, a.ldq, st, wave, lane);
-  dma_tile<HD>(a.dout + ((int64_t)b * S + q0) * a.lddo + (int64_t)h * HD, a.lddo, st + kTile, wave, lane);
+  if (wave < 4)
+    dma_tile<HD>(a.q + ((int64_t)b * S + q0) * a.ldq + (int64_t)h * HD, a.ldq, st, wave, lane);
+  else
+    dma_tile<HD>(a.dout + ((int64_t)b * S + q0) * a.lddo + (int64_t)h * HD, a.lddo, st + kTile, wave - 4, lane);
   if (wave == 0) {
     const int64_t off = ((int64_t)b * a.H + h) * S + q0;
     dma_rows64(a.lse + off, a.delta + off, st + 2 * kTile, lane);
   }
 }
 
-// dK/dV on tiles: 128 keys per workgroup (32 per wave), 64-query steps over
-// every query head of the kv head's group, from the diagonal on.
+// dK/dV with two waves per SIMD: 256 keys per workgroup of 8 waves (32 keys
+// per wave), K fragments in registers, the workgroup's V tile in LDS (read
+// back as fragments), 64-query steps over every query head of the kv head's
+// group from the diagonal on: S^T = K Q^T and dP^T = V dO^T per 32-query
+// half, P = exp(S*scale - lse), dS = P (dP - delta), then dV += P^T dO and
+// dK += dS^T Q from transposed LDS reads.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_bwd_dkdv_tile_kernel(AttnArgs a) {
-  constexpr int BKV = 128, BQ = 64;
+__global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
+  constexpr int BKV = 256, BQ = 64;
   constexpr int kTile = BQ * HD * 2;
+  constexpr int kVTile = BKV * HD * 2;
   constexpr int kStage = 2 * kTile + 512;  // Q, dO, lse[64], delta[64]
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) char smem[kVTile + 2 * kStage];
 
   const int S = a.S, H = a.H, KV = a.KV, rep = H / KV;
   const int bkv = a.B * KV;
@@ -814,17 +838,25 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_tile_kernel(AttnArgs a) {
   const int k0 = kvb * BKV, kw0 = k0 + 32 * wave;
   const int kvrow = kw0 + l32;
   const float c = a.scale * kLog2e;
+  const char* Vt = smem;
+  char* stages = smem + kVTile;
 
-  bf16x8_t kf[HD / 16], vf[HD / 16];
+  {  // the V tile: 64-row quarters 2*(wave/4) and 2*(wave/4)+1
+    const int quarter0 = 2 * (wave >> 2);
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) {
+      const int r0 = k0 + 64 * (quarter0 + qq);
+      dma_tile_rows<HD>(a.v + ((int64_t)b * S + min(r0, S - 1)) * a.ldv + (int64_t)g * HD, a.ldv, S - min(r0, S - 1),
+                        smem + (quarter0 + qq) * kTile, wave & 3, lane);
+    }
+  }
+  bf16x8_t kf[HD / 16];
   {
     const int64_t r = (int64_t)b * S + min(kvrow, S - 1);
     const uint16_t* kp = a.k + r * a.ldk + (int64_t)g * HD + 8 * half;
-    const uint16_t* vp = a.v + r * a.ldv + (int64_t)g * HD + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < HD / 16; ++kk) {
+    for (int kk = 0; kk < HD / 16; ++kk)
       kf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kp + kk * 16));
-      vf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(vp + kk * 16));
-    }
   }
   f32x16_t dk[HD / 32], dv[HD / 32];
 #pragma unroll
@@ -838,12 +870,13 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_tile_kernel(AttnArgs a) {
   const int qstart = (k0 / BQ) * BQ;
   const int nqs = (S - qstart) / BQ;
   const int nsteps = rep * nqs;
-  dkdv_issue<HD>(a, 0, nqs, qstart, b, g, rep, smem, wave, lane);
+  dkdv8_issue<HD>(a, 0, nqs, qstart, b, g, rep, stages, wave, lane);
   for (int step = 0; step < nsteps; ++step) {
-    __syncthreads();  // this step's tiles landed (every wave's loads), last step's reads retired
-    if (step + 1 < nsteps) dkdv_issue<HD>(a, step + 1, nqs, qstart, b, g, rep, smem + ((step + 1) & 1) * kStage, wave, lane);
+    __syncthreads();  // this step's tiles (and the V tile) landed, last step's reads retired
+    if (step + 1 < nsteps)
+      dkdv8_issue<HD>(a, step + 1, nqs, qstart, b, g, rep, stages + ((step + 1) & 1) * kStage, wave, lane);
     const int hq = step / nqs, q0 = qstart + (step - hq * nqs) * BQ;
-    const char* Qt = smem + (step & 1) * kStage;
+    const char* Qt = stages + (step & 1) * kStage;
     const char* dOt = Qt + kTile;
     const float* lse_s = reinterpret_cast<const float*>(Qt + 2 * kTile);
     const float* D_s = lse_s + BQ;
@@ -859,8 +892,10 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_tile_kernel(AttnArgs a) {
 #pragma unroll
         for (int kk = 0; kk < HD / 16; ++kk) {
           sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Qt, t, kk), kf[kk], sc, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(dOt, t, kk), vf[kk], dp, 0,
-                                                       0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(dOt, t, kk), to.frag(Vt, wave, kk), dp, 0, 0, 0);
+          // keeps the fragment reads next to their MFMAs: two waves per SIMD
+          // hide the latency, and the register budget is 256
+          __builtin_amdgcn_sched_barrier(0);
         }
         // lane holds key column kvrow; query rows t*32 + 8*(r/4) + 4*half + r%4
 #pragma unroll
@@ -888,6 +923,7 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_tile_kernel(AttnArgs a) {
           for (int i = 0; i < HD / 32; ++i) {
             dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(dOt, ks, i), pb, dv[i], 0, 0, 0);
             dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Qt, ks, i), dsb, dk[i], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
       }
@@ -1334,13 +1370,13 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
     a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
-    const unsigned grid_kv = (unsigned)(lz_cdiv(S, 128) * B * KV);
+    const unsigned grid_kv = (unsigned)(lz_cdiv(S, 256) * B * KV);
     const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
     if (hd == 128) {
-      attn_bwd_dkdv_tile_kernel<128><<<grid_kv, 256, 0, s>>>(a);
+      attn_bwd_dkdv_wide_kernel<128><<<grid_kv, 512, 0, s>>>(a);
       attn_bwd_dq_tile_kernel<128><<<grid_q, 256, 0, s>>>(a);
     } else {
-      attn_bwd_dkdv_tile_kernel<64><<<grid_kv, 256, 0, s>>>(a);
+      attn_bwd_dkdv_wide_kernel<64><<<grid_kv, 512, 0, s>>>(a);
       attn_bwd_dq_tile_kernel<64><<<grid_q, 256, 0, s>>>(a);
     }
     return lz_check_launch("lz_attn_bwd");
