@@ -382,6 +382,7 @@ def main() -> int:
                     help="7B ZeRO-3 fit-to-memory sweep: micro-batch 1, 2, 4, ... (S=2048) until the device is "
                          "out of memory or --fit-max-batch; prints one JSON line and exits")
     ap.add_argument("--fit-max-batch", type=int, default=64)
+    ap.add_argument("--skip-plumbing", action="store_true", help="skip the train.py plumbing leg")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the 1B ZeRO-3 step (no recompute=False, 125M, AdamW or pointwise legs)")
     args = ap.parse_args()
@@ -457,7 +458,7 @@ def main() -> int:
         del m2, e2
         torch.cuda.empty_cache()
     plumbing = None
-    if not args.headline_only:
+    if not args.headline_only and not args.skip_plumbing:
         log("plumbing workload (train.py config)")
         plumbing = bench_plumbing(dev, cpu=not args.no_cpu_baseline)
         log("AdamW 124M")

@@ -44,11 +44,12 @@ __host__ __device__ static inline int64_t lz_cdiv(int64_t a, int64_t b) { return
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
+// One v_cvt_pk_bf16_f32: round to nearest even, NaN kept quiet with its sign.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  const f32x2_v v = {f, 0.0f};
+  return (uint16_t)(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v)) & 0xffffu);
 }
 
 // Rounds a float to the nearest bfloat16 value, kept as float.

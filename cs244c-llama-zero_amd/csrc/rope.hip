@@ -73,36 +73,20 @@ __global__ void rope_kernel(T* __restrict__ x, int64_t ld, int64_t rows, int64_t
   }
 }
 
-// Vectorized rotation: one thread per (row, head, group of V consecutive
-// i < hd/2), V = 16 bytes of elements; the two halves of the head, cos and sin
-// are read as 16-byte vectors.  Same per-element arithmetic as rope_kernel.
+// Vectorized rotation: one thread per (row, group of V consecutive i < hd/2,
+// four heads), V = 16 bytes of elements: the cos/sin vectors of the row's
+// position are read once for the four heads, whose loads are in flight
+// together.  Same per-element arithmetic as rope_kernel.
 template <typename T, bool kBwd>
-__global__ void __launch_bounds__(256) rope_vec_kernel(T* __restrict__ x, int64_t ld, int64_t rows, int64_t seq,
-                                                       int nheads, int hd, const T* __restrict__ cos_t,
-                                                       const T* __restrict__ sin_t, int64_t pos_offset) {
+__device__ __forceinline__ void rope_vec_rotate(const uint4& av, const uint4& bv, const uint4& c1v, const uint4& c2v,
+                                                const uint4& s1v, const uint4& s2v, uint4& o1v, uint4& o2v) {
   constexpr int V = 16 / sizeof(T);
-  const int half = hd / 2, groups = half / V;
-  const int64_t per_row = (int64_t)nheads * groups;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * per_row) return;
-  const int64_t row = idx / per_row;
-  const int rem = (int)(idx - row * per_row);
-  const int head = rem / groups;
-  const int i = (rem - head * groups) * V;
-  const int64_t pos = row % seq + pos_offset;
-  T* p = x + row * ld + (int64_t)head * hd;
-  const T* cp = cos_t + pos * hd;
-  const T* sp = sin_t + pos * hd;
-  const uint4 av = *reinterpret_cast<const uint4*>(p + i), bv = *reinterpret_cast<const uint4*>(p + i + half);
-  const uint4 c1v = *reinterpret_cast<const uint4*>(cp + i), c2v = *reinterpret_cast<const uint4*>(cp + i + half);
-  const uint4 s1v = *reinterpret_cast<const uint4*>(sp + i), s2v = *reinterpret_cast<const uint4*>(sp + i + half);
   const T* a = reinterpret_cast<const T*>(&av);
   const T* b = reinterpret_cast<const T*>(&bv);
   const T* c1 = reinterpret_cast<const T*>(&c1v);
   const T* c2 = reinterpret_cast<const T*>(&c2v);
   const T* s1 = reinterpret_cast<const T*>(&s1v);
   const T* s2 = reinterpret_cast<const T*>(&s2v);
-  uint4 o1v, o2v;
   T* o1 = reinterpret_cast<T*>(&o1v);
   T* o2 = reinterpret_cast<T*>(&o2v);
 #pragma unroll
@@ -119,8 +103,53 @@ __global__ void __launch_bounds__(256) rope_vec_kernel(T* __restrict__ x, int64_
     Elem<T>::store(o1, e, r1);
     Elem<T>::store(o2, e, r2);
   }
-  *reinterpret_cast<uint4*>(p + i) = o1v;
-  *reinterpret_cast<uint4*>(p + i + half) = o2v;
+}
+
+template <typename T, bool kBwd>
+__global__ void __launch_bounds__(256) rope_vec_kernel(T* __restrict__ x, int64_t ld, int rows, int seq, int nheads,
+                                                       int hd, const T* __restrict__ cos_t, const T* __restrict__ sin_t,
+                                                       int64_t pos_offset) {
+  constexpr int V = 16 / sizeof(T);
+  constexpr int kHeads = 4;  // heads per thread, in flight together
+  const int half = hd / 2, groups = half / V;
+  const int hquads = (nheads + kHeads - 1) / kHeads;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * groups * hquads) return;
+  const int row = idx / (groups * hquads);
+  const int rem = idx - row * (groups * hquads);
+  const int hq = rem / groups;
+  const int i = (rem - hq * groups) * V;
+  const int64_t pos = row % seq + pos_offset;
+  T* p = x + (int64_t)row * ld;
+  const T* cp = cos_t + pos * hd;
+  const T* sp = sin_t + pos * hd;
+  const uint4 c1v = *reinterpret_cast<const uint4*>(cp + i), c2v = *reinterpret_cast<const uint4*>(cp + i + half);
+  const uint4 s1v = *reinterpret_cast<const uint4*>(sp + i), s2v = *reinterpret_cast<const uint4*>(sp + i + half);
+  int h = hq * kHeads;
+  const int hend = min(nheads, h + kHeads);
+  for (; h + kHeads <= hend; h += kHeads) {
+    uint4 av[kHeads], bv[kHeads];
+#pragma unroll
+    for (int j = 0; j < kHeads; ++j) {
+      av[j] = *reinterpret_cast<const uint4*>(p + (h + j) * hd + i);
+      bv[j] = *reinterpret_cast<const uint4*>(p + (h + j) * hd + i + half);
+    }
+#pragma unroll
+    for (int j = 0; j < kHeads; ++j) {
+      uint4 o1v, o2v;
+      rope_vec_rotate<T, kBwd>(av[j], bv[j], c1v, c2v, s1v, s2v, o1v, o2v);
+      *reinterpret_cast<uint4*>(p + (h + j) * hd + i) = o1v;
+      *reinterpret_cast<uint4*>(p + (h + j) * hd + i + half) = o2v;
+    }
+  }
+  for (; h < hend; ++h) {
+    const uint4 av = *reinterpret_cast<const uint4*>(p + h * hd + i);
+    const uint4 bv = *reinterpret_cast<const uint4*>(p + h * hd + i + half);
+    uint4 o1v, o2v;
+    rope_vec_rotate<T, kBwd>(av, bv, c1v, c2v, s1v, s2v, o1v, o2v);
+    *reinterpret_cast<uint4*>(p + h * hd + i) = o1v;
+    *reinterpret_cast<uint4*>(p + h * hd + i + half) = o2v;
+  }
 }
 
 inline int grid_for(int64_t n) {
@@ -169,15 +198,16 @@ LZ_EXPORT int lz_rope(void* x, int dtype, int64_t ld, int64_t rows, int64_t seq,
   const int esz = dtype == LZ_BF16 ? 2 : 4, vec = 16 / esz;
   if ((dtype == LZ_BF16 || dtype == LZ_F32) && (hd / 2) % vec == 0 && (ld * esz) % 16 == 0 && lz_aligned16(x) &&
       lz_aligned16(cos_t) && lz_aligned16(sin_t)) {
-    const int64_t work = rows * nheads * (hd / 2 / vec);
-    LZ_REQUIRE(lz_cdiv(work, 256) < (1ll << 31), "lz_rope: too many rows");
+    const int64_t work = rows * (hd / 2 / vec) * ((nheads + 3) / 4);
+    LZ_REQUIRE(work < (1ll << 31) && seq < (1ll << 31), "lz_rope: too many rows");
     const unsigned grid = (unsigned)lz_cdiv(work, 256);
+    const int r32 = (int)rows, s32 = (int)seq;
     if (dtype == LZ_BF16) {
-      if (backward) rope_vec_kernel<uint16_t, true><<<grid, 256, 0, s>>>((uint16_t*)x, ld, rows, seq, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);
-      else rope_vec_kernel<uint16_t, false><<<grid, 256, 0, s>>>((uint16_t*)x, ld, rows, seq, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);
+      if (backward) rope_vec_kernel<uint16_t, true><<<grid, 256, 0, s>>>((uint16_t*)x, ld, r32, s32, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);
+      else rope_vec_kernel<uint16_t, false><<<grid, 256, 0, s>>>((uint16_t*)x, ld, r32, s32, (int)nheads, (int)hd, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos_offset);
     } else {
-      if (backward) rope_vec_kernel<float, true><<<grid, 256, 0, s>>>((float*)x, ld, rows, seq, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
-      else rope_vec_kernel<float, false><<<grid, 256, 0, s>>>((float*)x, ld, rows, seq, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
+      if (backward) rope_vec_kernel<float, true><<<grid, 256, 0, s>>>((float*)x, ld, r32, s32, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
+      else rope_vec_kernel<float, false><<<grid, 256, 0, s>>>((float*)x, ld, r32, s32, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
     }
     return lz_check_launch("lz_rope");
   }
