@@ -79,7 +79,7 @@ def run_steps(model, engine, batches, steps: int, warmup: int):
     return time.perf_counter() - t0, losses
 
 
-def bench_adamw(dev: torch.device, n: int = 124_000_000, iters: int = 10):
+def bench_adamw(dev: torch.device, ceilings=None, n: int = 124_000_000, iters: int = 10):
     from lzhip import ops
 
     g = torch.Generator(device=dev).manual_seed(0)
@@ -97,7 +97,10 @@ def bench_adamw(dev: torch.device, n: int = 124_000_000, iters: int = 10):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / iters
     gbs = 28.0 * n / (ms * 1e-3) / 1e9
-    return {"elements": n, "bytes_per_elem": 28, "ms": ms, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
+    out = {"elements": n, "bytes_per_elem": 28, "ms": ms, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
+    if ceilings:
+        out["frac_of_measured_copy"] = gbs / ceilings["copy_GB/s"]
+    return out
 
 
 def run_no_recompute(args, B, S, dev, batches, tokens, model_flops):
@@ -293,7 +296,44 @@ def _time_ms(fn, iters: int = 20) -> float:
     return start.elapsed_time(end) / iters
 
 
-def bench_pointwise(dev: torch.device, rows: int = 16384, dim: int = 2048, ffn: int = 5632, heads: int = 16):
+def bench_ceilings(dev: torch.device) -> dict:
+    """What this box's HBM and MFMA deliver, measured, beside the published
+    8 TB/s and 2.5 PFLOP/s: a STREAM-style 1 GiB -> 1 GiB copy and a 2 GiB
+    read-only pass (both this library's kernels: copy2d and the fp32 sum of
+    squares), and hipBLASLt's bf16 GEMM (torch.matmul) at the 1B step's QKV,
+    gate|up and down projection shapes."""
+    from lzhip import ops
+
+    out = {}
+    a = torch.ones(1 << 14, 1 << 15, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    ms = _time_ms(lambda: ops.copy2d(a, b), 10)
+    out["copy_GB/s"] = 2.0 * 2 * a.numel() / (ms * 1e-3) / 1e9
+    del a, b
+    r = torch.ones(1 << 29, dtype=torch.float32, device=dev)
+    acc = torch.zeros((), dtype=torch.float64, device=dev)
+    ms = _time_ms(lambda: ops.sumsq_(r, acc), 10)
+    out["read_GB/s"] = 4.0 * r.numel() / (ms * 1e-3) / 1e9
+    del r
+    out["copy_frac_of_8TBs"] = out["copy_GB/s"] / PEAK_HBM_GBS
+    out["read_frac_of_8TBs"] = out["read_GB/s"] / PEAK_HBM_GBS
+    g = torch.Generator(device=dev).manual_seed(0)
+    shapes = {"qkv 16384x4096x2048": (16384, 4096, 2048), "gate|up 16384x11264x2048": (16384, 11264, 2048),
+              "down 16384x2048x5632": (16384, 2048, 5632)}
+    lib = {}
+    for name, (M, N, K) in shapes.items():
+        x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        w = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+        ms = _time_ms(lambda: torch.matmul(x, w.t()), 20)
+        lib[name] = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        del x, w
+    out["hipblaslt_bf16_TFLOP/s"] = lib
+    out["hipblaslt_best_frac_of_2.5PF"] = max(lib.values()) / PEAK_BF16_TFLOPS
+    return out
+
+
+def bench_pointwise(dev: torch.device, ceilings=None, rows: int = 16384, dim: int = 2048, ffn: int = 5632,
+                    heads: int = 16):
     """The step's HBM-bound kernels at the 1B step's shapes (bf16, 8x2048
     tokens): bytes moved (each input read once, each output written once) per
     launch time.  A plain 1 GiB device copy is timed beside them as the
@@ -308,12 +348,14 @@ def bench_pointwise(dev: torch.device, rows: int = 16384, dim: int = 2048, ffn: 
     def rec(name, ms, nbytes):
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
+        if ceilings:
+            out[name]["frac_of_measured_copy"] = gbs / ceilings["copy_GB/s"]
 
-    # plain copy of 1 GiB with this library's copy2d_kernel (also the known-size
+    # plain copy of 1 GiB with this library's copy2d_vec_kernel (also the known-size
     # kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters)
     a = torch.ones(1 << 14, 1 << 15, dtype=bf, device=dev)
     b = torch.empty_like(a)
-    rec("device copy 1 GiB (copy2d_kernel)", _time_ms(lambda: ops.copy2d(a, b), 10), 2 * 2 * a.numel())
+    rec("device copy 1 GiB (copy2d_vec_kernel)", _time_ms(lambda: ops.copy2d(a, b), 10), 2 * 2 * a.numel())
     del a, b
     x = torch.randn(rows, dim, device=dev, generator=g).to(bf)
     w = (1 + 0.02 * torch.randn(dim, device=dev, generator=g)).to(bf)
@@ -374,7 +416,7 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-125m", action="store_true")
@@ -457,14 +499,17 @@ def main() -> int:
                     "workload": "125m ZeRO-1 (d768 L12 12q/4kv ffn2048 V32000), B=16 S=1024"}
         del m2, e2
         torch.cuda.empty_cache()
-    plumbing = None
+    plumbing = ceilings = None
     if not args.headline_only and not args.skip_plumbing:
         log("plumbing workload (train.py config)")
         plumbing = bench_plumbing(dev, cpu=not args.no_cpu_baseline)
+    if not args.headline_only:
+        log("measured ceilings")
+        ceilings = bench_ceilings(dev)
         log("AdamW 124M")
-        adamw = bench_adamw(dev)
+        adamw = bench_adamw(dev, ceilings)
         log("pointwise kernels")
-        pointwise = bench_pointwise(dev)
+        pointwise = bench_pointwise(dev, ceilings)
 
     cpu = cpu_ops = None
     if not args.no_cpu_baseline:
@@ -502,6 +547,7 @@ def main() -> int:
         "llama_1b_zero3_recompute_off": res_norecompute,
         "plumbing_train_py": plumbing,
         "llama_125m_zero1": res_125m,
+        "measured_ceilings": ceilings,
         "adamw_124m": adamw,
         "pointwise": pointwise,
         "gemm_all_launches": {"launches": n_launch, "ms_per_step": gemm_ms / args.steps, "TFLOP/s": gemm_tflops,

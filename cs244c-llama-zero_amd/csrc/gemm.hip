@@ -693,6 +693,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // stage's loads and then syncs the workgroup with a bare barrier.  K must be
 // a multiple of DBK in every split; an M-major A needs M % 8 == 0 (N-major B:
 // N % 8 == 0).
+//
+// Layouts with an M- or N-major operand (input and weight gradients) run a
+// different step (kMid): half of the waves (one per SIMD) issue all stage
+// loads, so the other wave on each SIMD keeps issuing MFMAs while the loads
+// queue, and the barrier sits in the middle of a step, after the last LDS
+// reads of the current stage, so that the MFMAs of its last two slices run
+// while the next stage's first fragments are read.  Measured on the 1B
+// step's shapes: input gradients 1-6 % faster, weight gradients 5-20 %; the
+// K-major x K-major product is unchanged either way and keeps the plain step.
 template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   constexpr int BM = 256, BN = 256;
@@ -700,9 +709,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage
   constexpr int kStage = 2 * kOpBytes;
-  constexpr int kPerWave = kOpBytes / 1024 / kWaves;  // wave loads per operand per stage
+  constexpr bool kMid = !(AK && BK);
+  constexpr int kLoadWaves = kMid ? kWaves / 2 : kWaves;  // waves that issue the stage loads
+  constexpr int kPerWave = kOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
   constexpr int kSlices = DBK / 16;
-  static_assert(kPerWave * kWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
+  static_assert(kPerWave * kLoadWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
+  static_assert(!kMid || (NST == 2 && kSlices == 4), "the mid-step barrier runs two stages of four slices");
   static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
   static_assert(kSlices == 2 || kSlices == 4, "stages hold 2 or 4 K slices");
 
@@ -719,8 +731,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
 
   DmaOperand<AK, kPerWave, DBK> la;
   DmaOperand<BK, kPerWave, DBK> lb;
-  la.init(g.A, g.lda, m0, g.M, kbeg, wave, lane);
-  lb.init(g.B, g.ldb, n0, g.N, kbeg, wave, lane);
+  const int lwave = wave % kLoadWaves;     // this wave's part of a stage
+  const bool loader = wave < kLoadWaves;  // wave-uniform
+  la.init(g.A, g.lda, m0, g.M, kbeg, lwave, lane);
+  lb.init(g.B, g.ldb, n0, g.N, kbeg, lwave, lane);
   DmaFrags<AK, FM, DBK> fra;
   DmaFrags<BK, FN, DBK> frb;
   fra.init(wm * FM, lane);
@@ -734,57 +748,114 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-#pragma unroll
-  for (int st = 0; st < NST - 1; ++st)
-    if (st < ktiles) {
-      la.issue(smem + st * kStage, wave, st);
-      lb.issue(smem + st * kStage + kOpBytes, wave, st);
-    }
-  for (int kt = 0; kt < ktiles; ++kt) {
-    if constexpr (NST == 2) {
-      // only stage kt's loads are in flight here: the barrier's fence waits
-      // for them, publishes every wave's part and retires the reads of stage
-      // kt-1, whose slot is refilled next
-      __syncthreads();
-    } else {
-      // stage kt's loads are this wave's oldest: let the (up to NST-2) later
-      // stages stay in flight, then the barrier publishes every wave's part
-      // and retires the reads of stage kt-1, whose slot is refilled next
-      static_assert(NST == 4, "the wait ladder below covers four stages");
-      constexpr int kLoads = 2 * kPerWave;  // DMA instructions per wave per stage
-      const int ahead = ktiles - 1 - kt;
-      asm volatile("" ::: "memory");
-      if (ahead >= 2) wait_vmcnt<2 * kLoads>();
-      else if (ahead == 1) wait_vmcnt<kLoads>();
-      else wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-    }
-    if (kt + NST - 1 < ktiles) {
-      char* nxt = smem + ((kt + NST - 1) % NST) * kStage;
-      la.issue(nxt, wave, kt + NST - 1);
-      lb.issue(nxt + kOpBytes, wave, kt + NST - 1);
-    }
-    const char* sa = smem + (kt % NST) * kStage;
-    const char* sb = sa + kOpBytes;
-    // fragments double-buffered in registers: slice kk+1 is read while the
-    // MFMAs of slice kk run
-    bf16x8_t fa0[FN], fb0[FM], fa1[FN], fb1[FM];
+  if constexpr (kMid) {
     constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);
-    dma_load_frags(fra, frb, sa, sb, 0, fa0, fb0);
-    dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
-    dma_mfma(acc, fa0, fb0);
-    if constexpr (kSlices == 4) {
+    if (ktiles > 0 && loader) {
+      la.issue(smem, lwave, 0);
+      lb.issue(smem + kOpBytes, lwave, 0);
+    }
+    __syncthreads();
+    if (ktiles > 1 && loader) {
+      la.issue(smem + kStage, lwave, 1);
+      lb.issue(smem + kStage + kOpBytes, lwave, 1);
+    }
+    // slices 0 and 1 of stage kt are in registers when step kt begins
+    bf16x8_t fa0[FN], fb0[FM], fa1[FN], fb1[FM];
+    dma_load_frags(fra, frb, smem, smem + kOpBytes, 0, fa0, fb0);
+    dma_load_frags(fra, frb, smem, smem + kOpBytes, 1, fa1, fb1);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      const char* sa = smem + (kt & 1) * kStage;
+      const char* sb = sa + kOpBytes;
+      dma_mfma(acc, fa0, fb0);
       dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
       dma_mfma(acc, fa1, fb1);
       dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
+      sched_slice<kReads, FM * FN>();
+      sched_slice<kReads, FM * FN>();
+      // the fence waits for this wave's loads of stage kt+1 and its reads of
+      // stage kt; past the barrier stage kt+1 is complete and no wave reads
+      // stage kt's slot any more, so stage kt+2 may refill it
+      __syncthreads();
+      if (kt + 2 < ktiles && loader) {
+        char* nxt = smem + (kt & 1) * kStage;
+        la.issue(nxt, lwave, kt + 2);
+        lb.issue(nxt + kOpBytes, lwave, kt + 2);
+      }
+      // slices 0 and 1 of stage kt+1 (after the last step: unused reads of
+      // the other slot) while the MFMAs of slices 2 and 3 run
+      const char* na = smem + ((kt + 1) & 1) * kStage;
+      const char* nb = na + kOpBytes;
+      bf16x8_t ga0[FN], gb0[FM], ga1[FN], gb1[FM];
       dma_mfma(acc, fa0, fb0);
-    }
-    dma_mfma(acc, fa1, fb1);
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+      dma_load_frags(fra, frb, na, nb, 0, ga0, gb0);
+      dma_mfma(acc, fa1, fb1);
+      dma_load_frags(fra, frb, na, nb, 1, ga1, gb1);
+      sched_slice<kReads, FM * FN>();
+      sched_slice<kReads, FM * FN>();
 #pragma unroll
-    for (int q = 0; q < kSlices - 1; ++q) sched_slice<kReads, FM * FN>();
-    sched_slice<0, FM * FN>();
+      for (int j = 0; j < FN; ++j) {
+        fa0[j] = ga0[j];
+        fa1[j] = ga1[j];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        fb0[i] = gb0[i];
+        fb1[i] = gb1[i];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < NST - 1; ++st)
+      if (st < ktiles) {
+        la.issue(smem + st * kStage, lwave, st);
+        lb.issue(smem + st * kStage + kOpBytes, lwave, st);
+      }
+    for (int kt = 0; kt < ktiles; ++kt) {
+      if constexpr (NST == 2) {
+        // only stage kt's loads are in flight here: the barrier's fence waits
+        // for them, publishes every wave's part and retires the reads of stage
+        // kt-1, whose slot is refilled next
+        __syncthreads();
+      } else {
+        // stage kt's loads are this wave's oldest: let the (up to NST-2) later
+        // stages stay in flight, then the barrier publishes every wave's part
+        // and retires the reads of stage kt-1, whose slot is refilled next
+        static_assert(NST == 4, "the wait ladder below covers four stages");
+        constexpr int kLoads = 2 * kPerWave;  // DMA instructions per wave per stage
+        const int ahead = ktiles - 1 - kt;
+        asm volatile("" ::: "memory");
+        if (ahead >= 2) wait_vmcnt<2 * kLoads>();
+        else if (ahead == 1) wait_vmcnt<kLoads>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      if (kt + NST - 1 < ktiles) {
+        char* nxt = smem + ((kt + NST - 1) % NST) * kStage;
+        la.issue(nxt, lwave, kt + NST - 1);
+        lb.issue(nxt + kOpBytes, lwave, kt + NST - 1);
+      }
+      const char* sa = smem + (kt % NST) * kStage;
+      const char* sb = sa + kOpBytes;
+      // fragments double-buffered in registers: slice kk+1 is read while the
+      // MFMAs of slice kk run
+      bf16x8_t fa0[FN], fb0[FM], fa1[FN], fb1[FM];
+      constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);
+      dma_load_frags(fra, frb, sa, sb, 0, fa0, fb0);
+      dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
+      dma_mfma(acc, fa0, fb0);
+      if constexpr (kSlices == 4) {
+        dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
+        dma_mfma(acc, fa1, fb1);
+        dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
+        dma_mfma(acc, fa0, fb0);
+      }
+      dma_mfma(acc, fa1, fb1);
+      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+#pragma unroll
+      for (int q = 0; q < kSlices - 1; ++q) sched_slice<kReads, FM * FN>();
+      sched_slice<0, FM * FN>();
+    }
   }
   __syncthreads();  // every wave is done with the stages before the epilogue may reuse LDS
 

@@ -44,6 +44,20 @@ __global__ void __launch_bounds__(256) copy2d_kernel(const T* __restrict__ src, 
   }
 }
 
+// 16-byte chunks: thread x of row y copies chunk blockIdx.x*256 + x of that
+// row (rows past gridDim.y are taken in steps of gridDim.y).  One chunk per
+// thread and no loop over columns measured fastest for plain copies here
+// (6.1-6.2 TB/s at 128 MB-2 GB); nontemporal loads keep the stream out of L2.
+typedef unsigned int chunk16_t __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256) copy2d_vec_kernel(const chunk16_t* __restrict__ src, int64_t lds,
+                                                          chunk16_t* __restrict__ dst, int64_t ldd, int64_t rows,
+                                                          int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) dst[r * ldd + c] = __builtin_nontemporal_load(src + r * lds + c);
+}
+
 }  // namespace
 
 // dst[r][c] = src[r][c] for a rows x cols window of two row-major matrices.
@@ -51,8 +65,21 @@ LZ_EXPORT int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, in
                         void* stream) {
   LZ_REQUIRE(rows >= 0 && cols >= 0 && lds >= cols && ldd >= cols, "lz_copy2d: bad shape");
   if (rows == 0 || cols == 0) return LZ_OK;
-  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(lz_cdiv(rows * cols, 256), (int64_t)lz_num_cus() * 16));
   hipStream_t s = lz_stream(stream);
+  const int64_t esz = dtype == LZ_BF16 ? 2 : 4;
+  if ((dtype == LZ_BF16 || dtype == LZ_F32) && lz_aligned16(src) && lz_aligned16(dst) && (cols * esz) % 16 == 0 &&
+      (lds * esz) % 16 == 0 && (ldd * esz) % 16 == 0) {
+    int64_t vr = rows, vc = cols * esz / 16, vls = lds * esz / 16, vld = ldd * esz / 16;
+    if (vls == vc && vld == vc) {  // both contiguous: one long row
+      vc *= vr;
+      vr = 1;
+    }
+    LZ_REQUIRE(lz_cdiv(vc, 256) < (1ll << 31), "lz_copy2d: too many columns");
+    const dim3 grid((unsigned)lz_cdiv(vc, 256), (unsigned)std::min<int64_t>(vr, 65535));
+    copy2d_vec_kernel<<<grid, 256, 0, s>>>((const chunk16_t*)src, vls, (chunk16_t*)dst, vld, vr, vc);
+    return lz_check_launch("lz_copy2d");
+  }
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(lz_cdiv(rows * cols, 256), (int64_t)lz_num_cus() * 16));
   if (dtype == LZ_BF16) copy2d_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols);
   else if (dtype == LZ_F32) copy2d_kernel<float><<<grid, 256, 0, s>>>((const float*)src, lds, (float*)dst, ldd, rows, cols);
   else return lz_set_error(LZ_EINVAL, "lz_copy2d: bad dtype %d", dtype);

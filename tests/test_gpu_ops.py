@@ -471,3 +471,29 @@ def test_transpose_and_cast_exact():
     assert torch.equal(ops.cast(f, torch.bfloat16).cpu(), f.cpu().to(torch.bfloat16))
     z = ops.zeros((37,), torch.float32, DEV)
     assert torch.count_nonzero(z) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_copy2d_exact(dtype):
+    """Window copies, bit-exact: contiguous (one long row), strided windows on
+    the 16-byte path, rows beyond one grid column (70 000 > 65 535) and
+    unaligned shapes on the element-wise path."""
+    g = _seed(13)
+    cases = [((64, 256), (64, 256), 64, 256),      # contiguous
+             ((40, 96), (40, 160), 40, 64),        # strided window, 16-byte path
+             ((70000, 8), (70000, 16), 70000, 8),  # rows past one grid column
+             ((33, 21), (33, 37), 33, 21)]         # element-wise path
+    for (sr, sc), (dr, dc), rows, cols in cases:
+        src = torch.randn(sr, sc, generator=g).to(dtype).to(DEV)
+        dst = torch.full((dr, dc), -7.0, dtype=dtype, device=DEV)
+        ops.copy2d(src[:rows, :cols], dst[:rows, :cols])
+        want = torch.full((dr, dc), -7.0, dtype=dtype)
+        want[:rows, :cols] = src.cpu()[:rows, :cols]
+        assert torch.equal(dst.cpu(), want), (sr, sc, dr, dc)
+    # a window that starts 4 elements in (not 16-byte aligned for bf16)
+    src = torch.randn(16, 64, generator=g).to(dtype).to(DEV)
+    dst = torch.zeros(16, 64, dtype=dtype, device=DEV)
+    ops.copy2d(src[:, 4:36], dst[:, 4:36])
+    want = torch.zeros(16, 64, dtype=dtype)
+    want[:, 4:36] = src.cpu()[:, 4:36]
+    assert torch.equal(dst.cpu(), want)
