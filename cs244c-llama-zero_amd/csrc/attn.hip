@@ -54,16 +54,6 @@ struct AttnArgs {
   float scale;
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Two floats -> two bf16 (round to nearest even) packed low/high, one
-// v_cvt_pk_bf16_f32.
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const f32x2_t f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-}
-
 // Elements e0..e0+7 of an accumulator -> an 8 x bf16 MFMA operand.
 __device__ __forceinline__ bf16x8_t pack8(const f32x16_t& v, int e0) {
   const uint4 w = make_uint4(pack_bf16x2(v[e0], v[e0 + 1]), pack_bf16x2(v[e0 + 2], v[e0 + 3]),

@@ -49,16 +49,6 @@ struct GemmArgs {
   int64_t slab;   // elements between the fp32 partial slabs of consecutive splits
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-// Two floats -> two bf16 (round to nearest even) packed low/high, one
-// v_cvt_pk_bf16_f32.
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const float2 f = make_float2(lo, hi);
-  const bf16x2_t b = __builtin_convertvector(__builtin_bit_cast(__attribute__((ext_vector_type(2))) float, f), bf16x2_t);
-  return __builtin_bit_cast(uint32_t, b);
-}
-
 __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t n, const float (&v)[4]) {
   float o[4] = {v[0] * g.alpha, v[1] * g.alpha, v[2] * g.alpha, v[3] * g.alpha};
   if (g.vec_store && n + 3 < g.N) {
@@ -578,14 +568,18 @@ struct DmaOperand {
   const uint16_t* src[kPerWave];
   int64_t kadv;  // elements to advance per DBK-deep K step
 
+  // pair > 0 (K-major only): tile rows 0-127 are rows row0.. and tile rows
+  // 128-255 are rows pair+row0.. of the operand (two 128-row halves taken
+  // `pair` rows apart, e.g. matching gate and up rows of a fused weight).
   __device__ __forceinline__ void init(const uint16_t* p, int64_t ld, int64_t row0, int64_t nrows, int64_t kbeg,
-                                       int wave, int lane) {
+                                       int wave, int lane, int64_t pair = 0) {
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
       if constexpr (KMAJOR) {
         const int r = (wave * kPerWave + q) * kRowsK + lane / kChunksK;
         const int c = (lane % kChunksK) ^ (DBK == 64 ? swz<8>(r) : swz_k4(r));
-        src[q] = p + min(row0 + r, nrows - 1) * ld + kbeg + c * 8;
+        const int64_t gr = pair > 0 ? row0 + (r & 127) + (r >> 7) * pair : min(row0 + r, nrows - 1);
+        src[q] = p + gr * ld + kbeg + c * 8;
       } else {
         const int r = (wave * kPerWave + q) * 2 + (lane >> 5);
         const int c = (lane & 31) ^ swz_mn(r);
@@ -702,8 +696,26 @@ __device__ __forceinline__ void wait_vmcnt() {
 // while the next stage's first fragments are read.  Measured on the 1B
 // step's shapes: input gradients 1-6 % faster, weight gradients 5-20 %; the
 // K-major x K-major product is unchanged either way and keeps the plain step.
-template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
+// Outputs of the fused gate|up projection + SwiGLU: h = silu(gate) * up
+// ([M, F] bf16); the GEMM's own output (gate|up, [M, 2F]) goes to GemmArgs::C
+// when that is not null.
+struct SwigluOut {
+  uint16_t* h;
+  int64_t ldh;
+  int64_t F;
+};
+
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
+                                             f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t tn,
+                                             char* smem, int lane, int wave);
+
+// One workgroup's 256x256 tile of the direct-to-LDS GEMM (main loop, then the
+// epilogue).  kSwiGLU: the tile's 256 B rows are 128 gate rows and the
+// matching 128 up rows of a [gate; up] weight (o.F rows apart), and the
+// epilogue writes silu(gate) * up.
+template <int WM, int WN, bool AK, bool BK, int DBK, int NST, bool kSwiGLU>
+__device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o) {
   constexpr int BM = 256, BN = 256;
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -734,7 +746,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   const int lwave = wave % kLoadWaves;     // this wave's part of a stage
   const bool loader = wave < kLoadWaves;  // wave-uniform
   la.init(g.A, g.lda, m0, g.M, kbeg, lwave, lane);
-  lb.init(g.B, g.ldb, n0, g.N, kbeg, lwave, lane);
+  if constexpr (kSwiGLU) lb.init(g.B, g.ldb, tn * 128, g.N, kbeg, lwave, lane, o.F);
+  else lb.init(g.B, g.ldb, n0, g.N, kbeg, lwave, lane);
   DmaFrags<AK, FM, DBK> fra;
   DmaFrags<BK, FN, DBK> frb;
   fra.init(wm * FM, lane);
@@ -859,9 +872,78 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   }
   __syncthreads();  // every wave is done with the stages before the epilogue may reuse LDS
 
-  GemmArgs go = g;  // split-K: this split's fp32 slab
-  if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
-  store_tile<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+  if constexpr (kSwiGLU) {
+    store_swiglu<BM, BN, WM, WN>(g, o, acc, m0, tn, smem, lane, wave);
+  } else {
+    GemmArgs go = g;  // split-K: this split's fp32 slab
+    if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
+    store_tile<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+  }
+}
+
+template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
+  gemm_dma_tile<WM, WN, AK, BK, DBK, NST, false>(g, SwigluOut{});
+}
+
+// Fused gate|up projection + SwiGLU (both operands K-major): tile (tm, tn)
+// covers rows 256 tm.. of x and gate/up columns 128 tn.. of the [M, F] result.
+__global__ void __launch_bounds__(512) gemm_swiglu_kernel(GemmArgs g, SwigluOut o) {
+  gemm_dma_tile<2, 4, true, true, 64, 2, true>(g, o);
+}
+
+// SwiGLU epilogue.  Each wave stages its 128x64 tile as bf16 in its own LDS
+// region (the layout store_tile16 uses), optionally writes it to gate|up,
+// then, after a workgroup barrier, the gate wave (wn = 0, 1) and the up wave
+// with the same columns (wn + 2) each take half of the rows: h is computed
+// from the two staged bf16 tiles exactly as the unfused SwiGLU kernel does
+// from the stored gate|up, and written as whole 128-byte rows.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
+                                             f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t tn,
+                                             char* smem, int lane, int wave) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static_assert(WN == 4 && TN == 64, "gate and up are two 64-column waves each");
+  constexpr int kRow = TN * 2, kChunks = kRow / 16, kWaveBytes = TM * kRow;
+  const int wm = wave / WN, wn = wave % WN;
+  const int frag_row = lane & 31, half = lane >> 5;
+  const int64_t mrow0 = m0 + wm * TM;
+  const int64_t col = tn * 128 + (wn & 1) * 64;  // gate (and up) column of this wave's tile
+  char* st = smem + wave * kWaveBytes;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = i * 32 + frag_row, chunk = j * 4 + q;
+        *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
+            make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                       pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
+      }
+  if (g.C) {
+    asm volatile("" ::: "memory");
+    uint16_t* gu = static_cast<uint16_t*>(g.C) + (wn < 2 ? 0 : o.F) + col;
+#pragma unroll
+    for (int t = 0; t < TM * kChunks / 64; ++t) {
+      const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+      const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+      *reinterpret_cast<uint4*>(gu + (mrow0 + row) * g.ldc + chunk * 8) = v;
+    }
+  }
+  __syncthreads();
+  const int gw = wn < 2 ? wave : wave - 2;  // the gate wave of this pair
+  const char* sg = smem + gw * kWaveBytes;
+  const char* su = sg + 2 * kWaveBytes;
+  const int r0 = wn < 2 ? 0 : TM / 2;
+#pragma unroll
+  for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
+    const int idx = t * 64 + lane, row = r0 + idx / kChunks, chunk = idx % kChunks;
+    const int off = row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4);
+    const uint4 gv = *reinterpret_cast<const uint4*>(sg + off);
+    const uint4 uv = *reinterpret_cast<const uint4*>(su + off);
+    *reinterpret_cast<uint4*>(o.h + (mrow0 + row) * o.ldh + col + chunk * 8) = swiglu_fwd8(gv, uv);
+  }
 }
 
 // Sums the fp32 partial slabs of a split-K product and applies the epilogue
@@ -1072,4 +1154,47 @@ LZ_EXPORT int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb,
                          const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta,
                          void* stream) {
   return lz_gemm(A, lda, 1, B, ldb, 1, C, ldc, c_dtype, R, ldr, M, N, K, alpha, beta, nullptr, 0, stream);
+}
+
+// Fused gate|up projection + SwiGLU (reference model/llama.py:136-146, the
+// gate_proj / up_proj products and silu(gate) * up): for x [M, K] and
+// w = [gate rows; up rows] ([2F, K], row-major), writes h = silu(x.Wg^T) *
+// (x.Wu^T) as bf16 [M, F], and the product x.w^T itself to gu ([M, 2F]) when
+// gu is not null.  Every value equals what lz_gemm (bf16 output) followed by
+// lz_swiglu_fwd produces: same K order, same bf16 roundings.  Needs
+// M % 256 == 0, F % 128 == 0, K % 64 == 0 and 16-byte aligned rows.
+LZ_EXPORT int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, void* gu, int64_t ldgu, void* h,
+                             int64_t ldh, int64_t M, int64_t F, int64_t K, void* stream) {
+  LZ_REQUIRE(x && w && h, "lz_gemm_swiglu: null pointer");
+  LZ_REQUIRE(M > 0 && F > 0 && K > 0 && M % 256 == 0 && F % 128 == 0 && K % 64 == 0,
+             "lz_gemm_swiglu: needs M %% 256, F %% 128 and K %% 64 == 0 (M %lld, F %lld, K %lld)", (long long)M,
+             (long long)F, (long long)K);
+  LZ_REQUIRE(ldx >= K && ldw >= K && ldh >= F && (gu == nullptr || ldgu >= 2 * F),
+             "lz_gemm_swiglu: bad leading dimension");
+  LZ_REQUIRE(lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(h) && (gu == nullptr || lz_aligned16(gu)) &&
+                 ldx % 8 == 0 && ldw % 8 == 0 && ldh % 8 == 0 && (gu == nullptr || ldgu % 8 == 0),
+             "lz_gemm_swiglu: rows must be 16-byte aligned");
+  const int64_t tiles = (M / 256) * (F / 128);
+  LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm_swiglu: too many tiles");
+  GemmArgs g{};
+  g.A = (const uint16_t*)x;
+  g.B = (const uint16_t*)w;
+  g.C = gu;
+  g.R = nullptr;
+  g.lda = ldx;
+  g.ldb = ldw;
+  g.ldc = gu ? ldgu : 2 * F;
+  g.ldr = 0;
+  g.M = M;
+  g.N = 2 * F;
+  g.K = K;
+  g.alpha = 1.f;
+  g.beta = 0.f;
+  g.c_f32 = 0;
+  g.vec_store = 1;
+  g.vec16 = 1;
+  g.kper = K;
+  g.slab = 0;
+  gemm_swiglu_kernel<<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(g, SwigluOut{(uint16_t*)h, ldh, F});
+  return lz_check_launch("lz_gemm_swiglu");
 }

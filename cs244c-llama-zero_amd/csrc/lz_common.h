@@ -44,16 +44,43 @@ __host__ __device__ static inline int64_t lz_cdiv(int64_t a, int64_t b) { return
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// One v_cvt_pk_bf16_f32: round to nearest even, NaN kept quiet with its sign.
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
-  typedef float f32x2_v __attribute__((ext_vector_type(2)));
-  const f32x2_v v = {f, 0.0f};
-  return (uint16_t)(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v)) & 0xffffu);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 packed low/high with one v_cvt_pk_bf16_f32: round to
+// nearest even, NaN kept quiet with its sign.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
+
+__device__ __forceinline__ uint16_t f2bf(float f) { return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu); }
 
 // Rounds a float to the nearest bfloat16 value, kept as float.
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal
+// (about 1 ulp in fp32, below the bf16 rounding of every output).
+__device__ __forceinline__ float sigmoid_hw(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+}
+
+// SwiGLU forward on 8 bf16 pairs (16 bytes of gate, 16 of up): rounds
+// silu(g) to bf16 before multiplying by u, as the reference's bf16 ops do
+// (F.silu then the product), and rounds the product.
+__device__ __forceinline__ uint4 swiglu_fwd8(const uint4& gv, const uint4& uv) {
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float g0 = bf2f(gw[k] & 0xffff), g1 = bf2f(gw[k] >> 16);
+    const float u0 = bf2f(uw[k] & 0xffff), u1 = bf2f(uw[k] >> 16);
+    const float h0 = round_bf(g0 * sigmoid_hw(g0)) * u0, h1 = round_bf(g1 * sigmoid_hw(g1)) * u1;
+    ow[k] = pack_bf16x2(h0, h1);
+  }
+  return make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
 
 template <typename T>
 struct Elem;

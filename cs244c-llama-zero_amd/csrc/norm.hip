@@ -15,14 +15,6 @@ namespace {
 constexpr int kRowsPerBlock = 4;  // one wave per row
 constexpr int kThreads = 64 * kRowsPerBlock;
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Two floats -> two bf16 (round to nearest even, one v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const f32x2_t f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-}
 
 template <typename T>
 struct Pack8;
@@ -103,8 +95,8 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(const T* __restri
 }
 
 // bf16 backward: workgroup b owns rows [b*rpb, (b+1)*rpb), its wave w takes
-// rows w, w+4, ... of that range and loads the next one while it computes the
-// current one.  The 4 waves' dw contributions are summed in LDS (in a fixed
+// rows w, w+4, ... of that range and loads the next one (x, dy and the
+// residual gradient) while it computes the current one.  The 4 waves' dw contributions are summed in LDS (in a fixed
 // order) into one fp32 partial row per workgroup: dw_part[b][cols].
 template <int NC>
 __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
@@ -127,7 +119,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
     if (c < nchunk) Pack8<uint16_t>::load(w + 8 * c, wv[j]);
   }
   const float inv_n = 1.0f / (float)cols;
-  uint4 xn[NC], gn[NC];
+  uint4 xn[NC], gn[NC], rn[NC] = {};
   auto fetch = [&](int64_t row) {
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
@@ -135,17 +127,19 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
       if (c < nchunk) {
         xn[j] = *reinterpret_cast<const uint4*>(x + row * ldx + 8 * c);
         gn[j] = *reinterpret_cast<const uint4*>(dy + row * lddy + 8 * c);
+        if (dres) rn[j] = *reinterpret_cast<const uint4*>(dres + row * lddx + 8 * c);
       }
     }
   };
   int64_t row = r0 + wave;
   if (row < r1) fetch(row);
   for (; row < r1; row += kRowsPerBlock) {
-    uint4 xc[NC], gc[NC];
+    uint4 xc[NC], gc[NC], rc[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       xc[j] = xn[j];
       gc[j] = gn[j];
+      rc[j] = rn[j];
     }
     if (row + kRowsPerBlock < r1) fetch(row + kRowsPerBlock);
     const float r = rstd[row];
@@ -176,7 +170,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
         for (int e = 0; e < 8; ++e) o[e] = r * wv[j][e] * gv[e] - coef * xv[e];
         if (dres) {
           float rv[8];
-          Pack8<uint16_t>::load(dres + row * lddx + 8 * c, rv);
+          Pack8<uint16_t>::unpack(rc[j], rv);
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[e] += rv[e];
         }

@@ -13,6 +13,15 @@
 
 namespace {
 
+// 16-byte nontemporal load for operands that are streamed once (measured on
+// [16384, 5632]: forward 17 % faster; together with the one-row-per-grid-row
+// launch below, forward 106 -> 82 us and backward 180 -> 160 us).
+__device__ __forceinline__ uint4 ntl16(const uint16_t* p) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
 template <typename T>
@@ -28,19 +37,6 @@ __global__ void swiglu_fwd_kernel(const T* __restrict__ g, int64_t ldg, const T*
   }
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const f32x2_t f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-}
-// bf16 round trip through the hardware converter (round to nearest even).
-__device__ __forceinline__ float hw_round_bf(float x) { return bf2f((uint16_t)(pack_bf16x2(x, 0.f) & 0xffff)); }
-// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal.
-__device__ __forceinline__ float sigmoid_hw(float g) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
-}
 
 // Vector path: 8 bf16 per thread (16-byte accesses).  blockIdx.x covers a
 // row's 16-byte chunks, blockIdx.y strides over rows, so no index division.
@@ -52,19 +48,7 @@ __global__ void __launch_bounds__(256) swiglu_fwd_bf16x8_kernel(const uint16_t* 
   if (cc >= cpr) return;
   const int64_t c = (int64_t)cc << 3;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-    const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
-    const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
-    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
-    uint32_t ow[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float g0 = bf2f(gw[k] & 0xffff), g1 = bf2f(gw[k] >> 16);
-      const float u0 = bf2f(uw[k] & 0xffff), u1 = bf2f(uw[k] >> 16);
-      const float h0 = hw_round_bf(g0 * sigmoid_hw(g0)) * u0, h1 = hw_round_bf(g1 * sigmoid_hw(g1)) * u1;
-      ow[k] = pack_bf16x2(h0, h1);
-    }
-    *reinterpret_cast<uint4*>(h + r * ldh + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    *reinterpret_cast<uint4*>(h + r * ldh + c) = swiglu_fwd8(ntl16(g + r * ldg + c), ntl16(u + r * ldu + c));
   }
 }
 
@@ -99,9 +83,9 @@ __global__ void __launch_bounds__(256) swiglu_bwd_bf16x8_kernel(
   if (cc >= cpr) return;
   const int64_t c = (int64_t)cc << 3;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-    const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
-    const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
-    const uint4 hv = *reinterpret_cast<const uint4*>(dh + r * lddh + c);
+    const uint4 gv = ntl16(g + r * ldg + c);
+    const uint4 uv = ntl16(u + r * ldu + c);
+    const uint4 hv = ntl16(dh + r * lddh + c);
     const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
     const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
@@ -114,8 +98,8 @@ __global__ void __launch_bounds__(256) swiglu_bwd_bf16x8_kernel(
         const float gx = bf2f((uint16_t)(gw[k] >> (16 * e))), ux = bf2f((uint16_t)(uw[k] >> (16 * e)));
         const float dx = bf2f((uint16_t)(hw[k] >> (16 * e)));
         const float sig = sigmoid_hw(gx);
-        const float sl = hw_round_bf(gx * sig);
-        const float ds = hw_round_bf(dx * ux);
+        const float sl = round_bf(gx * sig);
+        const float ds = round_bf(dx * ux);
         duv[e] = dx * sl;
         dgv[e] = ds * sig * (1.0f + gx * (1.0f - sig));
       }
@@ -127,11 +111,13 @@ __global__ void __launch_bounds__(256) swiglu_bwd_bf16x8_kernel(
   }
 }
 
-// 2-D grid of the vector kernels: enough workgroups for ~16 per CU.
+// 2-D grid of the vector kernels: one row per grid row (rows past 65535 are
+// taken in strides), so each thread handles one 8-element chunk per row and
+// the hardware spreads the whole launch; measured faster than a grid sized to
+// the CUs with each thread looping over rows.
 inline dim3 vec_grid(int64_t rows, int cpr) {
   const int bx = (int)lz_cdiv(cpr, 256);
-  const int64_t by = std::min<int64_t>(rows, std::max<int64_t>(1, (int64_t)lz_num_cus() * 16 / bx));
-  return dim3((unsigned)bx, (unsigned)std::min<int64_t>(by, 65535));
+  return dim3((unsigned)bx, (unsigned)std::min<int64_t>(std::max<int64_t>(rows, 1), 65535));
 }
 
 inline int grid_for(int64_t n) {

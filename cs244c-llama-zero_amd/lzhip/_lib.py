@@ -62,6 +62,7 @@ SIGNATURES = {
     "lz_transpose": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "lz_copy2d": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp]),
     "lz_gemm_nt": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
+    "lz_gemm_swiglu": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "lz_gemm": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp,
                        _i64, _vp]),
     "lz_gemm_workspace": (_i64, [_i64, _i64, _i64, _i32, _i32]),

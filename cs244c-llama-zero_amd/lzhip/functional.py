@@ -234,15 +234,22 @@ class MLPFn(Function):
     epilogue."""
 
     @staticmethod
-    def forward(ctx, x, wg, wu, wd, residual):
+    def forward(ctx, x, wg, wu, wd, residual, grad_wanted=True):
         x2 = _rows(x)
         F_ = wg.shape[0]
         w = fused_weight([wg, wu])
-        gu = _linear_fwd(x2, w)                 # [T, 2F]
-        m = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
+        if ops.swiglu_fusable(x2, w):
+            # one kernel: the gate|up product and silu(gate) * up from its
+            # epilogue; gate|up is stored only when the backward needs it
+            gu = torch.empty((x2.shape[0], 2 * F_), dtype=x2.dtype, device=x2.device) if grad_wanted else None
+            m = ops.gemm_swiglu(x2, w, gu=gu)
+        else:
+            gu = _linear_fwd(x2, w)                 # [T, 2F]
+            m = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
         r2 = _rows(residual) if residual is not None else None
         y = _linear_fwd(m, wd, r2)
-        ctx.save_for_backward(x2, wg, wu, wd, gu, m)
+        if grad_wanted:
+            ctx.save_for_backward(x2, wg, wu, wd, gu, m)
         ctx.has_residual = residual is not None
         ctx.in_shape = x.shape
         return y.view(*x.shape[:-1], wd.shape[0])
@@ -263,7 +270,7 @@ class MLPFn(Function):
             dwg, dwu = dw[:F_], dw[F_:]
         dx = dx2.view(ctx.in_shape) if dx2 is not None else None
         dres = dy if (ctx.has_residual and ctx.needs_input_grad[4]) else None
-        return dx, dwg, dwu, dwd, dres
+        return dx, dwg, dwu, dwd, dres, None
 
 
 class SwiGLUPointwiseFn(Function):

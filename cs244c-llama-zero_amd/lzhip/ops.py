@@ -439,8 +439,9 @@ def transpose_padded(src2: torch.Tensor) -> torch.Tensor:
 class LaunchProbe:
     """Opt-in timing of GEMM launches with HIP events recorded on the launch
     stream: (flops, start, end, kernel key) per launch, the key being
-    (a_kmajor, b_kmajor, lz_gemm_plan code).  Used by the benchmark to measure
-    the MFMA kernel inside a timed training step."""
+    (a_kmajor, b_kmajor, lz_gemm_plan code), or (True, True, "swiglu") for the
+    fused gate|up + SwiGLU product.  Used by the benchmark to measure the MFMA
+    kernels inside a timed training step."""
 
     def __init__(self) -> None:
         self.records = []
@@ -463,6 +464,8 @@ class LaunchProbe:
 def gemm_kernel_name(key) -> str:
     """Kernel name (as profilers print it) of a LaunchProbe key."""
     ak, bk, code = key
+    if code == "swiglu":
+        return "gemm_swiglu_kernel"
     cfg, splits = code // 16, code % 16
     tf = lambda b: "true" if b else "false"
     if cfg == 5:
@@ -548,6 +551,44 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
         probe.add(2.0 * M * N * K, start, end, (bool(a_kmajor), bool(b_kmajor),
                                                 int(lib.lz_gemm_plan(M, N, Kp, int(a_kmajor), int(b_kmajor)))))
     return out
+
+
+def swiglu_fusable(x2: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether gemm_swiglu takes x2 [M, K] and w [2F, K]: M % 256, F % 128 and
+    K % 64 == 0, bf16, unit column stride and 16-byte aligned rows."""
+    if x2.dim() != 2 or w.dim() != 2 or x2.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        return False
+    M, K = x2.shape
+    n2, k2 = w.shape
+    if k2 != K or n2 % 256 or M % 256 or K % 64 or M == 0:
+        return False
+    return all(t.stride(1) == 1 and _row_stride(t) % 8 == 0 and t.data_ptr() % 16 == 0 for t in (x2, w))
+
+
+def gemm_swiglu(x2: torch.Tensor, w: torch.Tensor, gu: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """h = silu(x2 . w[:F]^T) * (x2 . w[F:]^T) ([M, F] bf16) for w = [gate; up]
+    ([2F, K]) in one kernel; the product x2 . w^T also goes to gu ([M, 2F])
+    when given.  Bit-identical to gemm(x2, w) followed by swiglu_fwd."""
+    require_gpu(x2, w, gu)
+    if not swiglu_fusable(x2, w):
+        raise ValueError(f"gemm_swiglu: unsupported shapes/layout x {tuple(x2.shape)}, w {tuple(w.shape)}")
+    M, K = x2.shape
+    F = w.shape[0] // 2
+    if gu is not None and (tuple(gu.shape) != (M, 2 * F) or gu.dtype != torch.bfloat16 or gu.stride(1) != 1
+                           or _row_stride(gu) % 8 or gu.data_ptr() % 16):
+        raise ValueError("gu must be an aligned bf16 [M, 2F] view")
+    h = torch.empty((M, F), dtype=torch.bfloat16, device=x2.device)
+    probe = _gemm_probe
+    if probe is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+    _lib.call("lz_gemm_swiglu", x2.data_ptr(), _row_stride(x2), w.data_ptr(), _row_stride(w), _ptr(gu),
+              _row_stride(gu) if gu is not None else 0, h.data_ptr(), F, M, F, K, stream_ptr(x2.device))
+    if probe is not None:
+        end.record()
+        probe.add(2.0 * M * 2 * F * K, start, end, (True, True, "swiglu"))
+    return h
 
 
 def ce_fwd(logits2: torch.Tensor, labels: torch.Tensor, seq: int, ignore_index: int = -100,

@@ -182,7 +182,8 @@ class SwiGLU(nn.Module):
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         _no_dropout(self.dropout.p, self.training, "mlp")
-        return LF.MLPFn.apply(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight, residual)
+        return LF.MLPFn.apply(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight, residual,
+                              torch.is_grad_enabled())
 
 
 class TransformerBlock(nn.Module):

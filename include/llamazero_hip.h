@@ -191,6 +191,14 @@ int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb
 /* lz_gemm with both operands K-major and no workspace. */
 int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype, const void* R,
                int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* stream);
+/* Fused gate/up projections + SwiGLU (model/llama.py:139-145: gate_proj(x),
+ * up_proj(x), silu(gate) * up): w = [gate rows; up rows] ([2F, K]);
+ * h = silu(x.Wg^T) * (x.Wu^T) as bf16 [M, F], and x.w^T itself to gu
+ * ([M, 2F], may be NULL).  Bit-identical to lz_gemm (bf16 out) followed by
+ * lz_swiglu_fwd.  Needs M % 256 == 0, F % 128 == 0, K % 64 == 0 and
+ * 16-byte aligned rows. */
+int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, void* gu, int64_t ldgu, void* h,
+                   int64_t ldh, int64_t M, int64_t F, int64_t K, void* stream);
 
 /* Causal GQA flash attention (model/llama.py:88-117: repeat_kv +
  * F.scaled_dot_product_attention(is_causal=True)).  lz_attn_path reports the

@@ -253,6 +253,39 @@ def test_swiglu_fwd_bwd(rows, cols, dtype):
     assert _rel_err(dgu[:, cols:], ur.grad) < tol
 
 
+@pytest.mark.parametrize("M,F_,K", [(256, 128, 64), (512, 384, 192), (768, 256, 2048)])
+def test_gemm_swiglu_fused_matches_unfused(M, F_, K):
+    """The fused gate|up GEMM + SwiGLU equals the unfused pair bit for bit
+    (gate|up and h), with and without the gate|up output, and h stays within
+    bf16 rounding of the float64 oracle on the same bf16 operands."""
+    g = _seed(M + F_ + K)
+    x = (0.5 * torch.randn(M, K, generator=g)).to(torch.bfloat16)
+    w = (0.05 * torch.randn(2 * F_, K, generator=g)).to(torch.bfloat16)
+    xd, wd = x.to(DEV), w.to(DEV)
+    gu_ref = ops.gemm(xd, wd)
+    h_ref = ops.swiglu_fwd(gu_ref[:, :F_], gu_ref[:, F_:])
+    gu = torch.full((M, 2 * F_), 7.0, dtype=torch.bfloat16, device=DEV)
+    h = ops.gemm_swiglu(xd, wd, gu=gu)
+    assert torch.equal(gu.cpu(), gu_ref.cpu())
+    assert torch.equal(h.cpu(), h_ref.cpu())
+    h2 = ops.gemm_swiglu(xd, wd)
+    assert torch.equal(h2.cpu(), h_ref.cpu())
+    prod = x.double() @ w.double().t()
+    want = R.swiglu(prod[:, :F_], prod[:, F_:])
+    diff = (h.cpu().double() - want).abs()
+    assert float(diff.max()) <= 2 ** -6 * float(want.abs().max() + 1)
+
+
+def test_gemm_swiglu_rejects_unsupported_shapes():
+    x = torch.zeros(300, 64, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(256, 64, dtype=torch.bfloat16, device=DEV)
+    assert not ops.swiglu_fusable(x, w)
+    with pytest.raises(ValueError):
+        ops.gemm_swiglu(x, w)
+    with pytest.raises(_lib.HipLibraryError):
+        _lib.call("lz_gemm_swiglu", x.data_ptr(), 64, w.data_ptr(), 64, 0, 0, x.data_ptr(), 128, 300, 128, 64, 0)
+
+
 # ---------------------------------------------------------------------------
 # Attention
 # ---------------------------------------------------------------------------
