@@ -106,7 +106,7 @@ __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t
 // logical tiles, and the logical order walks groups of kGroupM M-tiles across
 // all N-tiles so an XCD's concurrently running tiles share A rows and B rows.
 __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
-  constexpr int kXcd = 8, kGroupM = 8;
+  constexpr int kXcd = 8, kGroupM = 4;
   const int64_t nblk = tiles_m * tiles_n;
   if (nblk % kXcd == 0) pid = (pid % kXcd) * (nblk / kXcd) + pid / kXcd;
   const int64_t per_group = (int64_t)kGroupM * tiles_n;
