@@ -1062,6 +1062,38 @@ __global__ void __launch_bounds__(256) attn_delta_kernel(const T* __restrict__ o
   }
 }
 
+// bf16 vector path: CPR = hd / 8 consecutive lanes share one (b, s, h) row,
+// each loading 16 bytes of O and of dO (nontemporal: both are streamed
+// once), so a workgroup reads 256 x 16 contiguous bytes of each; the row's
+// partial sums meet through lane shuffles.  rows = B*S*H < 2^31.
+template <int CPR>
+__global__ void __launch_bounds__(256) attn_delta_vec_kernel(const uint16_t* __restrict__ o, int64_t ldo,
+                                                              const uint16_t* __restrict__ dout, int64_t lddo,
+                                                              float* __restrict__ delta, int S, int H, int rows) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int row = i / CPR, c = i % CPR;
+  float acc = 0.f;
+  if (row < rows) {
+    const int bs = row / H, h = row - bs * H;
+    const int64_t off = (int64_t)h * (CPR * 8) + c * 8;
+    const v4u ov = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(o + bs * ldo + off));
+    const v4u dv = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(dout + bs * lddo + off));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc = fmaf(bf2f(ov[k] & 0xffff), bf2f(dv[k] & 0xffff), acc);
+      acc = fmaf(bf2f(ov[k] >> 16), bf2f(dv[k] >> 16), acc);
+    }
+  }
+#pragma unroll
+  for (int m = CPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (row < rows && c == 0) {
+    const int bs = row / H, h = row - bs * H;
+    const int b = bs / S, s = bs - b * S;
+    delta[((int64_t)b * H + h) * S + s] = acc;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Generic path (any even head dim up to 256, bf16 or fp32): one wave per
 // query row (forward, dQ) or key row (dK/dV), lanes split the head dim, fp32
@@ -1328,7 +1360,17 @@ LZ_EXPORT int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_
   LZ_REQUIRE(B > 0 && S > 0 && H > 0 && hd > 0 && delta, "lz_attn_delta: bad arguments");
   const unsigned grid = (unsigned)lz_cdiv(B * S * H, 4);
   hipStream_t s = lz_stream(stream);
-  if (dtype == LZ_BF16)
+  const int64_t rows = B * S * H;
+  const bool vec = dtype == LZ_BF16 && (hd == 32 || hd == 64 || hd == 128 || hd == 256) && lz_aligned16(o) &&
+                   lz_aligned16(dout) && ldo % 8 == 0 && lddo % 8 == 0 && rows * (hd / 8) < (1ll << 31);
+  if (vec) {
+    const unsigned vgrid = (unsigned)lz_cdiv(rows * (hd / 8), 256);
+    const uint16_t *o16 = (const uint16_t*)o, *d16 = (const uint16_t*)dout;
+    if (hd == 32) attn_delta_vec_kernel<4><<<vgrid, 256, 0, s>>>(o16, ldo, d16, lddo, delta, (int)S, (int)H, (int)rows);
+    else if (hd == 64) attn_delta_vec_kernel<8><<<vgrid, 256, 0, s>>>(o16, ldo, d16, lddo, delta, (int)S, (int)H, (int)rows);
+    else if (hd == 128) attn_delta_vec_kernel<16><<<vgrid, 256, 0, s>>>(o16, ldo, d16, lddo, delta, (int)S, (int)H, (int)rows);
+    else attn_delta_vec_kernel<32><<<vgrid, 256, 0, s>>>(o16, ldo, d16, lddo, delta, (int)S, (int)H, (int)rows);
+  } else if (dtype == LZ_BF16)
     attn_delta_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)o, ldo, (const uint16_t*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);
   else if (dtype == LZ_F32)
     attn_delta_kernel<float><<<grid, 256, 0, s>>>((const float*)o, ldo, (const float*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);

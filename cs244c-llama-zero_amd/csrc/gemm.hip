@@ -705,17 +705,35 @@ struct SwigluOut {
   int64_t F;
 };
 
+// RoPE applied in the epilogue of the fused QKV projection: columns below
+// nrope are heads of 128 rotated with the bf16 cos/sin tables ([>= S, 128]),
+// at position m % S of output row m.
+struct RopeIn {
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int64_t S;
+  int64_t nrope;
+};
+
+enum { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
+
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
                                              f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t tn,
                                              char* smem, int lane, int wave);
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
+                                           f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t n0,
+                                           char* smem, int lane, int wave);
 
 // One workgroup's 256x256 tile of the direct-to-LDS GEMM (main loop, then the
-// epilogue).  kSwiGLU: the tile's 256 B rows are 128 gate rows and the
+// epilogue).  kEpiSwiGLU: the tile's 256 B rows are 128 gate rows and the
 // matching 128 up rows of a [gate; up] weight (o.F rows apart), and the
-// epilogue writes silu(gate) * up.
-template <int WM, int WN, bool AK, bool BK, int DBK, int NST, bool kSwiGLU>
-__device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o) {
+// epilogue writes silu(gate) * up.  kEpiRope: the epilogue rotates the tile's
+// columns below r.nrope as RoPE heads of 128.
+template <int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi>
+__device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o, const RopeIn& rope) {
+  constexpr bool kSwiGLU = kEpi == kEpiSwiGLU;
   constexpr int BM = 256, BN = 256;
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -874,6 +892,8 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
 
   if constexpr (kSwiGLU) {
     store_swiglu<BM, BN, WM, WN>(g, o, acc, m0, tn, smem, lane, wave);
+  } else if constexpr (kEpi == kEpiRope) {
+    store_rope<BM, BN, WM, WN>(g, rope, acc, m0, n0, smem, lane, wave);
   } else {
     GemmArgs go = g;  // split-K: this split's fp32 slab
     if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
@@ -883,13 +903,19 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
 
 template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
-  gemm_dma_tile<WM, WN, AK, BK, DBK, NST, false>(g, SwigluOut{});
+  gemm_dma_tile<WM, WN, AK, BK, DBK, NST, kEpiPlain>(g, SwigluOut{}, RopeIn{});
 }
 
 // Fused gate|up projection + SwiGLU (both operands K-major): tile (tm, tn)
 // covers rows 256 tm.. of x and gate/up columns 128 tn.. of the [M, F] result.
 __global__ void __launch_bounds__(512) gemm_swiglu_kernel(GemmArgs g, SwigluOut o) {
-  gemm_dma_tile<2, 4, true, true, 64, 2, true>(g, o);
+  gemm_dma_tile<2, 4, true, true, 64, 2, kEpiSwiGLU>(g, o, RopeIn{});
+}
+
+// Fused QKV projection + RoPE on the q and k heads (both operands K-major,
+// M and N multiples of 256, head dim 128).
+__global__ void __launch_bounds__(512) gemm_rope_kernel(GemmArgs g, RopeIn r) {
+  gemm_dma_tile<2, 4, true, true, 64, 2, kEpiRope>(g, SwigluOut{}, r);
 }
 
 // SwiGLU epilogue.  Each wave stages its 128x64 tile as bf16 in its own LDS
@@ -943,6 +969,80 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
     const uint4 gv = *reinterpret_cast<const uint4*>(sg + off);
     const uint4 uv = *reinterpret_cast<const uint4*>(su + off);
     *reinterpret_cast<uint4*>(o.h + (mrow0 + row) * o.ldh + col + chunk * 8) = swiglu_fwd8(gv, uv);
+  }
+}
+
+// RoPE epilogue.  Tiles at or past nrope (the v heads) take the plain store.
+// Otherwise each wave stages its 128x64 bf16 tile (the rounded GEMM output)
+// in LDS; after a workgroup barrier the waves holding the two halves of one
+// head (wn = 2j: columns 0-63 = x1, wn = 2j+1: columns 64-127 = x2) each take
+// half of the rows and write
+//   y1 = r(r(x1*c) + r(-x2*s)),  y2 = r(r(x2*c) + r(x1*s))
+// with the table row of the output row's position: the reference's bf16
+// per-op rounding, as the RoPE kernel computes it.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
+                                           f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t n0,
+                                           char* smem, int lane, int wave) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static_assert(WN == 4 && TN == 64, "a head of 128 is two 64-column waves");
+  if (n0 >= r.nrope) {
+    store_tile<BM, BN, WM, WN>(g, acc, m0, n0, smem, lane, wave);
+    return;
+  }
+  constexpr int kRow = TN * 2, kChunks = kRow / 16, kWaveBytes = TM * kRow, kHd = 2 * TN;
+  const int wm = wave / WN, wn = wave % WN;
+  const int frag_row = lane & 31, half = lane >> 5;
+  const int64_t mrow0 = m0 + wm * TM;
+  char* st = smem + wave * kWaveBytes;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = i * 32 + frag_row, chunk = j * 4 + q;
+        *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
+            make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                       pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
+      }
+  __syncthreads();
+  const int xw = wave & ~1;  // the wave holding x1 of this head
+  const char* s1 = smem + xw * kWaveBytes;
+  const char* s2 = s1 + kWaveBytes;
+  const int r0 = (wn & 1) ? TM / 2 : 0;
+  uint16_t* out = static_cast<uint16_t*>(g.C) + n0 + (wn >> 1) * kHd;
+#pragma unroll
+  for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
+    const int idx = t * 64 + lane, row = r0 + idx / kChunks, chunk = idx % kChunks;
+    const int off = row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4);
+    const uint4 av = *reinterpret_cast<const uint4*>(s1 + off);
+    const uint4 bv = *reinterpret_cast<const uint4*>(s2 + off);
+    const int64_t m = mrow0 + row;
+    const int64_t tab = (m % r.S) * kHd + chunk * 8;
+    const uint4 c1 = *reinterpret_cast<const uint4*>(r.cos + tab), c2 = *reinterpret_cast<const uint4*>(r.cos + tab + TN);
+    const uint4 n1 = *reinterpret_cast<const uint4*>(r.sin + tab), n2 = *reinterpret_cast<const uint4*>(r.sin + tab + TN);
+    const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+    const uint32_t c1w[4] = {c1.x, c1.y, c1.z, c1.w}, c2w[4] = {c2.x, c2.y, c2.z, c2.w};
+    const uint32_t s1w[4] = {n1.x, n1.y, n1.z, n1.w}, s2w[4] = {n2.x, n2.y, n2.z, n2.w};
+    uint32_t y1[4], y2[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float o1[2], o2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float a = bf2f((uint16_t)(aw[k] >> (16 * e))), b = bf2f((uint16_t)(bw[k] >> (16 * e)));
+        const float cc1 = bf2f((uint16_t)(c1w[k] >> (16 * e))), cc2 = bf2f((uint16_t)(c2w[k] >> (16 * e)));
+        const float ss1 = bf2f((uint16_t)(s1w[k] >> (16 * e))), ss2 = bf2f((uint16_t)(s2w[k] >> (16 * e)));
+        o1[e] = __fadd_rn(round_bf(__fmul_rn(a, cc1)), round_bf(__fmul_rn(-b, ss1)));
+        o2[e] = __fadd_rn(round_bf(__fmul_rn(b, cc2)), round_bf(__fmul_rn(a, ss2)));
+      }
+      y1[k] = pack_bf16x2(o1[0], o1[1]);
+      y2[k] = pack_bf16x2(o2[0], o2[1]);
+    }
+    uint16_t* dst = out + m * g.ldc + chunk * 8;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(y1[0], y1[1], y1[2], y1[3]);
+    *reinterpret_cast<uint4*>(dst + TN) = make_uint4(y2[0], y2[1], y2[2], y2[3]);
   }
 }
 
@@ -1197,4 +1297,50 @@ LZ_EXPORT int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t 
   g.slab = 0;
   gemm_swiglu_kernel<<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(g, SwigluOut{(uint16_t*)h, ldh, F});
   return lz_check_launch("lz_gemm_swiglu");
+}
+
+// Fused QKV projection + RoPE (reference model/llama.py:95-103: the q/k/v
+// projections and apply_rotary_pos_emb on q and k): out = x.w^T ([M, N]
+// bf16) with columns [0, nrope) rotated as heads of 128, row m at position
+// m % S of the bf16 cos/sin tables ([>= S, 128] each, halves duplicated as
+// the reference's cache is).  Every value equals lz_gemm (bf16 output)
+// followed by lz_rope on those columns.  Needs M % 256 == 0, N % 256 == 0,
+// nrope % 256 == 0, K % 64 == 0 and 16-byte aligned rows.
+LZ_EXPORT int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
+                           const void* cos_t, const void* sin_t, int64_t S, int64_t nrope, int64_t M, int64_t N,
+                           int64_t K, void* stream) {
+  LZ_REQUIRE(x && w && out && cos_t && sin_t, "lz_gemm_rope: null pointer");
+  LZ_REQUIRE(M > 0 && N > 0 && K > 0 && S > 0 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0,
+             "lz_gemm_rope: needs M %% 256, N %% 256 and K %% 64 == 0 (M %lld, N %lld, K %lld)", (long long)M,
+             (long long)N, (long long)K);
+  LZ_REQUIRE(nrope >= 0 && nrope <= N && nrope % 256 == 0, "lz_gemm_rope: nrope (%lld) must be a multiple of 256 <= N",
+             (long long)nrope);
+  LZ_REQUIRE(ldx >= K && ldw >= K && ldo >= N, "lz_gemm_rope: bad leading dimension");
+  LZ_REQUIRE(lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(out) && lz_aligned16(cos_t) && lz_aligned16(sin_t) &&
+                 ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0,
+             "lz_gemm_rope: rows must be 16-byte aligned");
+  const int64_t tiles = (M / 256) * (N / 256);
+  LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm_rope: too many tiles");
+  GemmArgs g{};
+  g.A = (const uint16_t*)x;
+  g.B = (const uint16_t*)w;
+  g.C = out;
+  g.R = nullptr;
+  g.lda = ldx;
+  g.ldb = ldw;
+  g.ldc = ldo;
+  g.ldr = 0;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.alpha = 1.f;
+  g.beta = 0.f;
+  g.c_f32 = 0;
+  g.vec_store = 1;
+  g.vec16 = 1;
+  g.kper = K;
+  g.slab = 0;
+  gemm_rope_kernel<<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(
+      g, RopeIn{(const uint16_t*)cos_t, (const uint16_t*)sin_t, S, nrope});
+  return lz_check_launch("lz_gemm_rope");
 }

@@ -183,8 +183,12 @@ class AttnProjFn(Function):
         hd = wq.shape[0] // n_heads
         h2 = _rows(h)
         w = fused_weight([wq, wk, wv])
-        qkv = _linear_fwd(h2, w)                         # [B*S, (H+2KV)*hd]
-        ops.rope_(qkv, S, n_heads + n_kv, hd, cos, sin)  # q and k heads, in place
+        nrope = (n_heads + n_kv) * hd
+        if ops.rope_fusable(h2, w, nrope, hd, cos):
+            qkv = ops.gemm_rope(h2, w, cos, sin, S, nrope)   # RoPE in the GEMM's epilogue
+        else:
+            qkv = _linear_fwd(h2, w)                         # [B*S, (H+2KV)*hd]
+            ops.rope_(qkv, S, n_heads + n_kv, hd, cos, sin)  # q and k heads, in place
         H, KV = n_heads, n_kv
         q2 = qkv[:, : H * hd]
         k2 = qkv[:, H * hd : (H + KV) * hd]

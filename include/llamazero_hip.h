@@ -199,6 +199,14 @@ int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, 
  * 16-byte aligned rows. */
 int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, void* gu, int64_t ldgu, void* h,
                    int64_t ldh, int64_t M, int64_t F, int64_t K, void* stream);
+/* Fused QKV projection + RoPE (model/llama.py:95-103: q/k/v_proj and
+ * apply_rotary_pos_emb on q and k): out = x.w^T ([M, N] bf16) with columns
+ * [0, nrope) rotated as heads of 128, output row m taking position m % S of
+ * the bf16 cos/sin tables ([>= S, 128]).  Bit-identical to lz_gemm (bf16 out)
+ * followed by lz_rope on those columns.  Needs M, N and nrope multiples of
+ * 256, K % 64 == 0 and 16-byte aligned rows. */
+int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo, const void* cos_t,
+                 const void* sin_t, int64_t S, int64_t nrope, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Causal GQA flash attention (model/llama.py:88-117: repeat_kv +
  * F.scaled_dot_product_attention(is_causal=True)).  lz_attn_path reports the

@@ -276,6 +276,32 @@ def test_gemm_swiglu_fused_matches_unfused(M, F_, K):
     assert float(diff.max()) <= 2 ** -6 * float(want.abs().max() + 1)
 
 
+@pytest.mark.parametrize("M,N,nrope,K,S", [(256, 512, 256, 64, 256), (512, 1024, 768, 192, 128), (768, 512, 512, 2048, 384)])
+def test_gemm_rope_fused_matches_unfused(M, N, nrope, K, S):
+    """The fused QKV GEMM + RoPE equals gemm followed by the RoPE kernel bit
+    for bit (rotated q/k columns and the plain v columns), and the rotation
+    matches the float64 oracle on the same bf16 product within bf16
+    rounding."""
+    g = _seed(M + N + K)
+    x = (0.5 * torch.randn(M, K, generator=g)).to(torch.bfloat16)
+    w = (0.05 * torch.randn(N, K, generator=g)).to(torch.bfloat16)
+    xd, wd = x.to(DEV), w.to(DEV)
+    hd = 128
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    cos, sin = ops.rope_table(S, hd, inv.to(DEV), torch.bfloat16)
+    ref = ops.gemm(xd, wd)
+    ops.rope_(ref, S, nrope // hd, hd, cos, sin)
+    got = ops.gemm_rope(xd, wd, cos, sin, S, nrope)
+    assert torch.equal(got.cpu(), ref.cpu())
+    prod = (x.double() @ w.double().t()).view(M // S, S, N)
+    heads = prod[:, :, :nrope].reshape(M // S, S, nrope // hd, hd).transpose(1, 2)
+    c64 = cos.cpu().double()[None, None]
+    s64 = sin.cpu().double()[None, None]
+    want = heads * c64 + torch.cat([-heads[..., hd // 2 :], heads[..., : hd // 2]], -1) * s64
+    got_h = got.cpu().double().view(M // S, S, N)[:, :, :nrope].reshape(M // S, S, nrope // hd, hd).transpose(1, 2)
+    assert float((got_h - want).abs().max()) <= 2 ** -6 * float(want.abs().max() + 1)
+
+
 def test_gemm_swiglu_rejects_unsupported_shapes():
     x = torch.zeros(300, 64, dtype=torch.bfloat16, device=DEV)
     w = torch.zeros(256, 64, dtype=torch.bfloat16, device=DEV)
@@ -336,6 +362,24 @@ def test_attention_fwd_bwd(B, S, H, KV, hd):
     assert _rel_err(dq, qr.grad) < 2e-2
     assert _rel_err(dk, kr.grad) < 2e-2
     assert _rel_err(dv, vr.grad) < 2e-2
+
+
+@pytest.mark.parametrize("B,S,H,hd,pad", [(2, 64, 4, 128, 0), (1, 96, 8, 64, 64), (2, 33, 3, 32, 0), (1, 40, 2, 256, 8),
+                                          (2, 24, 4, 48, 0)])
+def test_attention_delta(B, S, H, hd, pad):
+    """delta[b, h, s] = sum_d O * dO (the softmax-backward row term), fp32
+    sums of bf16 products: 1e-5 relative against float64, on the vector path
+    (hd 32..256, strided rows) and the element-wise one (hd 48)."""
+    g = _seed(B * S * H + hd)
+    ld = H * hd + pad
+    o = torch.randn(B * S, ld, generator=g).to(torch.bfloat16)
+    do = torch.randn(B * S, ld, generator=g).to(torch.bfloat16)
+    delta = torch.empty(B, H, S, dtype=torch.float32, device=DEV)
+    od, dod = o.to(DEV), do.to(DEV)
+    _lib.call("lz_attn_delta", od.data_ptr(), ld, dod.data_ptr(), ld, delta.data_ptr(), B, S, H, hd,
+              ops.dtype_code(od), 0)
+    want = (o[:, : H * hd].double() * do[:, : H * hd].double()).view(B, S, H, hd).sum(-1).permute(0, 2, 1)
+    assert _rel_err(delta, want) < 1e-5
 
 
 def test_attention_fp32_generic():
