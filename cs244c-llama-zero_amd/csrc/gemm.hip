@@ -744,6 +744,10 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   constexpr int kPerWave = kOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
   constexpr int kSlices = DBK / 16;
   static_assert(kPerWave * kLoadWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
+  // 8 or 16 stage loads per loading wave are the counts the tests exercise;
+  // an experiment with 32 per wave (two loading waves of eight) gave wrong
+  // products, so larger counts are refused until that is understood
+  static_assert(2 * kPerWave <= 16, "at most 16 stage loads per wave");
   static_assert(!kMid || (NST == 2 && kSlices == 4), "the mid-step barrier runs two stages of four slices");
   static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
   static_assert(kSlices == 2 || kSlices == 4, "stages hold 2 or 4 K slices");
