@@ -72,10 +72,13 @@ def run_steps(model, engine, batches, steps: int, warmup: int):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     losses = []
+    marks = [t0]
     for i in range(steps):
-        loss, _ = one(batches[(warmup + i) % len(batches)])
+        loss, _ = one(batches[(warmup + i) % len(batches)])  # reads the loss: the host waits for the step
         losses.append(loss)
+        marks.append(time.perf_counter())
     torch.cuda.synchronize()
+    run_steps.step_ms = [(b - a) * 1000.0 for a, b in zip(marks, marks[1:])]
     return time.perf_counter() - t0, losses
 
 
@@ -461,6 +464,8 @@ def main() -> int:
     finally:
         ops.set_gemm_probe(None)
     ms = elapsed * 1000.0 / args.steps
+    step_ms = sorted(run_steps.step_ms)
+    ms_median = step_ms[len(step_ms) // 2]
     tokens = B * S
     value = tokens * args.steps / elapsed
     model_flops = estimate_transformer_train_flops(cfg, B, S, stage=0)
@@ -527,6 +532,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_median": ms_median,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

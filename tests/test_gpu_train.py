@@ -138,6 +138,54 @@ def test_plumbing_100_steps_gradient_fidelity():
     assert min(cos) >= 0.999
 
 
+def test_fused_epilogues_30_steps_gradient_fidelity():
+    """The same per-step check (loss within 1e-2 relative, gradient cosine >=
+    0.999 at the reference trainer's parameters) on a shape that takes the
+    fused kernels: head dim 128 (the QKV GEMM with RoPE in its epilogue, the
+    LDS-tiled attention) and ffn 1024 with 512 tokens per micro-batch (the
+    gate|up GEMM with SwiGLU in its epilogue), 30 steps."""
+    from model import ModelConfig
+
+    steps, B, S, GA = 30, 2, 256, 1
+    cfg = ModelConfig(name="t", vocab_size=2000, max_seq_len=S, dim=512, n_layers=2, n_heads=4, n_kv_heads=2,
+                      ffn_dim=1024, rope_theta=10_000.0)
+    torch.manual_seed(1)
+    model = LlamaForCausalLM(cfg)
+    ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
+                  n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta,
+                  rope_angle_dtype=torch.bfloat16)
+    P = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
+    order = [n for n, _ in model.named_parameters()]
+    model = model.to(device=DEV, dtype=torch.bfloat16)
+    from lzhip import ops
+
+    w_gu = torch.cat([model.layers[0].mlp.gate_proj.weight, model.layers[0].mlp.up_proj.weight])
+    assert ops.swiglu_fusable(torch.empty(B * S, cfg.dim, dtype=torch.bfloat16, device=DEV), w_gu)
+    gen = OD.uniform_chunks(S, cfg.vocab_size, B, seed=1)
+    batches = [next(gen) for _ in range(steps * GA)]
+    rel, cos = [], []
+
+    def on_step(step, loss, gn, grads, params):
+        with torch.no_grad():
+            model.load_state_dict({k: v.to(torch.bfloat16) for k, v in params.items()}, strict=False)
+        model.zero_grad(set_to_none=True)
+        ids = batches[step - 1][:, :-1].contiguous().to(DEV)
+        l = model(input_ids=ids, labels=ids, return_logits=False).loss
+        l.backward()
+        g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
+        rel.append(abs(float(l) - loss) / abs(loss))
+        cos.append(float(F.cosine_similarity(g, _flat_grad(grads, order), dim=0)))
+
+    OE.train_reference(ocfg, P, iter(batches), steps=steps, grad_accum_steps=GA, lr=3e-4, betas=(0.9, 0.95),
+                       weight_decay=0.1, max_grad_norm=1.0, loss_chunk_size=0, on_step=on_step,
+                       param_dtype=torch.bfloat16)
+    print("per-step grad cosine:", " ".join(f"{c:.5f}" for c in cos))
+    print(f"max loss rel diff {max(rel):.2e}, min grad cosine {min(cos):.5f}")
+    assert len(cos) == steps
+    assert max(rel) <= 1e-2
+    assert min(cos) >= 0.999
+
+
 def test_plumbing_100_steps_free_running():
     """Both trainers on their own trajectories for 100 steps (HIP path in
     bf16; reference semantics with bf16 parameters / its fp32 path): loss
