@@ -1060,11 +1060,21 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
   const int64_t m = idx / n4, n = (idx - m * n4) * 4;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   const int64_t mn = g.M * g.N;
-  for (int sp = 0; sp < splits; ++sp) {
-    const float* row = slabs + sp * mn + m * g.N;
+  if (g.N % 4 == 0) {  // 16-byte slab reads (the workspace is 16-byte aligned)
+    for (int sp = 0; sp < splits; ++sp) {
+      const float4 x = *reinterpret_cast<const float4*>(slabs + sp * mn + m * g.N + n);
+      v[0] += x.x;
+      v[1] += x.y;
+      v[2] += x.z;
+      v[3] += x.w;
+    }
+  } else {
+    for (int sp = 0; sp < splits; ++sp) {
+      const float* row = slabs + sp * mn + m * g.N;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (n + e < g.N) v[e] += row[n + e];
+      for (int e = 0; e < 4; ++e)
+        if (n + e < g.N) v[e] += row[n + e];
+    }
   }
   store_out4(g, m, n, v);
 }
@@ -1095,17 +1105,22 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
     const double c128 = (double)lz_cdiv(small, 2 * cus) * 2.0 / 0.75;
     if (c128 < c256) p.cfg = 2;
   }
-  if (p.cfg != 2 && big < 2 * cus && K >= 2048) {
-    // Long K over few output tiles: split K so the grid covers the chip.
-    // Cost in units of one un-split tile: rounds of the grid over the CUs,
-    // each 1/S as long, plus a small charge per split for the slab traffic.
-    // Splits are whole multiples of 64 in K.
+  if (p.cfg != 2 && K >= 1024) {
+    // Long K: split it when that fills the chip better.  Cost in units of one
+    // 64-deep K step of one 256x256 tile on one CU (about 2 us): the grid's
+    // rounds over the CUs times the steps of one split plus 2 for a tile's
+    // prologue and epilogue; a split product also pays its fp32 slabs' round
+    // trip through HBM (written, then read by the reduce) and its output
+    // write, at about 10 MB per unit, plus 3 units for the reduce launch.
+    // Splits are whole multiples of 64 in K and at least 256 deep.
+    const double mn = (double)M * (double)N;
     double best = 1e30;
-    for (int sp = 1; sp <= 8; ++sp) {
+    for (int sp = 1; sp <= 32; ++sp) {
       const int64_t kper = lz_cdiv(lz_cdiv(K, sp), 64) * 64;
-      if (sp > 1 && kper < 512) break;
+      if (sp > 1 && kper < 256) break;
       if (lz_cdiv(K, kper) != sp) continue;
-      const double cost = (double)lz_cdiv(big * sp, cus) / sp + 0.05 * (sp - 1);
+      double cost = (double)lz_cdiv(big * sp, cus) * (double)(kper / 64 + 2);
+      if (sp > 1) cost += (2.0 * sp * mn * 4.0 + mn * 4.0) / 10e6 + 3.0;
       if (cost < best - 1e-9) {
         best = cost;
         p.splits = sp;
@@ -1172,13 +1187,13 @@ LZ_EXPORT int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajo
 }
 
 // The kernel lz_gemm launches for this shape and layout, encoded as
-// 16 * cfg + splits: cfg 5 = direct-to-LDS 256x256 tile with 8 waves,
+// 64 * cfg + splits: cfg 5 = direct-to-LDS 256x256 tile with 8 waves,
 // 0 / 1 = register-staged 256x256 with 8 / 4 waves, 2 = 128x128 with 4 waves;
 // splits = number of K slices (1 = unsplit; more need the workspace).
 LZ_EXPORT int lz_gemm_plan(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const Plan p = make_plan(M, N, K, a_kmajor != 0, b_kmajor != 0);
-  return 16 * p.cfg + p.splits;
+  return 64 * p.cfg + p.splits;
 }
 
 // C = alpha * sum_k A(m,k) B(n,k) (+ beta*C) (+ R), see the top of this file

@@ -469,7 +469,7 @@ def gemm_kernel_name(key) -> str:
         return "gemm_swiglu_kernel"
     if code == "rope":
         return "gemm_rope_kernel"
-    cfg, splits = code // 16, code % 16
+    cfg, splits = code // 64, code % 64
     tf = lambda b: "true" if b else "false"
     if cfg == 5:
         name = f"gemm_dma_kernel<2, 4, {tf(ak)}, {tf(bk)}, 64, 2>"

@@ -179,7 +179,7 @@ int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows
  * fp32 partial slabs in `ws` (lz_gemm_workspace bytes) and summed in a fixed
  * order; with a smaller workspace it runs unsplit. */
 int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor);
-/* The kernel lz_gemm picks for a shape and layout, as 16 * cfg + splits
+/* The kernel lz_gemm picks for a shape and layout, as 64 * cfg + splits
  * (cfg 5: direct-to-LDS 256x256 tile, 8 waves; 0 / 1: register-staged
  * 256x256, 8 / 4 waves; 2: 128x128, 4 waves; splits: K slices, 1 = unsplit).
  * Diagnostic only (used to attribute timings to kernels); no reference
