@@ -325,3 +325,31 @@ def test_library_defines_every_kernel_launch_stub():
     out = subprocess.run([nm, "-C", "--undefined-only", str(L.LIB_PATH)], capture_output=True, text=True, check=True)
     stubs = [line for line in out.stdout.splitlines() if "__device_stub__" in line]
     assert not stubs, stubs[:5]
+
+
+def test_gemm_plan_codes_and_workspace():
+    """lz_gemm_plan (host only, no launch): 64 * cfg + splits with a known
+    kernel configuration and 1..32 splits; the workspace is splits x M x N
+    fp32 exactly when the product is split; the benchmark decodes the same
+    names.  Weight gradients over 16384 tokens split, the 1B forward does
+    not."""
+    import lzhip._lib as L
+    from lzhip import ops
+
+    if not L.LIB_PATH.exists():
+        pytest.skip("libllamazero_hip.so not built (run __graft_entry__.build())")
+    lib = L.load()
+    shapes = [(4096, 2048, 16384, 0, 0), (768, 768, 16384, 0, 0), (32000, 768, 16384, 0, 0),
+              (16384, 2048, 5632, 1, 0), (16384, 4096, 2048, 1, 1), (16384, 1280, 768, 1, 1), (1000, 1000, 520, 0, 1)]
+    for M, N, K, ak, bk in shapes:
+        code = int(lib.lz_gemm_plan(M, N, K, ak, bk))
+        cfg, splits = code // 64, code % 64
+        assert cfg in (0, 1, 2, 5) and 1 <= splits <= 32, (M, N, K, code)
+        ws = int(lib.lz_gemm_workspace(M, N, K, ak, bk))
+        assert ws == (splits * M * N * 4 if splits > 1 else 0), (M, N, K, splits, ws)
+        name = ops.gemm_kernel_name((bool(ak), bool(bk), code))
+        assert name.startswith("gemm_dma_kernel<" if cfg == 5 else "gemm_kernel<")
+        assert ("split-K x%d" % splits in name) == (splits > 1)
+    assert int(lib.lz_gemm_plan(768, 768, 16384, 0, 0)) % 64 > 8  # the 125M weight gradient splits widely
+    assert int(lib.lz_gemm_plan(16384, 4096, 2048, 1, 1)) % 64 == 1
+    assert int(lib.lz_gemm_plan(0, 10, 10, 1, 1)) == 0
