@@ -687,7 +687,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
   dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
   for (int it = 0; it < nsteps; ++it) {
-    __syncthreads();  // this step's tiles landed (every wave's loads), last step's reads retired
+    dma_barrier();  // this step's tiles landed (every wave's loads), last step's reads retired
     if (it + 1 < nsteps) {
       char* nxt = smem + ((it + 1) & 1) * kStage;
       dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, nxt, wave, lane);
@@ -862,7 +862,7 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   const int nsteps = rep * nqs;
   dkdv8_issue<HD>(a, 0, nqs, qstart, b, g, rep, stages, wave, lane);
   for (int step = 0; step < nsteps; ++step) {
-    __syncthreads();  // this step's tiles (and the V tile) landed, last step's reads retired
+    dma_barrier();  // this step's tiles (and the V tile) landed, last step's reads retired
     if (step + 1 < nsteps)
       dkdv8_issue<HD>(a, step + 1, nqs, qstart, b, g, rep, stages + ((step + 1) & 1) * kStage, wave, lane);
     const int hq = step / nqs, q0 = qstart + (step - hq * nqs) * BQ;
@@ -985,7 +985,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
   dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
   for (int it = 0; it < nsteps; ++it) {
-    __syncthreads();  // this step's tiles landed (every wave's loads), last step's reads retired
+    dma_barrier();  // this step's tiles landed (every wave's loads), last step's reads retired
     if (it + 1 < nsteps) {
       char* nxt = smem + ((it + 1) & 1) * kStage;
       dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, nxt, wave, lane);

@@ -7,7 +7,8 @@
 // sequence, ignore_index targets and out-of-range targets contribute nothing.
 // With seq == 0 rows are scored against labels[r] (no shift).
 //
-// Forward: one workgroup per row, online log-sum-exp over 16-byte chunks,
+// Forward: one workgroup per row, online log-sum-exp over 16-byte chunks
+// (bf16 logits: in base 2 with the hardware exp2, about 1 ulp per term),
 // writes lse[r] and the row loss (lse - x[target]); a single-block reduction
 // then forms the mean deterministically.  Backward writes
 // (softmax - onehot) * grad / count per element; it may run in place over the
@@ -18,6 +19,7 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr float kLog2E = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ int64_t row_target(const int64_t* labels, int64_t r, int64_t seq, int64_t vocab,
                                               int64_t ignore_index) {
@@ -42,6 +44,8 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_kernel(const T* __restrict__ 
     const T* x = logits + r * ld;
     float m = -INFINITY, s = 0.f;
     if (kVec) {
+      // base-2 domain: u = x log2(e), s = sum 2^(u - m) with the hardware
+      // exp2 (libm expf made this pass ALU-bound); converted back below
       const int64_t nchunk = vocab >> 3;
       for (int64_t c = threadIdx.x; c < nchunk; c += kThreads) {
         float v[8];
@@ -49,18 +53,18 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_kernel(const T* __restrict__ 
         const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          v[2 * k] = bf2f(w[k] & 0xffff);
-          v[2 * k + 1] = bf2f(w[k] >> 16);
+          v[2 * k] = bf2f(w[k] & 0xffff) * kLog2E;
+          v[2 * k + 1] = bf2f(w[k] >> 16) * kLog2E;
         }
         float cm = v[0];
 #pragma unroll
         for (int k = 1; k < 8; ++k) cm = fmaxf(cm, v[k]);
         if (cm > m) {
-          s = s * expf(m - cm);
+          s = s * __builtin_amdgcn_exp2f(m - cm);
           m = cm;
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) s += expf(v[k] - m);
+        for (int k = 0; k < 8; ++k) s += __builtin_amdgcn_exp2f(v[k] - m);
       }
     } else {
       for (int64_t c = threadIdx.x; c < vocab; c += kThreads) {
@@ -73,10 +77,10 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_kernel(const T* __restrict__ 
       }
     }
     const float M = block_max(m, red);
-    const float part = (m == -INFINITY) ? 0.f : s * expf(m - M);
+    const float part = (m == -INFINITY) ? 0.f : s * (kVec ? __builtin_amdgcn_exp2f(m - M) : expf(m - M));
     const float S = block_sum(part, red);
     if (threadIdx.x == 0) {
-      const float lse = M + logf(S);
+      const float lse = kVec ? (M + log2f(S)) * kLn2 : M + logf(S);
       lse_out[r] = lse;
       const int64_t t = row_target(labels, r, seq, vocab, ignore_index);
       row_loss[r] = t >= 0 ? lse - Elem<T>::load(x, t) : 0.f;
@@ -142,8 +146,8 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(const T* logits, int64
           const int64_t v0 = 8 * c + 2 * k;
           float g0 = 0.f, g1 = 0.f;
           if (t >= 0) {
-            g0 = (expf(bf2f(w[k] & 0xffff) - l) - (v0 == t ? 1.f : 0.f)) * scale;
-            g1 = (expf(bf2f(w[k] >> 16) - l) - (v0 + 1 == t ? 1.f : 0.f)) * scale;
+            g0 = (__builtin_amdgcn_exp2f((bf2f(w[k] & 0xffff) - l) * kLog2E) - (v0 == t ? 1.f : 0.f)) * scale;
+            g1 = (__builtin_amdgcn_exp2f((bf2f(w[k] >> 16) - l) * kLog2E) - (v0 + 1 == t ? 1.f : 0.f)) * scale;
           }
           o[k] = (uint32_t)f2bf(g0) | ((uint32_t)f2bf(g1) << 16);
         }

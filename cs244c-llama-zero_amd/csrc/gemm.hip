@@ -672,13 +672,6 @@ __device__ __forceinline__ void sched_slice() {
   }
 }
 
-// s_waitcnt with only the vector-memory counter limited to N (gfx9 encoding:
-// vmcnt bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 // Direct-to-LDS kernel, any operand layouts: 256x256 tile, DBK-deep K steps
 // over NST LDS stages of 2 x 512 x DBK bytes.  NST == 2: one stage loads while
@@ -744,10 +737,6 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   constexpr int kPerWave = kOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
   constexpr int kSlices = DBK / 16;
   static_assert(kPerWave * kLoadWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
-  // 8 or 16 stage loads per loading wave are the counts the tests exercise;
-  // an experiment with 32 per wave (two loading waves of eight) gave wrong
-  // products, so larger counts are refused until that is understood
-  static_assert(2 * kPerWave <= 16, "at most 16 stage loads per wave");
   static_assert(!kMid || (NST == 2 && kSlices == 4), "the mid-step barrier runs two stages of four slices");
   static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
   static_assert(kSlices == 2 || kSlices == 4, "stages hold 2 or 4 K slices");
@@ -789,7 +778,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
       la.issue(smem, lwave, 0);
       lb.issue(smem + kOpBytes, lwave, 0);
     }
-    __syncthreads();
+    dma_barrier();
     if (ktiles > 1 && loader) {
       la.issue(smem + kStage, lwave, 1);
       lb.issue(smem + kStage + kOpBytes, lwave, 1);
@@ -807,10 +796,10 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
       dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
       sched_slice<kReads, FM * FN>();
       sched_slice<kReads, FM * FN>();
-      // the fence waits for this wave's loads of stage kt+1 and its reads of
-      // stage kt; past the barrier stage kt+1 is complete and no wave reads
-      // stage kt's slot any more, so stage kt+2 may refill it
-      __syncthreads();
+      // this wave's loads of stage kt+1 and its reads of stage kt are done;
+      // past the barrier stage kt+1 is complete and no wave reads stage kt's
+      // slot any more, so stage kt+2 may refill it
+      dma_barrier();
       if (kt + 2 < ktiles && loader) {
         char* nxt = smem + (kt & 1) * kStage;
         la.issue(nxt, lwave, kt + 2);
@@ -847,10 +836,10 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
       }
     for (int kt = 0; kt < ktiles; ++kt) {
       if constexpr (NST == 2) {
-        // only stage kt's loads are in flight here: the barrier's fence waits
-        // for them, publishes every wave's part and retires the reads of stage
+        // only stage kt's loads are in flight here: wait for them, then the
+        // barrier publishes every wave's part and retires the reads of stage
         // kt-1, whose slot is refilled next
-        __syncthreads();
+        dma_barrier();
       } else {
         // stage kt's loads are this wave's oldest: let the (up to NST-2) later
         // stages stay in flight, then the barrier publishes every wave's part

@@ -56,6 +56,25 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ uint16_t f2bf(float f) { return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu); }
 
+// s_waitcnt with only the vector-memory counter limited to N (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that publishes LDS written by this workgroup's
+// global_load_lds (direct-to-LDS) loads: each wave first waits until its own
+// loads have landed (vmcnt(0)), then the barrier orders every wave's reads
+// after every wave's loads.  __syncthreads() alone does not wait for these
+// loads: its fence covers stores and LDS instructions only, and the compiler
+// does not always add the wait.
+__device__ __forceinline__ void dma_barrier() {
+  wait_vmcnt<0>();
+  __syncthreads();
+}
+
 // Rounds a float to the nearest bfloat16 value, kept as float.
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 

@@ -218,6 +218,12 @@ __global__ void fill16_kernel(uint4* __restrict__ x, int64_t n16, uint4 value) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) x[i] = value;
 }
 
+// One 16-byte store per thread over the whole range (no loop for ranges up to
+// 2^39 bytes): the launch shape that measured fastest for streaming stores.
+inline int flat_grid(int64_t n16) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(lz_cdiv(n16, kThreads), (int64_t)INT32_MAX));
+}
+
 template <typename S, typename D>
 __global__ void cast_kernel(const S* __restrict__ src, D* __restrict__ dst, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -565,7 +571,7 @@ LZ_EXPORT int lz_fill(void* x, int dtype, int64_t n, double value, void* stream)
     const float f = (float)value;
     if (lz_aligned16(x) && n % 4 == 0) {
       uint32_t u = __builtin_bit_cast(uint32_t, f);
-      fill16_kernel<<<stream_grid(n / 4), kThreads, 0, s>>>((uint4*)x, n / 4, make_uint4(u, u, u, u));
+      fill16_kernel<<<flat_grid(n / 4), kThreads, 0, s>>>((uint4*)x, n / 4, make_uint4(u, u, u, u));
     } else {
       fill_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)x, n, f);
     }
@@ -575,7 +581,7 @@ LZ_EXPORT int lz_fill(void* x, int dtype, int64_t n, double value, void* stream)
     uint16_t h = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
     if (lz_aligned16(x) && n % 8 == 0) {
       uint32_t w = (uint32_t)h | ((uint32_t)h << 16);
-      fill16_kernel<<<stream_grid(n / 8), kThreads, 0, s>>>((uint4*)x, n / 8, make_uint4(w, w, w, w));
+      fill16_kernel<<<flat_grid(n / 8), kThreads, 0, s>>>((uint4*)x, n / 8, make_uint4(w, w, w, w));
     } else {
       fill_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, h);
     }

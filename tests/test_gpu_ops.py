@@ -149,6 +149,43 @@ def test_gemm_split_k_workspace_and_determinism():
     assert torch.allclose(c1, c3, rtol=1e-4, atol=1e-3)
 
 
+def test_gemm_and_attention_repeat_bit_identically():
+    """Every kernel that stages operands with direct-to-LDS loads must wait for
+    them before the barrier that publishes a stage; a missing wait reads a
+    stage that is still landing, which shows up as run-to-run differences.
+    Each product below (input gradient, split weight gradient, forward, the
+    attention forward and backward) is repeated and must match bit for bit."""
+    g = _seed(21)
+    dy = torch.randn(2048, 4096, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    x = torch.randn(2048, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    runs = {
+        "dgrad": lambda: ops.gemm(dy, w, True, False),
+        "wgrad": lambda: ops.gemm(dy, x, False, False, out_dtype=torch.float32),
+        "fwd": lambda: ops.gemm(x, w),
+    }
+    for name, fn in runs.items():
+        first = fn().cpu()
+        for _ in range(8):
+            assert torch.equal(fn().cpu(), first), name
+    B, S, H, KV, hd = 2, 1024, 8, 4, 128
+    ld = (H + 2 * KV) * hd
+    d = torch.randn(B * S, ld, generator=g).to(torch.bfloat16).to(DEV)
+    q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
+    do = torch.randn(B * S, H * hd, generator=g).to(torch.bfloat16).to(DEV)
+    o0, lse0 = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, hd**-0.5, None)
+    grads0 = None
+    for _ in range(6):
+        o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, hd**-0.5, None)
+        assert torch.equal(o, o0) and torch.equal(lse, lse0)
+        dqkv = torch.zeros_like(d)
+        ops.attn_bwd(q2, k2, v2, o, do, lse, B, S, H, KV, hd, hd**-0.5, dqkv[:, : H * hd],
+                     dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :])
+        if grads0 is None:
+            grads0 = dqkv.cpu()
+        assert torch.equal(dqkv.cpu(), grads0)
+
+
 def test_gemm_unaligned_mn_major_operands_fall_back():
     g = _seed(13)
     M, N, K = 37, 29, 45
