@@ -170,7 +170,7 @@ def fit_sweep(dev: torch.device, max_batch: int, seq: int = 2048, steps: int = 2
             "params": n_params, "device_memory_gib": total / 2**30, "sweep": rows}
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_dma_kernel_nt_1b_zero3_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_1b_zero3_traffic.md")
 
 
 def measured_traffic(kernel: str):
