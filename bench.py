@@ -186,6 +186,34 @@ def measured_traffic(kernel: str):
     return None
 
 
+def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev: torch.device) -> dict:
+    """The same workload with the whole step (both micro-batches, clip, AdamW
+    with a device-resident step count) replayed from one HIP graph; each timed
+    step copies its micro-batch ids into the graph's static inputs."""
+    from lzhip.graph import GraphedTrainStep
+    from lzhip.optim import FusedAdamW
+    from model import LlamaForCausalLM
+
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, capturable=True)
+    gs = GraphedTrainStep(model, opt, (B, S), GA, 1.0, dev)
+    for i in range(3):
+        gs.warmup(ids_all[GA * i:GA * (i + 1)])
+    gs.capture()
+    for i in range(3, 5):
+        gs(ids_all[GA * i:GA * (i + 1)])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        loss = gs(ids_all[GA * (5 + i):GA * (6 + i)])
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    return {"hip_graph_tokens_per_s": B * S * GA * steps / el, "hip_graph_ms_per_step": el * 1000 / steps,
+            "hip_graph_final_loss": float(loss)}
+
+
 def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: int = 3):
     """The CPU-runnable train.py workload (d256, 4 layers, 8/4 heads, ffn 688,
     vocab 32000, B=4, S=128, grad accumulation 2, AdamW lr 3e-4, clip 1.0,
@@ -229,6 +257,8 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
     res = {"workload": "train.py plumbing (d256 L4 8/4 heads ffn688 V32000), B=4 S=128 GA=2, 100 steps",
            "hip_tokens_per_s": B * S * GA * steps / el, "hip_ms_per_step": el * 1000 / steps,
            "hip_final_loss": float(loss)}
+    del model, opt
+    res.update(bench_plumbing_graph(cfg, ids_all, B, S, GA, steps, dev))
     if cpu:
         from oracle import engine as OE
         from oracle import model as OM

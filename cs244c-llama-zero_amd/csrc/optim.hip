@@ -43,11 +43,24 @@ __device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g,
   p = fmaf(a.neg_step, m / denom, p);
 }
 
+// The step-dependent factors from device memory (written by
+// adamw_step_kernel) when `hyper` is set: -lr/bc1, sqrt(bc2), 1 - lr*wd.
+__device__ __forceinline__ AdamArgs with_hyper(AdamArgs a, const float* hyper) {
+  if (hyper) {
+    a.neg_step = hyper[0];
+    a.sqrt_bc2 = hyper[1];
+    a.wd_factor = hyper[2];
+  }
+  return a;
+}
+
 template <typename G, typename PO>
 __global__ void __launch_bounds__(kThreads) adamw_scalar_kernel(float* __restrict__ p, float* __restrict__ m,
                                                                  float* __restrict__ v, const G* __restrict__ g,
-                                                                 PO* __restrict__ pout, int64_t n, AdamArgs a,
-                                                                 const float* __restrict__ scale_ptr) {
+                                                                 PO* __restrict__ pout, int64_t n, AdamArgs a0,
+                                                                 const float* __restrict__ scale_ptr,
+                                                                 const float* __restrict__ hyper) {
+  const AdamArgs a = with_hyper(a0, hyper);
   const float scale = scale_ptr ? *scale_ptr : 1.0f;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     float pp = p[i], mm = m[i], vv = v[i];
@@ -101,10 +114,12 @@ constexpr int kAdamThreads = 128;
 template <typename G, typename PO>
 __global__ void __launch_bounds__(kAdamThreads) adamw_vec_kernel(float* __restrict__ p, float* __restrict__ m,
                                                                   float* __restrict__ v, const G* __restrict__ g,
-                                                                  PO* __restrict__ pout, int64_t n4, AdamArgs a,
-                                                                  const float* __restrict__ scale_ptr) {
+                                                                  PO* __restrict__ pout, int64_t n4, AdamArgs a0,
+                                                                  const float* __restrict__ scale_ptr,
+                                                                  const float* __restrict__ hyper) {
   const int64_t q = (int64_t)blockIdx.x * kAdamThreads + threadIdx.x;
   if (q >= n4) return;
+  const AdamArgs a = with_hyper(a0, hyper);
   const int64_t i = q << 2;
   float pp[4], mm[4], vv[4], gg[4];
   Vec4<float>::load(p, i, pp);
@@ -125,7 +140,7 @@ __global__ void __launch_bounds__(kAdamThreads) adamw_vec_kernel(float* __restri
 
 template <typename G, typename PO>
 int launch_adamw(float* p, float* m, float* v, const void* g, void* pout, int64_t n, const AdamArgs& a,
-                 const float* scale, hipStream_t s) {
+                 const float* scale, const float* hyper, hipStream_t s) {
   const G* gp = static_cast<const G*>(g);
   PO* po = static_cast<PO*>(pout);
   const bool vec = lz_aligned16(p) && lz_aligned16(m) && lz_aligned16(v) &&
@@ -135,13 +150,13 @@ int launch_adamw(float* p, float* m, float* v, const void* g, void* pout, int64_
     const int64_t n4 = n / 4, tail = n - 4 * n4;
     LZ_REQUIRE(lz_cdiv(n4, kAdamThreads) < (1ll << 31), "lz_adamw: too many elements");
     if (n4 > 0)
-      adamw_vec_kernel<G, PO><<<(unsigned)lz_cdiv(n4, kAdamThreads), kAdamThreads, 0, s>>>(p, m, v, gp, po, n4, a, scale);
+      adamw_vec_kernel<G, PO><<<(unsigned)lz_cdiv(n4, kAdamThreads), kAdamThreads, 0, s>>>(p, m, v, gp, po, n4, a, scale, hyper);
     if (tail > 0)
       adamw_scalar_kernel<G, PO><<<1, kThreads, 0, s>>>(p + 4 * n4, m + 4 * n4, v + 4 * n4, gp + 4 * n4,
-                                                        po ? po + 4 * n4 : nullptr, tail, a, scale);
+                                                        po ? po + 4 * n4 : nullptr, tail, a, scale, hyper);
   } else {
     int grid = stream_grid(n);
-    adamw_scalar_kernel<G, PO><<<grid, kThreads, 0, s>>>(p, m, v, gp, po, n, a, scale);
+    adamw_scalar_kernel<G, PO><<<grid, kThreads, 0, s>>>(p, m, v, gp, po, n, a, scale, hyper);
   }
   return lz_check_launch("lz_adamw");
 }
@@ -512,10 +527,11 @@ int check_host_table(const int64_t* host, int nseg) {
 // read on the device) and optionally writing the updated parameter in a low
 // precision copy (p_out).  Hyper-parameters arrive as doubles, like the
 // reference's Python floats; bias corrections use `step` (1-based).
-LZ_EXPORT int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype,
-                            int64_t n, double lr, double beta1, double beta2, double eps, double weight_decay,
-                            int64_t step, const float* grad_scale, void* stream) {
-  LZ_REQUIRE(step >= 1, "lz_adamw: step must be >= 1");
+namespace {
+
+int adamw_entry(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype, int64_t n,
+                double lr, double beta1, double beta2, double eps, double weight_decay, int64_t step,
+                const float* grad_scale, const float* hyper, void* stream) {
   if (n == 0) return LZ_OK;
   LZ_REQUIRE(p && m && v && g && n > 0, "lz_adamw: bad arguments");
   const double bc1 = 1.0 - pow(beta1, (double)step);
@@ -534,12 +550,52 @@ LZ_EXPORT int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype,
   const bool gb = g_dtype == LZ_BF16;
   LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32, "lz_adamw: bad grad dtype %d", g_dtype);
   if (p_out == nullptr || p_out_dtype == LZ_F32) {
-    return gb ? launch_adamw<uint16_t, float>(p, m, v, g, p_out, n, a, grad_scale, s)
-              : launch_adamw<float, float>(p, m, v, g, p_out, n, a, grad_scale, s);
+    return gb ? launch_adamw<uint16_t, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s)
+              : launch_adamw<float, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
   }
   LZ_REQUIRE(p_out_dtype == LZ_BF16, "lz_adamw: bad output dtype %d", p_out_dtype);
-  return gb ? launch_adamw<uint16_t, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, s)
-            : launch_adamw<float, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, s);
+  return gb ? launch_adamw<uint16_t, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, hyper, s)
+            : launch_adamw<float, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+}
+
+// One thread: advances the device step counter and writes the factors that
+// depend on it, in the same double arithmetic as the host path of lz_adamw.
+__global__ void adamw_step_kernel(int64_t* __restrict__ step, double lr, double beta1, double beta2,
+                                  double weight_decay, float* __restrict__ hyper) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const int64_t t = *step + 1;
+  *step = t;
+  const double bc1 = 1.0 - pow(beta1, (double)t);
+  const double bc2 = 1.0 - pow(beta2, (double)t);
+  hyper[0] = (float)(-(lr / bc1));
+  hyper[1] = (float)sqrt(bc2);
+  hyper[2] = (float)(1.0 - lr * weight_decay);
+}
+
+}  // namespace
+
+LZ_EXPORT int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype,
+                            int64_t n, double lr, double beta1, double beta2, double eps, double weight_decay,
+                            int64_t step, const float* grad_scale, void* stream) {
+  LZ_REQUIRE(step >= 1, "lz_adamw: step must be >= 1");
+  return adamw_entry(p, m, v, g, g_dtype, p_out, p_out_dtype, n, lr, beta1, beta2, eps, weight_decay, step, grad_scale,
+                     nullptr, stream);
+}
+
+LZ_EXPORT int lz_adamw_step(int64_t* step, double lr, double beta1, double beta2, double weight_decay, float* hyper,
+                            void* stream) {
+  LZ_REQUIRE(step && hyper, "lz_adamw_step: null pointer");
+  adamw_step_kernel<<<1, 64, 0, lz_stream(stream)>>>(step, lr, beta1, beta2, weight_decay, hyper);
+  return lz_check_launch("lz_adamw_step");
+}
+
+LZ_EXPORT int lz_adamw_dev(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype,
+                           int64_t n, double beta1, double beta2, double eps, double weight_decay, const float* hyper,
+                           const float* grad_scale, void* stream) {
+  LZ_REQUIRE(hyper, "lz_adamw_dev: null step factors");
+  // lr and the step come from `hyper`; the host factors are placeholders
+  return adamw_entry(p, m, v, g, g_dtype, p_out, p_out_dtype, n, 0.0, beta1, beta2, eps, weight_decay, 1, grad_scale,
+                     hyper, stream);
 }
 
 LZ_EXPORT int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* stream) {

@@ -32,6 +32,8 @@ SIGNATURES = {
     "lz_version": (_i32, []),
     "lz_device_cus": (_i32, []),
     "lz_adamw": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _f64, _f64, _f64, _f64, _f64, _i64, _vp, _vp]),
+    "lz_adamw_step": (_i32, [_vp, _f64, _f64, _f64, _f64, _vp, _vp]),
+    "lz_adamw_dev": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _f64, _f64, _f64, _f64, _vp, _vp, _vp]),
     "lz_sumsq": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "lz_clip_finalize": (_i32, [_vp, _f32, _vp, _vp, _vp]),
     "lz_mt_gather": (_i32, [_vp, _i32, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),

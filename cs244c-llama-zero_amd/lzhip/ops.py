@@ -70,9 +70,12 @@ def adamw_(
     step: int,
     grad_scale: Optional[torch.Tensor] = None,
     p_out: Optional[torch.Tensor] = None,
+    hyper: Optional[torch.Tensor] = None,
 ) -> None:
-    """In-place fused AdamW on flat fp32 p/m/v with gradient g (fp32 or bf16)."""
-    require_gpu(p, m, v, g, grad_scale, p_out)
+    """In-place fused AdamW on flat fp32 p/m/v with gradient g (fp32 or bf16).
+    With `hyper` (float32 [3] on the device, written by adamw_step_) lr and
+    step are ignored: the step-dependent factors come from device memory."""
+    require_gpu(p, m, v, g, grad_scale, p_out, hyper)
     n = p.numel()
     for t, name in ((m, "exp_avg"), (v, "exp_avg_sq"), (g, "grad")):
         if t.numel() != n:
@@ -86,6 +89,17 @@ def adamw_(
         raise ValueError("grad_scale must be a float32 device scalar")
     if p_out is not None and (p_out.numel() != n or not p_out.is_contiguous()):
         raise ValueError("p_out must be contiguous with the same number of elements")
+    if hyper is not None:
+        if hyper.dtype != torch.float32 or hyper.numel() < 3:
+            raise ValueError("hyper must hold 3 float32 values")
+        _lib.call(
+            "lz_adamw_dev",
+            p.data_ptr(), m.data_ptr(), v.data_ptr(), g.data_ptr(), dtype_code(g),
+            _ptr(p_out), dtype_code(p_out) if p_out is not None else F32, n,
+            float(beta1), float(beta2), float(eps), float(weight_decay), hyper.data_ptr(),
+            _ptr(grad_scale), stream_ptr(p.device),
+        )
+        return
     _lib.call(
         "lz_adamw",
         p.data_ptr(), m.data_ptr(), v.data_ptr(), g.data_ptr(), dtype_code(g),
@@ -93,6 +107,18 @@ def adamw_(
         float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(step),
         _ptr(grad_scale), stream_ptr(p.device),
     )
+
+
+def adamw_step_(step: torch.Tensor, lr: float, beta1: float, beta2: float, weight_decay: float,
+                hyper: torch.Tensor) -> None:
+    """step (int64 device scalar) += 1 and hyper (float32 [3]) = the AdamW
+    factors of the new step, on the device: for optimizer steps replayed from
+    a HIP graph."""
+    require_gpu(step, hyper)
+    if step.dtype != torch.int64 or step.numel() != 1 or hyper.dtype != torch.float32 or hyper.numel() < 3:
+        raise ValueError("step must be one int64, hyper three float32 values")
+    _lib.call("lz_adamw_step", step.data_ptr(), float(lr), float(beta1), float(beta2), float(weight_decay),
+              hyper.data_ptr(), stream_ptr(step.device))
 
 
 def sumsq_(x: torch.Tensor, acc: torch.Tensor) -> None:

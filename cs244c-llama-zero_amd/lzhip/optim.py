@@ -20,12 +20,17 @@ from . import ops
 
 class FusedAdamW(torch.optim.Optimizer):
     def __init__(self, params: Iterable, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
-                 weight_decay: float = 1e-2) -> None:
+                 weight_decay: float = 1e-2, capturable: bool = False) -> None:
+        """capturable=True keeps each group's step count on the device
+        (advanced by a kernel each step), so that a step recorded in a HIP
+        graph (torch.cuda.graph) is correct on every replay; the learning rate
+        is then fixed at capture time."""
         if lr < 0.0 or eps < 0.0 or weight_decay < 0.0:
             raise ValueError("lr, eps and weight_decay must be non-negative")
         if not (0.0 <= betas[0] < 1.0 and 0.0 <= betas[1] < 1.0):
             raise ValueError(f"invalid betas {betas}")
         super().__init__(params, dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay))
+        self.capturable = bool(capturable)
         self._grad_scale: Optional[torch.Tensor] = None
         self._norm_buf: Optional[torch.Tensor] = None
 
@@ -61,6 +66,19 @@ class FusedAdamW(torch.optim.Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+        hypers = {}
+        if self.capturable:
+            for group in self.param_groups:
+                if not any(p.grad is not None for p in group["params"]):
+                    continue
+                dev = next(p.device for p in group["params"] if p.grad is not None)
+                if "step_dev" not in group:
+                    group["step_dev"] = torch.zeros((1,), dtype=torch.int64, device=dev)
+                    group["hyper_dev"] = ops.zeros((3,), torch.float32, dev)
+                beta1, beta2 = group["betas"]
+                ops.adamw_step_(group["step_dev"], group["lr"], beta1, beta2, group["weight_decay"],
+                                group["hyper_dev"])
+                hypers[id(group)] = group["hyper_dev"]
         for group, p in self._params_with_grad():
             ops.require_gpu(p)
             st = self.state[p]
@@ -80,8 +98,9 @@ class FusedAdamW(torch.optim.Optimizer):
                 target, out = p.data, None
             else:
                 target, out = master, p.data
+            hyper = hypers.get(id(group))
             ops.adamw_(target, st["exp_avg"], st["exp_avg_sq"], g, lr=group["lr"], beta1=beta1, beta2=beta2,
                        eps=group["eps"], weight_decay=group["weight_decay"], step=st["step"],
-                       grad_scale=self._grad_scale, p_out=out)
+                       grad_scale=self._grad_scale, p_out=out, hyper=hyper)
         self._grad_scale = None
         return loss

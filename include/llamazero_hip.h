@@ -50,6 +50,18 @@ int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype, void* p_o
              double lr, double beta1, double beta2, double eps, double weight_decay, int64_t step,
              const float* grad_scale, void* stream);
 
+/* Device-resident step count for callers that capture the optimizer in a HIP
+ * graph, where launch arguments are frozen (no reference counterpart; the
+ * reference's torch.optim.AdamW keeps the step on the host).
+ * lz_adamw_step advances *step (device int64) and writes hyper[3] =
+ * {-lr / (1 - beta1^t), sqrt(1 - beta2^t), 1 - lr * weight_decay} for the new
+ * t; lz_adamw_dev is lz_adamw with those three factors read from hyper. */
+int lz_adamw_step(int64_t* step, double lr, double beta1, double beta2, double weight_decay, float* hyper,
+                  void* stream);
+int lz_adamw_dev(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype, int64_t n,
+                 double beta1, double beta2, double eps, double weight_decay, const float* hyper,
+                 const float* grad_scale, void* stream);
+
 /* *acc += sum(x^2) (acc is a device double).  Replaces flat_grads.norm(2)
  * (zero/stage0_ddp.py:66) and sum(g*g) (zero/stage2_optimizer.py:162-166,
  * zero/stage3_optimizer.py:438-444). */

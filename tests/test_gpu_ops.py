@@ -523,6 +523,30 @@ def test_adamw_grad_scale_and_unaligned_views():
     assert _rel_err(pd, pr) < 1e-5
 
 
+def test_adamw_device_step_matches_host_step():
+    """adamw_step_ (step count and bias-correction factors on the device) then
+    adamw_ with those factors: bit-identical to adamw_ with the host step over
+    10 steps, and the device counter reads 10 at the end."""
+    g = _seed(21)
+    n = 300_007
+    p = 0.02 * torch.randn(n, generator=g)
+    ph, mh, vh = p.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+    pd, md, vd = p.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+    step = torch.zeros(1, dtype=torch.int64, device=DEV)
+    hyper = torch.zeros(3, dtype=torch.float32, device=DEV)
+    hp = dict(beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    for t in range(1, 11):
+        gr = (1e-3 * torch.randn(n, generator=g)).to(torch.bfloat16).to(DEV)
+        ops.adamw_(ph, mh, vh, gr, lr=3e-4, step=t, **hp)
+        ops.adamw_step_(step, 3e-4, 0.9, 0.95, 0.1, hyper)
+        ops.adamw_(pd, md, vd, gr, lr=0.0, step=1, hyper=hyper, **hp)
+    assert int(step.item()) == 10
+    bc1, bc2 = 1 - 0.9 ** 10, 1 - 0.95 ** 10
+    assert torch.allclose(hyper.cpu().double(), torch.tensor([-3e-4 / bc1, math.sqrt(bc2), 1 - 3e-5],
+                                                             dtype=torch.float64), rtol=1e-6, atol=0)
+    assert torch.equal(pd, ph) and torch.equal(md, mh) and torch.equal(vd, vh)
+
+
 def test_sumsq_and_clip():
     g = _seed(4)
     a = torch.randn(3_000_001, generator=g)
