@@ -1279,6 +1279,248 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_generic_kernel(GenArgs<T> a
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small head dims (16, 32): one lane per query row (forward, dQ) or key row
+// (dK/dV), holding that row, its accumulators and its running softmax in
+// registers; the other side's rows pass through LDS 64 at a time as fp32
+// (written by consecutive lanes, read by all lanes at one address, which
+// the LDS broadcasts).  A workgroup is one wave, so the barriers around each
+// chunk are cheap, and no lane reduction is needed anywhere.
+// ---------------------------------------------------------------------------
+
+// rows [row0, row0 + n) of base[., ld] (columns 0 .. HD) into dst[64][HD];
+// rows from n on are zero.  Lane l writes elements l, l + 64, ...  Every
+// load is unconditional (rows past n re-read row n-1), so they all issue
+// before the first wait.
+template <typename T, int HD>
+__device__ __forceinline__ void stage_rows(float* dst, const T* base, int64_t ld, int64_t row0, int n, int lane) {
+  float x[HD];
+#pragma unroll
+  for (int i = 0; i < HD; ++i) {
+    const int e = lane + 64 * i;
+    const int r = min(e / HD, n - 1), d = e % HD;
+    x[i] = Elem<T>::load(base + (row0 + r) * ld, d);
+  }
+#pragma unroll
+  for (int i = 0; i < HD; ++i) {
+    const int e = lane + 64 * i;
+    dst[e] = e / HD < n ? x[i] : 0.f;
+  }
+}
+
+// one row of HD values as fp32; rows the caller does not own read as zero
+template <typename T, int HD>
+__device__ __forceinline__ void load_row(float (&x)[HD], const T* p, bool own) {
+#pragma unroll
+  for (int d = 0; d < HD; ++d) x[d] = Elem<T>::load(p, d);
+#pragma unroll
+  for (int d = 0; d < HD; ++d) x[d] = own ? x[d] : 0.f;
+}
+
+template <int HD>
+__device__ __forceinline__ float dot_lds(const float (&x)[HD], const float* row) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < HD / 4; ++i) {
+    const float4 t = r4[i];
+    acc = fmaf(x[4 * i], t.x, acc);
+    acc = fmaf(x[4 * i + 1], t.y, acc);
+    acc = fmaf(x[4 * i + 2], t.z, acc);
+    acc = fmaf(x[4 * i + 3], t.w, acc);
+  }
+  return acc;
+}
+
+// acc = acc * c + p * row
+template <int HD>
+__device__ __forceinline__ void axpby_lds(float (&acc)[HD], float c, float p, const float* row) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+  for (int i = 0; i < HD / 4; ++i) {
+    const float4 t = r4[i];
+    acc[4 * i] = fmaf(p, t.x, acc[4 * i] * c);
+    acc[4 * i + 1] = fmaf(p, t.y, acc[4 * i + 1] * c);
+    acc[4 * i + 2] = fmaf(p, t.z, acc[4 * i + 2] * c);
+    acc[4 * i + 3] = fmaf(p, t.w, acc[4 * i + 3] * c);
+  }
+}
+
+// grid: B * H * ceil(S / 64) one-wave workgroups, query block fastest
+template <typename T, int HD>
+__global__ void __launch_bounds__(64) attn_fwd_lane_kernel(GenArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) float ks[64 * HD];
+  __shared__ __attribute__((aligned(16))) float vs[64 * HD];
+  const int lane = threadIdx.x;
+  const int nqb = (a.S + 63) / 64;
+  const int qb = (int)(blockIdx.x % nqb);
+  const int64_t bh = blockIdx.x / nqb;
+  const int h = (int)(bh % a.H), b = (int)(bh / a.H);
+  const int g = h / (a.H / a.KV);
+  const int s = qb * 64 + lane;
+  const bool valid = s < a.S;
+  const T* qp = a.q + ((int64_t)b * a.S + (valid ? s : 0)) * a.ldq + (int64_t)h * HD;
+  float q[HD], o[HD];
+  load_row<T, HD>(q, qp, valid);
+#pragma unroll
+  for (int d = 0; d < HD; ++d) o[d] = 0.f;
+  const T* kb = a.k + (int64_t)b * a.S * a.ldk + (int64_t)g * HD;
+  const T* vb = a.v + (int64_t)b * a.S * a.ldv + (int64_t)g * HD;
+  const int kv_end = min(a.S, qb * 64 + 64);
+  const int last = valid ? s : -1;  // causal: keys 0 .. s
+  float m = -INFINITY, l = 0.f;
+  for (int c0 = 0; c0 < kv_end; c0 += 64) {
+    const int n = min(64, kv_end - c0);
+    __syncthreads();  // the previous chunk's reads are done
+    stage_rows<T, HD>(ks, kb, a.ldk, c0, n, lane);
+    stage_rows<T, HD>(vs, vb, a.ldv, c0, n, lane);
+    __syncthreads();
+    const int jn = min(n, last - c0 + 1);
+    for (int j = 0; j < jn; ++j) {
+      const float sc = dot_lds<HD>(q, ks + j * HD) * a.scale;
+      const float m_new = fmaxf(m, sc);
+      const float corr = expf(m - m_new), p = expf(sc - m_new);
+      l = l * corr + p;
+      axpby_lds<HD>(o, corr, p, vs + j * HD);
+      m = m_new;
+    }
+  }
+  if (valid) {
+    T* op = a.o + ((int64_t)b * a.S + s) * a.ldo + (int64_t)h * HD;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) Elem<T>::store(op, d, o[d] * inv);
+    a.lse[((int64_t)b * a.H + h) * a.S + s] = m + logf(l);
+  }
+}
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(64) attn_bwd_dq_lane_kernel(GenArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) float ks[64 * HD];
+  __shared__ __attribute__((aligned(16))) float vs[64 * HD];
+  const int lane = threadIdx.x;
+  const int nqb = (a.S + 63) / 64;
+  const int qb = (int)(blockIdx.x % nqb);
+  const int64_t bh = blockIdx.x / nqb;
+  const int h = (int)(bh % a.H), b = (int)(bh / a.H);
+  const int g = h / (a.H / a.KV);
+  const int s = qb * 64 + lane;
+  const bool valid = s < a.S;
+  const int64_t row = (int64_t)b * a.S + (valid ? s : 0);
+  const T* qp = a.q + row * a.ldq + (int64_t)h * HD;
+  const T* dop = a.dout + row * a.lddo + (int64_t)h * HD;
+  float q[HD], dov[HD], acc[HD];
+  load_row<T, HD>(q, qp, valid);
+  load_row<T, HD>(dov, dop, valid);
+#pragma unroll
+  for (int d = 0; d < HD; ++d) acc[d] = 0.f;
+  const int64_t li = ((int64_t)b * a.H + h) * a.S + (valid ? s : 0);
+  const float lse = a.lse[li], D = a.delta[li];
+  const T* kb = a.k + (int64_t)b * a.S * a.ldk + (int64_t)g * HD;
+  const T* vb = a.v + (int64_t)b * a.S * a.ldv + (int64_t)g * HD;
+  const int kv_end = min(a.S, qb * 64 + 64);
+  const int last = valid ? s : -1;
+  for (int c0 = 0; c0 < kv_end; c0 += 64) {
+    const int n = min(64, kv_end - c0);
+    __syncthreads();
+    stage_rows<T, HD>(ks, kb, a.ldk, c0, n, lane);
+    stage_rows<T, HD>(vs, vb, a.ldv, c0, n, lane);
+    __syncthreads();
+    const int jn = min(n, last - c0 + 1);
+    for (int j = 0; j < jn; ++j) {
+      const float p = expf(dot_lds<HD>(q, ks + j * HD) * a.scale - lse);
+      const float ds = p * (dot_lds<HD>(dov, vs + j * HD) - D);
+      axpby_lds<HD>(acc, 1.f, ds, ks + j * HD);
+    }
+  }
+  if (valid) {
+    T* dqp = a.dq + ((int64_t)b * a.S + s) * a.lddq + (int64_t)h * HD;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) Elem<T>::store(dqp, d, acc[d] * a.scale);
+  }
+}
+
+// grid: B * KV * ceil(S / 64) one-wave workgroups; a lane owns one key row
+// and sums over the queries of every head in its group
+template <typename T, int HD>
+__global__ void __launch_bounds__(64) attn_bwd_dkdv_lane_kernel(GenArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) float qs[64 * HD];
+  __shared__ __attribute__((aligned(16))) float dos[64 * HD];
+  __shared__ float ls[64], dl[64];
+  const int lane = threadIdx.x;
+  const int nkb = (a.S + 63) / 64;
+  const int kbk = (int)(blockIdx.x % nkb);
+  const int64_t bg = blockIdx.x / nkb;
+  const int g = (int)(bg % a.KV), b = (int)(bg / a.KV);
+  const int rep = a.H / a.KV;
+  const int kv = kbk * 64 + lane;
+  const bool valid = kv < a.S;
+  const int64_t row = (int64_t)b * a.S + (valid ? kv : 0);
+  const T* kp = a.k + row * a.ldk + (int64_t)g * HD;
+  const T* vp = a.v + row * a.ldv + (int64_t)g * HD;
+  float kr[HD], vr[HD], dk[HD], dv[HD];
+  load_row<T, HD>(kr, kp, valid);
+  load_row<T, HD>(vr, vp, valid);
+#pragma unroll
+  for (int d = 0; d < HD; ++d) {
+    dk[d] = 0.f;
+    dv[d] = 0.f;
+  }
+  const int first = valid ? kv : a.S;  // causal: queries kv .. S-1
+  for (int hq = 0; hq < rep; ++hq) {
+    const int h = g * rep + hq;
+    const T* qb = a.q + (int64_t)b * a.S * a.ldq + (int64_t)h * HD;
+    const T* dob = a.dout + (int64_t)b * a.S * a.lddo + (int64_t)h * HD;
+    const int64_t li0 = ((int64_t)b * a.H + h) * a.S;
+    for (int c0 = kbk * 64; c0 < a.S; c0 += 64) {
+      const int n = min(64, a.S - c0);
+      __syncthreads();
+      stage_rows<T, HD>(qs, qb, a.ldq, c0, n, lane);
+      stage_rows<T, HD>(dos, dob, a.lddo, c0, n, lane);
+      const int lr = min(lane, n - 1);
+      const float lv = a.lse[li0 + c0 + lr], dvv = a.delta[li0 + c0 + lr];
+      ls[lane] = lv;
+      dl[lane] = dvv;
+      __syncthreads();
+      for (int j = max(0, first - c0); j < n; ++j) {
+        const float p = expf(dot_lds<HD>(kr, qs + j * HD) * a.scale - ls[j]);
+        const float ds = p * (dot_lds<HD>(vr, dos + j * HD) - dl[j]);
+        axpby_lds<HD>(dv, 1.f, p, dos + j * HD);
+        axpby_lds<HD>(dk, 1.f, ds, qs + j * HD);
+      }
+    }
+  }
+  if (valid) {
+    T* dkp = a.dk + row * a.lddk + (int64_t)g * HD;
+    T* dvp = a.dv + row * a.lddv + (int64_t)g * HD;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) {
+      Elem<T>::store(dkp, d, dk[d] * a.scale);
+      Elem<T>::store(dvp, d, dv[d]);
+    }
+  }
+}
+
+template <typename T>
+void launch_fwd_small(const GenArgs<T>& a, hipStream_t s) {
+  const unsigned grid = (unsigned)((int64_t)a.B * a.H * ((a.S + 63) / 64));
+  if (a.hd == 16) attn_fwd_lane_kernel<T, 16><<<grid, 64, 0, s>>>(a);
+  else attn_fwd_lane_kernel<T, 32><<<grid, 64, 0, s>>>(a);
+}
+
+template <typename T>
+void launch_bwd_small(const GenArgs<T>& a, hipStream_t s) {
+  const unsigned grid_q = (unsigned)((int64_t)a.B * a.H * ((a.S + 63) / 64));
+  const unsigned grid_kv = (unsigned)((int64_t)a.B * a.KV * ((a.S + 63) / 64));
+  if (a.hd == 16) {
+    attn_bwd_dq_lane_kernel<T, 16><<<grid_q, 64, 0, s>>>(a);
+    attn_bwd_dkdv_lane_kernel<T, 16><<<grid_kv, 64, 0, s>>>(a);
+  } else {
+    attn_bwd_dq_lane_kernel<T, 32><<<grid_q, 64, 0, s>>>(a);
+    attn_bwd_dkdv_lane_kernel<T, 32><<<grid_kv, 64, 0, s>>>(a);
+  }
+}
+
 bool mfma_ok(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, const void* q, const void* k,
              const void* v, const void* o) {
   return dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 &&
@@ -1342,13 +1584,15 @@ LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
     a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
-    attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
+    if (hd == 16 || hd == 32) launch_fwd_small(a, s);
+    else attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
     a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
     a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.o = (float*)o; a.ldo = ldo; a.lse = lse;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
-    attn_fwd_generic_kernel<float><<<grid, 256, 0, s>>>(a);
+    if (hd == 16 || hd == 32) launch_fwd_small(a, s);
+    else attn_fwd_generic_kernel<float><<<grid, 256, 0, s>>>(a);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_attn_fwd: bad dtype %d", dtype);
   }
@@ -1444,8 +1688,12 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.dout = (const uint16_t*)dout; a.lddo = lddo; a.delta = delta;
     a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
-    attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
-    attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
+    if (hd == 16 || hd == 32) {
+      launch_bwd_small(a, s);
+    } else {
+      attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
+      attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
+    }
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
     a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
@@ -1453,8 +1701,12 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.dout = (const float*)dout; a.lddo = lddo; a.delta = delta;
     a.dq = (float*)dq; a.dk = (float*)dk; a.dv = (float*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
-    attn_bwd_dq_generic_kernel<float><<<grid_q, 256, 0, s>>>(a);
-    attn_bwd_dkdv_generic_kernel<float><<<grid_kv, 256, 0, s>>>(a);
+    if (hd == 16 || hd == 32) {
+      launch_bwd_small(a, s);
+    } else {
+      attn_bwd_dq_generic_kernel<float><<<grid_q, 256, 0, s>>>(a);
+      attn_bwd_dkdv_generic_kernel<float><<<grid_kv, 256, 0, s>>>(a);
+    }
   } else {
     return lz_set_error(LZ_EINVAL, "lz_attn_bwd: bad dtype %d", dtype);
   }
