@@ -1280,49 +1280,58 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_generic_kernel(GenArgs<T> a
 }
 
 // ---------------------------------------------------------------------------
-// Small head dims (16, 32): one lane per query row (forward, dQ) or key row
-// (dK/dV), holding that row, its accumulators and its running softmax in
-// registers; the other side's rows pass through LDS 64 at a time as fp32
-// (written by consecutive lanes, read by all lanes at one address, which
-// the LDS broadcasts).  A workgroup is one wave, so the barriers around each
-// chunk are cheap, and no lane reduction is needed anywhere.
+// Small head dims (16, 32): four lanes (a quad) per query row (forward, dQ)
+// or key row (dK/dV), each holding a quarter of that row, its accumulators
+// and the row's running softmax in registers; a workgroup of four waves owns
+// 64 rows.  The other side's rows pass through LDS 64 at a time as fp32
+// (written by consecutive threads, read by the 16 quads of a wave at four
+// distinct addresses).  Dot products are summed over the quad with two DPP
+// steps, which give all four lanes the same bits.
 // ---------------------------------------------------------------------------
 
-// rows [row0, row0 + n) of base[., ld] (columns 0 .. HD) into dst[64][HD];
-// rows from n on are zero.  Lane l writes elements l, l + 64, ...  Every
-// load is unconditional (rows past n re-read row n-1), so they all issue
-// before the first wait.
+// rows [row0, row0 + n) of base[., ld] (columns 0 .. HD) into dst[64][HD] by
+// 256 threads; rows from n on are zero.  Every load is unconditional (rows
+// past n re-read row n-1), so they all issue before the first wait.
 template <typename T, int HD>
-__device__ __forceinline__ void stage_rows(float* dst, const T* base, int64_t ld, int64_t row0, int n, int lane) {
-  float x[HD];
+__device__ __forceinline__ void stage_rows(float* dst, const T* base, int64_t ld, int64_t row0, int n, int tid) {
+  constexpr int kPass = 64 * HD / 256;
+  float x[kPass];
 #pragma unroll
-  for (int i = 0; i < HD; ++i) {
-    const int e = lane + 64 * i;
+  for (int i = 0; i < kPass; ++i) {
+    const int e = tid + 256 * i;
     const int r = min(e / HD, n - 1), d = e % HD;
     x[i] = Elem<T>::load(base + (row0 + r) * ld, d);
   }
 #pragma unroll
-  for (int i = 0; i < HD; ++i) {
-    const int e = lane + 64 * i;
+  for (int i = 0; i < kPass; ++i) {
+    const int e = tid + 256 * i;
     dst[e] = e / HD < n ? x[i] : 0.f;
   }
 }
 
-// one row of HD values as fp32; rows the caller does not own read as zero
-template <typename T, int HD>
-__device__ __forceinline__ void load_row(float (&x)[HD], const T* p, bool own) {
+// DL values of a row from column c0 as fp32; rows the caller does not own
+// read as zero
+template <typename T, int DL>
+__device__ __forceinline__ void load_part(float (&x)[DL], const T* p, bool own) {
 #pragma unroll
-  for (int d = 0; d < HD; ++d) x[d] = Elem<T>::load(p, d);
+  for (int d = 0; d < DL; ++d) x[d] = Elem<T>::load(p, d);
 #pragma unroll
-  for (int d = 0; d < HD; ++d) x[d] = own ? x[d] : 0.f;
+  for (int d = 0; d < DL; ++d) x[d] = own ? x[d] : 0.f;
 }
 
-template <int HD>
-__device__ __forceinline__ float dot_lds(const float (&x)[HD], const float* row) {
+// sum over the four lanes of a quad (quad_perm [1,0,3,2] then [2,3,0,1])
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+  return x;
+}
+
+template <int DL>
+__device__ __forceinline__ float dot_part(const float (&x)[DL], const float* row) {
   const float4* r4 = reinterpret_cast<const float4*>(row);
   float acc = 0.f;
 #pragma unroll
-  for (int i = 0; i < HD / 4; ++i) {
+  for (int i = 0; i < DL / 4; ++i) {
     const float4 t = r4[i];
     acc = fmaf(x[4 * i], t.x, acc);
     acc = fmaf(x[4 * i + 1], t.y, acc);
@@ -1333,11 +1342,11 @@ __device__ __forceinline__ float dot_lds(const float (&x)[HD], const float* row)
 }
 
 // acc = acc * c + p * row
-template <int HD>
-__device__ __forceinline__ void axpby_lds(float (&acc)[HD], float c, float p, const float* row) {
+template <int DL>
+__device__ __forceinline__ void axpby_part(float (&acc)[DL], float c, float p, const float* row) {
   const float4* r4 = reinterpret_cast<const float4*>(row);
 #pragma unroll
-  for (int i = 0; i < HD / 4; ++i) {
+  for (int i = 0; i < DL / 4; ++i) {
     const float4 t = r4[i];
     acc[4 * i] = fmaf(p, t.x, acc[4 * i] * c);
     acc[4 * i + 1] = fmaf(p, t.y, acc[4 * i + 1] * c);
@@ -1346,24 +1355,24 @@ __device__ __forceinline__ void axpby_lds(float (&acc)[HD], float c, float p, co
   }
 }
 
-// grid: B * H * ceil(S / 64) one-wave workgroups, query block fastest
+// grid: B * H * ceil(S / 64) workgroups of 256, query block fastest
 template <typename T, int HD>
-__global__ void __launch_bounds__(64) attn_fwd_lane_kernel(GenArgs<T> a) {
+__global__ void __launch_bounds__(256) attn_fwd_quad_kernel(GenArgs<T> a) {
+  constexpr int DL = HD / 4;
   __shared__ __attribute__((aligned(16))) float ks[64 * HD];
   __shared__ __attribute__((aligned(16))) float vs[64 * HD];
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, qd = tid & 3, rl = tid >> 2;
   const int nqb = (a.S + 63) / 64;
   const int qb = (int)(blockIdx.x % nqb);
   const int64_t bh = blockIdx.x / nqb;
   const int h = (int)(bh % a.H), b = (int)(bh / a.H);
   const int g = h / (a.H / a.KV);
-  const int s = qb * 64 + lane;
+  const int s = qb * 64 + rl;
   const bool valid = s < a.S;
-  const T* qp = a.q + ((int64_t)b * a.S + (valid ? s : 0)) * a.ldq + (int64_t)h * HD;
-  float q[HD], o[HD];
-  load_row<T, HD>(q, qp, valid);
+  float q[DL], o[DL];
+  load_part<T, DL>(q, a.q + ((int64_t)b * a.S + (valid ? s : 0)) * a.ldq + (int64_t)h * HD + qd * DL, valid);
 #pragma unroll
-  for (int d = 0; d < HD; ++d) o[d] = 0.f;
+  for (int d = 0; d < DL; ++d) o[d] = 0.f;
   const T* kb = a.k + (int64_t)b * a.S * a.ldk + (int64_t)g * HD;
   const T* vb = a.v + (int64_t)b * a.S * a.ldv + (int64_t)g * HD;
   const int kv_end = min(a.S, qb * 64 + 64);
@@ -1372,48 +1381,47 @@ __global__ void __launch_bounds__(64) attn_fwd_lane_kernel(GenArgs<T> a) {
   for (int c0 = 0; c0 < kv_end; c0 += 64) {
     const int n = min(64, kv_end - c0);
     __syncthreads();  // the previous chunk's reads are done
-    stage_rows<T, HD>(ks, kb, a.ldk, c0, n, lane);
-    stage_rows<T, HD>(vs, vb, a.ldv, c0, n, lane);
+    stage_rows<T, HD>(ks, kb, a.ldk, c0, n, tid);
+    stage_rows<T, HD>(vs, vb, a.ldv, c0, n, tid);
     __syncthreads();
-    const int jn = min(n, last - c0 + 1);
+    const int jn = min(n, last - c0 + 1);  // the same for the four lanes of a row
     for (int j = 0; j < jn; ++j) {
-      const float sc = dot_lds<HD>(q, ks + j * HD) * a.scale;
+      const float sc = quad_sum(dot_part<DL>(q, ks + j * HD + qd * DL)) * a.scale;
       const float m_new = fmaxf(m, sc);
       const float corr = expf(m - m_new), p = expf(sc - m_new);
       l = l * corr + p;
-      axpby_lds<HD>(o, corr, p, vs + j * HD);
+      axpby_part<DL>(o, corr, p, vs + j * HD + qd * DL);
       m = m_new;
     }
   }
   if (valid) {
-    T* op = a.o + ((int64_t)b * a.S + s) * a.ldo + (int64_t)h * HD;
+    T* op = a.o + ((int64_t)b * a.S + s) * a.ldo + (int64_t)h * HD + qd * DL;
     const float inv = 1.f / l;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) Elem<T>::store(op, d, o[d] * inv);
-    a.lse[((int64_t)b * a.H + h) * a.S + s] = m + logf(l);
+    for (int d = 0; d < DL; ++d) Elem<T>::store(op, d, o[d] * inv);
+    if (qd == 0) a.lse[((int64_t)b * a.H + h) * a.S + s] = m + logf(l);
   }
 }
 
 template <typename T, int HD>
-__global__ void __launch_bounds__(64) attn_bwd_dq_lane_kernel(GenArgs<T> a) {
+__global__ void __launch_bounds__(256) attn_bwd_dq_quad_kernel(GenArgs<T> a) {
+  constexpr int DL = HD / 4;
   __shared__ __attribute__((aligned(16))) float ks[64 * HD];
   __shared__ __attribute__((aligned(16))) float vs[64 * HD];
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, qd = tid & 3, rl = tid >> 2;
   const int nqb = (a.S + 63) / 64;
   const int qb = (int)(blockIdx.x % nqb);
   const int64_t bh = blockIdx.x / nqb;
   const int h = (int)(bh % a.H), b = (int)(bh / a.H);
   const int g = h / (a.H / a.KV);
-  const int s = qb * 64 + lane;
+  const int s = qb * 64 + rl;
   const bool valid = s < a.S;
   const int64_t row = (int64_t)b * a.S + (valid ? s : 0);
-  const T* qp = a.q + row * a.ldq + (int64_t)h * HD;
-  const T* dop = a.dout + row * a.lddo + (int64_t)h * HD;
-  float q[HD], dov[HD], acc[HD];
-  load_row<T, HD>(q, qp, valid);
-  load_row<T, HD>(dov, dop, valid);
+  float q[DL], dov[DL], acc[DL];
+  load_part<T, DL>(q, a.q + row * a.ldq + (int64_t)h * HD + qd * DL, valid);
+  load_part<T, DL>(dov, a.dout + row * a.lddo + (int64_t)h * HD + qd * DL, valid);
 #pragma unroll
-  for (int d = 0; d < HD; ++d) acc[d] = 0.f;
+  for (int d = 0; d < DL; ++d) acc[d] = 0.f;
   const int64_t li = ((int64_t)b * a.H + h) * a.S + (valid ? s : 0);
   const float lse = a.lse[li], D = a.delta[li];
   const T* kb = a.k + (int64_t)b * a.S * a.ldk + (int64_t)g * HD;
@@ -1423,46 +1431,46 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_lane_kernel(GenArgs<T> a) {
   for (int c0 = 0; c0 < kv_end; c0 += 64) {
     const int n = min(64, kv_end - c0);
     __syncthreads();
-    stage_rows<T, HD>(ks, kb, a.ldk, c0, n, lane);
-    stage_rows<T, HD>(vs, vb, a.ldv, c0, n, lane);
+    stage_rows<T, HD>(ks, kb, a.ldk, c0, n, tid);
+    stage_rows<T, HD>(vs, vb, a.ldv, c0, n, tid);
     __syncthreads();
     const int jn = min(n, last - c0 + 1);
     for (int j = 0; j < jn; ++j) {
-      const float p = expf(dot_lds<HD>(q, ks + j * HD) * a.scale - lse);
-      const float ds = p * (dot_lds<HD>(dov, vs + j * HD) - D);
-      axpby_lds<HD>(acc, 1.f, ds, ks + j * HD);
+      const float* kr = ks + j * HD + qd * DL;
+      const float p = expf(quad_sum(dot_part<DL>(q, kr)) * a.scale - lse);
+      const float ds = p * (quad_sum(dot_part<DL>(dov, vs + j * HD + qd * DL)) - D);
+      axpby_part<DL>(acc, 1.f, ds, kr);
     }
   }
   if (valid) {
-    T* dqp = a.dq + ((int64_t)b * a.S + s) * a.lddq + (int64_t)h * HD;
+    T* dqp = a.dq + ((int64_t)b * a.S + s) * a.lddq + (int64_t)h * HD + qd * DL;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) Elem<T>::store(dqp, d, acc[d] * a.scale);
+    for (int d = 0; d < DL; ++d) Elem<T>::store(dqp, d, acc[d] * a.scale);
   }
 }
 
-// grid: B * KV * ceil(S / 64) one-wave workgroups; a lane owns one key row
-// and sums over the queries of every head in its group
+// grid: B * KV * ceil(S / 64) workgroups of 256; a quad owns one key row and
+// sums over the queries of every head in its group
 template <typename T, int HD>
-__global__ void __launch_bounds__(64) attn_bwd_dkdv_lane_kernel(GenArgs<T> a) {
+__global__ void __launch_bounds__(256) attn_bwd_dkdv_quad_kernel(GenArgs<T> a) {
+  constexpr int DL = HD / 4;
   __shared__ __attribute__((aligned(16))) float qs[64 * HD];
   __shared__ __attribute__((aligned(16))) float dos[64 * HD];
   __shared__ float ls[64], dl[64];
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, qd = tid & 3, rl = tid >> 2;
   const int nkb = (a.S + 63) / 64;
   const int kbk = (int)(blockIdx.x % nkb);
   const int64_t bg = blockIdx.x / nkb;
   const int g = (int)(bg % a.KV), b = (int)(bg / a.KV);
   const int rep = a.H / a.KV;
-  const int kv = kbk * 64 + lane;
+  const int kv = kbk * 64 + rl;
   const bool valid = kv < a.S;
   const int64_t row = (int64_t)b * a.S + (valid ? kv : 0);
-  const T* kp = a.k + row * a.ldk + (int64_t)g * HD;
-  const T* vp = a.v + row * a.ldv + (int64_t)g * HD;
-  float kr[HD], vr[HD], dk[HD], dv[HD];
-  load_row<T, HD>(kr, kp, valid);
-  load_row<T, HD>(vr, vp, valid);
+  float kr[DL], vr[DL], dk[DL], dv[DL];
+  load_part<T, DL>(kr, a.k + row * a.ldk + (int64_t)g * HD + qd * DL, valid);
+  load_part<T, DL>(vr, a.v + row * a.ldv + (int64_t)g * HD + qd * DL, valid);
 #pragma unroll
-  for (int d = 0; d < HD; ++d) {
+  for (int d = 0; d < DL; ++d) {
     dk[d] = 0.f;
     dv[d] = 0.f;
   }
@@ -1475,26 +1483,30 @@ __global__ void __launch_bounds__(64) attn_bwd_dkdv_lane_kernel(GenArgs<T> a) {
     for (int c0 = kbk * 64; c0 < a.S; c0 += 64) {
       const int n = min(64, a.S - c0);
       __syncthreads();
-      stage_rows<T, HD>(qs, qb, a.ldq, c0, n, lane);
-      stage_rows<T, HD>(dos, dob, a.lddo, c0, n, lane);
-      const int lr = min(lane, n - 1);
-      const float lv = a.lse[li0 + c0 + lr], dvv = a.delta[li0 + c0 + lr];
-      ls[lane] = lv;
-      dl[lane] = dvv;
+      stage_rows<T, HD>(qs, qb, a.ldq, c0, n, tid);
+      stage_rows<T, HD>(dos, dob, a.lddo, c0, n, tid);
+      if (tid < 64) {
+        const int lr = min(tid, n - 1);
+        const float lv = a.lse[li0 + c0 + lr], dvv = a.delta[li0 + c0 + lr];
+        ls[tid] = lv;
+        dl[tid] = dvv;
+      }
       __syncthreads();
       for (int j = max(0, first - c0); j < n; ++j) {
-        const float p = expf(dot_lds<HD>(kr, qs + j * HD) * a.scale - ls[j]);
-        const float ds = p * (dot_lds<HD>(vr, dos + j * HD) - dl[j]);
-        axpby_lds<HD>(dv, 1.f, p, dos + j * HD);
-        axpby_lds<HD>(dk, 1.f, ds, qs + j * HD);
+        const float* qr = qs + j * HD + qd * DL;
+        const float* dr = dos + j * HD + qd * DL;
+        const float p = expf(quad_sum(dot_part<DL>(kr, qr)) * a.scale - ls[j]);
+        const float ds = p * (quad_sum(dot_part<DL>(vr, dr)) - dl[j]);
+        axpby_part<DL>(dv, 1.f, p, dr);
+        axpby_part<DL>(dk, 1.f, ds, qr);
       }
     }
   }
   if (valid) {
-    T* dkp = a.dk + row * a.lddk + (int64_t)g * HD;
-    T* dvp = a.dv + row * a.lddv + (int64_t)g * HD;
+    T* dkp = a.dk + row * a.lddk + (int64_t)g * HD + qd * DL;
+    T* dvp = a.dv + row * a.lddv + (int64_t)g * HD + qd * DL;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) {
+    for (int d = 0; d < DL; ++d) {
       Elem<T>::store(dkp, d, dk[d] * a.scale);
       Elem<T>::store(dvp, d, dv[d]);
     }
@@ -1504,8 +1516,8 @@ __global__ void __launch_bounds__(64) attn_bwd_dkdv_lane_kernel(GenArgs<T> a) {
 template <typename T>
 void launch_fwd_small(const GenArgs<T>& a, hipStream_t s) {
   const unsigned grid = (unsigned)((int64_t)a.B * a.H * ((a.S + 63) / 64));
-  if (a.hd == 16) attn_fwd_lane_kernel<T, 16><<<grid, 64, 0, s>>>(a);
-  else attn_fwd_lane_kernel<T, 32><<<grid, 64, 0, s>>>(a);
+  if (a.hd == 16) attn_fwd_quad_kernel<T, 16><<<grid, 256, 0, s>>>(a);
+  else attn_fwd_quad_kernel<T, 32><<<grid, 256, 0, s>>>(a);
 }
 
 template <typename T>
@@ -1513,11 +1525,11 @@ void launch_bwd_small(const GenArgs<T>& a, hipStream_t s) {
   const unsigned grid_q = (unsigned)((int64_t)a.B * a.H * ((a.S + 63) / 64));
   const unsigned grid_kv = (unsigned)((int64_t)a.B * a.KV * ((a.S + 63) / 64));
   if (a.hd == 16) {
-    attn_bwd_dq_lane_kernel<T, 16><<<grid_q, 64, 0, s>>>(a);
-    attn_bwd_dkdv_lane_kernel<T, 16><<<grid_kv, 64, 0, s>>>(a);
+    attn_bwd_dq_quad_kernel<T, 16><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_quad_kernel<T, 16><<<grid_kv, 256, 0, s>>>(a);
   } else {
-    attn_bwd_dq_lane_kernel<T, 32><<<grid_q, 64, 0, s>>>(a);
-    attn_bwd_dkdv_lane_kernel<T, 32><<<grid_kv, 64, 0, s>>>(a);
+    attn_bwd_dq_quad_kernel<T, 32><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_quad_kernel<T, 32><<<grid_kv, 256, 0, s>>>(a);
   }
 }
 

@@ -431,7 +431,7 @@ def test_attention_delta(B, S, H, hd, pad):
 
 @pytest.mark.parametrize("hd,S,H,KV", [(32, 130, 4, 2), (16, 64, 2, 1), (32, 1, 2, 2)])
 def test_attention_fp32_small_head(hd, S, H, KV):
-    """Head dims 16 and 32 (one lane per row, rows staged through LDS) in
+    """Head dims 16 and 32 (a quad of lanes per row, rows staged through LDS) in
     fp32: output, lse and all three gradients within 1e-5 of float64, over
     several 64-row chunks, a ragged tail, GQA and a one-token sequence."""
     g = _seed(hd * S + H)
