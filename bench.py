@@ -458,6 +458,8 @@ def main() -> int:
                          "out of memory or --fit-max-batch; prints one JSON line and exits")
     ap.add_argument("--fit-max-batch", type=int, default=64)
     ap.add_argument("--skip-plumbing", action="store_true", help="skip the train.py plumbing leg")
+    ap.add_argument("--plumbing-only", action="store_true",
+                    help="only the train.py plumbing leg (eager and HIP-graph replay); prints its JSON and exits")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the 1B ZeRO-3 step (no recompute=False, 125M, AdamW or pointwise legs)")
     args = ap.parse_args()
@@ -472,6 +474,12 @@ def main() -> int:
     import lzhip
     from lzhip import ops
     from profiler import estimate_transformer_train_flops
+
+    if args.plumbing_only:
+        lzhip.load()
+        print(json.dumps({"plumbing_train_py": bench_plumbing(torch.device("cuda:0"),
+                                                              cpu=not args.no_cpu_baseline)}), flush=True)
+        return 0
 
     lzhip.load()
     dev = torch.device("cuda:0")
