@@ -518,6 +518,83 @@ int check_host_table(const int64_t* host, int nseg) {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Multi-tensor AdamW and sum of squares: one launch over up to kMultiSegs
+// tensors, whose pointers travel by value in the kernel arguments.  Every
+// workgroup takes one chunk of kMultiChunk elements of one tensor (chunks are
+// numbered tensor after tensor; chunk0 holds each tensor's first chunk), so
+// the element math is exactly that of the one-tensor kernels.
+// ---------------------------------------------------------------------------
+constexpr int kMultiSegs = 24;
+constexpr int64_t kMultiChunk = 4096;
+
+struct MultiSegs {
+  int64_t p[kMultiSegs], m[kMultiSegs], v[kMultiSegs], g[kMultiSegs], po[kMultiSegs];
+  int64_t numel[kMultiSegs];
+  int64_t chunk0[kMultiSegs + 1];
+  int n;
+};
+
+// the tensor whose chunk range holds chunk c (the last with chunk0 <= c)
+__device__ __forceinline__ int multi_segment(const int64_t* chunk0, int n, int64_t c) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (chunk0[mid] <= c) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename G, typename PO>
+__global__ void __launch_bounds__(kThreads) adamw_multi_kernel(const MultiSegs t, AdamArgs a0,
+                                                               const float* __restrict__ scale_ptr,
+                                                               const float* __restrict__ hyper) {
+  const AdamArgs a = with_hyper(a0, hyper);
+  const float scale = scale_ptr ? *scale_ptr : 1.0f;
+  const int64_t c = blockIdx.x;
+  const int sg = multi_segment(t.chunk0, t.n, c);
+  const int64_t i0 = (c - t.chunk0[sg]) * kMultiChunk, i1 = min(i0 + kMultiChunk, t.numel[sg]);
+  float* p = reinterpret_cast<float*>(t.p[sg]);
+  float* m = reinterpret_cast<float*>(t.m[sg]);
+  float* v = reinterpret_cast<float*>(t.v[sg]);
+  const G* g = reinterpret_cast<const G*>(t.g[sg]);
+  PO* po = reinterpret_cast<PO*>(t.po[sg]);
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    float pp = p[i], mm = m[i], vv = v[i];
+    float gg = Elem<G>::load(g, i);
+    if (scale_ptr) gg = gg * scale;
+    adam_elem(pp, mm, vv, gg, a);
+    p[i] = pp;
+    m[i] = mm;
+    v[i] = vv;
+    if (po) Elem<PO>::store(po, i, pp);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) sumsq_multi_kernel(const MultiSegs t, double* __restrict__ acc) {
+  __shared__ double red[kThreads / 64];
+  const int64_t c = blockIdx.x;
+  const int sg = multi_segment(t.chunk0, t.n, c);
+  const int64_t i0 = (c - t.chunk0[sg]) * kMultiChunk, i1 = min(i0 + kMultiChunk, t.numel[sg]);
+  const T* x = reinterpret_cast<const T*>(t.g[sg]);
+  float local = 0.f;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    const float e = Elem<T>::load(x, i);
+    local = fmaf(e, e, local);
+  }
+  double d = wave_sum_d((double)local);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = d;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int w = 0; w < kThreads / 64; ++w) sum += red[w];
+    atomicAdd(acc, sum);
+  }
+}
+
 // ===========================================================================
 // Exported entry points.
 // ===========================================================================
@@ -611,6 +688,105 @@ LZ_EXPORT int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* s
     return lz_set_error(LZ_EINVAL, "lz_sumsq: bad dtype %d", dtype);
   }
   return lz_check_launch("lz_sumsq");
+}
+
+namespace {
+
+// Fills `t` with rows [r0, r1) of a host table of `cols` int64 columns (the
+// tensor pointer columns given by `ptr_cols`, numel last), skipping empty
+// tensors; returns the number of chunks.
+int64_t fill_multi(MultiSegs& t, const int64_t* table, int cols, int r0, int r1) {
+  t = MultiSegs{};
+  int64_t chunks = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int64_t* row = table + (int64_t)r * cols;
+    const int64_t n = row[cols - 1];
+    if (n <= 0) continue;
+    const int k = t.n++;
+    if (cols == 6) {
+      t.p[k] = row[0];
+      t.m[k] = row[1];
+      t.v[k] = row[2];
+      t.g[k] = row[3];
+      t.po[k] = row[4];
+    } else {
+      t.g[k] = row[0];
+    }
+    t.numel[k] = n;
+    t.chunk0[k] = chunks;
+    chunks += lz_cdiv(n, kMultiChunk);
+  }
+  t.chunk0[t.n] = chunks;
+  return chunks;
+}
+
+}  // namespace
+
+// AdamW over nseg tensors in one launch per 24 tensors: table holds nseg rows
+// {p (fp32 master), m, v, g, p_out (0 = none), numel}; every row shares
+// g_dtype and p_out_dtype.  The same update as lz_adamw on each tensor, bit
+// for bit.  With hyper set (written by lz_adamw_step) lr and step are unused.
+LZ_EXPORT int lz_adamw_multi(const int64_t* table, int nseg, int g_dtype, int p_out_dtype, double lr, double beta1,
+                             double beta2, double eps, double weight_decay, int64_t step, const float* hyper,
+                             const float* grad_scale, void* stream) {
+  LZ_REQUIRE(table && nseg >= 0, "lz_adamw_multi: bad table");
+  LZ_REQUIRE(hyper || step >= 1, "lz_adamw_multi: step must be >= 1");
+  LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32, "lz_adamw_multi: bad grad dtype %d", g_dtype);
+  LZ_REQUIRE(p_out_dtype == LZ_BF16 || p_out_dtype == LZ_F32, "lz_adamw_multi: bad output dtype %d", p_out_dtype);
+  for (int r = 0; r < nseg; ++r) {
+    const int64_t* row = table + (int64_t)r * 6;
+    LZ_REQUIRE(row[5] >= 0, "lz_adamw_multi: negative size in row %d", r);
+    LZ_REQUIRE(row[5] == 0 || (row[0] && row[1] && row[2] && row[3]), "lz_adamw_multi: null pointer in row %d", r);
+  }
+  const double bc1 = 1.0 - pow(beta1, (double)(hyper ? 1 : step));
+  const double bc2 = 1.0 - pow(beta2, (double)(hyper ? 1 : step));
+  AdamArgs a;
+  a.beta1 = (float)beta1;
+  a.beta2 = (float)beta2;
+  a.omb1 = (float)(1.0 - beta1);
+  a.omb2 = (float)(1.0 - beta2);
+  a.wd_factor = (float)(1.0 - lr * weight_decay);
+  a.apply_wd = weight_decay != 0.0;
+  a.sqrt_bc2 = (float)sqrt(bc2);
+  a.eps = (float)eps;
+  a.neg_step = (float)(-(lr / bc1));
+  hipStream_t s = lz_stream(stream);
+  const bool gb = g_dtype == LZ_BF16, ob = p_out_dtype == LZ_BF16;
+  for (int r0 = 0; r0 < nseg; r0 += kMultiSegs) {
+    MultiSegs t;
+    const int64_t chunks = fill_multi(t, table, 6, r0, min(nseg, r0 + kMultiSegs));
+    if (chunks == 0) continue;
+    LZ_REQUIRE(chunks < (1ll << 31), "lz_adamw_multi: too many chunks");
+    const unsigned grid = (unsigned)chunks;
+    if (gb && ob) adamw_multi_kernel<uint16_t, uint16_t><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    else if (gb) adamw_multi_kernel<uint16_t, float><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    else if (ob) adamw_multi_kernel<float, uint16_t><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    else adamw_multi_kernel<float, float><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    int rc = lz_check_launch("lz_adamw_multi");
+    if (rc) return rc;
+  }
+  return LZ_OK;
+}
+
+// *acc += sum of squares over nseg tensors of one dtype (table rows {x, numel}),
+// one launch per 24 tensors.
+LZ_EXPORT int lz_sumsq_multi(const int64_t* table, int nseg, int dtype, double* acc, void* stream) {
+  LZ_REQUIRE(table && nseg >= 0 && acc, "lz_sumsq_multi: bad arguments");
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_sumsq_multi: bad dtype %d", dtype);
+  for (int r = 0; r < nseg; ++r)
+    LZ_REQUIRE(table[2 * r + 1] >= 0 && (table[2 * r + 1] == 0 || table[2 * r]), "lz_sumsq_multi: bad row %d", r);
+  hipStream_t s = lz_stream(stream);
+  for (int r0 = 0; r0 < nseg; r0 += kMultiSegs) {
+    MultiSegs t;
+    const int64_t chunks = fill_multi(t, table, 2, r0, min(nseg, r0 + kMultiSegs));
+    if (chunks == 0) continue;
+    LZ_REQUIRE(chunks < (1ll << 31), "lz_sumsq_multi: too many chunks");
+    if (dtype == LZ_BF16) sumsq_multi_kernel<uint16_t><<<(unsigned)chunks, kThreads, 0, s>>>(t, acc);
+    else sumsq_multi_kernel<float><<<(unsigned)chunks, kThreads, 0, s>>>(t, acc);
+    int rc = lz_check_launch("lz_sumsq_multi");
+    if (rc) return rc;
+  }
+  return LZ_OK;
 }
 
 LZ_EXPORT int lz_clip_finalize(const double* acc, float max_norm, float* norm_out, float* scale_out, void* stream) {

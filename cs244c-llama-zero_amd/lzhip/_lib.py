@@ -35,6 +35,8 @@ SIGNATURES = {
     "lz_adamw_step": (_i32, [_vp, _f64, _f64, _f64, _f64, _vp, _vp]),
     "lz_adamw_dev": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _f64, _f64, _f64, _f64, _vp, _vp, _vp]),
     "lz_sumsq": (_i32, [_vp, _i32, _i64, _vp, _vp]),
+    "lz_adamw_multi": (_i32, [_vp, _i32, _i32, _i32, _f64, _f64, _f64, _f64, _f64, _i64, _vp, _vp, _vp]),
+    "lz_sumsq_multi": (_i32, [_vp, _i32, _i32, _vp, _vp]),
     "lz_clip_finalize": (_i32, [_vp, _f32, _vp, _vp, _vp]),
     "lz_mt_gather": (_i32, [_vp, _i32, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),
     "lz_mt_scatter": (_i32, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp]),

@@ -131,6 +131,61 @@ def sumsq_(x: torch.Tensor, acc: torch.Tensor) -> None:
     _lib.call("lz_sumsq", x.data_ptr(), dtype_code(x), x.numel(), acc.data_ptr(), stream_ptr(x.device))
 
 
+def sumsq_multi_(xs: Sequence[torch.Tensor], acc: torch.Tensor) -> None:
+    """acc (float64 device scalar) += sum of x^2 over every tensor in xs
+    (contiguous, one dtype), one launch per 24 tensors."""
+    require_gpu(acc, *xs)
+    if acc.dtype != torch.float64:
+        raise ValueError("accumulator must be float64")
+    if not xs:
+        return
+    dt = xs[0].dtype
+    rows = []
+    for x in xs:
+        if x.dtype != dt or not x.is_contiguous():
+            raise ValueError("sumsq_multi_ needs contiguous tensors of one dtype")
+        rows += [x.data_ptr(), x.numel()]
+    table = (ctypes.c_int64 * len(rows))(*rows)
+    _lib.call("lz_sumsq_multi", ctypes.addressof(table), len(xs), dtype_code(xs[0]), acc.data_ptr(),
+              stream_ptr(acc.device))
+
+
+def adamw_multi_(ps, ms, vs, gs, p_outs, lr: float, beta1: float, beta2: float, eps: float, weight_decay: float,
+                 step: int, grad_scale: Optional[torch.Tensor] = None, hyper: Optional[torch.Tensor] = None) -> None:
+    """adamw_ on every (p, m, v, g, p_out) in one launch per 24 tensors: fp32
+    p/m/v, gradients of one dtype, p_out all None or all of one dtype.  The
+    same bits as adamw_ tensor by tensor."""
+    n = len(ps)
+    if not (len(ms) == len(vs) == len(gs) == len(p_outs) == n):
+        raise ValueError("adamw_multi_: list lengths differ")
+    if n == 0:
+        return
+    require_gpu(*ps, *ms, *vs, *gs, grad_scale, hyper)
+    gdt = gs[0].dtype
+    odt = None if p_outs[0] is None else p_outs[0].dtype
+    rows = []
+    for p, m, v, g, po in zip(ps, ms, vs, gs, p_outs):
+        if p.dtype != torch.float32 or m.dtype != torch.float32 or v.dtype != torch.float32:
+            raise ValueError("p, m and v must be float32")
+        if g.dtype != gdt or (None if po is None else po.dtype) != odt:
+            raise ValueError("adamw_multi_: mixed gradient or output dtypes")
+        k = p.numel()
+        if m.numel() != k or v.numel() != k or g.numel() != k or (po is not None and po.numel() != k):
+            raise ValueError("adamw_multi_: size mismatch")
+        for t in (p, m, v, g, po):
+            if t is not None and not t.is_contiguous():
+                raise ValueError("adamw_multi_ needs contiguous tensors")
+        if po is not None:
+            require_gpu(po)
+        rows += [p.data_ptr(), m.data_ptr(), v.data_ptr(), g.data_ptr(), _ptr(po) or 0, k]
+    if hyper is not None and (hyper.dtype != torch.float32 or hyper.numel() < 3):
+        raise ValueError("hyper must hold 3 float32 values")
+    table = (ctypes.c_int64 * len(rows))(*rows)
+    _lib.call("lz_adamw_multi", ctypes.addressof(table), n, dtype_code(gs[0]),
+              F32 if odt is None else _DTYPES[odt], float(lr), float(beta1), float(beta2), float(eps),
+              float(weight_decay), int(step), _ptr(hyper), _ptr(grad_scale), stream_ptr(ps[0].device))
+
+
 def clip_finalize(acc: torch.Tensor, max_norm: float, norm_out: torch.Tensor, scale_out: torch.Tensor) -> None:
     require_gpu(acc, norm_out, scale_out)
     _lib.call(

@@ -3,7 +3,8 @@ trainer (reference train.py:206-211,259-271: torch.optim.AdamW with
 clip_grad_norm_).
 
 FusedAdamW implements torch.optim.AdamW's update (decoupled weight decay,
-bias-corrected moments) with one kernel launch per parameter.  Parameters in a
+bias-corrected moments) with one multi-tensor kernel launch per 24
+parameters.  Parameters in a
 low-precision dtype get an fp32 master copy and fp32 moments; the kernel writes
 the rounded parameter back.  clip_grad_norm_() computes the global gradient
 norm and the clip factor on the device; the factor is folded into the next
@@ -51,9 +52,12 @@ class FusedAdamW(torch.optim.Optimizer):
         if dev is None:
             return torch.zeros((), dtype=torch.float32)
         acc = ops.zeros((1,), torch.float64, dev)
+        by_dtype = {}
         for _, p in self._params_with_grad():
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
-            ops.sumsq_(g, acc)
+            by_dtype.setdefault(g.dtype, []).append(g)
+        for grads in by_dtype.values():
+            ops.sumsq_multi_(grads, acc)
         norm = torch.empty((1,), dtype=torch.float32, device=dev)
         scale = torch.empty((1,), dtype=torch.float32, device=dev)
         ops.clip_finalize(acc, float(max_norm), norm, scale)
@@ -79,6 +83,7 @@ class FusedAdamW(torch.optim.Optimizer):
                 ops.adamw_step_(group["step_dev"], group["lr"], beta1, beta2, group["weight_decay"],
                                 group["hyper_dev"])
                 hypers[id(group)] = group["hyper_dev"]
+        batches = {}
         for group, p in self._params_with_grad():
             ops.require_gpu(p)
             st = self.state[p]
@@ -91,16 +96,21 @@ class FusedAdamW(torch.optim.Optimizer):
             st["step"] += 1
             master = st.get("master")
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
-            beta1, beta2 = group["betas"]
             if master is None:
                 if not p.is_contiguous():
                     raise ValueError("FusedAdamW needs contiguous parameters")
                 target, out = p.data, None
             else:
                 target, out = master, p.data
-            hyper = hypers.get(id(group))
-            ops.adamw_(target, st["exp_avg"], st["exp_avg_sq"], g, lr=group["lr"], beta1=beta1, beta2=beta2,
-                       eps=group["eps"], weight_decay=group["weight_decay"], step=st["step"],
-                       grad_scale=self._grad_scale, p_out=out, hyper=hyper)
+            key = (id(group), g.dtype, None if out is None else out.dtype, st["step"])
+            batch = batches.setdefault(key, (group, [], [], [], [], []))
+            for lst, t in zip(batch[1:], (target, st["exp_avg"], st["exp_avg_sq"], g, out)):
+                lst.append(t)
+        # one multi-tensor launch per (group, dtypes, step) batch
+        for key, (group, ps, ms, vs, gs, outs) in batches.items():
+            beta1, beta2 = group["betas"]
+            ops.adamw_multi_(ps, ms, vs, gs, outs, lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
+                             weight_decay=group["weight_decay"], step=key[3], grad_scale=self._grad_scale,
+                             hyper=hypers.get(id(group)))
         self._grad_scale = None
         return loss

@@ -66,6 +66,18 @@ int lz_adamw_dev(float* p, float* m, float* v, const void* g, int g_dtype, void*
  * (zero/stage0_ddp.py:66) and sum(g*g) (zero/stage2_optimizer.py:162-166,
  * zero/stage3_optimizer.py:438-444). */
 int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* stream);
+/* Multi-tensor forms of lz_adamw and lz_sumsq for per-parameter optimizers
+ * (reference train.py:206-211,259-271: torch.optim.AdamW over the model's
+ * parameter list and clip_grad_norm_ over their gradients): one launch per 24
+ * tensors instead of one per tensor.  table is a HOST array of nseg rows:
+ * lz_adamw_multi rows are {p, m, v, g, p_out (0 = none), numel} (int64; every
+ * row shares g_dtype and p_out_dtype; hyper as in lz_adamw_dev, or NULL to use
+ * lr and step); lz_sumsq_multi rows are {x, numel}.  Element math is that of
+ * lz_adamw / lz_sumsq. */
+int lz_adamw_multi(const int64_t* table, int nseg, int g_dtype, int p_out_dtype, double lr, double beta1, double beta2,
+                   double eps, double weight_decay, int64_t step, const float* hyper, const float* grad_scale,
+                   void* stream);
+int lz_sumsq_multi(const int64_t* table, int nseg, int dtype, double* acc, void* stream);
 
 /* norm = sqrt(*acc); scale = max/(norm+1e-6) if 0 < max < norm else 1.
  * Replaces the clip decision of zero/stage0_ddp.py:66-71 (and stage1/2/3). */

@@ -588,6 +588,51 @@ def test_adamw_device_step_matches_host_step():
     assert torch.equal(pd, ph) and torch.equal(md, mh) and torch.equal(vd, vh)
 
 
+def test_adamw_multi_matches_per_tensor():
+    """adamw_multi_ over 30 tensors (two launches of at most 24; sizes from 0
+    to 100k across the 4096-element chunk boundaries) against adamw_ tensor by
+    tensor over 3 steps with a grad scale: the same bits for p, m, v and the
+    bf16 copy, for bf16 and fp32 gradients and with device-resident factors;
+    sumsq_multi_ against float64 and per-tensor sumsq_ to 1e-6 (fp32 per-thread
+    partials)."""
+    g = _seed(31)
+    sizes = [0, 1, 7, 4095, 4096, 4097, 100_003] + [int(x) for x in torch.randint(1, 20000, (23,), generator=g)]
+    hp = dict(beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    scale = torch.tensor([0.5], device=DEV)
+    for gdt, with_out, use_hyper in ((torch.bfloat16, True, False), (torch.float32, False, False),
+                                     (torch.bfloat16, True, True)):
+        p0 = [0.02 * torch.randn(n, generator=g) for n in sizes]
+        A = [[p.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)] for p, n in zip(p0, sizes)]
+        B = [[p.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)] for p, n in zip(p0, sizes)]
+        oa = [torch.zeros(n, dtype=torch.bfloat16, device=DEV) if with_out else None for n in sizes]
+        ob = [torch.zeros(n, dtype=torch.bfloat16, device=DEV) if with_out else None for n in sizes]
+        step = torch.zeros(1, dtype=torch.int64, device=DEV)
+        hyper = torch.zeros(3, dtype=torch.float32, device=DEV)
+        for t in range(1, 4):
+            grads = [(1e-3 * torch.randn(n, generator=g)).to(gdt).to(DEV) for n in sizes]
+            for (pa, ma, va), gr, o in zip(A, grads, oa):
+                if pa.numel():
+                    ops.adamw_(pa, ma, va, gr, lr=3e-4, step=t, grad_scale=scale, p_out=o, **hp)
+            if use_hyper:
+                ops.adamw_step_(step, 3e-4, 0.9, 0.95, 0.1, hyper)
+            ops.adamw_multi_([b[0] for b in B], [b[1] for b in B], [b[2] for b in B], grads, ob,
+                             lr=3e-4, step=t, grad_scale=scale, hyper=hyper if use_hyper else None, **hp)
+        for (pa, ma, va), (pb, mb, vb), x, y in zip(A, B, oa, ob):
+            assert torch.equal(pa, pb) and torch.equal(ma, mb) and torch.equal(va, vb)
+            if with_out:
+                assert torch.equal(x, y)
+        acc1 = torch.zeros(1, dtype=torch.float64, device=DEV)
+        acc2 = torch.zeros(1, dtype=torch.float64, device=DEV)
+        for gr in grads:
+            if gr.numel():
+                ops.sumsq_(gr, acc1)
+        ops.sumsq_multi_(grads, acc2)
+        # both sum fp32 partials per thread (over different partitions) in fp64
+        ref = float(sum(gr.double().pow(2).sum() for gr in grads))
+        assert abs(float(acc2.item()) - ref) <= 1e-6 * ref
+        assert abs(float(acc1.item()) - float(acc2.item())) <= 1e-6 * ref
+
+
 def test_sumsq_and_clip():
     g = _seed(4)
     a = torch.randn(3_000_001, generator=g)
