@@ -365,7 +365,7 @@ def test_gemm_swiglu_rejects_unsupported_shapes():
     "B,S,H,KV,hd",
     [(2, 128, 4, 2, 64), (1, 256, 4, 1, 128), (2, 200, 4, 4, 64), (1, 130, 2, 2, 128), (2, 64, 8, 4, 32),
      (2, 16, 4, 2, 16), (1, 1024, 16, 8, 128), (3, 200, 8, 2, 32), (2, 128, 8, 4, 32), (1, 1, 2, 1, 16),
-     (1, 70, 2, 2, 16)],
+     (1, 70, 2, 2, 16), (4, 1024, 8, 8, 32)],
 )
 def test_attention_fwd_bwd(B, S, H, KV, hd):
     g = _seed(B * S + H * hd)
