@@ -190,12 +190,14 @@ def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev:
     """The same workload with the whole step (both micro-batches, clip, AdamW
     with a device-resident step count) replayed from one HIP graph; each timed
     step copies its micro-batch ids into the graph's static inputs."""
+    from lzhip.functional import pack_parameters_
     from lzhip.graph import GraphedTrainStep
     from lzhip.optim import FusedAdamW
     from model import LlamaForCausalLM
 
     torch.manual_seed(0)
     model = LlamaForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16)
+    pack_parameters_(model)
     model.set_loss_chunk_size(128)
     opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, capturable=True)
     gs = GraphedTrainStep(model, opt, (B, S), GA, 1.0, dev)
@@ -220,6 +222,7 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
     uniform ids from torch.Generator seed 0) for `steps` steps on the HIP path
     (bf16), and the CPU oracle's train.py loop (fp32, every host thread) on
     `cpu_steps` steps of the same stream."""
+    from lzhip.functional import pack_parameters_
     from lzhip.optim import FusedAdamW
     from model import LlamaForCausalLM, build_config
 
@@ -229,6 +232,7 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
     model = LlamaForCausalLM(cfg)
     P = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
     model = model.to(device=dev, dtype=torch.bfloat16)
+    pack_parameters_(model)
     model.set_loss_chunk_size(128)
     opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
     gen = torch.Generator().manual_seed(0)

@@ -24,6 +24,35 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
     return t.view(-1, t.shape[-1])
 
 
+@torch.no_grad()
+def pack_parameters_(module: torch.nn.Module) -> int:
+    """Re-points every parameter of `module` (tied ones once) at a view of one
+    flat device buffer per dtype, in registration order, so that q/k/v and
+    gate/up sit adjacent and fused_weight returns views instead of copying
+    them on every forward and backward.  Values, Parameter objects and
+    state_dict are unchanged.  Returns the number of parameters packed."""
+    params, seen = [], set()
+    for prm in module.parameters():
+        if id(prm) not in seen:
+            seen.add(id(prm))
+            params.append(prm)
+    by_dtype = {}
+    for prm in params:
+        ops.require_gpu(prm)
+        by_dtype.setdefault(prm.dtype, []).append(prm)
+    for dtype, group in by_dtype.items():
+        flat = torch.empty(sum(prm.numel() for prm in group), dtype=dtype, device=group[0].device)
+        off = 0
+        for prm in group:
+            n = prm.numel()
+            view = flat[off : off + n].view(prm.shape)
+            ops.copy2d(prm.data.contiguous().view(-1, prm.shape[-1] if prm.dim() else 1),
+                       view.view(-1, prm.shape[-1] if prm.dim() else 1))
+            prm.data = view
+            off += n
+    return len(params)
+
+
 def fused_weight(weights: Sequence[torch.Tensor]) -> torch.Tensor:
     """Concatenation of weight matrices along their output rows.  When the
     storages are already adjacent (parameters that are views of one flat

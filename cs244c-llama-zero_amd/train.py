@@ -29,6 +29,7 @@ from data import (
     load_fineweb_stream,
     load_llama_tokenizer,
 )
+from lzhip.functional import pack_parameters_
 from lzhip.optim import FusedAdamW
 from model import MODEL_SIZES, LlamaForCausalLM, build_config, estimate_num_parameters, human_readable_count
 
@@ -165,6 +166,7 @@ def train(args: argparse.Namespace) -> None:
         cfg = cfg.with_vocab_size(detected_vocab)
 
     model = LlamaForCausalLM(cfg).to(device=device, dtype=model_param_dtype(device, args.dtype))
+    pack_parameters_(model)  # fused q/k/v and gate/up weights become views, not per-step copies
     model.set_loss_chunk_size(args.loss_chunk_size)
     model.set_activation_checkpointing(args.activation_checkpointing)
     optimizer = FusedAdamW(model.parameters(), lr=args.learning_rate, betas=(args.beta1, args.beta2),

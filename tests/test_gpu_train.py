@@ -256,6 +256,41 @@ def test_graphed_step_replays_match_eager():
     assert int(og.param_groups[0]["step_dev"].item()) == steps
 
 
+def test_packed_parameters_train_bit_identically():
+    """pack_parameters_ (every parameter a view of one flat buffer, so the
+    fused q/k/v and gate/up weights are views instead of per-step copies):
+    3 training steps of the plumbing model give the same loss bits and the
+    same parameters as the unpacked model."""
+    from lzhip.functional import pack_parameters_
+
+    B, S = 4, 128
+    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
+
+    def run(pack):
+        torch.manual_seed(0)
+        m = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+        if pack:
+            assert pack_parameters_(m) == len({id(p) for p in m.parameters()})
+        m.set_loss_chunk_size(128)
+        o = FusedAdamW(m.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+        gen = torch.Generator().manual_seed(2)
+        losses = []
+        for _ in range(3):
+            ids = torch.randint(0, 32000, (B, S), generator=gen).to(DEV)
+            o.zero_grad(set_to_none=True)
+            loss = m(input_ids=ids, labels=ids, return_logits=False).loss
+            loss.backward()
+            o.clip_grad_norm_(1.0)
+            o.step()
+            losses.append(float(loss))
+        return losses, {k: v.float().cpu() for k, v in m.state_dict().items()}
+
+    la, sa = run(False)
+    lb, sb = run(True)
+    assert la == lb
+    assert sa.keys() == sb.keys() and all(torch.equal(sa[k], sb[k]) for k in sa)
+
+
 def _run(args, timeout=600):
     env = dict(os.environ)
     env["PYTHONPATH"] = f"{PKG}:{ROOT}:" + env.get("PYTHONPATH", "")
