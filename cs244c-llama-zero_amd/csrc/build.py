@@ -29,6 +29,7 @@ SOURCES = [
     "ce.hip",
     "transpose.hip",
     "gemm.hip",
+    "gemm_f32.hip",
     "attn.hip",
 ]
 

@@ -550,6 +550,8 @@ def gemm_kernel_name(key) -> str:
         return "gemm_swiglu_kernel"
     if code == "rope":
         return "gemm_rope_kernel"
+    if code == "f32":
+        return f"gemm_f32_kernel<{'true' if ak else 'false'}, {'true' if bk else 'false'}>"
     cfg, splits = code // 64, code % 64
     tf = lambda b: "true" if b else "false"
     if cfg == 5:
@@ -596,10 +598,11 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
     dy.W is gemm(dy, W, b_kmajor=False) and dy^T.x is
     gemm(dy, x, a_kmajor=False, b_kmajor=False)."""
     require_gpu(a, b, out, residual)
+    if a.dtype == torch.float32 and b.dtype == torch.float32:
+        return _gemm_f32(a, b, a_kmajor, b_kmajor, out, out_dtype, residual, alpha, beta)
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise TypeError(
-            f"the MFMA GEMM takes bfloat16 operands (got {a.dtype}, {b.dtype}); "
-            "run the model in bfloat16 (--dtype bfloat16)"
+            f"the MFMA GEMM takes two bfloat16 or two float32 operands (got {a.dtype}, {b.dtype})"
         )
     M, K = a.shape if a_kmajor else (a.shape[1], a.shape[0])
     N, K2 = b.shape if b_kmajor else (b.shape[1], b.shape[0])
@@ -634,6 +637,46 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
         end.record()
         probe.add(2.0 * M * N * K, start, end, (bool(a_kmajor), bool(b_kmajor),
                                                 int(lib.lz_gemm_plan(M, N, Kp, int(a_kmajor), int(b_kmajor)))))
+    return out
+
+
+def _unit_stride_2d(t: torch.Tensor, name: str) -> int:
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.size(1) > 1 and t.stride(1) != 1:
+        raise ValueError(f"{name} needs unit stride in its last dimension")
+    return _row_stride(t)
+
+
+def _gemm_f32(a, b, a_kmajor, b_kmajor, out, out_dtype, residual, alpha, beta) -> torch.Tensor:
+    """gemm() for float32 operands: the fp32 MFMA kernel (any shape and
+    leading dimension, fp32 accumulation, fp32 or bf16 output, fp32 residual)."""
+    M, K = a.shape if a_kmajor else (a.shape[1], a.shape[0])
+    N, K2 = b.shape if b_kmajor else (b.shape[1], b.shape[0])
+    if K != K2:
+        raise ValueError(f"GEMM reduction mismatch {K} vs {K2}")
+    lda, ldb = _unit_stride_2d(a, "A"), _unit_stride_2d(b, "B")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or torch.float32, device=a.device)
+    if tuple(out.shape) != (M, N) or out.dtype not in _DTYPES:
+        raise ValueError(f"out must be a float32 or bfloat16 [{M}, {N}] view")
+    ldc = _unit_stride_2d(out, "out")
+    ldr = 0
+    if residual is not None:
+        if residual.dtype != torch.float32 or tuple(residual.shape) != (M, N):
+            raise ValueError("residual of a float32 GEMM must be a float32 [M, N] view")
+        ldr = _unit_stride_2d(residual, "residual")
+    probe = _gemm_probe
+    if probe is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+    _lib.call("lz_gemm_f32", a.data_ptr(), lda, int(bool(a_kmajor)), b.data_ptr(), ldb, int(bool(b_kmajor)),
+              out.data_ptr(), ldc, dtype_code(out), _ptr(residual), ldr, M, N, K, float(alpha), float(beta),
+              stream_ptr(a.device))
+    if probe is not None:
+        end.record()
+        probe.add(2.0 * M * N * K, start, end, (bool(a_kmajor), bool(b_kmajor), "f32"))
     return out
 
 

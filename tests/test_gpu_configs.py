@@ -1,0 +1,256 @@
+"""The benchmark training configurations through the ZeRO engines, against the
+oracle (reference: zero/tests/test_zero_stages.py:72-157,195-271 pin every
+stage to torch.optim.AdamW on the same batch; zero/stage3_optimizer.py:106-243
+is the executor under test).
+
+Teacher-forced parity: every step the engine is given the oracle trainer's
+current fp32 master (so both see the same bf16 parameters), runs its real
+forward/backward — for stage 3 through _ShardedModuleFunction (materialise,
+no-grad forward, recompute or kept graph, autograd.grad, bucketed flatten
+into the fp32 shard, the tied embedding/LM-head handle called twice) — and
+then its own optimizer step.  Bars, at every step:
+  - loss within 1e-2 relative of the oracle's (bf16 training bar);
+  - gradient cosine >= 0.999 overall and for every parameter (a lost
+    contribution, e.g. one of the tied weight's two, fails the per-parameter
+    bar);
+  - given the engine's own gradient, its fp32 master after the step within
+    1e-5 relative of EngineRef's (zero/stage0_ddp.py:66-88 order).
+
+Layouts: the 1B model's (d2048, 16 q / 8 kv heads of 128, ffn 5632, vocab
+32000, tied) at 2 layers with its full sequence length 2048, through stage 3
+with recompute on and off; the 125M model's full depth (d768, 12 layers,
+12 q / 4 kv heads of 64, ffn 2048, S 1024) through stage 1.  Micro-batch 1,
+gradient accumulation 2, clip 1.0.
+
+Full-size properties (too large for the CPU oracle): the 1B step at B=8,
+S=2048 (finite loss, recompute on/off equal, peak HBM) and one 7B step at
+micro-batch 1 (peak HBM near the 16 B/parameter floor of the ZeRO-3 state).
+"""
+from __future__ import annotations
+
+import gc
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from lzhip import ops
+from model import LlamaForCausalLM, ModelConfig, build_config
+from oracle import data as OD
+from oracle import engine as OE
+from oracle import model as OM
+from zero import ZeROStage1Optimizer, ZeROStage3Optimizer
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+LAYOUT_1B = dict(vocab_size=32000, dim=2048, n_heads=16, n_kv_heads=8, ffn_dim=5632, rope_theta=10_000.0)
+
+
+def _ocfg(cfg: ModelConfig) -> OM.Cfg:
+    return OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
+                  n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta,
+                  rms_norm_eps=cfg.rms_norm_eps, tie_word_embeddings=cfg.tie_word_embeddings,
+                  rope_angle_dtype=torch.bfloat16)
+
+
+def _set_master(eng, flat: torch.Tensor) -> None:
+    """Overwrites the engine's fp32 master with `flat` (model.parameters()
+    order) and its bf16 parameters with the rounding of it."""
+    flat = flat.to(DEV, torch.float32)
+    if isinstance(eng, ZeROStage3Optimizer):
+        eng._master_all.copy_(flat)
+        if eng._param_flat is not None:
+            ops.cast(eng._master_all, eng._param_flat.dtype, out=eng._param_flat)
+    else:
+        eng.local_master_param_shard.copy_(flat)
+        eng._write_params_from_master()
+
+
+def _engine_master(eng) -> torch.Tensor:
+    return eng._master_all if isinstance(eng, ZeROStage3Optimizer) else eng.local_master_param_shard
+
+
+def _engine_grad(eng, model) -> torch.Tensor:
+    """The gradient the engine's optimizer will consume (fp32 shard for stage
+    3, the parameters' gradients for stage 1), flat in parameter order."""
+    if isinstance(eng, ZeROStage3Optimizer):
+        eng._finish_grads()
+        return eng._grad_all.double().cpu()
+    return torch.cat([p.grad.double().reshape(-1).cpu() for p in eng.meta.params])
+
+
+def _run_teacher_forced(cfg: ModelConfig, make_engine, B: int, S: int, GA: int, steps: int, max_norm: float):
+    torch.manual_seed(0)
+    cpu_model = LlamaForCausalLM(cfg)
+    P = {k: v.detach().clone() for k, v in cpu_model.state_dict().items() if k != "lm_head.weight"}
+    named = [(n, p.numel()) for n, p in cpu_model.named_parameters()]
+    order = [n for n, _ in named]
+    model = cpu_model.to(device=DEV, dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    eng = make_engine(model)
+    mirror = None
+    gen = OD.uniform_chunks(S, cfg.vocab_size, B, seed=0)
+    batches = [next(gen) for _ in range(steps * GA)]
+    rows = []
+
+    def on_step(step, loss, gn, grads, params):
+        nonlocal mirror
+        flat_p = torch.cat([params[n].reshape(-1) for n in order]).float()
+        _set_master(eng, flat_p)
+        eng.zero_grad()
+        eng.prepare_forward()
+        losses = []
+        for i in range(GA):
+            ids = batches[(step - 1) * GA + i][:, :-1].contiguous().to(DEV)
+            l = model(input_ids=ids, labels=ids, return_logits=False).loss
+            losses.append(float(l.detach()))
+            eng.backward(l / GA)
+        g = _engine_grad(eng, model)
+        r = torch.cat([grads[n].double().reshape(-1) for n in order])
+        cos = float(F.cosine_similarity(g, r, dim=0))
+        worst, off = (1.0, ""), 0
+        for n, k in named:
+            c = float(F.cosine_similarity(g[off:off + k], r[off:off + k], dim=0))
+            worst = min(worst, (c, n))
+            off += k
+        if mirror is None:
+            mirror = OE.EngineRef(flat_p.double(), lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+        mirror.master = flat_p.double().clone()
+        rnorm = mirror.step(g, max_grad_norm=max_norm)
+        norm = eng.step(max_grad_norm=max_norm)
+        master = _engine_master(eng).double().cpu()
+        m_rel = float((master - mirror.master).norm() / mirror.master.norm())
+        rows.append({"step": step, "loss": sum(losses) / GA, "oracle_loss": loss, "cos": cos, "worst": worst,
+                     "norm": norm, "mirror_norm": rnorm, "oracle_norm": gn, "master_rel": m_rel})
+
+    OE.train_reference(_ocfg(cfg), P, iter(batches), steps=steps, grad_accum_steps=GA, lr=3e-4, betas=(0.9, 0.95),
+                       weight_decay=0.1, max_grad_norm=max_norm, loss_chunk_size=128, on_step=on_step,
+                       param_dtype=torch.bfloat16)
+    for r in rows:
+        print(f"step {r['step']}: loss {r['loss']:.5f} (oracle {r['oracle_loss']:.5f}) grad cos {r['cos']:.6f} "
+              f"worst {r['worst'][0]:.5f} ({r['worst'][1]}) norm {r['norm']:.4f} (oracle {r['oracle_norm']:.4f}) "
+              f"master rel {r['master_rel']:.2e}")
+    assert len(rows) == steps
+    for r in rows:
+        assert abs(r["loss"] - r["oracle_loss"]) <= 1e-2 * abs(r["oracle_loss"]), r
+        assert r["cos"] >= 0.999 and r["worst"][0] >= 0.999, r
+        assert abs(r["norm"] - r["mirror_norm"]) <= 1e-5 * r["mirror_norm"], r
+        assert abs(r["norm"] - r["oracle_norm"]) <= 2e-2 * r["oracle_norm"], r
+        assert r["master_rel"] <= 1e-5, r
+    return rows
+
+
+@pytest.mark.parametrize("recompute", [True, False])
+def test_1b_layout_zero3_vs_oracle(recompute):
+    cfg = ModelConfig(name="1b_2layer", max_seq_len=2048, n_layers=2, **LAYOUT_1B)
+
+    def make(model):
+        return ZeROStage3Optimizer(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                                   recompute=recompute)
+
+    _run_teacher_forced(cfg, make, B=1, S=2048, GA=2, steps=3, max_norm=1.0)
+
+
+def test_125m_zero1_vs_oracle():
+    cfg = build_config("125m", vocab_size=32000, max_seq_len=1024)
+    assert (cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.ffn_dim) == (768, 12, 12, 4, 2048)
+
+    def make(model):
+        return ZeROStage1Optimizer(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+    _run_teacher_forced(cfg, make, B=1, S=1024, GA=2, steps=3, max_norm=1.0)
+
+
+def _release() -> float:
+    """Frees what earlier tests left for the garbage collector (an engine and
+    its model reference each other) and returns the bytes still allocated,
+    which the peak-memory bars below do not count."""
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return torch.cuda.memory_allocated(DEV)
+
+
+def _device_model(size: str, seq: int):
+    cfg = build_config(size, vocab_size=32000, max_seq_len=seq)
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(dtype=torch.bfloat16)
+    model.set_loss_chunk_size(128)
+    return cfg, model
+
+
+def _initial_loss(cfg) -> float:
+    """Expected loss at initialisation: the final RMSNorm output has unit RMS
+    and the tied head's weights are N(0, 0.02^2), so each logit is about
+    N(0, s2) with s2 = dim * 0.02^2, and E[log sum_v exp(z_v)] - E[z_label]
+    = ln V + s2 / 2 (the mean of a log-normal)."""
+    return math.log(cfg.vocab_size) + cfg.dim * 0.02 ** 2 / 2
+
+
+def _step(model, eng, ids, max_norm=1.0):
+    eng.zero_grad()
+    eng.prepare_forward()
+    loss = model(input_ids=ids, labels=ids, return_logits=False).loss
+    eng.backward(loss)
+    norm = eng.step(max_grad_norm=max_norm)
+    return float(loss.detach()), norm
+
+
+def test_1b_full_size_zero3_properties():
+    """1B at B=8, S=2048 (the benchmark step), 2 steps with recompute on and
+    off from the same initial weights: finite losses, the expected loss at
+    initialisation at step 1, equal losses and norms (the kernels are
+    deterministic; the norm's fp64 partial order may move its last bits), and
+    the recompute step's peak HBM within 16 GiB."""
+    B, S = 8, 2048
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    batches = [torch.randint(0, 32000, (B, S), device=DEV, generator=gen) for _ in range(2)]
+    out = {}
+    for recompute in (True, False):
+        base = _release()
+        cfg, model = _device_model("1b", S)
+        eng = ZeROStage3Optimizer(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                                  recompute=recompute)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(DEV)
+        out[recompute] = [_step(model, eng, ids) for ids in batches]
+        out[recompute].append((torch.cuda.max_memory_allocated(DEV) - base) / 2**30)
+        del model, eng
+    print("recompute on:", out[True], "off:", out[False])
+    (l1, n1), (l2, n2), peak = out[True]
+    assert all(math.isfinite(v) for v in (l1, n1, l2, n2))
+    assert abs(l1 - _initial_loss(cfg)) < 0.05
+    for (la, na), (lb, nb) in zip(out[True][:2], out[False][:2]):
+        assert abs(la - lb) <= 1e-4 * abs(la)
+        assert abs(na - nb) <= 1e-4 * abs(na)
+    assert peak <= 16.0
+
+
+def test_7b_one_step_memory_floor():
+    """7B (d4096, 32 layers, 32/8 heads, ffn 11008) through ZeRO-3 at
+    micro-batch 1, S=2048: one finite step at the expected initial loss, and
+    a peak HBM within 5 % of the
+    persistent state (fp32 master, exp_avg, exp_avg_sq and gradient shard:
+    16 B per parameter) plus one handle's bf16 parameters and gradients."""
+    S = 2048
+    base = _release()
+    cfg, model = _device_model("7b", S)
+    eng = ZeROStage3Optimizer(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    n_params = sum(h.meta.total_numel for h in eng._handle_order)
+    assert n_params == 5_802_037_248
+    ids = torch.randint(0, 32000, (1, S), device=DEV, generator=torch.Generator(device=DEV).manual_seed(0))
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(DEV)
+    loss, norm = _step(model, eng, ids)
+    peak = torch.cuda.max_memory_allocated(DEV) - base
+    floor = 16 * n_params
+    largest = max(h.meta.total_numel for h in eng._handle_order)
+    bound = 1.05 * (floor + 2 * 2 * largest)
+    print(f"7B step: loss {loss:.4f} norm {norm:.4f} peak {peak / 2**30:.2f} GiB, floor {floor / 2**30:.2f} GiB, "
+          f"bound {bound / 2**30:.2f} GiB")
+    assert math.isfinite(loss) and math.isfinite(norm)
+    assert abs(loss - _initial_loss(cfg)) < 0.05
+    assert floor <= peak <= bound
