@@ -362,15 +362,29 @@ def rmsnorm_fwd(x2: torch.Tensor, w: torch.Tensor, eps: float) -> Tuple[torch.Te
     return y, rstd
 
 
+_norm_workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _rmsnorm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The RMSNorm backward's workspace for the current stream: kept between
+    calls because its leading counters must start at zero (they are zeroed
+    once here and every call leaves them zero); calls on one stream never
+    overlap."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_ptr(device))
+    ws = _norm_workspaces.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = zeros(((max(nbytes, 16) + 15) // 16 * 4,), torch.float32, device)
+        _norm_workspaces[key] = ws
+    return ws
+
+
 def rmsnorm_bwd(x2: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy2: torch.Tensor,
                 dres: Optional[torch.Tensor] = None, need_dw: bool = True) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     require_gpu(x2, w, rstd, dy2, dres)
     rows, cols = x2.shape
     dx = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
     dw = torch.empty((cols,), dtype=w.dtype, device=w.device) if need_dw else None
-    lib = _lib.load()
-    ws_bytes = int(lib.lz_rmsnorm_bwd_workspace(rows, cols))
-    ws = torch.empty((max(ws_bytes, 16) + 3) // 4, dtype=torch.float32, device=x2.device)
+    ws = _rmsnorm_workspace(x2.device, int(_lib.load().lz_rmsnorm_bwd_workspace(rows, cols)))
     if dres is not None:
         if dres.shape != dx.shape or dres.dtype != dx.dtype:
             raise ValueError("residual gradient must match dx")

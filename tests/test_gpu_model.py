@@ -155,11 +155,11 @@ def test_activation_checkpointing_matches_plain():
         assert torch.allclose(p1.grad.float(), p2.grad.float(), rtol=1e-2, atol=1e-4), n
 
 
-def test_float32_gemm_is_refused_clearly():
+def test_unsupported_dtype_is_refused_clearly():
     cfg = ModelConfig(name="t", vocab_size=64, max_seq_len=16, dim=64, n_layers=1, n_heads=2, n_kv_heads=1,
                       ffn_dim=128)
-    model = LlamaForCausalLM(cfg).to(DEV)
-    with pytest.raises(TypeError, match="bfloat16"):
+    model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.float16)
+    with pytest.raises(TypeError, match="float32 and bfloat16"):
         model(torch.zeros(1, 16, dtype=torch.long, device=DEV))
 
 

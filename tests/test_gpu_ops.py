@@ -235,6 +235,37 @@ def test_rmsnorm_fwd_bwd(rows, cols, dtype):
     assert _rel_err(dw, wd.grad) < tol
 
 
+@pytest.mark.parametrize("rows,cols", [(512, 256), (333, 768), (16 * 1024, 2048), (1000, 4096)])
+def test_rmsnorm_bwd_dw_in_one_launch_repeats_and_accumulates(rows, cols):
+    """The bf16 backward sums dw in the same launch through per-group counters
+    that each call leaves at zero: repeated calls give the same bits (any
+    workgroup may finish last; the sums run in a fixed order), and
+    dw_accumulate adds the new dw to the old one."""
+    g = _seed(rows * 3 + cols)
+    x = torch.randn(rows, cols, generator=g).to(torch.bfloat16).to(DEV)
+    w = (1.0 + 0.02 * torch.randn(cols, generator=g)).to(torch.bfloat16).to(DEV)
+    dy = torch.randn(rows, cols, generator=g).to(torch.bfloat16).to(DEV)
+    _, rstd = ops.rmsnorm_fwd(x, w, 1e-5)
+    runs = [ops.rmsnorm_bwd(x, w, rstd, dy) for _ in range(3)]
+    for dx, dw in runs[1:]:
+        assert torch.equal(dx, runs[0][0]) and torch.equal(dw, runs[0][1])
+    ref = (dy.double() * x.double() * rstd.double()[:, None]).sum(0)
+    assert _rel_err(runs[0][1], ref) < 1e-2
+    base = torch.full((cols,), 0.5, dtype=torch.bfloat16, device=DEV)
+    acc = base.clone()
+    dx = torch.empty_like(x)
+    lib = _lib.load()
+    ws = ops._rmsnorm_workspace(DEV, int(lib.lz_rmsnorm_bwd_workspace(rows, cols)))
+    _lib.call("lz_rmsnorm_bwd", x.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr(), None, dx.data_ptr(),
+              acc.data_ptr(), 1, ws.data_ptr(), ws.numel() * 4, 1, rows, cols, cols, cols, cols,
+              ops.stream_ptr(DEV))
+    # the fp32 sum plus the old bf16 value, rounded once: within a rounding of
+    # the result and of dw from adding the rounded dw
+    dw0 = runs[0][1].double()
+    assert torch.allclose(acc.double(), base.double() + dw0, rtol=2 ** -8, atol=2 ** -8 * float(dw0.abs().max()))
+    assert torch.count_nonzero(ws[:256]) == 0  # the counters are left at zero
+
+
 # ---------------------------------------------------------------------------
 # RoPE: bit-exact against the reference's bf16 op sequence given equal tables
 # ---------------------------------------------------------------------------
