@@ -8,6 +8,8 @@
 // optional residual-gradient add), 6 B/element, and reduces dw through fp32
 // partial rows (one per workgroup for bf16, per wave otherwise) and a
 // two-level column sum.
+#include <mutex>
+
 #include "lz_common.h"
 
 namespace {
@@ -569,4 +571,81 @@ LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, co
     return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (char*)workspace, workspace_bytes, rows,
                                (int)cols, ldx, lddy, lddx, lz_stream(stream));
   return lz_set_error(LZ_EINVAL, "lz_rmsnorm_bwd: bad dtype %d", dtype);
+}
+
+// ---------------------------------------------------------------------------
+// Backward without a caller workspace, for callers that cannot allocate
+// device memory (code under HIP graph capture, serving loops, harnesses that
+// forbid allocation).  The partial rows and counters live in `scratch`, a
+// fixed array of kScratchBytes per device that stays allocated until the
+// process ends.  Every call on a device shares that device's array, so calls
+// that overlap in time on one device (other streams, other threads) race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = 8ll << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ void zero_counters_kernel(int* c, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) c[i] = 0;
+}
+
+// This device's address of `scratch` (the host-side symbol is a stand-in,
+// not a device address), looked up once per device; the counters are zeroed
+// on the caller's stream at that first call (a kernel, no memset).
+int scratch_for_device(hipStream_t s, char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return lz_set_error(LZ_ERUNTIME, "lz_rmsnorm_bwd_noalloc: no current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return lz_set_error(LZ_ERUNTIME, "lz_rmsnorm_bwd_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                          hipGetErrorString(e));
+    const int n = (int)(kCounterBytes / 4);
+    zero_counters_kernel<<<(n + 255) / 256, 256, 0, s>>>(static_cast<int*>(p), n);
+    const int rc = lz_check_launch("lz_rmsnorm_bwd_noalloc(zero counters)");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return LZ_OK;
+}
+
+}  // namespace
+
+// lz_rmsnorm_bwd with the library's own scratch instead of a workspace:
+// same arguments without workspace/workspace_bytes, same results bit for
+// bit.  Shapes whose workspace (lz_rmsnorm_bwd_workspace for the path taken)
+// exceeds the scratch are refused; bf16 rows of up to 4096 columns fit at
+// any row count.
+LZ_EXPORT int lz_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, const void* dres,
+                                     void* dx, void* dw, int dw_accumulate, int dtype, int64_t rows, int64_t cols,
+                                     int64_t ldx, int64_t lddy, int64_t lddx, void* stream) {
+  LZ_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30), "lz_rmsnorm_bwd_noalloc: bad shape");
+  LZ_REQUIRE(ldx >= cols && lddy >= cols && lddx >= cols, "lz_rmsnorm_bwd_noalloc: bad leading dimension");
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_rmsnorm_bwd_noalloc: bad dtype %d", dtype);
+  if (rows == 0) return LZ_OK;
+  const int64_t need = dtype == LZ_BF16
+      ? bwd_bytes<uint16_t>(bwd_vec<uint16_t>(x, w, dy, dres, dx, dw, cols, ldx, lddy, lddx), rows, cols)
+      : bwd_bytes<float>(bwd_vec<float>(x, w, dy, dres, dx, dw, cols, ldx, lddy, lddx), rows, cols);
+  LZ_REQUIRE(need <= kScratchBytes,
+             "lz_rmsnorm_bwd_noalloc: rows %lld x cols %lld need %lld bytes of scratch, more than its %lld",
+             (long long)rows, (long long)cols, (long long)need, (long long)kScratchBytes);
+  hipStream_t s = lz_stream(stream);
+  char* ws = nullptr;
+  const int rc = scratch_for_device(s, &ws);
+  if (rc) return rc;
+  if (dtype == LZ_BF16)
+    return bwd_dispatch<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, ws, kScratchBytes, rows, (int)cols, ldx,
+                                  lddy, lddx, s);
+  return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, ws, kScratchBytes, rows, (int)cols, ldx,
+                             lddy, lddx, s);
 }

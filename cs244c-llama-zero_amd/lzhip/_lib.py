@@ -54,6 +54,7 @@ SIGNATURES = {
         _i32,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _vp],
     ),
+    "lz_rmsnorm_bwd_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _vp]),
     "lz_rope_table": (_i32, [_vp, _vp, _i32, _i64, _i64, _vp, _i32, _vp]),
     "lz_rope": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp]),
     "lz_swiglu_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp]),

@@ -144,6 +144,18 @@ int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
                    int dw_accumulate, void* workspace, int64_t workspace_bytes, int dtype, int64_t rows, int64_t cols,
                    int64_t ldx, int64_t lddy, int64_t lddx, void* stream);
 
+/* lz_rmsnorm_bwd without a workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).  The
+ * dw partial rows and counters live in the library's own 8 MiB device array,
+ * one per device, held until the process ends; shapes that need more are
+ * refused (bf16 rows of up to 4096 columns fit at any row count).  Same
+ * results as lz_rmsnorm_bwd bit for bit.  Every call on a device shares that
+ * array: calls that overlap in time on one device race. */
+int lz_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,
+                           void* dw, int dw_accumulate, int dtype, int64_t rows, int64_t cols, int64_t ldx,
+                           int64_t lddy, int64_t lddx, void* stream);
+
 /* RoPE table (model/llama.py:42-69 RotaryEmbedding._build_cache): cos/sin
  * [seq, hd] in dtype from the module's inv_freq buffer (hd/2 values of
  * freq_dtype); position, angle and cos/sin are rounded to freq_dtype, as the
