@@ -171,6 +171,22 @@ def fit_sweep(dev: torch.device, max_batch: int, seq: int = 2048, steps: int = 2
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_1b_zero3_traffic.md")
+MFMA_PROFILE = os.path.join(ROOT, "profiles", "mfma_busy_1b_zero3_step.md")
+
+
+def measured_mfma_busy(kernel: str):
+    """MFMA-busy fraction of `kernel` (SQ_VALU_MFMA_BUSY_CYCLES over the SIMD
+    cycles it occupied) from the committed counter profile of the same step
+    (a line `mfma_busy <kernel> = x`), or None."""
+    name = kernel.split(" split-K")[0]
+    try:
+        with open(MFMA_PROFILE) as f:
+            for line in f:
+                if line.startswith("mfma_busy ") and line[len("mfma_busy "):].rsplit(" = ", 1)[0] == name:
+                    return float(line.rsplit("=", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def measured_traffic(kernel: str):
@@ -425,7 +441,7 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
     from oracle import engine as OE
     from oracle import model as OM
 
-    threads = torch.get_num_threads()
+    threads = torch.get_num_threads()  # the box's CPU share (OMP_NUM_THREADS), not every host CPU
     ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
                   n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta)
     torch.manual_seed(0)
@@ -443,6 +459,8 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
         "value": tokens / sec,
         "unit": "tokens/s",
         "cores": threads,
+        "host_cpu_count": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
         "kind": "port",
         "sample": f"1 step of the same 1B workload on {tokens} tokens ({tokens // seq}x{seq}) in fp32: forward, "
                   f"backward and the AdamW update of all {sum(p.numel() for p in P.values()):,} parameters "
@@ -610,6 +628,8 @@ def main() -> int:
             "frac": top_tflops / PEAK_BF16_TFLOPS,
             "traffic": measured_traffic(ops.gemm_kernel_name(top_key)),
             "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
+            "mfma_busy": measured_mfma_busy(ops.gemm_kernel_name(top_key)),
+            "mfma_busy_source": os.path.relpath(MFMA_PROFILE, ROOT),
             "launches": top_n,
             "avg_launch_ms": top_ms / max(top_n, 1),
             "flop_per_launch": top_flops / max(top_n, 1),

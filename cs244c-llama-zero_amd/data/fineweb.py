@@ -1,19 +1,39 @@
-"""Token streams for training (reference: data/fineweb.py).
+"""Token streams for training, with the reference's names (data/fineweb.py).
 
-SyntheticPatternDataset, RankShardIterableDataset and PackedFineWebDataset keep
-the reference's behaviour.  SyntheticUniformDataset is an addition: iid uniform
-token ids over [0, vocab) from one seeded torch.Generator, drawn as [S+1]
-chunks (the benchmark workloads' synthetic data).  The FineWeb loaders need
-the Hugging Face hub (network); they raise with a clear message when the
-libraries or the network are unavailable.
+- SyntheticPatternDataset reproduces the reference's ramp stream exactly
+  (data/fineweb.py:100-122): chunk i is (cursor + arange(S+1)) % V with the
+  cursor advancing by S+1 modulo V.  Its bytes are part of the contract.
+- SyntheticUniformDataset (not in the reference): iid uniform ids over
+  [0, V) from one seeded torch.Generator, one [S+1] draw per chunk; the
+  benchmark workloads' synthetic data.
+- PackedFineWebDataset packs any text stream with any tokenizer into
+  [S+1] chunks (documents separated by EOS), through TokenPacker, a fixed
+  buffer that is filled and emitted in place.
+- RankShardIterableDataset strides a stream over ranks.
+- The Hugging Face pieces the reference's `--data-mode fineweb` needs (the
+  meta-llama tokenizer and the FineWeb-Edu stream, data/fineweb.py:17-55)
+  are downloads, which this build does not do: load_llama_tokenizer and
+  load_fineweb_stream raise FineWebUnavailable with what to use instead, and
+  the trainers' --allow-synthetic-fallback switches to synthetic data as the
+  reference's does.
 """
 from __future__ import annotations
 
+import itertools
 from dataclasses import dataclass
-from typing import Iterable, Iterator, Optional
+from typing import Iterable, Iterator, List, Optional, Sequence
 
 import torch
 from torch.utils.data import IterableDataset
+
+
+class FineWebUnavailable(RuntimeError):
+    """The real-data pipeline needs network downloads this build does not make."""
+
+
+_OFFLINE_HINT = ("use --data-mode synthetic or --data-mode synthetic-uniform, or pass "
+                 "--allow-synthetic-fallback; PackedFineWebDataset also packs any local text "
+                 "iterable with a tokenizer object you supply")
 
 
 @dataclass
@@ -24,30 +44,49 @@ class TokenizerBundle:
 
 
 def load_llama_tokenizer(tokenizer_name: str) -> TokenizerBundle:
-    try:
-        from transformers import AutoTokenizer
-    except ImportError as exc:
-        raise RuntimeError("transformers is required for real-data training") from exc
-    tok = AutoTokenizer.from_pretrained(tokenizer_name, use_fast=True)
-    if tok.eos_token_id is None:
-        raise ValueError(f"Tokenizer '{tokenizer_name}' has no eos_token_id")
-    if tok.pad_token_id is None:
-        tok.pad_token = tok.eos_token
-    return TokenizerBundle(tokenizer=tok, vocab_size=tok.vocab_size, eos_token_id=tok.eos_token_id)
+    raise FineWebUnavailable(f"tokenizer '{tokenizer_name}' would be downloaded from the Hugging Face hub; "
+                             + _OFFLINE_HINT)
 
 
 def load_fineweb_stream(subset: str, split: str = "train", shuffle_buffer: int = 10_000, seed: int = 42):
-    try:
-        from datasets import load_dataset
-    except ImportError as exc:
-        raise RuntimeError("datasets is required for FineWeb-Edu streaming") from exc
-    ds = load_dataset("HuggingFaceFW/fineweb-edu", subset, split=split, streaming=True)
-    return ds.shuffle(buffer_size=shuffle_buffer, seed=seed)
+    raise FineWebUnavailable(f"FineWeb-Edu '{subset}/{split}' would be streamed from the Hugging Face hub; "
+                             + _OFFLINE_HINT)
+
+
+class TokenPacker:
+    """Concatenates token id sequences into fixed chunks of `chunk_len`
+    ids.  Ids are written into one preallocated int64 buffer at a cursor;
+    whenever the buffer is full it is emitted (as a copy) and the cursor
+    restarts, so a long document fills several chunks and its tail starts
+    the next one."""
+
+    def __init__(self, chunk_len: int) -> None:
+        if chunk_len <= 0:
+            raise ValueError("chunk_len must be positive")
+        self.chunk_len = chunk_len
+        self._buf = torch.empty(chunk_len, dtype=torch.long)
+        self._fill = 0
+
+    def push(self, ids: Sequence[int]) -> List[torch.Tensor]:
+        out: List[torch.Tensor] = []
+        src = torch.as_tensor(ids, dtype=torch.long).reshape(-1)
+        pos = 0
+        while pos < src.numel():
+            take = min(self.chunk_len - self._fill, src.numel() - pos)
+            self._buf[self._fill:self._fill + take] = src[pos:pos + take]
+            self._fill += take
+            pos += take
+            if self._fill == self.chunk_len:
+                out.append(self._buf.clone())
+                self._fill = 0
+        return out
 
 
 class PackedFineWebDataset(IterableDataset):
-    """Packs a text stream into fixed [seq_len + 1] token chunks, optionally
-    separating documents with EOS (data/fineweb.py:58-97)."""
+    """Packs rows of a text stream (dicts holding `text_key`, or strings) into
+    [seq_len + 1] token chunks with `tokenizer.encode(text,
+    add_special_tokens=False)`, appending `eos_token_id` after each
+    non-empty document when add_eos_between_samples is set."""
 
     def __init__(self, text_iterable: Iterable, tokenizer, seq_len: int, eos_token_id: int, text_key: str = "text",
                  add_eos_between_samples: bool = True) -> None:
@@ -59,22 +98,19 @@ class PackedFineWebDataset(IterableDataset):
         self.text_key = text_key
         self.add_eos_between_samples = add_eos_between_samples
 
-    def __iter__(self) -> Iterator[torch.Tensor]:
-        buf: list = []
-        size = self.seq_len + 1
+    def _texts(self) -> Iterator[str]:
         for row in self.text_iterable:
             text = row.get(self.text_key, "") if isinstance(row, dict) else str(row)
-            if not text:
-                continue
-            ids = self.tokenizer.encode(text, add_special_tokens=False)
-            if not ids:
-                continue
-            buf.extend(ids)
-            if self.add_eos_between_samples:
-                buf.append(self.eos_token_id)
-            while len(buf) >= size:
-                chunk, buf = buf[:size], buf[size:]
-                yield torch.tensor(chunk, dtype=torch.long)
+            if text:
+                yield text
+
+    def __iter__(self) -> Iterator[torch.Tensor]:
+        packer = TokenPacker(self.seq_len + 1)
+        eos = [self.eos_token_id] if self.add_eos_between_samples else []
+        for text in self._texts():
+            ids = list(self.tokenizer.encode(text, add_special_tokens=False))
+            if ids:
+                yield from packer.push(ids + eos)
 
 
 class SyntheticPatternDataset(IterableDataset):
@@ -88,12 +124,11 @@ class SyntheticPatternDataset(IterableDataset):
         self.num_sequences = num_sequences
 
     def __iter__(self) -> Iterator[torch.Tensor]:
-        produced, cursor = 0, 0
         length = self.seq_len + 1
-        while self.num_sequences is None or produced < self.num_sequences:
-            yield torch.arange(cursor, cursor + length, dtype=torch.long) % self.vocab_size
-            cursor = (cursor + length) % self.vocab_size
-            produced += 1
+        counter = itertools.count() if self.num_sequences is None else range(self.num_sequences)
+        for i in counter:
+            start = (i * length) % self.vocab_size
+            yield torch.arange(start, start + length, dtype=torch.long) % self.vocab_size
 
 
 class SyntheticUniformDataset(IterableDataset):
@@ -109,24 +144,21 @@ class SyntheticUniformDataset(IterableDataset):
 
     def __iter__(self) -> Iterator[torch.Tensor]:
         gen = torch.Generator().manual_seed(self.seed)
-        produced = 0
-        while self.num_sequences is None or produced < self.num_sequences:
+        counter = itertools.count() if self.num_sequences is None else range(self.num_sequences)
+        for _ in counter:
             yield torch.randint(0, self.vocab_size, (self.seq_len + 1,), generator=gen, dtype=torch.long)
-            produced += 1
 
 
 class RankShardIterableDataset(IterableDataset):
-    """Strides an iterable dataset so each rank sees a disjoint shard."""
+    """Rank r of world_size sees items r, r + world_size, ... of the stream."""
 
     def __init__(self, dataset: IterableDataset, rank: int, world_size: int) -> None:
         super().__init__()
-        if rank < 0 or world_size <= 0 or rank >= world_size:
+        if world_size <= 0 or not 0 <= rank < world_size:
             raise ValueError(f"invalid rank/world_size: rank={rank}, world_size={world_size}")
         self.dataset = dataset
         self.rank = rank
         self.world_size = world_size
 
     def __iter__(self):
-        for idx, sample in enumerate(self.dataset):
-            if idx % self.world_size == self.rank:
-                yield sample
+        return itertools.islice(iter(self.dataset), self.rank, None, self.world_size)

@@ -1,15 +1,19 @@
-"""Named step timers (reference: profiler/timer.py:24-99).
+"""Named step timers with the reference's API (profiler/timer.py:24-99:
+NamedTimer.start/stop/summary, TimerRegistry.timer/summarize, TimerSummary).
 
-On a GPU device a timer records a start/stop event pair on the current HIP
-stream and synchronizes at stop (the reference's protocol); on the host it uses
-wall-clock time.
+Design: on a GPU a timer records HIP events on the current stream and keeps
+them as pending intervals.  stop() waits only for its own end event (not for
+the whole device) and returns the interval; stop(wait=False) returns
+immediately and leaves the interval to be resolved when a summary is taken,
+so a caller that only needs the aggregate never stalls the stream.  Events
+are pooled per timer.  On the host the timer reads time.perf_counter().
 """
 from __future__ import annotations
 
-import statistics
+import math
 import time
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -26,58 +30,82 @@ class TimerSummary:
     max_ms: float
 
 
+def _quantile(sorted_ms: List[float], q: float) -> float:
+    """Linear interpolation between the two samples that bracket rank
+    q*(n-1) of the sorted samples."""
+    pos = q * (len(sorted_ms) - 1)
+    lo = math.floor(pos)
+    hi = min(lo + 1, len(sorted_ms) - 1)
+    frac = pos - lo
+    return sorted_ms[lo] * (1.0 - frac) + sorted_ms[hi] * frac
+
+
+def _on_gpu(device: Optional[torch.device]) -> bool:
+    return device is not None and device.type == "cuda" and torch.cuda.is_available()
+
+
 @dataclass
 class NamedTimer:
     name: str
     device: Optional[torch.device] = None
-    _samples_ms: List[float] = field(default_factory=list)
-    _start_wall: Optional[float] = None
-    _start_event: Optional[object] = None
-    _end_event: Optional[object] = None
+    _done_ms: List[float] = field(default_factory=list)
+    _pending: List[Tuple[object, object]] = field(default_factory=list)
+    _pool: List[object] = field(default_factory=list)
+    _open: Optional[object] = None  # start event (GPU) or start time (host)
 
-    def _gpu(self) -> bool:
-        return self.device is not None and self.device.type == "cuda" and torch.cuda.is_available()
+    def _event(self):
+        return self._pool.pop() if self._pool else torch.cuda.Event(enable_timing=True)
 
     def start(self) -> None:
-        if self._gpu():
-            self._start_event = torch.cuda.Event(enable_timing=True)
-            self._end_event = torch.cuda.Event(enable_timing=True)
-            self._start_event.record()
+        if _on_gpu(self.device):
+            ev = self._event()
+            ev.record()
+            self._open = ev
         else:
-            self._start_wall = time.perf_counter()
+            self._open = time.perf_counter()
 
-    def stop(self) -> float:
-        if self._start_event is not None and self._end_event is not None:
-            self._end_event.record()
-            torch.cuda.synchronize()
-            elapsed = float(self._start_event.elapsed_time(self._end_event))
-            self._start_event = self._end_event = None
-        elif self._start_wall is not None:
-            elapsed = (time.perf_counter() - self._start_wall) * 1000.0
-            self._start_wall = None
-        else:
+    def stop(self, wait: bool = True) -> float:
+        """Ends the interval opened by start().  Returns its length in ms;
+        with wait=False on a GPU it returns NaN and the interval is resolved
+        by the next summary()."""
+        if self._open is None:
             raise RuntimeError("Timer.stop() called before Timer.start()")
-        self._samples_ms.append(elapsed)
-        return elapsed
+        begin, self._open = self._open, None
+        if not isinstance(begin, torch.cuda.Event):
+            ms = (time.perf_counter() - begin) * 1000.0
+            self._done_ms.append(ms)
+            return ms
+        end = self._event()
+        end.record()
+        if not wait:
+            self._pending.append((begin, end))
+            return math.nan
+        end.synchronize()
+        ms = float(begin.elapsed_time(end))
+        self._done_ms.append(ms)
+        self._pool.extend((begin, end))
+        return ms
+
+    def _resolve(self) -> None:
+        for begin, end in self._pending:
+            end.synchronize()
+            self._done_ms.append(float(begin.elapsed_time(end)))
+            self._pool.extend((begin, end))
+        self._pending.clear()
+
+    @property
+    def _samples_ms(self) -> List[float]:
+        self._resolve()
+        return self._done_ms
 
     def summary(self) -> TimerSummary:
-        if not self._samples_ms:
+        samples = sorted(self._samples_ms)
+        if not samples:
             raise RuntimeError(f"Timer '{self.name}' has no samples")
-        s = sorted(self._samples_ms)
-
-        def pct(p: float) -> float:
-            return float(s[int(round((len(s) - 1) * p))])
-
-        return TimerSummary(
-            name=self.name,
-            count=len(s),
-            total_ms=float(sum(s)),
-            mean_ms=float(statistics.mean(s)),
-            p50_ms=pct(0.50),
-            p95_ms=pct(0.95),
-            min_ms=float(s[0]),
-            max_ms=float(s[-1]),
-        )
+        total = math.fsum(samples)
+        return TimerSummary(name=self.name, count=len(samples), total_ms=total, mean_ms=total / len(samples),
+                            p50_ms=_quantile(samples, 0.50), p95_ms=_quantile(samples, 0.95), min_ms=samples[0],
+                            max_ms=samples[-1])
 
 
 @dataclass
@@ -86,9 +114,10 @@ class TimerRegistry:
     _timers: Dict[str, NamedTimer] = field(default_factory=dict)
 
     def timer(self, name: str) -> NamedTimer:
-        if name not in self._timers:
-            self._timers[name] = NamedTimer(name=name, device=self.device)
-        return self._timers[name]
+        t = self._timers.get(name)
+        if t is None:
+            t = self._timers[name] = NamedTimer(name=name, device=self.device)
+        return t
 
     def summarize(self) -> Dict[str, TimerSummary]:
-        return {n: t.summary() for n, t in self._timers.items() if t._samples_ms}
+        return {name: t.summary() for name, t in self._timers.items() if t._samples_ms}

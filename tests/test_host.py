@@ -174,8 +174,33 @@ def test_rank_shard_and_packed_dataset():
         def encode(self, text, add_special_tokens=False):
             return [ord(c) % 32 for c in text]
 
-    chunks = list(PackedFineWebDataset([{"text": "abcd"}, {"text": "efgh"}, {"text": "ijkl"}], Tok(), 4, eos_token_id=1))
-    assert len(chunks) >= 2 and all(c.shape == (5,) for c in chunks)
+    docs = [{"text": "abcd"}, {"text": ""}, "efgh", {"text": "ijklmnopq"}]
+    chunks = list(PackedFineWebDataset(docs, Tok(), 4, eos_token_id=1))
+    # the concatenation of the non-empty documents, each followed by EOS, cut
+    # into [5] chunks; the remainder is held back
+    stream = []
+    for t in ("abcd", "efgh", "ijklmnopq"):
+        stream += [ord(c) % 32 for c in t] + [1]
+    n = len(stream) // 5
+    assert len(chunks) == n and all(c.shape == (5,) and c.dtype == torch.long for c in chunks)
+    assert torch.equal(torch.stack(chunks).reshape(-1), torch.tensor(stream[:5 * n]))
+
+
+def test_token_packer_and_offline_fineweb():
+    from data import FineWebUnavailable, TokenPacker, load_fineweb_stream, load_llama_tokenizer
+
+    p = TokenPacker(3)
+    assert p.push([]) == []
+    assert p.push([1, 2]) == []
+    out = p.push(list(range(3, 11)))  # 1..10 so far: chunks [1,2,3] [4,5,6] [7,8,9], 10 held
+    assert [c.tolist() for c in out] == [[1, 2, 3], [4, 5, 6], [7, 8, 9]]
+    assert [c.tolist() for c in p.push([11, 12])] == [[10, 11, 12]]
+    with pytest.raises(ValueError):
+        TokenPacker(0)
+    with pytest.raises(FineWebUnavailable, match="synthetic"):
+        load_llama_tokenizer("meta-llama/Llama-3.1-8B")
+    with pytest.raises(FineWebUnavailable):
+        load_fineweb_stream("sample-10BT")
 
 
 # ---------------------------------------------------------------------------
@@ -198,8 +223,15 @@ def test_profiler_helpers():
     t = reg.timer("sleep")
     t.start()
     time.sleep(0.01)
-    t.stop()
+    assert t.stop() >= 10.0
     assert reg.summarize()["sleep"].count == 1 and reg.summarize()["sleep"].total_ms > 0
+    with pytest.raises(RuntimeError):
+        t.stop()
+    for ms in (1.0, 2.0, 3.0, 4.0):  # summary statistics over known samples
+        t._done_ms.append(ms)
+    s = reg.timer("sleep").summary()
+    assert s.count == 5 and s.min_ms == 1.0 and s.max_ms >= 10.0
+    assert s.p50_ms == 3.0 and abs(s.mean_ms - s.total_ms / 5) < 1e-12
     mt = MemoryTracker(device=None)
     mt.record("before")
     mt.record("after")
