@@ -206,7 +206,7 @@ def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev:
     """The same workload with the whole step (both micro-batches, clip, AdamW
     with a device-resident step count) replayed from one HIP graph; each timed
     step copies its micro-batch ids into the graph's static inputs."""
-    from lzhip.functional import pack_parameters_
+    from lzhip.functional import GradSink, pack_parameters_
     from lzhip.graph import GraphedTrainStep
     from lzhip.optim import FusedAdamW
     from model import LlamaForCausalLM
@@ -216,7 +216,7 @@ def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev:
     pack_parameters_(model)
     model.set_loss_chunk_size(128)
     opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, capturable=True)
-    gs = GraphedTrainStep(model, opt, (B, S), GA, 1.0, dev)
+    gs = GraphedTrainStep(model, opt, (B, S), GA, 1.0, dev, grads=GradSink(model))
     for i in range(3):
         gs.warmup(ids_all[GA * i:GA * (i + 1)])
     gs.capture()
@@ -238,7 +238,8 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
     uniform ids from torch.Generator seed 0) for `steps` steps on the HIP path
     (bf16), and the CPU oracle's train.py loop (fp32, every host thread) on
     `cpu_steps` steps of the same stream."""
-    from lzhip.functional import pack_parameters_
+    from lzhip import ops
+    from lzhip.functional import GradSink, pack_parameters_
     from lzhip.optim import FusedAdamW
     from model import LlamaForCausalLM, build_config
 
@@ -251,17 +252,20 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
     pack_parameters_(model)
     model.set_loss_chunk_size(128)
     opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    grads = GradSink(model)  # as train.py: the kernels write and accumulate the gradients
+    seed = ops.fill_(torch.empty((), dtype=torch.float32, device=dev), 1.0 / GA)
     gen = torch.Generator().manual_seed(0)
     chunks = [torch.randint(0, 32000, (B, S + 1), generator=gen) for _ in range(GA * (steps + 5))]
     ids_all = [c[:, :-1].contiguous().to(dev) for c in chunks]
 
     def one(step):
-        opt.zero_grad(set_to_none=True)
+        grads.begin_step()
         loss = None
         for a in range(GA):
             ids = ids_all[GA * step + a]
             loss = model(input_ids=ids, labels=ids, return_logits=False).loss
-            (loss / GA).backward()
+            loss.backward(gradient=seed)  # = (loss / GA).backward()
+        grads.finish()
         opt.clip_grad_norm_(1.0)
         opt.step()
         return loss

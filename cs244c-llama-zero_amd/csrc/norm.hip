@@ -96,69 +96,15 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(const T* __restri
   }
 }
 
-// Column sums of dw in the same launch, without a grid-wide wait.  Workgroups
-// form groups of kGroup; the last one of a group to finish (its ticket from
-// the group's counter) adds the group's partial rows into a group row, and
-// the last group to finish adds the group rows into dw.  Every sum runs in
-// a fixed order, so dw does not depend on which workgroup finishes last.
-// The counters start at zero and each last arrival resets its own, so the
-// workspace is left ready for the next launch.
-constexpr int kGroup = 16;
-constexpr int kMaxGroups = 255;                       // counters[255] is the top counter
-constexpr int64_t kCounterBytes = 256 * 4;            // leading workspace bytes
-
-__device__ __forceinline__ bool last_arrival(int* counter, int expected) {
-  __shared__ int s_last;
-  __threadfence();  // this workgroup's partial-row stores before its ticket
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == expected - 1;
-  __syncthreads();
-  if (!s_last) return false;
-  __threadfence();  // the other workgroups' rows, seen after their tickets
-  if (threadIdx.x == 0) *counter = 0;
-  return true;
-}
-
-// out[c] = sum_{r in [r0, r1)} part[r * cols + c] for every column, 8 columns
-// per thread per pass (cols % 8 == 0, 16-byte aligned rows).
-__device__ __forceinline__ void sum_rows8(const float* part, int64_t r0, int64_t r1, int cols, float* out,
-                                          uint16_t* out_bf16, int accumulate) {
-  for (int c = 8 * threadIdx.x; c < cols; c += 8 * kThreads) {
-    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int64_t r = r0; r < r1; ++r) {
-      const float4 u = reinterpret_cast<const float4*>(part + r * cols + c)[0];
-      const float4 v = reinterpret_cast<const float4*>(part + r * cols + c)[1];
-      a[0] += u.x; a[1] += u.y; a[2] += u.z; a[3] += u.w;
-      a[4] += v.x; a[5] += v.y; a[6] += v.z; a[7] += v.w;
-    }
-    if (out_bf16) {
-      if (accumulate) {
-        float o[8];
-        Pack8<uint16_t>::load(out_bf16 + c, o);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] += o[e];
-      }
-      Pack8<uint16_t>::store(out_bf16 + c, a);
-    } else {
-      reinterpret_cast<float4*>(out + c)[0] = make_float4(a[0], a[1], a[2], a[3]);
-      reinterpret_cast<float4*>(out + c)[1] = make_float4(a[4], a[5], a[6], a[7]);
-    }
-  }
-}
-
 // bf16 backward: workgroup b owns rows [b*rpb, (b+1)*rpb), its wave w takes
 // rows w, w+4, ... of that range and loads the next one (x, dy and the
-// residual gradient) while it computes the current one.  The 4 waves' dw
-// contributions are summed in LDS (in a fixed order) into one fp32 partial
-// row per workgroup, dw_part[b][cols]; with dw given, the column sums follow
-// in the same launch (kGroup above): group rows in gpart[ngroups][cols],
-// counters[0, ngroups) per group and counters[kMaxGroups] on top.
+// residual gradient) while it computes the current one.  The 4 waves' dw contributions are summed in LDS (in a fixed
+// order) into one fp32 partial row per workgroup: dw_part[b][cols].
 template <int NC>
 __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ rstd,
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ dres, uint16_t* __restrict__ dx,
-    float* __restrict__ dw_part, int64_t rows, int64_t rpb, int cols, int64_t ldx, int64_t lddy, int64_t lddx,
-    int* __restrict__ counters, float* __restrict__ gpart, uint16_t* __restrict__ dw, int dw_accumulate) {
+    float* __restrict__ dw_part, int64_t rows, int64_t rpb, int cols, int64_t ldx, int64_t lddy, int64_t lddx) {
   __shared__ float red[2][NC * 512];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nchunk = cols >> 3;
@@ -272,14 +218,6 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
       }
     }
   }
-  if (dw == nullptr) return;
-  const int nblk = (int)gridDim.x;
-  const int grp = (int)blockIdx.x / kGroup, ngroups = (nblk + kGroup - 1) / kGroup;
-  const int b0 = grp * kGroup, b1 = min(nblk, b0 + kGroup);
-  if (!last_arrival(counters + grp, b1 - b0)) return;
-  sum_rows8(dw_part, b0, b1, cols, gpart + (int64_t)grp * cols, nullptr, 0);
-  if (!last_arrival(counters + kMaxGroups, ngroups)) return;
-  sum_rows8(gpart, 0, ngroups, cols, nullptr, dw, dw_accumulate);
 }
 
 // Generic path for any cols (scalar accesses, two passes over the row).
@@ -448,6 +386,21 @@ inline int64_t bwd_waves(int64_t rows) {
   return std::max<int64_t>(kRowsPerBlock, (n / kRowsPerBlock) * kRowsPerBlock);
 }
 
+// Workspace bytes of one backward on the path its shape and layout take.
+template <typename T>
+bool bwd_vec(const void* x, const void* w, const void* dy, const void* dres, const void* dx, int64_t cols, int64_t ldx,
+             int64_t lddy, int64_t lddx) {
+  return cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(dy) && lz_aligned16(dx) &&
+         (dres == nullptr || lz_aligned16(dres)) && (ldx * (int64_t)sizeof(T)) % 16 == 0 &&
+         (lddy * (int64_t)sizeof(T)) % 16 == 0 && (lddx * (int64_t)sizeof(T)) % 16 == 0;
+}
+
+template <typename T>
+int64_t bwd_bytes(bool vec, int64_t rows, int64_t cols) {
+  if (sizeof(T) == 2 && vec && cols <= 4096) return (bwd_blocks(rows, cols) + kSlices) * cols * 4;
+  return (bwd_waves(rows) + kSlices) * cols * 4;
+}
+
 template <typename T>
 int fwd_dispatch(const void* x, const void* w, void* y, float* rstd, int64_t rows, int cols, int64_t ldx, int64_t ldy,
                  float eps, hipStream_t s) {
@@ -465,70 +418,55 @@ int fwd_dispatch(const void* x, const void* w, void* y, float* rstd, int64_t row
   return lz_check_launch("lz_rmsnorm_fwd");
 }
 
-// Bytes of the bf16 vector path's workspace after the counters: the partial
-// rows and the group rows.
-inline int64_t bwd_bf16_bytes(int64_t nblk, int64_t cols) {
-  return (nblk + lz_cdiv(nblk, kGroup)) * cols * 4;
-}
-
-template <typename T>
-bool bwd_vec(const void* x, const void* w, const void* dy, const void* dres, const void* dx, const void* dw,
-             int64_t cols, int64_t ldx, int64_t lddy, int64_t lddx) {
-  return cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(dy) && lz_aligned16(dx) &&
-         (dres == nullptr || lz_aligned16(dres)) && (dw == nullptr || lz_aligned16(dw)) &&
-         (ldx * (int64_t)sizeof(T)) % 16 == 0 && (lddy * (int64_t)sizeof(T)) % 16 == 0 &&
-         (lddx * (int64_t)sizeof(T)) % 16 == 0;
-}
-
-// Workspace bytes of one backward: the counters, then the partial rows of
-// the path the shape takes.
-template <typename T>
-int64_t bwd_bytes(bool vec, int64_t rows, int64_t cols) {
-  if (sizeof(T) == 2 && vec && cols <= 4096) return kCounterBytes + bwd_bf16_bytes(bwd_blocks(rows, cols), cols);
-  return kCounterBytes + (bwd_waves(rows) + kSlices) * cols * 4;
-}
-
-// ws: kCounterBytes of counters (zero on entry, left zero), then the partial
-// rows (bwd_bytes).
 template <typename T>
 int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
-                 int dw_accumulate, char* ws, int64_t ws_bytes, int64_t rows, int cols, int64_t ldx, int64_t lddy,
+                 int dw_accumulate, float* ws, int64_t ws_bytes, int64_t rows, int cols, int64_t ldx, int64_t lddy,
                  int64_t lddx, hipStream_t s) {
-  const bool vec = bwd_vec<T>(x, w, dy, dres, dx, dw, cols, ldx, lddy, lddx);
-  LZ_REQUIRE(ws_bytes >= bwd_bytes<T>(vec, rows, cols), "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
-             (long long)ws_bytes);
-  int* counters = reinterpret_cast<int*>(ws);
-  float* part = reinterpret_cast<float*>(ws + kCounterBytes);
+  // workspace: one fp32 partial row per wave (per workgroup on the bf16
+  // vector path), then kSlices rows of slice sums
+  const bool vec = cols % 8 == 0 && lz_aligned16(x) && lz_aligned16(w) && lz_aligned16(dy) && lz_aligned16(dx) &&
+                   (dres == nullptr || lz_aligned16(dres)) && (ldx * (int64_t)sizeof(T)) % 16 == 0 &&
+                   (lddy * (int64_t)sizeof(T)) % 16 == 0 && (lddx * (int64_t)sizeof(T)) % 16 == 0;
   const T *xp = (const T*)x, *wp = (const T*)w, *gp = (const T*)dy, *rp = (const T*)dres;
   T* dxp = (T*)dx;
   if constexpr (sizeof(T) == 2) {
     if (vec && cols <= 4096) {
       const int64_t nblk = bwd_blocks(rows, cols), rpb = lz_cdiv(rows, nblk);
-      LZ_REQUIRE(lz_cdiv(nblk, kGroup) <= kMaxGroups, "lz_rmsnorm_bwd: too many workgroups (%lld)", (long long)nblk);
+      LZ_REQUIRE(ws_bytes >= (nblk + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
+                 (long long)ws_bytes);
       const uint16_t *x16 = (const uint16_t*)x, *w16 = (const uint16_t*)w, *g16 = (const uint16_t*)dy,
                      *r16 = (const uint16_t*)dres;
-      uint16_t *dx16 = (uint16_t*)dx, *dw16 = (uint16_t*)dw;
-      float* gpart = part + nblk * (int64_t)cols;
+      uint16_t* dx16 = (uint16_t*)dx;
       const unsigned grid = (unsigned)nblk;
-      if (cols <= 512) rmsnorm_bwd_bf16_kernel<1><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, part, rows, rpb, cols, ldx, lddy, lddx, counters, gpart, dw16, dw_accumulate);
-      else if (cols <= 1024) rmsnorm_bwd_bf16_kernel<2><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, part, rows, rpb, cols, ldx, lddy, lddx, counters, gpart, dw16, dw_accumulate);
-      else if (cols <= 2048) rmsnorm_bwd_bf16_kernel<4><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, part, rows, rpb, cols, ldx, lddy, lddx, counters, gpart, dw16, dw_accumulate);
-      else rmsnorm_bwd_bf16_kernel<8><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, part, rows, rpb, cols, ldx, lddy, lddx, counters, gpart, dw16, dw_accumulate);
-      return lz_check_launch("lz_rmsnorm_bwd");
+      if (cols <= 512) rmsnorm_bwd_bf16_kernel<1><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else if (cols <= 1024) rmsnorm_bwd_bf16_kernel<2><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else if (cols <= 2048) rmsnorm_bwd_bf16_kernel<4><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else rmsnorm_bwd_bf16_kernel<8><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      int rc = lz_check_launch("lz_rmsnorm_bwd");
+      if (rc) return rc;
+      if (dw) {
+        float* slices = ws + nblk * (int64_t)cols;
+        dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(ws, nblk, cols, slices);
+        dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, (T*)dw, dw_accumulate);
+        rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
+      }
+      return rc;
     }
   }
   const int64_t nwaves = bwd_waves(rows);
+  LZ_REQUIRE(ws_bytes >= (nwaves + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
+             (long long)ws_bytes);
   const int grid = (int)(nwaves / kRowsPerBlock);
-  if (vec && cols <= 512) rmsnorm_bwd_kernel<T, 1><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, part, rows, cols, ldx, lddy, lddx);
-  else if (vec && cols <= 1024) rmsnorm_bwd_kernel<T, 2><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, part, rows, cols, ldx, lddy, lddx);
-  else if (vec && cols <= 2048) rmsnorm_bwd_kernel<T, 4><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, part, rows, cols, ldx, lddy, lddx);
-  else if (vec && cols <= 4096) rmsnorm_bwd_kernel<T, 8><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, part, rows, cols, ldx, lddy, lddx);
-  else rmsnorm_bwd_scalar_kernel<T><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, part, rows, cols, ldx, lddy, lddx);
+  if (vec && cols <= 512) rmsnorm_bwd_kernel<T, 1><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else if (vec && cols <= 1024) rmsnorm_bwd_kernel<T, 2><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else if (vec && cols <= 2048) rmsnorm_bwd_kernel<T, 4><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else if (vec && cols <= 4096) rmsnorm_bwd_kernel<T, 8><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
+  else rmsnorm_bwd_scalar_kernel<T><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
   int rc = lz_check_launch("lz_rmsnorm_bwd");
   if (rc) return rc;
   if (dw) {
-    float* slices = part + nwaves * (int64_t)cols;
-    dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(part, nwaves, cols, slices);
+    float* slices = ws + nwaves * (int64_t)cols;
+    dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(ws, nwaves, cols, slices);
     dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, (T*)dw, dw_accumulate);
     rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
   }
@@ -547,28 +485,23 @@ LZ_EXPORT int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,
   return lz_set_error(LZ_EINVAL, "lz_rmsnorm_fwd: bad dtype %d", dtype);
 }
 
-// Workspace bytes the backward wants: kCounterBytes of counters, then the
-// dw partial rows (the largest either path takes for this shape).
+// Workspace bytes the backward wants for its dw partials.
 LZ_EXPORT int64_t lz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
-  if (rows <= 0 || cols <= 0) return kCounterBytes;
-  return std::max(bwd_bytes<uint16_t>(true, rows, cols), bwd_bytes<float>(false, rows, cols));
+  return (std::max(bwd_waves(rows), bwd_blocks(rows, cols)) + kSlices) * cols * 4;
 }
 
-// The workspace's first kCounterBytes must be zero before the first call
-// that uses it; every call leaves them zero.  Calls that share a workspace
-// must not overlap in time.
 LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,
                              void* dw, int dw_accumulate, void* workspace, int64_t workspace_bytes, int dtype, int64_t rows,
                              int64_t cols, int64_t ldx, int64_t lddy, int64_t lddx, void* stream) {
   LZ_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30), "lz_rmsnorm_bwd: bad shape");
   LZ_REQUIRE(ldx >= cols && lddy >= cols && lddx >= cols, "lz_rmsnorm_bwd: bad leading dimension");
-  LZ_REQUIRE(workspace != nullptr && lz_aligned16(workspace), "lz_rmsnorm_bwd: null or unaligned workspace");
+  LZ_REQUIRE(workspace != nullptr, "lz_rmsnorm_bwd: null workspace");
   if (rows == 0) return LZ_OK;
   if (dtype == LZ_BF16)
-    return bwd_dispatch<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (char*)workspace, workspace_bytes, rows,
+    return bwd_dispatch<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (float*)workspace, workspace_bytes, rows,
                                   (int)cols, ldx, lddy, lddx, lz_stream(stream));
   if (dtype == LZ_F32)
-    return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (char*)workspace, workspace_bytes, rows,
+    return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (float*)workspace, workspace_bytes, rows,
                                (int)cols, ldx, lddy, lddx, lz_stream(stream));
   return lz_set_error(LZ_EINVAL, "lz_rmsnorm_bwd: bad dtype %d", dtype);
 }
@@ -576,10 +509,11 @@ LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, co
 // ---------------------------------------------------------------------------
 // Backward without a caller workspace, for callers that cannot allocate
 // device memory (code under HIP graph capture, serving loops, harnesses that
-// forbid allocation).  The partial rows and counters live in `scratch`, a
-// fixed array of kScratchBytes per device that stays allocated until the
-// process ends.  Every call on a device shares that device's array, so calls
-// that overlap in time on one device (other streams, other threads) race.
+// forbid allocation).  The dw partial rows live in `scratch`, a fixed array of
+// kScratchBytes per device that stays allocated until the process ends.
+// Every call writes the partial rows it reads, so nothing in it has to start
+// at zero.  Every call on a device shares that device's array, so calls that
+// overlap in time on one device (other streams, other threads) race.
 // ---------------------------------------------------------------------------
 constexpr int64_t kScratchBytes = 8ll << 20;
 static __device__ __align__(256) char scratch[kScratchBytes];
@@ -588,17 +522,11 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-char* g_scratch_ptr[kMaxDevices] = {};
-
-__global__ void zero_counters_kernel(int* c, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) c[i] = 0;
-}
+float* g_scratch_ptr[kMaxDevices] = {};
 
 // This device's address of `scratch` (the host-side symbol is a stand-in,
-// not a device address), looked up once per device; the counters are zeroed
-// on the caller's stream at that first call (a kernel, no memset).
-int scratch_for_device(hipStream_t s, char** out) {
+// not a device address), looked up once per device.
+int scratch_for_device(float** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return lz_set_error(LZ_ERUNTIME, "lz_rmsnorm_bwd_noalloc: no current device (%d)", dev);
@@ -609,11 +537,7 @@ int scratch_for_device(hipStream_t s, char** out) {
     if (e != hipSuccess || p == nullptr)
       return lz_set_error(LZ_ERUNTIME, "lz_rmsnorm_bwd_noalloc: hipGetSymbolAddress(scratch) failed: %s",
                           hipGetErrorString(e));
-    const int n = (int)(kCounterBytes / 4);
-    zero_counters_kernel<<<(n + 255) / 256, 256, 0, s>>>(static_cast<int*>(p), n);
-    const int rc = lz_check_launch("lz_rmsnorm_bwd_noalloc(zero counters)");
-    if (rc) return rc;
-    g_scratch_ptr[dev] = static_cast<char*>(p);
+    g_scratch_ptr[dev] = static_cast<float*>(p);
   }
   *out = g_scratch_ptr[dev];
   return LZ_OK;
@@ -634,15 +558,15 @@ LZ_EXPORT int lz_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* 
   LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_rmsnorm_bwd_noalloc: bad dtype %d", dtype);
   if (rows == 0) return LZ_OK;
   const int64_t need = dtype == LZ_BF16
-      ? bwd_bytes<uint16_t>(bwd_vec<uint16_t>(x, w, dy, dres, dx, dw, cols, ldx, lddy, lddx), rows, cols)
-      : bwd_bytes<float>(bwd_vec<float>(x, w, dy, dres, dx, dw, cols, ldx, lddy, lddx), rows, cols);
+      ? bwd_bytes<uint16_t>(bwd_vec<uint16_t>(x, w, dy, dres, dx, cols, ldx, lddy, lddx), rows, cols)
+      : bwd_bytes<float>(bwd_vec<float>(x, w, dy, dres, dx, cols, ldx, lddy, lddx), rows, cols);
   LZ_REQUIRE(need <= kScratchBytes,
              "lz_rmsnorm_bwd_noalloc: rows %lld x cols %lld need %lld bytes of scratch, more than its %lld",
              (long long)rows, (long long)cols, (long long)need, (long long)kScratchBytes);
-  hipStream_t s = lz_stream(stream);
-  char* ws = nullptr;
-  const int rc = scratch_for_device(s, &ws);
+  float* ws = nullptr;
+  const int rc = scratch_for_device(&ws);
   if (rc) return rc;
+  hipStream_t s = lz_stream(stream);
   if (dtype == LZ_BF16)
     return bwd_dispatch<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, ws, kScratchBytes, rows, (int)cols, ldx,
                                   lddy, lddx, s);

@@ -53,6 +53,96 @@ def pack_parameters_(module: torch.nn.Module) -> int:
     return len(params)
 
 
+class GradSink:
+    """Parameter gradients written by the backward kernels themselves, for
+    gradient accumulation over micro-batches (reference train.py:236-257:
+    zero_grad, then (loss / GA).backward() per micro-batch).
+
+    Every parameter's .grad is a view of one flat buffer per dtype.  The
+    first backward of a step writes each weight gradient over its .grad (the
+    GEMM with beta 0, the RMSNorm and embedding kernels without their
+    accumulate flag); later ones add into it (beta 1, accumulate), and the
+    autograd Functions return no gradient for the parameter.  So autograd
+    neither adds the micro-batches' gradients nor sums the tied weight's two
+    contributions with its own kernels.  Call begin_step() where the
+    reference calls optimizer.zero_grad(); finish() zeroes the gradients of
+    parameters no backward reached.  Engines that read gradients through
+    autograd hooks (ZeRO stage 2) must not be combined with a sink."""
+
+    def __init__(self, module: torch.nn.Module) -> None:
+        self.params: List[torch.nn.Parameter] = []
+        seen = set()
+        for prm in module.parameters():
+            if prm.requires_grad and id(prm) not in seen:
+                seen.add(id(prm))
+                self.params.append(prm)
+        by_dtype = {}
+        for prm in self.params:
+            ops.require_gpu(prm)
+            by_dtype.setdefault(prm.dtype, []).append(prm)
+        self.flat = {}
+        self._views = {}
+        for dtype, group in by_dtype.items():
+            flat = ops.zeros((sum(prm.numel() for prm in group),), dtype, group[0].device)
+            self.flat[dtype] = flat
+            off = 0
+            for prm in group:
+                self._views[id(prm)] = flat[off : off + prm.numel()].view(prm.shape)
+                off += prm.numel()
+        self._fresh = {id(prm): True for prm in self.params}
+        for prm in self.params:
+            prm._lz_grad_sink = self
+        self.begin_step()
+
+    def begin_step(self) -> None:
+        for prm in self.params:
+            prm.grad = self._views[id(prm)]
+            self._fresh[id(prm)] = True
+
+    def take(self, prm: torch.Tensor) -> Tuple[torch.Tensor, bool]:
+        """(gradient buffer, accumulate?) for the next write of prm's gradient."""
+        fresh = self._fresh[id(prm)]
+        self._fresh[id(prm)] = False
+        if prm.grad is not self._views[id(prm)]:
+            prm.grad = self._views[id(prm)]
+        return self._views[id(prm)], not fresh
+
+    def finish(self) -> None:
+        for prm in self.params:
+            if self._fresh[id(prm)]:
+                ops.fill_(self._views[id(prm)], 0.0)
+                self._fresh[id(prm)] = False
+
+    def detach(self) -> None:
+        for prm in self.params:
+            if getattr(prm, "_lz_grad_sink", None) is self:
+                del prm._lz_grad_sink
+
+
+def _sink(weight: torch.Tensor) -> Optional[GradSink]:
+    return getattr(weight, "_lz_grad_sink", None)
+
+
+def _sink_views(weights: Sequence[torch.Tensor]) -> Optional[Tuple[torch.Tensor, bool]]:
+    """The fused gradient buffer of weights that share one sink, as a view
+    over their adjacent .grad buffers, and whether it accumulates; None when
+    any weight has no sink or the buffers are not adjacent."""
+    sinks = [_sink(w) for w in weights]
+    if sinks[0] is None or any(sk is not sinks[0] for sk in sinks):
+        return None
+    sink = sinks[0]
+    views = [sink._views[id(w)] for w in weights]
+    fused = fused_weight(views)
+    if len(views) > 1 and fused.data_ptr() != views[0].data_ptr():
+        return None
+    if fused.untyped_storage().data_ptr() != views[0].untyped_storage().data_ptr():
+        return None
+    accs = [sink.take(w)[1] for w in weights]
+    if len(set(accs)) != 1:
+        raise RuntimeError("fused weights reached the gradient sink out of step")
+    return fused, accs[0]
+
+
 def fused_weight(weights: Sequence[torch.Tensor]) -> torch.Tensor:
     """Concatenation of weight matrices along their output rows.  When the
     storages are already adjacent (parameters that are views of one flat
@@ -88,15 +178,35 @@ def _linear_fwd(x2: torch.Tensor, w: torch.Tensor, residual2: Optional[torch.Ten
     return ops.gemm(x2, w, residual=residual2)
 
 
-def _linear_bwd(dy2: torch.Tensor, x2: torch.Tensor, w: torch.Tensor, need_dx: bool, need_dw: bool
+def _linear_bwd(dy2: torch.Tensor, x2: torch.Tensor, w: torch.Tensor, need_dx: bool, need_dw: bool,
+                sink_weights: Optional[Sequence[torch.Tensor]] = None
                 ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
     """dx = dy . W (W read N-major), dW = dy^T . x (both read M/N-major): the
-    GEMM consumes the stored layouts directly, nothing is transposed."""
+    GEMM consumes the stored layouts directly, nothing is transposed.  With
+    `sink_weights` (the weights whose rows make up w) in a GradSink, dW goes
+    straight into their gradient buffers and None is returned for it."""
     dx = dw = None
     if need_dx:
         dx = ops.gemm(dy2, w, b_kmajor=False)  # [M, K]
     if need_dw:
-        dw = ops.gemm(dy2, x2, a_kmajor=False, b_kmajor=False, out_dtype=w.dtype)  # [N, K]
+        target = _sink_views(sink_weights) if sink_weights is not None else None
+        if target is not None:
+            buf, acc = target
+            ops.gemm(dy2, x2, a_kmajor=False, b_kmajor=False, out=buf.view(w.shape), beta=1.0 if acc else 0.0)
+        else:
+            dw = ops.gemm(dy2, x2, a_kmajor=False, b_kmajor=False, out_dtype=w.dtype)  # [N, K]
+            if sink_weights is not None and _sink(sink_weights[0]) is not None:
+                # sink buffers that are not adjacent: hand each weight its rows
+                r = 0
+                for wt in sink_weights:
+                    buf, acc = _sink(wt).take(wt)
+                    part = dw[r : r + wt.shape[0]]
+                    if acc:
+                        ops.add_(buf, part)
+                    else:
+                        ops.copy2d(part, buf.view(part.shape))
+                    r += wt.shape[0]
+                dw = None
     return dx, dw
 
 
@@ -119,7 +229,7 @@ class LinearFn(Function):
     def backward(ctx, dy: torch.Tensor):
         x2, weight = ctx.saved_tensors
         dy2 = _rows(dy)
-        dx, dw = _linear_bwd(dy2, x2, weight, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        dx, dw = _linear_bwd(dy2, x2, weight, ctx.needs_input_grad[0], ctx.needs_input_grad[1], [weight])
         if dx is not None:
             dx = dx.view(ctx.in_shape)
         dres = dy if (ctx.has_residual and ctx.needs_input_grad[2]) else None
@@ -144,7 +254,8 @@ class RMSNormFn(Function):
     @staticmethod
     def backward(ctx, dy: torch.Tensor):
         x2, weight, rstd = ctx.saved_tensors
-        dx, dw = ops.rmsnorm_bwd(x2, weight, rstd, _rows(dy), need_dw=ctx.needs_input_grad[1])
+        dx, dw = ops.rmsnorm_bwd(x2, weight, rstd, _rows(dy), need_dw=ctx.needs_input_grad[1],
+                                 dw_sink=_sink(weight) if ctx.needs_input_grad[1] else None)
         return dx.view(ctx.in_shape), dw, None
 
 
@@ -172,7 +283,8 @@ class RMSNormResidualFn(Function):
         if dy is None:
             return dres, None, None
         r2 = _rows(dres) if dres is not None else None
-        dx, dw = ops.rmsnorm_bwd(x2, weight, rstd, _rows(dy), dres=r2, need_dw=ctx.needs_input_grad[1])
+        dx, dw = ops.rmsnorm_bwd(x2, weight, rstd, _rows(dy), dres=r2, need_dw=ctx.needs_input_grad[1],
+                                 dw_sink=_sink(weight) if ctx.needs_input_grad[1] else None)
         return dx.view(ctx.in_shape), dw, None
 
 
@@ -252,7 +364,7 @@ class AttnProjFn(Function):
         ops.rope_(dqkv, S, H + KV, hd, cos, sin, backward=True)
         need_w = any(ctx.needs_input_grad[1:4])
         w = fused_weight([wq, wk, wv])
-        dh2, dw = _linear_bwd(dqkv, h2, w, ctx.needs_input_grad[0], need_w)
+        dh2, dw = _linear_bwd(dqkv, h2, w, ctx.needs_input_grad[0], need_w, [wq, wk, wv])
         dwq = dwk = dwv = None
         if dw is not None:
             nq, nk = wq.shape[0], wk.shape[0]
@@ -292,12 +404,12 @@ class MLPFn(Function):
         x2, wg, wu, wd, gu, m = ctx.saved_tensors
         F_ = wg.shape[0]
         dy2 = _rows(dy)
-        dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3])
+        dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3], [wd])
         dgu = torch.empty_like(gu)
         ops.swiglu_bwd(gu[:, :F_], gu[:, F_:], dm, dgu[:, :F_], dgu[:, F_:])
         w = fused_weight([wg, wu])
         need_w = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
-        dx2, dw = _linear_bwd(dgu, x2, w, ctx.needs_input_grad[0], need_w)
+        dx2, dw = _linear_bwd(dgu, x2, w, ctx.needs_input_grad[0], need_w, [wg, wu])
         dwg = dwu = None
         if dw is not None:
             dwg, dwu = dw[:F_], dw[F_:]
@@ -333,12 +445,17 @@ class EmbeddingFn(Function):
         out = ops.embedding_fwd(ids, weight)
         ctx.save_for_backward(ids)
         ctx.vocab, ctx.dtype = weight.shape[0], weight.dtype
+        ctx.sink_weight = weight if _sink(weight) is not None else None
         return out
 
     @staticmethod
     def backward(ctx, dout):
         (ids,) = ctx.saved_tensors
         if not ctx.needs_input_grad[1]:
+            return None, None
+        if ctx.sink_weight is not None:
+            buf, acc = _sink(ctx.sink_weight).take(ctx.sink_weight)
+            ops.embedding_bwd(ids, _rows(dout), ctx.vocab, ctx.dtype, grad=buf, accumulate=acc)
             return None, None
         grad = ops.embedding_bwd(ids, _rows(dout), ctx.vocab, ctx.dtype)
         return None, grad
@@ -428,6 +545,7 @@ class LMHeadCEFn(Function):
         loss, _ = ops.ce_reduce(row_loss, lab, T, S, V, clamp)
         ctx.save_for_backward(dx, dw32)
         ctx.x_shape, ctx.w_dtype = x.shape, weight.dtype
+        ctx.weight_ref = weight if _sink(weight) is not None else None
         return loss
 
     @staticmethod
@@ -440,7 +558,15 @@ class LMHeadCEFn(Function):
             gx = dx.view(ctx.x_shape)
         if dw32 is not None and ctx.needs_input_grad[1]:
             ops.scale_dev_(dw32, g)
-            gw = ops.cast(dw32, ctx.w_dtype)
+            sink = _sink(ctx.weight_ref) if ctx.weight_ref is not None else None
+            if sink is not None:
+                buf, acc = sink.take(ctx.weight_ref)
+                if acc:
+                    ops.add_(buf.view(-1), ops.cast(dw32, ctx.w_dtype).view(-1))
+                else:
+                    ops.cast(dw32, ctx.w_dtype, out=buf)
+            else:
+                gw = ops.cast(dw32, ctx.w_dtype)
         return gx, gw, None, None, None, None
 
 

@@ -17,25 +17,36 @@ from typing import Sequence
 
 import torch
 
+from . import ops
+
 
 class GraphedTrainStep:
-    def __init__(self, model, opt, batch_shape, grad_accum: int, max_grad_norm: float, device) -> None:
+    def __init__(self, model, opt, batch_shape, grad_accum: int, max_grad_norm: float, device, grads=None) -> None:
+        """grads: an optional functional.GradSink over the model's parameters
+        (the backward kernels then write the gradients; no autograd
+        accumulation kernels are recorded)."""
         if not getattr(opt, "capturable", False):
             raise ValueError("GraphedTrainStep needs an optimizer built with capturable=True")
         if grad_accum < 1:
             raise ValueError("grad_accum must be >= 1")
-        self.model, self.opt = model, opt
+        self.model, self.opt, self.grads = model, opt, grads
         self.grad_accum, self.max_grad_norm = int(grad_accum), float(max_grad_norm)
         self.ids = [torch.zeros(tuple(batch_shape), dtype=torch.int64, device=device) for _ in range(grad_accum)]
+        self.seed = ops.fill_(torch.empty((), dtype=torch.float32, device=device), 1.0 / self.grad_accum)
         self.graph = None
         self.loss = None
 
     def _body(self) -> torch.Tensor:
-        self.opt.zero_grad(set_to_none=True)
+        if self.grads is not None:
+            self.grads.begin_step()
+        else:
+            self.opt.zero_grad(set_to_none=True)
         loss = None
         for ids in self.ids:
             loss = self.model(input_ids=ids, labels=ids, return_logits=False).loss
-            (loss / self.grad_accum).backward()
+            loss.backward(gradient=self.seed)  # = (loss / grad_accum).backward()
+        if self.grads is not None:
+            self.grads.finish()
         if self.max_grad_norm > 0:
             self.opt.clip_grad_norm_(self.max_grad_norm)
         self.opt.step()

@@ -366,24 +366,32 @@ _norm_workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
 
 
 def _rmsnorm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The RMSNorm backward's workspace for the current stream: kept between
-    calls because its leading counters must start at zero (they are zeroed
-    once here and every call leaves them zero); calls on one stream never
-    overlap."""
+    """The RMSNorm backward's dw partials for the current stream, kept
+    between calls (one allocation per stream instead of one per call); calls
+    on one stream never overlap."""
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream_ptr(device))
     ws = _norm_workspaces.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
-        ws = zeros(((max(nbytes, 16) + 15) // 16 * 4,), torch.float32, device)
+        ws = torch.empty(((max(nbytes, 16) + 15) // 16 * 4,), dtype=torch.float32, device=device)
         _norm_workspaces[key] = ws
     return ws
 
 
 def rmsnorm_bwd(x2: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy2: torch.Tensor,
-                dres: Optional[torch.Tensor] = None, need_dw: bool = True) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+                dres: Optional[torch.Tensor] = None, need_dw: bool = True, dw_sink=None
+                ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """dx and dw; with dw_sink (a GradSink holding w) dw is written or added
+    into w's gradient buffer there and None is returned for it."""
     require_gpu(x2, w, rstd, dy2, dres)
     rows, cols = x2.shape
     dx = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
-    dw = torch.empty((cols,), dtype=w.dtype, device=w.device) if need_dw else None
+    dw_acc = 0
+    if dw_sink is not None and need_dw:
+        dw_buf, acc = dw_sink.take(w)
+        dw, dw_acc = None, int(acc)
+    else:
+        dw = torch.empty((cols,), dtype=w.dtype, device=w.device) if need_dw else None
+        dw_buf = dw
     ws = _rmsnorm_workspace(x2.device, int(_lib.load().lz_rmsnorm_bwd_workspace(rows, cols)))
     if dres is not None:
         if dres.shape != dx.shape or dres.dtype != dx.dtype:
@@ -391,7 +399,7 @@ def rmsnorm_bwd(x2: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy2: torc
         if _row_stride(dres) != cols or dres.stride(-1) != 1:
             dres = dres.contiguous()  # the kernel reads dres with dx's row stride
     _lib.call("lz_rmsnorm_bwd", x2.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(), _ptr(dres), dx.data_ptr(),
-              _ptr(dw), 0, ws.data_ptr(), ws.numel() * 4, dtype_code(x2), rows, cols, _row_stride(x2),
+              _ptr(dw_buf), dw_acc, ws.data_ptr(), ws.numel() * 4, dtype_code(x2), rows, cols, _row_stride(x2),
               _row_stride(dy2), cols, stream_ptr(x2.device))
     return dx, dw
 
@@ -452,14 +460,19 @@ def embedding_fwd(ids: torch.Tensor, table: torch.Tensor, bad_flag: Optional[tor
 
 
 def embedding_bwd(ids: torch.Tensor, dout2: torch.Tensor, vocab: int, dtype: torch.dtype,
-                  grad: Optional[torch.Tensor] = None) -> torch.Tensor:
-    require_gpu(ids, dout2)
+                  grad: Optional[torch.Tensor] = None, accumulate: Optional[bool] = None) -> torch.Tensor:
+    """The table gradient; written into `grad` when given, added to it when
+    accumulate (default: whenever grad is given)."""
+    require_gpu(ids, dout2, grad)
     ids_c = ids.contiguous()
     dim = dout2.size(1)
     out = torch.empty((vocab, dim), dtype=dtype, device=dout2.device) if grad is None else grad
+    if grad is not None and (grad.numel() != vocab * dim or not grad.is_contiguous() or grad.dtype != dtype):
+        raise ValueError("embedding gradient buffer must be a contiguous [vocab, dim] tensor of the table dtype")
+    acc = (grad is not None) if accumulate is None else bool(accumulate)
     ws = torch.empty((vocab * dim,), dtype=torch.float32, device=dout2.device)
     _lib.call("lz_embedding_bwd", ids_c.data_ptr(), ids_c.numel(), dout2.data_ptr(), _row_stride(dout2), vocab, dim,
-              out.data_ptr(), int(grad is not None), ws.data_ptr(), _DTYPES[dtype], stream_ptr(dout2.device))
+              out.data_ptr(), int(acc), ws.data_ptr(), _DTYPES[dtype], stream_ptr(dout2.device))
     return out
 
 

@@ -29,7 +29,8 @@ from data import (
     load_fineweb_stream,
     load_llama_tokenizer,
 )
-from lzhip.functional import pack_parameters_
+from lzhip.functional import GradSink, pack_parameters_
+from lzhip.ops import fill_
 from lzhip.optim import FusedAdamW
 from model import MODEL_SIZES, LlamaForCausalLM, build_config, estimate_num_parameters, human_readable_count
 
@@ -171,6 +172,12 @@ def train(args: argparse.Namespace) -> None:
     model.set_activation_checkpointing(args.activation_checkpointing)
     optimizer = FusedAdamW(model.parameters(), lr=args.learning_rate, betas=(args.beta1, args.beta2),
                            weight_decay=args.weight_decay)
+    # the backward kernels write and accumulate the parameter gradients
+    # themselves (no autograd accumulation kernels between micro-batches)
+    grads = GradSink(model)
+    # d(loss / GA) / d(loss), as the backward seed (the same value autograd
+    # forms for `(loss / GA).backward()`, without its division kernels)
+    seed = fill_(torch.empty((), dtype=torch.float32, device=device), 1.0 / args.grad_accum_steps)
 
     n_params = estimate_num_parameters(cfg)
     print(
@@ -185,7 +192,7 @@ def train(args: argparse.Namespace) -> None:
     t_start = time.perf_counter()
     for step in range(1, args.max_steps + 1):
         model.train()
-        optimizer.zero_grad(set_to_none=True)
+        grads.begin_step()  # in place of optimizer.zero_grad(set_to_none=True)
         t0 = time.perf_counter()
         micro_losses = []
         for _ in range(args.grad_accum_steps):
@@ -202,9 +209,9 @@ def train(args: argparse.Namespace) -> None:
                 loss = out.loss
                 if loss is None:
                     raise RuntimeError("Model did not return loss even though labels were provided")
-                scaled = loss / args.grad_accum_steps
             micro_losses.append(loss.detach().float().item())
-            scaled.backward()
+            loss.backward(gradient=seed.to(loss.dtype) if loss.dtype != seed.dtype else seed)
+        grads.finish()
         if args.max_grad_norm > 0:
             norm = optimizer.clip_grad_norm_(args.max_grad_norm)
             optimizer.step()

@@ -134,11 +134,10 @@ int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
 int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int dtype, int64_t rows, int64_t cols,
                    int64_t ldx, int64_t ldy, float eps, void* stream);
 /* Backward: dx = rstd*w*dy - rstd^3/n * (sum dy*w*x) * x (+ dres); dw (=/+=)
- * sum over rows of dy*x*rstd.  workspace (16-byte aligned) >=
- * lz_rmsnorm_bwd_workspace(rows, cols) bytes; its first 1024 bytes are
- * counters that must be zero before the first call and that every call leaves
- * zero (bf16 rows of <= 4096 columns sum dw in the same launch), so keep one
- * workspace per stream; calls sharing a workspace must not overlap. */
+ * sum over rows of dy*x*rstd (fp32 partial rows in the workspace, then a
+ * fixed-order column sum).  workspace (16-byte aligned) >=
+ * lz_rmsnorm_bwd_workspace(rows, cols) bytes; calls sharing a workspace must
+ * not overlap. */
 int64_t lz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols);
 int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
                    int dw_accumulate, void* workspace, int64_t workspace_bytes, int dtype, int64_t rows, int64_t cols,
@@ -147,7 +146,7 @@ int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
 /* lz_rmsnorm_bwd without a workspace argument: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation).  The
- * dw partial rows and counters live in the library's own 8 MiB device array,
+ * dw partial rows live in the library's own 8 MiB device array,
  * one per device, held until the process ends; shapes that need more are
  * refused (bf16 rows of up to 4096 columns fit at any row count).  Same
  * results as lz_rmsnorm_bwd bit for bit.  Every call on a device shares that

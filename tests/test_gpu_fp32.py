@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from lzhip import ops
+from lzhip.functional import GradSink
 from model import LlamaForCausalLM, ModelConfig, build_config
 from oracle import data as OD
 from oracle import engine as OE
@@ -138,6 +139,8 @@ def test_plumbing_fp32_100_steps_vs_oracle():
     free.load_state_dict(model.state_dict())
     free.set_loss_chunk_size(128)
     opt = FusedAdamW(free.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    sink = GradSink(free)  # the free-running trainer accumulates as train.py does
+    seed = torch.full((), 1.0 / GA, device=DEV)
     batches = []
     gen = OD.uniform_chunks(S, cfg.vocab_size, B, seed=0)
     for _ in range(steps * GA):
@@ -148,7 +151,7 @@ def test_plumbing_fp32_100_steps_vs_oracle():
         with torch.no_grad():
             model.load_state_dict({k: v.to(DEV) for k, v in params.items()}, strict=False)
         model.zero_grad(set_to_none=True)
-        opt.zero_grad(set_to_none=True)
+        sink.begin_step()
         losses, flosses = [], []
         for i in range(GA):
             ids = batches[(step - 1) * GA + i][:, :-1].contiguous().to(DEV)
@@ -157,7 +160,8 @@ def test_plumbing_fp32_100_steps_vs_oracle():
             (l / GA).backward()
             fl = free(input_ids=ids, labels=ids, return_logits=False).loss
             flosses.append(float(fl))
-            (fl / GA).backward()
+            fl.backward(gradient=seed)
+        sink.finish()
         opt.clip_grad_norm_(1.0)
         opt.step()
         g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])

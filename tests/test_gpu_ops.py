@@ -236,10 +236,9 @@ def test_rmsnorm_fwd_bwd(rows, cols, dtype):
 
 
 @pytest.mark.parametrize("rows,cols", [(512, 256), (333, 768), (16 * 1024, 2048), (1000, 4096)])
-def test_rmsnorm_bwd_dw_in_one_launch_repeats_and_accumulates(rows, cols):
-    """The bf16 backward sums dw in the same launch through per-group counters
-    that each call leaves at zero: repeated calls give the same bits (any
-    workgroup may finish last; the sums run in a fixed order), and
+def test_rmsnorm_bwd_repeats_and_accumulates(rows, cols):
+    """The bf16 backward's dw (per-workgroup fp32 partial rows, then a
+    fixed-order column sum) repeats bit for bit with a reused workspace, and
     dw_accumulate adds the new dw to the old one."""
     g = _seed(rows * 3 + cols)
     x = torch.randn(rows, cols, generator=g).to(torch.bfloat16).to(DEV)
@@ -263,7 +262,6 @@ def test_rmsnorm_bwd_dw_in_one_launch_repeats_and_accumulates(rows, cols):
     # the result and of dw from adding the rounded dw
     dw0 = runs[0][1].double()
     assert torch.allclose(acc.double(), base.double() + dw0, rtol=2 ** -8, atol=2 ** -8 * float(dw0.abs().max()))
-    assert torch.count_nonzero(ws[:256]) == 0  # the counters are left at zero
 
 
 # ---------------------------------------------------------------------------

@@ -21,7 +21,7 @@ import torch
 import torch.nn.functional as F
 
 from lzhip.optim import FusedAdamW
-from model import LlamaForCausalLM, build_config
+from model import LlamaForCausalLM, ModelConfig, build_config
 from oracle import data as OD
 from oracle import engine as OE
 from oracle import model as OM
@@ -198,6 +198,46 @@ def test_plumbing_100_steps_free_running():
         assert max(rel) <= 1e-2
         assert cos[0] >= 0.9999
         assert min(cos) >= 0.998
+
+
+def test_grad_sink_matches_autograd_accumulation():
+    """functional.GradSink (the backward kernels write the first
+    micro-batch's weight gradients and add the later ones, the tied
+    embedding/LM-head weight's two contributions included) against
+    autograd's own accumulation, on the plumbing model with GA=2 and on a
+    head-dim-128 model whose projections take the fused GEMM paths: every
+    parameter's gradient within bf16 rounding (the sink adds each
+    micro-batch in fp32 before rounding once; autograd rounds each
+    micro-batch's gradient, then the sum), and with neither an autograd
+    accumulation nor a seed-division kernel left to run."""
+    from lzhip.functional import GradSink
+
+    for cfg, B, S in ((build_config("plumbing", vocab_size=32000, max_seq_len=128), 4, 128),
+                      (ModelConfig(name="hd128", vocab_size=1000, max_seq_len=256, dim=512, n_layers=2, n_heads=4,
+                                   n_kv_heads=2, ffn_dim=1024, rope_theta=10_000.0), 2, 256)):
+        torch.manual_seed(0)
+        base = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+        base.set_loss_chunk_size(128)
+        sunk = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+        sunk.load_state_dict(base.state_dict())
+        sunk.set_loss_chunk_size(128)
+        sink = GradSink(sunk)
+        seed = torch.full((), 0.5, device=DEV)
+        gen = torch.Generator().manual_seed(3)
+        for step in range(2):
+            batches = [torch.randint(0, cfg.vocab_size, (B, S), generator=gen).to(DEV) for _ in range(2)]
+            base.zero_grad(set_to_none=True)
+            sink.begin_step()
+            for ids in batches:
+                (base(input_ids=ids, labels=ids, return_logits=False).loss / 2).backward()
+                sunk(input_ids=ids, labels=ids, return_logits=False).loss.backward(gradient=seed)
+            sink.finish()
+            for (n, a), (_, b) in zip(base.named_parameters(), sunk.named_parameters()):
+                assert b.grad is not None and b.grad.data_ptr() == sink._views[id(b)].data_ptr(), n
+                cos = float(F.cosine_similarity(a.grad.double().view(-1), b.grad.double().view(-1), dim=0))
+                err = float((a.grad.double() - b.grad.double()).norm() / a.grad.double().norm())
+                assert cos >= 0.99999 and err <= 2 ** -7, (cfg.name, step, n, cos, err)
+        sink.detach()
 
 
 def test_graphed_step_replays_match_eager():
