@@ -560,7 +560,41 @@ __global__ void __launch_bounds__(kThreads) adamw_multi_kernel(const MultiSegs t
   float* v = reinterpret_cast<float*>(t.v[sg]);
   const G* g = reinterpret_cast<const G*>(t.g[sg]);
   PO* po = reinterpret_cast<PO*>(t.po[sg]);
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+  // Four elements per thread and access when every array of this tensor is
+  // aligned to four of its elements (chunk starts are multiples of
+  // kMultiChunk, so alignment depends only on the base pointers); the same
+  // arithmetic per element as the scalar loop, so the same bits.
+  const bool vec = ((t.p[sg] | t.m[sg] | t.v[sg]) & 15) == 0 && (t.g[sg] & (4 * sizeof(G) - 1)) == 0 &&
+                   (t.po[sg] & (4 * sizeof(PO) - 1)) == 0;
+  int64_t tail = i0;
+  if (vec) {
+    const int64_t n4 = (i1 - i0) >> 2;
+    for (int64_t q = threadIdx.x; q < n4; q += blockDim.x) {
+      const int64_t i = i0 + 4 * q;
+      float4 pv = *reinterpret_cast<const float4*>(p + i);
+      float4 mv = *reinterpret_cast<const float4*>(m + i);
+      float4 vv = *reinterpret_cast<const float4*>(v + i);
+      float gv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gv[e] = Elem<G>::load(g, i + e);
+      float* pe = &pv.x;
+      float* me = &mv.x;
+      float* ve = &vv.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gg = scale_ptr ? gv[e] * scale : gv[e];
+        adam_elem(pe[e], me[e], ve[e], gg, a);
+      }
+      *reinterpret_cast<float4*>(p + i) = pv;
+      *reinterpret_cast<float4*>(m + i) = mv;
+      *reinterpret_cast<float4*>(v + i) = vv;
+      if (po)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Elem<PO>::store(po, i + e, pe[e]);
+    }
+    tail = i0 + 4 * n4;
+  }
+  for (int64_t i = tail + threadIdx.x; i < i1; i += blockDim.x) {
     float pp = p[i], mm = m[i], vv = v[i];
     float gg = Elem<G>::load(g, i);
     if (scale_ptr) gg = gg * scale;

@@ -88,6 +88,14 @@ class FusedAdamW(torch.optim.Optimizer):
             ops.require_gpu(p)
             st = self.state[p]
             if not st:
+                if self.capturable and group.get("_steps_taken", 0) > 0:
+                    # the group's one device step count would bias-correct this
+                    # parameter as if it had been stepped from the start
+                    raise RuntimeError(
+                        "FusedAdamW(capturable=True) keeps one device step count per parameter group: every "
+                        "parameter of a group must receive a gradient from the group's first step on "
+                        f"(a parameter of shape {tuple(p.shape)} got its first gradient at step "
+                        f"{group['_steps_taken'] + 1})")
                 st["step"] = 0
                 st["exp_avg"] = ops.zeros(p.shape, torch.float32, p.device)
                 st["exp_avg_sq"] = ops.zeros(p.shape, torch.float32, p.device)
@@ -106,6 +114,10 @@ class FusedAdamW(torch.optim.Optimizer):
             batch = batches.setdefault(key, (group, [], [], [], [], []))
             for lst, t in zip(batch[1:], (target, st["exp_avg"], st["exp_avg_sq"], g, out)):
                 lst.append(t)
+        if self.capturable:
+            for group in self.param_groups:
+                if any(p.grad is not None for p in group["params"]):
+                    group["_steps_taken"] = group.get("_steps_taken", 0) + 1
         # one multi-tensor launch per (group, dtypes, step) batch
         for key, (group, ps, ms, vs, gs, outs) in batches.items():
             beta1, beta2 = group["betas"]

@@ -621,20 +621,30 @@ def test_adamw_multi_matches_per_tensor():
     """adamw_multi_ over 30 tensors (two launches of at most 24; sizes from 0
     to 100k across the 4096-element chunk boundaries) against adamw_ tensor by
     tensor over 3 steps with a grad scale: the same bits for p, m, v and the
-    bf16 copy, for bf16 and fp32 gradients and with device-resident factors;
+    bf16 copy, for bf16 and fp32 gradients, with device-resident factors, and
+    with tensors 16-byte aligned (four elements per access) or not (scalar);
     sumsq_multi_ against float64 and per-tensor sumsq_ to 1e-6 (fp32 per-thread
     partials)."""
     g = _seed(31)
     sizes = [0, 1, 7, 4095, 4096, 4097, 100_003] + [int(x) for x in torch.randint(1, 20000, (23,), generator=g)]
     hp = dict(beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
     scale = torch.tensor([0.5], device=DEV)
-    for gdt, with_out, use_hyper in ((torch.bfloat16, True, False), (torch.float32, False, False),
-                                     (torch.bfloat16, True, True)):
+    def at_offset(t, off):
+        """t's values in a view `off` elements into a larger buffer (off=1:
+        not 16-byte aligned, so the multi-tensor kernel takes its scalar loop)."""
+        buf = torch.zeros(t.numel() + off, dtype=t.dtype, device=DEV)
+        v = buf[off:]
+        v.copy_(t.to(DEV))
+        return v
+
+    for gdt, with_out, use_hyper, off in ((torch.bfloat16, True, False, 0), (torch.float32, False, False, 0),
+                                          (torch.bfloat16, True, True, 0), (torch.bfloat16, True, False, 1)):
         p0 = [0.02 * torch.randn(n, generator=g) for n in sizes]
         A = [[p.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)] for p, n in zip(p0, sizes)]
-        B = [[p.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)] for p, n in zip(p0, sizes)]
+        B = [[at_offset(p, off), at_offset(torch.zeros(n), off), at_offset(torch.zeros(n), off)]
+             for p, n in zip(p0, sizes)]
         oa = [torch.zeros(n, dtype=torch.bfloat16, device=DEV) if with_out else None for n in sizes]
-        ob = [torch.zeros(n, dtype=torch.bfloat16, device=DEV) if with_out else None for n in sizes]
+        ob = [at_offset(torch.zeros(n, dtype=torch.bfloat16), off) if with_out else None for n in sizes]
         step = torch.zeros(1, dtype=torch.int64, device=DEV)
         hyper = torch.zeros(3, dtype=torch.float32, device=DEV)
         for t in range(1, 4):

@@ -240,6 +240,20 @@ def test_grad_sink_matches_autograd_accumulation():
         sink.detach()
 
 
+def test_capturable_adamw_refuses_a_late_parameter():
+    """With capturable=True the step count lives on the device per parameter
+    group, so a parameter whose first gradient arrives after the group's
+    first step would be bias-corrected as if stepped from the start: refused."""
+    a = torch.nn.Parameter(torch.randn(64, device=DEV))
+    b = torch.nn.Parameter(torch.randn(64, device=DEV))
+    opt = FusedAdamW([a, b], lr=1e-3, capturable=True)
+    a.grad = torch.randn(64, device=DEV)
+    opt.step()
+    b.grad = torch.randn(64, device=DEV)
+    with pytest.raises(RuntimeError, match="first gradient"):
+        opt.step()
+
+
 def test_graphed_step_replays_match_eager():
     """Plumbing model, B=4 S=128 GA=2, clip 1.0: the whole step recorded once
     in a HIP graph (optimizer step count kept on the device) and replayed 6
