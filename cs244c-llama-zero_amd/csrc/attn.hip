@@ -541,7 +541,7 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Tile path (S a multiple of 64).  Every operand tile is a [64][HD] bf16 block
 // of a row-major source (Q, dO, K or V rows), copied into LDS by
-// global_load_lds_dwordx4 with no staging registers, in unpadded rows whose
+// buffer_load_dwordx4 ... lds with no staging registers, in unpadded rows whose
 // 16-byte chunks are XOR-swizzled by tswz().  Operands that the MFMAs need
 // with the other dimension innermost (V^T, K^T, Q^T, dO^T) are read from the
 // same tiles with ds_read_b64_tr_b16: within each 16-lane group, lane 4j+q
@@ -568,17 +568,29 @@ __device__ __forceinline__ int toff(int r, int chunk) {
   return r * (HD * 2) + ((chunk ^ tswz<HD>(r)) << 4);
 }
 
+// Raw buffer starting at a tile's first row (src is the same for every
+// lane): the DMA loads below take a 32-bit per-lane offset within the tile's
+// 64 rows, which measured faster than 64-bit per-lane addresses.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* src) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), (short)0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, char* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
 // A [64][HD] tile of rows `src` (stride ld elements) into LDS at `dst` by DMA:
 // 64*HD*2/1024 wave loads split over the 4 waves.
 template <int HD>
 __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, char* dst, int wave, int lane) {
   constexpr int kRowsPerLoad = 1024 / (HD * 2), kChunks = HD / 8;
   constexpr int kPer = 64 / kRowsPerLoad / 4;
+  const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(src);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int r = (wave * kPer + q) * kRowsPerLoad + lane / kChunks;
     const int c = (lane % kChunks) ^ tswz<HD>(r);
-    __builtin_amdgcn_global_load_lds(src + (int64_t)r * ld + c * 8, dst + (wave * kPer + q) * 1024, 16, 0, 0);
+    lds_dma16(rsrc, (uint32_t)((r * ld + c * 8) * 2), dst + (wave * kPer + q) * 1024);
   }
 }
 
@@ -774,12 +786,12 @@ __device__ __forceinline__ void dma_tile_rows(const uint16_t* src, int64_t ld, i
                                               int lane) {
   constexpr int kRowsPerLoad = 1024 / (HD * 2), kChunks = HD / 8;
   constexpr int kPer = 64 / kRowsPerLoad / 4;
+  const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(src);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int r = (wg4 * kPer + q) * kRowsPerLoad + lane / kChunks;
     const int c = (lane % kChunks) ^ tswz<HD>(r);
-    __builtin_amdgcn_global_load_lds(src + (int64_t)min(r, nvalid - 1) * ld + c * 8, dst + (wg4 * kPer + q) * 1024,
-                                     16, 0, 0);
+    lds_dma16(rsrc, (uint32_t)((min(r, nvalid - 1) * ld + c * 8) * 2), dst + (wg4 * kPer + q) * 1024);
   }
 }
 
@@ -1533,9 +1545,18 @@ void launch_bwd_small(const GenArgs<T>& a, hipStream_t s) {
   }
 }
 
+// The tile loads address a tile's rows by 32-bit byte offsets from its first
+// row: row strides below 2^22 elements keep a 64-row tile below 2^31 bytes.
+constexpr int64_t kMaxTileLd = 1ll << 22;
+
+bool strides_ok(int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
+  return ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 && ldq < kMaxTileLd && ldk < kMaxTileLd &&
+         ldv < kMaxTileLd && ldo < kMaxTileLd;
+}
+
 bool mfma_ok(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, const void* q, const void* k,
              const void* v, const void* o) {
-  return dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 &&
+  return dtype == LZ_BF16 && (hd == 64 || hd == 128) && strides_ok(ldq, ldk, ldv, ldo) &&
          lz_aligned16(q) && lz_aligned16(k) && lz_aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7) == 0;
 }
 
@@ -1554,8 +1575,7 @@ int check_shape(int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd) {
 // operand buffers (V^T for the forward; Q^T, K^T, dO^T for the backward),
 // 0 = generic.
 LZ_EXPORT int lz_attn_path(int dtype, int64_t S, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
-  const bool mfma =
-      dtype == LZ_BF16 && (hd == 64 || hd == 128) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0;
+  const bool mfma = dtype == LZ_BF16 && (hd == 64 || hd == 128) && strides_ok(ldq, ldk, ldv, ldo);
   return mfma ? (S % 64 == 0 ? 2 : 1) : 0;
 }
 
