@@ -202,7 +202,7 @@ def measured_traffic(kernel: str):
     return None
 
 
-def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev: torch.device) -> dict:
+def bench_plumbing_graph(cfg, dtype, ids_all, B: int, S: int, GA: int, steps: int, dev: torch.device) -> dict:
     """The same workload with the whole step (both micro-batches, clip, AdamW
     with a device-resident step count) replayed from one HIP graph; each timed
     step copies its micro-batch ids into the graph's static inputs."""
@@ -212,7 +212,7 @@ def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev:
     from model import LlamaForCausalLM
 
     torch.manual_seed(0)
-    model = LlamaForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16)
+    model = LlamaForCausalLM(cfg).to(device=dev, dtype=dtype)
     pack_parameters_(model)
     model.set_loss_chunk_size(128)
     opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, capturable=True)
@@ -232,31 +232,21 @@ def bench_plumbing_graph(cfg, ids_all, B: int, S: int, GA: int, steps: int, dev:
             "hip_graph_final_loss": float(loss)}
 
 
-def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: int = 3):
-    """The CPU-runnable train.py workload (d256, 4 layers, 8/4 heads, ffn 688,
-    vocab 32000, B=4, S=128, grad accumulation 2, AdamW lr 3e-4, clip 1.0,
-    uniform ids from torch.Generator seed 0) for `steps` steps on the HIP path
-    (bf16), and the CPU oracle's train.py loop (fp32, every host thread) on
-    `cpu_steps` steps of the same stream."""
+def bench_plumbing_eager(cfg, dtype, ids_all, B: int, S: int, GA: int, steps: int, dev: torch.device) -> dict:
+    """train.py's step as it runs it, launched eagerly: GA micro-batches whose
+    kernels write and then accumulate the gradients, clip, fused AdamW."""
     from lzhip import ops
     from lzhip.functional import GradSink, pack_parameters_
     from lzhip.optim import FusedAdamW
-    from model import LlamaForCausalLM, build_config
+    from model import LlamaForCausalLM
 
-    B, S, GA = 4, 128, 2
-    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
     torch.manual_seed(0)
-    model = LlamaForCausalLM(cfg)
-    P = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
-    model = model.to(device=dev, dtype=torch.bfloat16)
+    model = LlamaForCausalLM(cfg).to(device=dev, dtype=dtype)
     pack_parameters_(model)
     model.set_loss_chunk_size(128)
     opt = FusedAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
-    grads = GradSink(model)  # as train.py: the kernels write and accumulate the gradients
+    grads = GradSink(model)
     seed = ops.fill_(torch.empty((), dtype=torch.float32, device=dev), 1.0 / GA)
-    gen = torch.Generator().manual_seed(0)
-    chunks = [torch.randint(0, 32000, (B, S + 1), generator=gen) for _ in range(GA * (steps + 5))]
-    ids_all = [c[:, :-1].contiguous().to(dev) for c in chunks]
 
     def one(step):
         grads.begin_step()
@@ -278,15 +268,38 @@ def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: in
         loss = one(5 + i)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    res = {"workload": "train.py plumbing (d256 L4 8/4 heads ffn688 V32000), B=4 S=128 GA=2, 100 steps",
-           "hip_tokens_per_s": B * S * GA * steps / el, "hip_ms_per_step": el * 1000 / steps,
-           "hip_final_loss": float(loss)}
-    del model, opt
-    res.update(bench_plumbing_graph(cfg, ids_all, B, S, GA, steps, dev))
+    return {"hip_tokens_per_s": B * S * GA * steps / el, "hip_ms_per_step": el * 1000 / steps,
+            "hip_final_loss": float(loss)}
+
+
+def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: int = 3):
+    """The CPU-runnable train.py workload (d256, 4 layers, 8/4 heads, ffn 688,
+    vocab 32000, B=4, S=128, grad accumulation 2, AdamW lr 3e-4, clip 1.0,
+    uniform ids from torch.Generator seed 0) for `steps` steps on the HIP path,
+    eagerly and replayed from a HIP graph, in fp32 (the reference's
+    train.py default: parameters, gradients, optimizer state and matmuls in
+    fp32) and in bf16 (bf16 parameters over an fp32 master); and the CPU
+    oracle's train.py loop (fp32, every host thread) on `cpu_steps` steps of
+    the same stream."""
+    from model import build_config
+
+    B, S, GA = 4, 128, 2
+    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
+    gen = torch.Generator().manual_seed(0)
+    chunks = [torch.randint(0, 32000, (B, S + 1), generator=gen) for _ in range(GA * (steps + 5))]
+    ids_all = [c[:, :-1].contiguous().to(dev) for c in chunks]
+    res = {"workload": f"train.py plumbing (d256 L4 8/4 heads ffn688 V32000), B=4 S=128 GA=2, {steps} steps"}
+    for name, dtype in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        leg = bench_plumbing_eager(cfg, dtype, ids_all, B, S, GA, steps, dev)
+        leg.update(bench_plumbing_graph(cfg, dtype, ids_all, B, S, GA, steps, dev))
+        res[name] = leg
     if cpu:
         from oracle import engine as OE
         from oracle import model as OM
+        from model import LlamaForCausalLM
 
+        torch.manual_seed(0)
+        P = {k: v.detach().clone() for k, v in LlamaForCausalLM(cfg).state_dict().items() if k != "lm_head.weight"}
         ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
                       n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta)
         out = OE.train_reference(ocfg, P, iter(chunks), steps=cpu_steps, grad_accum_steps=GA, lr=3e-4,

@@ -20,6 +20,13 @@
 // MFMA step s, so every lane reads its A and B fragments of four steps with
 // one 16-byte LDS read each.  The next stage's global loads are in flight
 // while the current stage's MFMAs run.
+//
+// Split-K: a product with few output tiles (under 192 of the 256 CUs busy)
+// and a long K (a language-model head's input gradient reduces over the
+// vocabulary) is cut into K slices of whole stages, one grid layer each; the
+// slices write fp32 partial tiles into a workspace and a second kernel sums
+// them in slice order, then applies alpha, beta*C and R as the unsplit
+// epilogue does.  The result does not depend on timing.
 #include "lz_common.h"
 
 namespace {
@@ -43,7 +50,30 @@ struct F32Args {
   int c_f32;   // fp32 output (else bf16)
   int a_vec;   // A rows 16-byte aligned (16-byte global loads)
   int b_vec;
+  int64_t kper;  // K per grid layer (a multiple of kBK when split)
+  int64_t slab;  // > 0: layer z writes raw fp32 partials at C + z * slab
 };
+
+struct Plan {
+  int splits;
+  int64_t kper;
+};
+
+Plan make_plan(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = lz_cdiv(M, kTile) * lz_cdiv(N, kTile);
+  Plan p{1, K};
+  if (tiles >= 192 || K < 4 * kBK) return p;
+  int64_t splits = std::min<int64_t>({lz_cdiv(256, tiles), K / (2 * kBK), 64});
+  if (splits < 2) return p;
+  p.kper = lz_cdiv(lz_cdiv(K, splits), kBK) * kBK;
+  p.splits = (int)lz_cdiv(K, p.kper);
+  if (p.splits < 2) p = Plan{1, K};
+  return p;
+}
+
+int64_t plan_workspace(const Plan& p, int64_t M, int64_t N) {
+  return p.splits > 1 ? (int64_t)p.splits * M * N * (int64_t)sizeof(float) : 0;
+}
 
 // Global -> registers for one operand tile: kTile rows of M (or N) x kBK of K.
 // Each thread holds 4 float4 of the tile.
@@ -128,6 +158,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(F32Args g) {
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, h = lane >> 5;
   const int64_t m0 = (int64_t)blockIdx.y * kTile, n0 = (int64_t)blockIdx.x * kTile;
+  const int64_t kbeg = (int64_t)blockIdx.z * g.kper, kend = min(g.K, kbeg + g.kper);
 
   f32x16_t acc[2][2];
 #pragma unroll
@@ -137,12 +168,12 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(F32Args g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int64_t nk = lz_cdiv(g.K, kBK);
+  const int64_t nk = kend > kbeg ? lz_cdiv(kend - kbeg, kBK) : 0;
   TileLoad<AK> la;
   TileLoad<BK> lb;
   if (nk > 0) {
-    la.load(g.A, g.lda, g.M, g.K, m0, 0, g.a_vec);
-    lb.load(g.B, g.ldb, g.N, g.K, n0, 0, g.b_vec);
+    la.load(g.A, g.lda, g.M, kend, m0, kbeg, g.a_vec);
+    lb.load(g.B, g.ldb, g.N, kend, n0, kbeg, g.b_vec);
     la.store(lds);
     lb.store(lds + kTile * kRow);
     __syncthreads();
@@ -150,8 +181,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(F32Args g) {
   for (int64_t kt = 0; kt < nk; ++kt) {
     const bool more = kt + 1 < nk;
     if (more) {
-      la.load(g.A, g.lda, g.M, g.K, m0, (kt + 1) * kBK, g.a_vec);
-      lb.load(g.B, g.ldb, g.N, g.K, n0, (kt + 1) * kBK, g.b_vec);
+      la.load(g.A, g.lda, g.M, kend, m0, kbeg + (kt + 1) * kBK, g.a_vec);
+      lb.load(g.B, g.ldb, g.N, kend, n0, kbeg + (kt + 1) * kBK, g.b_vec);
     }
     const float* As = lds + (kt & 1) * kStage;
     const float* Bs = As + kTile * kRow;
@@ -186,6 +217,22 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(F32Args g) {
   // Accumulator register r of lane (li, h) in block (i, j) holds
   // C[m][n] with m = 8*(r/4) + 4*h + r%4 and n = li inside the 32 x 32 block:
   // each store instruction writes two 128-byte row segments.
+  if (g.slab > 0) {
+    float* part = static_cast<float*>(g.C) + (int64_t)blockIdx.z * g.slab;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t n = n0 + wn * 64 + j * 32 + li;
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m < g.M) part[m * g.N + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -212,25 +259,68 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(F32Args g) {
     }
 }
 
+// C = alpha * sum_z part[z] (+ beta*C) (+ R), the slices summed in order.
+__global__ void __launch_bounds__(256) splitk_reduce_f32_kernel(F32Args g, const float* __restrict__ part,
+                                                                 int splits) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= g.M * g.N) return;
+  const int64_t m = i / g.N, n = i - m * g.N;
+  float acc = 0.f;
+  for (int z = 0; z < splits; ++z) acc += part[z * g.slab + i];
+  float val = acc * g.alpha;
+  if (g.c_f32) {
+    float* cp = static_cast<float*>(g.C) + m * g.ldc + n;
+    if (g.beta != 0.f) val = fmaf(g.beta, *cp, val);
+    if (g.R) val += g.R[m * g.ldr + n];
+    *cp = val;
+  } else {
+    uint16_t* cp = static_cast<uint16_t*>(g.C) + m * g.ldc + n;
+    if (g.beta != 0.f) val = fmaf(g.beta, bf2f(*cp), val);
+    if (g.R) val += g.R[m * g.ldr + n];
+    *cp = f2bf(val);
+  }
+}
+
 template <bool AK, bool BK>
-int launch_f32(const F32Args& g, hipStream_t s) {
+int launch_f32(const F32Args& g, int splits, hipStream_t s) {
   const int64_t tm = lz_cdiv(g.M, kTile), tn = lz_cdiv(g.N, kTile);
   LZ_REQUIRE(tm < 65536 && tn < (1ll << 31), "lz_gemm_f32: too many tiles (M %lld, N %lld)", (long long)g.M,
              (long long)g.N);
-  dim3 grid((unsigned)tn, (unsigned)tm);
+  dim3 grid((unsigned)tn, (unsigned)tm, (unsigned)splits);
   gemm_f32_kernel<AK, BK><<<grid, kThreads, 0, s>>>(g);
   return lz_check_launch("lz_gemm_f32");
 }
 
+int launch_layout(const F32Args& g, bool ak, bool bk, int splits, hipStream_t s) {
+  if (ak && bk) return launch_f32<true, true>(g, splits, s);
+  if (ak) return launch_f32<true, false>(g, splits, s);
+  if (bk) return launch_f32<false, true>(g, splits, s);
+  return launch_f32<false, false>(g, splits, s);
+}
+
 }  // namespace
+
+// Workspace bytes lz_gemm_f32 uses for this shape (0 when K is not split).
+LZ_EXPORT int64_t lz_gemm_f32_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return plan_workspace(make_plan(M, N, K), M, N);
+}
+
+// Number of K slices lz_gemm_f32 runs this shape in (1 = unsplit).
+LZ_EXPORT int lz_gemm_f32_plan(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return make_plan(M, N, K).splits;
+}
 
 // fp32 operands, fp32 accumulation: C = alpha * sum_k A(m,k) B(n,k)
 // (+ beta*C) (+ R), with the operand layouts of lz_gemm.  C: [M,N] fp32 or
 // bf16 (ldc); R: optional fp32 [M,N] (ldr).  No alignment or size
-// multiples are required; 16-byte aligned rows take 16-byte loads.
+// multiples are required; 16-byte aligned rows take 16-byte loads.  `ws`
+// (ws_bytes long, may be null) holds the partial products when K is split;
+// with less than lz_gemm_f32_workspace() bytes the product runs unsplit.
 LZ_EXPORT int lz_gemm_f32(const float* A, int64_t lda, int a_kmajor, const float* B, int64_t ldb, int b_kmajor, void* C,
                           int64_t ldc, int c_dtype, const float* R, int64_t ldr, int64_t M, int64_t N, int64_t K,
-                          float alpha, float beta, void* stream) {
+                          float alpha, float beta, void* ws, int64_t ws_bytes, void* stream) {
   LZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lz_gemm_f32: negative shape");
   if (M == 0 || N == 0) return LZ_OK;
   LZ_REQUIRE(C, "lz_gemm_f32: null output");
@@ -238,6 +328,7 @@ LZ_EXPORT int lz_gemm_f32(const float* A, int64_t lda, int a_kmajor, const float
   LZ_REQUIRE(c_dtype == LZ_F32 || c_dtype == LZ_BF16, "lz_gemm_f32: bad output dtype %d", c_dtype);
   LZ_REQUIRE(K == 0 || (lda >= (a_kmajor ? K : M) && ldb >= (b_kmajor ? K : N)), "lz_gemm_f32: bad operand stride");
   LZ_REQUIRE(ldc >= N && (R == nullptr || ldr >= N), "lz_gemm_f32: bad output stride");
+  LZ_REQUIRE(ws_bytes >= 0 && (ws == nullptr || lz_aligned16(ws)), "lz_gemm_f32: workspace must be 16-byte aligned");
   F32Args g;
   g.A = A;
   g.B = B;
@@ -255,9 +346,19 @@ LZ_EXPORT int lz_gemm_f32(const float* A, int64_t lda, int a_kmajor, const float
   g.c_f32 = c_dtype == LZ_F32;
   g.a_vec = lz_aligned16(A) && lda % 4 == 0;
   g.b_vec = lz_aligned16(B) && ldb % 4 == 0;
+  g.kper = K;
+  g.slab = 0;
   hipStream_t s = lz_stream(stream);
-  if (a_kmajor && b_kmajor) return launch_f32<true, true>(g, s);
-  if (a_kmajor) return launch_f32<true, false>(g, s);
-  if (b_kmajor) return launch_f32<false, true>(g, s);
-  return launch_f32<false, false>(g, s);
+  const bool ak = a_kmajor != 0, bk = b_kmajor != 0;
+  const Plan p = make_plan(M, N, K);
+  if (p.splits == 1 || ws == nullptr || ws_bytes < plan_workspace(p, M, N)) return launch_layout(g, ak, bk, 1, s);
+  F32Args gs = g;  // partial products into fp32 slabs [splits][M][N]
+  gs.C = ws;
+  gs.kper = p.kper;
+  gs.slab = M * N;
+  int rc = launch_layout(gs, ak, bk, p.splits, s);
+  if (rc) return rc;
+  g.slab = M * N;
+  splitk_reduce_f32_kernel<<<(unsigned)lz_cdiv(M * N, 256), 256, 0, s>>>(g, static_cast<const float*>(ws), p.splits);
+  return lz_check_launch("lz_gemm_f32(split-K reduce)");
 }

@@ -72,7 +72,9 @@ SIGNATURES = {
     "lz_gemm": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp,
                        _i64, _vp]),
     "lz_gemm_f32": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32,
-                           _f32, _vp]),
+                           _f32, _vp, _i64, _vp]),
+    "lz_gemm_f32_workspace": (_i64, [_i64, _i64, _i64]),
+    "lz_gemm_f32_plan": (_i32, [_i64, _i64, _i64]),
     "lz_gemm_workspace": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "lz_gemm_plan": (_i32, [_i64, _i64, _i64, _i32, _i32]),
     "lz_attn_path": (_i32, [_i32, _i64, _i64, _i64, _i64, _i64, _i64]),

@@ -693,6 +693,9 @@ def _gemm_f32(a, b, a_kmajor, b_kmajor, out, out_dtype, residual, alpha, beta) -
         if residual.dtype != torch.float32 or tuple(residual.shape) != (M, N):
             raise ValueError("residual of a float32 GEMM must be a float32 [M, N] view")
         ldr = _unit_stride_2d(residual, "residual")
+    lib = _lib.load()
+    ws_bytes = int(lib.lz_gemm_f32_workspace(M, N, K))
+    ws = torch.empty(((ws_bytes + 15) // 16) * 4, dtype=torch.float32, device=a.device) if ws_bytes else None
     probe = _gemm_probe
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
@@ -700,7 +703,7 @@ def _gemm_f32(a, b, a_kmajor, b_kmajor, out, out_dtype, residual, alpha, beta) -
         start.record()
     _lib.call("lz_gemm_f32", a.data_ptr(), lda, int(bool(a_kmajor)), b.data_ptr(), ldb, int(bool(b_kmajor)),
               out.data_ptr(), ldc, dtype_code(out), _ptr(residual), ldr, M, N, K, float(alpha), float(beta),
-              stream_ptr(a.device))
+              _ptr(ws), ws_bytes if ws is not None else 0, stream_ptr(a.device))
     if probe is not None:
         end.record()
         probe.add(2.0 * M * N * K, start, end, (bool(a_kmajor), bool(b_kmajor), "f32"))

@@ -233,10 +233,14 @@ int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, 
  * products when the model is kept in float32 (train.py:148-160 and
  * train_zero.py:74,150-164 with --dtype float32).  fp32 operands, fp32
  * accumulation, C fp32 or bf16, R an optional fp32 residual.  Any M, N, K
- * and leading dimensions; no workspace. */
+ * and leading dimensions.  Products with few output tiles and a long K are
+ * split along K into `ws` (at least lz_gemm_f32_workspace() bytes, 16-byte
+ * aligned; with less, or NULL, the product runs unsplit). */
+int64_t lz_gemm_f32_workspace(int64_t M, int64_t N, int64_t K);
+int lz_gemm_f32_plan(int64_t M, int64_t N, int64_t K);
 int lz_gemm_f32(const float* A, int64_t lda, int a_kmajor, const float* B, int64_t ldb, int b_kmajor, void* C,
                 int64_t ldc, int c_dtype, const float* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha,
-                float beta, void* stream);
+                float beta, void* ws, int64_t ws_bytes, void* stream);
 /* Fused gate/up projections + SwiGLU (model/llama.py:139-145: gate_proj(x),
  * up_proj(x), silu(gate) * up): w = [gate rows; up rows] ([2F, K]);
  * h = silu(x.Wg^T) * (x.Wu^T) as bf16 [M, F], and x.w^T itself to gu

@@ -50,7 +50,7 @@ def _operand(t: torch.Tensor, kmajor: bool) -> torch.Tensor:
 
 @pytest.mark.parametrize("ak,bk", [(True, True), (True, False), (False, True), (False, False)])
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (37, 29, 13), (128, 128, 32), (300, 200, 72), (515, 257, 1031),
-                                   (1024, 768, 2048), (256, 5632, 2048)])
+                                   (1024, 768, 2048), (256, 5632, 2048), (200, 100, 5000), (512, 256, 32000)])
 def test_gemm_f32_layouts_vs_float64(ak, bk, M, N, K):
     g = torch.Generator().manual_seed(M * 7 + N * 3 + K + 2 * ak + bk)
     a = torch.randn(M, K, generator=g)
@@ -59,6 +59,20 @@ def test_gemm_f32_layouts_vs_float64(ak, bk, M, N, K):
     out = ops.gemm(_operand(a, ak).to(DEV), _operand(b, bk).to(DEV), ak, bk)
     assert out.dtype == torch.float32 and out.shape == (M, N)
     assert _rel(out, ref) <= 1e-5
+
+
+def test_gemm_f32_split_plan():
+    """Few output tiles with a long K (a language-model head's input
+    gradient: 512 tokens x 256 features over a 32000 vocabulary) are split
+    along K; large products are not."""
+    from lzhip import _lib
+
+    lib = _lib.load()
+    assert lib.lz_gemm_f32_plan(512, 256, 32000) >= 16
+    assert lib.lz_gemm_f32_workspace(512, 256, 32000) == lib.lz_gemm_f32_plan(512, 256, 32000) * 512 * 256 * 4
+    assert lib.lz_gemm_f32_plan(333, 190, 517) > 1      # the epilogue test below runs split
+    assert lib.lz_gemm_f32_plan(4096, 4096, 4096) == 1 and lib.lz_gemm_f32_workspace(4096, 4096, 4096) == 0
+    assert lib.lz_gemm_f32_plan(64, 64, 64) == 1
 
 
 def test_gemm_f32_epilogue_and_views():
