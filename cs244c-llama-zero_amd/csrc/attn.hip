@@ -50,6 +50,10 @@ struct AttnArgs {
   uint16_t* dk;
   uint16_t* dv;
   int64_t lddq, lddk, lddv;
+  // backward with RoPE folded in: bf16 tables [>= S, hd] (row = position);
+  // dq and dk are then the gradients of the un-rotated q and k
+  const uint16_t* rcos;
+  const uint16_t* rsin;
   int B, S, H, KV;
   float scale;
 };
@@ -89,6 +93,54 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* p, float a, float b, floa
   w.x = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
   w.y = (uint32_t)f2bf(c) | ((uint32_t)f2bf(d) << 16);
   *reinterpret_cast<uint2*>(p) = w;
+}
+
+// One lane's row of a dQ or dK accumulator set (columns 32*i + 8*q4 +
+// 4*half + e, the MFMA output layout), times `scale`, stored as bf16 at dst.
+// With RoPE tables (cs/sn: the row's position, HD values each) the stored row
+// is the gradient of the un-rotated input: the bf16 gradient pair (d1, d2) of
+// columns (c, c + HD/2) becomes g1 = r(r(d1*c1) + r(d2*s2)) and
+// g2 = r(r(d2*c2) - r(d1*s1)), rounding each product and sum to bf16 as the
+// separate RoPE backward pass (and the reference's bf16 autograd of
+// x*cos + rotate_half(x)*sin, model/llama.py:35-39) does.  Columns c and
+// c + HD/2 sit in accumulator blocks i and i + HD/64 of the same lane.
+template <int HD>
+__device__ __forceinline__ void store_grad_row(uint16_t* dst, const f32x16_t (&acc)[HD / 32], float scale, int half,
+                                               const uint16_t* cs, const uint16_t* sn) {
+  if (cs == nullptr) {
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int c = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(dst + c, acc[i][4 * q4] * scale, acc[i][4 * q4 + 1] * scale, acc[i][4 * q4 + 2] * scale,
+                     acc[i][4 * q4 + 3] * scale);
+      }
+    return;
+  }
+  constexpr int kHalf = HD / 2, kBlk = HD / 64;
+#pragma unroll
+  for (int i = 0; i < kBlk; ++i)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int c = i * 32 + 8 * q4 + 4 * half;
+      const uint2 c1w = *reinterpret_cast<const uint2*>(cs + c), c2w = *reinterpret_cast<const uint2*>(cs + c + kHalf);
+      const uint2 s1w = *reinterpret_cast<const uint2*>(sn + c), s2w = *reinterpret_cast<const uint2*>(sn + c + kHalf);
+      const uint32_t c1a[2] = {c1w.x, c1w.y}, c2a[2] = {c2w.x, c2w.y}, s1a[2] = {s1w.x, s1w.y},
+                     s2a[2] = {s2w.x, s2w.y};
+      float g1[4], g2[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sh = (e & 1) * 16;
+        const float c1 = bf2f((uint16_t)(c1a[e >> 1] >> sh)), c2 = bf2f((uint16_t)(c2a[e >> 1] >> sh));
+        const float s1 = bf2f((uint16_t)(s1a[e >> 1] >> sh)), s2 = bf2f((uint16_t)(s2a[e >> 1] >> sh));
+        const float d1 = round_bf(acc[i][4 * q4 + e] * scale), d2 = round_bf(acc[i + kBlk][4 * q4 + e] * scale);
+        g1[e] = __fadd_rn(round_bf(__fmul_rn(d1, c1)), round_bf(__fmul_rn(d2, s2)));
+        g2[e] = __fadd_rn(round_bf(__fmul_rn(d2, c2)), -round_bf(__fmul_rn(d1, s1)));
+      }
+      store_bf16x4(dst + c, g1[0], g1[1], g1[2], g1[3]);
+      store_bf16x4(dst + c + kHalf, g2[0], g2[1], g2[2], g2[3]);
+    }
 }
 
 // Row tile [rows][HD] (row stride `rb` bytes) from a [S, ld] row-major source.
@@ -418,15 +470,10 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(AttnArgs a) {
   if (kvrow < S) {
     uint16_t* dkp = a.dk + ((int64_t)b * S + kvrow) * a.lddk + (int64_t)g * HD;
     uint16_t* dvp = a.dv + ((int64_t)b * S + kvrow) * a.lddv + (int64_t)g * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int hd = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(dkp + hd, dk[i][4 * q4] * a.scale, dk[i][4 * q4 + 1] * a.scale, dk[i][4 * q4 + 2] * a.scale,
-                     dk[i][4 * q4 + 3] * a.scale);
-        store_bf16x4(dvp + hd, dv[i][4 * q4], dv[i][4 * q4 + 1], dv[i][4 * q4 + 2], dv[i][4 * q4 + 3]);
-      }
+    const bool rope = a.rcos != nullptr;
+    store_grad_row<HD>(dkp, dk, a.scale, half, rope ? a.rcos + (int64_t)kvrow * HD : nullptr,
+                       rope ? a.rsin + (int64_t)kvrow * HD : nullptr);
+    store_grad_row<HD>(dvp, dv, 1.0f, half, nullptr, nullptr);
   }
 }
 
@@ -527,14 +574,9 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
   }
   if (qrow < S) {
     uint16_t* dqp = a.dq + ((int64_t)b * S + qrow) * a.lddq + (int64_t)h * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int hd = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(dqp + hd, dq[i][4 * q4] * a.scale, dq[i][4 * q4 + 1] * a.scale, dq[i][4 * q4 + 2] * a.scale,
-                     dq[i][4 * q4 + 3] * a.scale);
-      }
+    const bool rope = a.rcos != nullptr;
+    store_grad_row<HD>(dqp, dq, a.scale, half, rope ? a.rcos + (int64_t)qrow * HD : nullptr,
+                       rope ? a.rsin + (int64_t)qrow * HD : nullptr);
   }
 }
 
@@ -934,15 +976,10 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   if (kvrow < S) {
     uint16_t* dkp = a.dk + ((int64_t)b * S + kvrow) * a.lddk + (int64_t)g * HD;
     uint16_t* dvp = a.dv + ((int64_t)b * S + kvrow) * a.lddv + (int64_t)g * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int hd = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(dkp + hd, dk[i][4 * q4] * a.scale, dk[i][4 * q4 + 1] * a.scale, dk[i][4 * q4 + 2] * a.scale,
-                     dk[i][4 * q4 + 3] * a.scale);
-        store_bf16x4(dvp + hd, dv[i][4 * q4], dv[i][4 * q4 + 1], dv[i][4 * q4 + 2], dv[i][4 * q4 + 3]);
-      }
+    const bool rope = a.rcos != nullptr;
+    store_grad_row<HD>(dkp, dk, a.scale, half, rope ? a.rcos + (int64_t)kvrow * HD : nullptr,
+                       rope ? a.rsin + (int64_t)kvrow * HD : nullptr);
+    store_grad_row<HD>(dvp, dv, 1.0f, half, nullptr, nullptr);
   }
 }
 
@@ -1041,14 +1078,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   if (qrow < S) {
     uint16_t* dqp = a.dq + ((int64_t)b * S + qrow) * a.lddq + (int64_t)h * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int hd = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(dqp + hd, dq[i][4 * q4] * a.scale, dq[i][4 * q4 + 1] * a.scale, dq[i][4 * q4 + 2] * a.scale,
-                     dq[i][4 * q4 + 3] * a.scale);
-      }
+    const bool rope = a.rcos != nullptr;
+    store_grad_row<HD>(dqp, dq, a.scale, half, rope ? a.rcos + (int64_t)qrow * HD : nullptr,
+                       rope ? a.rsin + (int64_t)qrow * HD : nullptr);
   }
 }
 
@@ -1655,18 +1687,55 @@ LZ_EXPORT int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_
   return lz_check_launch("lz_attn_delta");
 }
 
+LZ_EXPORT int lz_rope(void* x, int dtype, int64_t ld, int64_t rows, int64_t seq, int64_t nheads, int64_t hd,
+                      const void* cos_t, const void* sin_t, int64_t pos_offset, int backward, void* stream);
+
+namespace {
+
+int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
+                  int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
+                  void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
+                  int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin,
+                  int dtype, hipStream_t s, bool& rope_done);
+
+}  // namespace
+
 // Backward.  On the MFMA path qt [B,H,hd,S], kt [B,KV,hd,S] and dot [B,H,hd,S]
 // are required; delta comes from lz_attn_delta.  dq/dk/dv are written (not
-// accumulated).
+// accumulated).  rope_cos/rope_sin (both or neither; tables [>= S, hd] in the
+// activation dtype, row = position, as lz_rope takes): dq and dk come back
+// as the gradients of q and k before RoPE, i.e. with lz_rope's backward
+// already applied (in the bf16 MFMA kernels' epilogue, otherwise by lz_rope
+// after them).
 LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
                           const void* dout, int64_t lddo, const float* lse, const float* delta, const void* qt,
                           const void* kt, const void* dot, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
-                          int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale, int dtype,
-                          void* stream) {
+                          int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
+                          const void* rope_cos, const void* rope_sin, int dtype, void* stream) {
   int rc = check_shape(B, S, H, KV, hd);
   if (rc) return rc;
   LZ_REQUIRE(q && k && v && dout && lse && delta && dq && dk && dv, "lz_attn_bwd: null pointer");
+  LZ_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), "lz_attn_bwd: give both RoPE tables or neither");
+  LZ_REQUIRE(rope_cos == nullptr || (hd % 2 == 0 && ((reinterpret_cast<uintptr_t>(rope_cos) |
+                                                        reinterpret_cast<uintptr_t>(rope_sin)) & 7) == 0),
+             "lz_attn_bwd: RoPE needs an even head dim and 8-byte aligned tables");
   hipStream_t s = lz_stream(stream);
+  bool rope_done = false;
+  rc = attn_bwd_impl(q, ldq, k, ldk, v, ldv, dout, lddo, lse, delta, qt, kt, dot, dq, lddq, dk, lddk, dv, lddv, B, S,
+                     H, KV, hd, scale, rope_cos, rope_sin, dtype, s, rope_done);
+  if (rc || rope_cos == nullptr || rope_done) return rc;
+  rc = lz_rope(dq, dtype, lddq, B * S, S, H, hd, rope_cos, rope_sin, 0, 1, stream);
+  if (rc) return rc;
+  return lz_rope(dk, dtype, lddk, B * S, S, KV, hd, rope_cos, rope_sin, 0, 1, stream);
+}
+
+namespace {
+
+int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
+                  int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
+                  void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
+                  int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin,
+                  int dtype, hipStream_t s, bool& rope_done) {
   const bool mfma = mfma_ok(dtype, hd, ldq, ldk, ldv, lddo, q, k, v, dout) && lddq % 4 == 0 && lddk % 4 == 0 &&
                     lddv % 4 == 0;
   if (mfma && S % 64 == 0) {
@@ -1677,6 +1746,8 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.dout = (const uint16_t*)dout; a.lddo = lddo; a.delta = delta;
     a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
     a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.rcos = (const uint16_t*)rope_cos; a.rsin = (const uint16_t*)rope_sin;
+    rope_done = true;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid_kv = (unsigned)(lz_cdiv(S, 256) * B * KV);
     const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
@@ -1699,6 +1770,8 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.dot = (const uint16_t*)dot; a.delta = delta;
     a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
     a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.rcos = (const uint16_t*)rope_cos; a.rsin = (const uint16_t*)rope_sin;
+    rope_done = true;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid_kv = (unsigned)(lz_cdiv(S, 128) * B * KV);
     const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
@@ -1744,3 +1817,5 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
   }
   return lz_check_launch("lz_attn_bwd(generic)");
 }
+
+}  // namespace

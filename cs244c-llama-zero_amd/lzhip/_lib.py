@@ -87,7 +87,7 @@ SIGNATURES = {
         _i32,
         [
             _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
-            _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
+            _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _i32, _vp,
         ],
     ),
 }

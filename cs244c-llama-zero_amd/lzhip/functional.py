@@ -359,9 +359,8 @@ class AttnProjFn(Function):
             qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :], o, do2, lse,
             B, S, H, KV, hd, scale,
             dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :],
-            qt=qt, kt=kt, dot=dot,
+            qt=qt, kt=kt, dot=dot, rope=(cos, sin),  # dq and dk come back through RoPE's backward
         )
-        ops.rope_(dqkv, S, H + KV, hd, cos, sin, backward=True)
         need_w = any(ctx.needs_input_grad[1:4])
         w = fused_weight([wq, wk, wv])
         dh2, dw = _linear_bwd(dqkv, h2, w, ctx.needs_input_grad[0], need_w, [wq, wk, wv])

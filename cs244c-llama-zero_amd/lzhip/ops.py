@@ -850,12 +850,24 @@ def attn_fwd(q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, B: int, S: in
     return o, lse
 
 
-def attn_bwd(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt=None, kt=None, dot=None) -> None:
+def attn_bwd(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt=None, kt=None, dot=None,
+             rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
+    """dq2/dk2/dv2 = gradients of causal GQA attention.  With rope = (cos,
+    sin) (rope_'s tables), dq2 and dk2 are the gradients of q and k before
+    RoPE: the RoPE backward is applied in the same call."""
     require_gpu(q2, k2, v2, o2, do2, lse, dq2, dk2, dv2)
+    rc = rs = None
+    if rope is not None:
+        rc, rs = rope
+        require_gpu(rc, rs)
+        if rc.dtype != q2.dtype or rs.dtype != q2.dtype or rc.size(0) < S or tuple(rc.shape[1:]) != (hd,) \
+                or rs.shape != rc.shape or not (rc.is_contiguous() and rs.is_contiguous()):
+            raise ValueError("RoPE tables must be contiguous [>= S, hd] in the activation dtype")
     delta = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
     _lib.call("lz_attn_delta", o2.data_ptr(), _row_stride(o2), do2.data_ptr(), _row_stride(do2), delta.data_ptr(),
               B, S, H, hd, dtype_code(o2), stream_ptr(q2.device))
     _lib.call("lz_attn_bwd", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
               _row_stride(v2), do2.data_ptr(), _row_stride(do2), lse.data_ptr(), delta.data_ptr(), _ptr(qt), _ptr(kt),
               _ptr(dot), dq2.data_ptr(), _row_stride(dq2), dk2.data_ptr(), _row_stride(dk2), dv2.data_ptr(),
-              _row_stride(dv2), B, S, H, KV, hd, float(scale), dtype_code(q2), stream_ptr(q2.device))
+              _row_stride(dv2), B, S, H, KV, hd, float(scale), _ptr(rc), _ptr(rs), dtype_code(q2),
+              stream_ptr(q2.device))

@@ -53,6 +53,23 @@ class ShardSpec:
     chunk_size: int
 
 
+_UNIT_SEEDS: dict = {}
+
+
+def backward_from_loss(loss: torch.Tensor) -> None:
+    """loss.backward() with the seed gradient 1 taken from a cached
+    device scalar (written once by this library's fill kernel) rather than
+    created by autograd's ones_like on every step."""
+    if loss.device.type != "cuda" or loss.numel() != 1:
+        loss.backward()
+        return
+    key = (loss.device, loss.dtype, tuple(loss.shape))
+    seed = _UNIT_SEEDS.get(key)
+    if seed is None:
+        seed = _UNIT_SEEDS[key] = ops.fill_(torch.empty(loss.shape, dtype=loss.dtype, device=loss.device), 1.0)
+    loss.backward(gradient=seed)
+
+
 def tensor_num_bytes(tensor: torch.Tensor | None) -> int:
     if tensor is None:
         return 0

@@ -24,6 +24,7 @@ from profiler import MemoryTracker
 
 from ._fused import FusedStep
 from .common import (
+    backward_from_loss,
     GRAD_BUCKET_NUMEL,
     assign_flat_params,
     bucket_ranges,
@@ -92,7 +93,7 @@ class ZeROStage0DDP:
 
     # engine API -------------------------------------------------------------
     def backward(self, loss: torch.Tensor) -> None:
-        loss.backward()
+        backward_from_loss(loss)
 
     def prepare_forward(self) -> Dict[str, float]:
         return {"prepare_comm_ms": 0.0}

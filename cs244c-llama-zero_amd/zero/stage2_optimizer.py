@@ -25,6 +25,7 @@ from profiler import MemoryTracker
 
 from ._fused import FusedStep
 from .common import (
+    backward_from_loss,
     ShardSpec,
     assign_flat_params,
     build_flat_param_metadata,
@@ -89,7 +90,7 @@ class ZeROStage2Optimizer:
         self._post_step_allgather_bytes = 0
 
     def backward(self, loss: torch.Tensor) -> None:
-        loss.backward()
+        backward_from_loss(loss)
         self._flush_flat_grad_buffer()
 
     def prepare_forward(self) -> Dict[str, float]:

@@ -45,6 +45,7 @@ from profiler import MemoryTracker
 
 from ._fused import FusedStep
 from .common import (
+    backward_from_loss,
     GRAD_BUCKET_NUMEL,
     FlatParamMetadata,
     ShardSpec,
@@ -494,7 +495,7 @@ class ZeROStage3Optimizer:
                 self._reshard_all_params()
 
     def backward(self, loss: torch.Tensor) -> None:
-        loss.backward()
+        backward_from_loss(loss)
 
     def prepare_forward(self) -> Dict[str, float]:
         self._reshard_all_params()

@@ -270,10 +270,15 @@ int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
                 int dtype, void* stream);
 int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_t lddo, float* delta, int64_t B, int64_t S,
                   int64_t H, int64_t hd, int dtype, void* stream);
+/* Backward.  rope_cos/rope_sin (both or NULL; lz_rope's tables): dq and dk
+ * are returned as the gradients of q and k before RoPE (model/llama.py:35-39
+ * backward), folded into the bf16 MFMA kernels' stores or, on the other
+ * paths, applied by lz_rope afterwards. */
 int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
                 int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
                 void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
-                int64_t H, int64_t KV, int64_t hd, float scale, int dtype, void* stream);
+                int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin, int dtype,
+                void* stream);
 
 #ifdef __cplusplus
 }

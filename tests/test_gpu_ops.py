@@ -440,6 +440,42 @@ def test_attention_fwd_bwd(B, S, H, KV, hd):
     assert _rel_err(dv, vr.grad) < 2e-2
 
 
+@pytest.mark.parametrize("B,S,H,KV,hd,dtype", [(2, 256, 8, 4, 128, torch.bfloat16), (1, 128, 4, 2, 64, torch.bfloat16),
+                                               (1, 200, 4, 2, 128, torch.bfloat16), (2, 64, 4, 2, 32, torch.bfloat16),
+                                               (1, 96, 4, 2, 64, torch.float32)])
+def test_attention_bwd_with_rope_equals_separate_rope(B, S, H, KV, hd, dtype):
+    """attn_bwd(rope=(cos, sin)) returns exactly what attn_bwd followed by
+    the RoPE backward pass on dq and dk returns, on every kernel path (the
+    bf16 tile and transposed-operand paths fold the rotation into their
+    stores; the others run the RoPE kernel after)."""
+    g = _seed(B * S * hd + H)
+    ld = (H + 2 * KV) * hd
+    d = torch.randn(B * S, ld, generator=g).to(dtype).to(DEV)
+    q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
+    scale = hd**-0.5
+    path = ops.attn_path(dtype, S, hd, ld, ld, ld, H * hd)
+    vt = ops.transpose_heads(d, B, S, KV, hd, col0=(H + KV) * hd) if path == 1 else None
+    o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
+    do = torch.randn(B * S, H * hd, generator=g).to(dtype).to(DEV)
+    tr = {}
+    if path == 1:
+        tr = dict(qt=ops.transpose_heads(d, B, S, H, hd, col0=0), kt=ops.transpose_heads(d, B, S, KV, hd, col0=H * hd),
+                  dot=ops.transpose_heads(do, B, S, H, hd, col0=0))
+    cos, sin = R.rope_tables(S, hd, 10_000.0, dtype=dtype)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    sep = torch.zeros_like(d)
+    ops.attn_bwd(q2, k2, v2, o, do, lse, B, S, H, KV, hd, scale, sep[:, : H * hd], sep[:, H * hd : (H + KV) * hd],
+                 sep[:, (H + KV) * hd :], **tr)
+    ops.rope_(sep, S, H + KV, hd, cos, sin, backward=True)
+    fused = torch.zeros_like(d)
+    ops.attn_bwd(q2, k2, v2, o, do, lse, B, S, H, KV, hd, scale, fused[:, : H * hd], fused[:, H * hd : (H + KV) * hd],
+                 fused[:, (H + KV) * hd :], rope=(cos, sin), **tr)
+    assert torch.equal(fused.cpu(), sep.cpu()), path
+    with pytest.raises(ValueError):
+        ops.attn_bwd(q2, k2, v2, o, do, lse, B, S, H, KV, hd, scale, fused[:, : H * hd],
+                     fused[:, H * hd : (H + KV) * hd], fused[:, (H + KV) * hd :], rope=(cos[:, : hd // 2], sin), **tr)
+
+
 @pytest.mark.parametrize("B,S,H,hd,pad", [(2, 64, 4, 128, 0), (1, 96, 8, 64, 64), (2, 33, 3, 32, 0), (1, 40, 2, 256, 8),
                                           (2, 24, 4, 48, 0)])
 def test_attention_delta(B, S, H, hd, pad):
