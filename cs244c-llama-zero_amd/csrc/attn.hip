@@ -204,7 +204,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int rem = blockIdx.x % bh;
   const int b = rem / H, h = rem % H;
   const int g = h / (H / KV);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
   const int qrow = qw0 + l32;
@@ -366,7 +367,8 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(AttnArgs a) {
   const int kvb = blockIdx.x / bkv;
   const int rem = blockIdx.x % bkv;
   const int b = rem / KV, g = rem % KV;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   const int k0 = kvb * BKV, kw0 = k0 + 32 * wave;
   const int kvrow = kw0 + l32;
@@ -497,7 +499,8 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
   const int rem = blockIdx.x % bh;
   const int b = rem / H, h = rem % H;
   const int g = h / (H / KV);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
   const int qrow = qw0 + l32;
@@ -613,13 +616,9 @@ __device__ __forceinline__ int toff(int r, int chunk) {
 // Raw buffer starting at a tile's first row (src is the same for every
 // lane): the DMA loads below take a 32-bit per-lane offset within the tile's
 // 64 rows, which measured faster than 64-bit per-lane addresses.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* src) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), (short)0, 0x7fffffff, 0x00020000);
-}
+__device__ __forceinline__ lz_v4i tile_rsrc(const uint16_t* src) { return lz_buffer_rsrc(src); }
 
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, char* dst) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
-}
+__device__ __forceinline__ void lds_dma16(lz_v4i rsrc, uint32_t voff, char* dst) { lz_dma16(rsrc, voff, 0, dst); }
 
 // A [64][HD] tile of rows `src` (stride ld elements) into LDS at `dst` by DMA:
 // 64*HD*2/1024 wave loads split over the 4 waves.
@@ -627,7 +626,7 @@ template <int HD>
 __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, char* dst, int wave, int lane) {
   constexpr int kRowsPerLoad = 1024 / (HD * 2), kChunks = HD / 8;
   constexpr int kPer = 64 / kRowsPerLoad / 4;
-  const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(src);
+  const lz_v4i rsrc = tile_rsrc(src);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int r = (wave * kPer + q) * kRowsPerLoad + lane / kChunks;
@@ -636,13 +635,11 @@ __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, char* 
   }
 }
 
-// 16 floats at src into LDS at dst by lanes 0-15 of the calling wave, and 16
-// floats at src2 into dst + 256 by lanes 16-31 (dst uniform).
+// 64 floats at src into LDS at dst by lanes 0-15 of the calling wave, and 64
+// floats at src2 into dst + 256 by lanes 16-31 (src, src2 and dst uniform).
 __device__ __forceinline__ void dma_rows64(const float* src, const float* src2, char* dst, int lane) {
-  if (lane < 32) {
-    const float* p = lane < 16 ? src + 4 * lane : src2 + 4 * (lane - 16);
-    __builtin_amdgcn_global_load_lds(p, dst, 16, 0, 0);
-  }
+  if (lane < 16) lz_dma16(lz_buffer_rsrc(src), 16 * lane, 0, dst);
+  else if (lane < 32) lz_dma16(lz_buffer_rsrc(src2), 16 * (lane - 16), 0, dst);
 }
 
 // Per-lane LDS offsets of the fragment reads of a tile.  tswz() depends only
@@ -711,7 +708,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int rem = blockIdx.x % bh;
   const int b = rem / H, h = rem % H;
   const int g = h / (H / KV);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   TileOffsets<HD> to;
   to.init(lane);
@@ -820,6 +818,153 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+// Forward on tiles, software-pipelined over key steps: 128 queries per
+// workgroup (32 per wave), 64-key steps.  The score MFMAs of step i+1 are
+// issued before the softmax of step i, so they run on the matrix cores while
+// the VALU computes the row maxima and exponentials.  K and V tiles have
+// separate double buffers: at the barrier that opens step i, K of step i+1
+// and V of step i have landed; then K of step i+2 and V of step i+1 are
+// issued into the slots that steps i and i-1 have finished with.  Each step's
+// arithmetic is the same as attn_fwd_tile_kernel's, so are the results.
+template <int HD>
+__device__ __forceinline__ void fwd_scores(f32x16_t (&s)[2], const TileOffsets<HD>& to, const char* Kt,
+                                           const bf16x8_t (&qf)[HD / 16]) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < HD / 16; ++kk)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], s[t], 0, 0, 0);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_pipe_kernel(AttnArgs a) {
+  constexpr int BQ = 128, BKV = 64;
+  constexpr int kTile = BKV * HD * 2;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];  // K slots 0, 1; V slots 0, 1
+  char* const Ks = smem;
+  char* const Vs = smem + 2 * kTile;
+
+  const int S = a.S, H = a.H, KV = a.KV;
+  const int nqb = (S + BQ - 1) / BQ;
+  const int bh = a.B * H;
+  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
+  const int rem = blockIdx.x % bh;
+  const int b = rem / H, h = rem % H;
+  const int g = h / (H / KV);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, l32 = lane & 31;
+  TileOffsets<HD> to;
+  to.init(lane);
+  const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
+  const int qrow = qw0 + l32;
+
+  bf16x8_t qf[HD / 16];
+  {
+    const uint16_t* qp = a.q + ((int64_t)b * S + min(qrow, S - 1)) * a.ldq + (int64_t)h * HD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qp + kk * 16));
+  }
+  f32x16_t o[HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float c = a.scale * kLog2e;
+
+  const int kv_end = min(S, q0 + BQ);  // a multiple of 64
+  const int kv_end_w = min(S, qw0 + 32);
+  const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
+  const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
+  const int nsteps = kv_end / BKV;
+
+  dma_tile<HD>(kbase, a.ldk, Ks, wave, lane);
+  dma_tile<HD>(vbase, a.ldv, Vs, wave, lane);
+  dma_barrier();
+  if (nsteps > 1) dma_tile<HD>(kbase + (int64_t)BKV * a.ldk, a.ldk, Ks + kTile, wave, lane);
+  f32x16_t s[2];
+  fwd_scores<HD>(s, to, Ks, qf);  // step 0 has keys for every wave (kv_end_w > 0)
+  for (int it = 0; it < nsteps; ++it) {
+    dma_barrier();  // K of step it+1 and V of step it landed; every wave is done with K(it) and V(it-1)
+    if (it + 2 < nsteps)
+      dma_tile<HD>(kbase + (int64_t)(it + 2) * BKV * a.ldk, a.ldk, Ks + (it & 1) * kTile, wave, lane);
+    if (it + 1 < nsteps)
+      dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, Vs + ((it + 1) & 1) * kTile, wave, lane);
+    const int k0 = it * BKV;
+    if (k0 >= kv_end_w) continue;  // past this wave's diagonal (it only joins the barriers)
+    // step it+1 has keys for this wave only away from the diagonal, where step
+    // it needs no mask
+    const bool next = it + 1 < nsteps && k0 + BKV < kv_end_w;
+    f32x16_t sn[2];
+    if (next) fwd_scores<HD>(sn, to, Ks + ((it + 1) & 1) * kTile, qf);
+    const bool need_mask = k0 + BKV - 1 > qw0;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (need_mask) {
+          const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (kv > qrow) s[t][r] = -INFINITY;
+        }
+        mx = fmaxf(mx, s[t][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx * c);
+    const float nm = -m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
+        s[t][r] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    if (__builtin_amdgcn_read_exec() & __ballot(m_new != m)) {  // some lane's max moved
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    }
+    l += rs;
+    m = m_new;
+    const char* Vt = Vs + (it & 1) * kTile;
+#pragma unroll
+    for (int ks = 0; ks < BKV / 16; ++ks) {
+      const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+      for (int i = 0; i < HD / 32; ++i)
+        o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Vt, ks, i), pb, o[i], 0, 0, 0);
+    }
+    if (next) {
+      s[0] = sn[0];
+      s[1] = sn[1];
+    }
+  }
+  if (qrow < S) {
+    const float inv_l = 1.0f / l;
+    uint16_t* op = a.o + ((int64_t)b * S + qrow) * a.ldo + (int64_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hd = i * 32 + 8 * q4 + 4 * half;
+        store_bf16x4(op + hd, o[i][4 * q4] * inv_l, o[i][4 * q4 + 1] * inv_l, o[i][4 * q4 + 2] * inv_l,
+                     o[i][4 * q4 + 3] * inv_l);
+      }
+    if (half == 0) a.lse[((int64_t)b * H + h) * S + qrow] = (m + log2f(l)) * kLn2;
+  }
+}
+
 // A [64][HD] tile like dma_tile, loaded by the four waves of group `wg4`
 // (wave index 0..3 within the group), rows past `nvalid` clamped to the last
 // valid row (their results are masked).
@@ -828,7 +973,7 @@ __device__ __forceinline__ void dma_tile_rows(const uint16_t* src, int64_t ld, i
                                               int lane) {
   constexpr int kRowsPerLoad = 1024 / (HD * 2), kChunks = HD / 8;
   constexpr int kPer = 64 / kRowsPerLoad / 4;
-  const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(src);
+  const lz_v4i rsrc = tile_rsrc(src);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int r = (wg4 * kPer + q) * kRowsPerLoad + lane / kChunks;
@@ -875,7 +1020,8 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   const int kvb = blockIdx.x / bkv;
   const int rem = blockIdx.x % bkv;
   const int b = rem / KV, g = rem % KV;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   TileOffsets<HD> to;
   to.init(lane);
@@ -998,7 +1144,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int rem = blockIdx.x % bh;
   const int b = rem / H, h = rem % H;
   const int g = h / (H / KV);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   TileOffsets<HD> to;
   to.init(lane);
@@ -1626,8 +1773,8 @@ LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid = (unsigned)(lz_cdiv(S, 128) * B * H);
-    if (hd == 128) attn_fwd_tile_kernel<128><<<grid, 256, 0, s>>>(a);
-    else attn_fwd_tile_kernel<64><<<grid, 256, 0, s>>>(a);
+    if (hd == 128) attn_fwd_pipe_kernel<128><<<grid, 256, 0, s>>>(a);
+    else attn_fwd_pipe_kernel<64><<<grid, 256, 0, s>>>(a);
     return lz_check_launch("lz_attn_fwd");
   }
   if (mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o)) {

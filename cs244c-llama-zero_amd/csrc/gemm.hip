@@ -569,7 +569,7 @@ struct DmaOperand {
   // buffer_load ... lds with a 32-bit per-lane offset and the K step in the
   // scalar offset, which measured 3-9 % faster than 64-bit per-lane
   // addresses.  The host keeps every offset below 2^31 (dma_spans_fit).
-  __amdgpu_buffer_rsrc_t rsrc;
+  lz_v4i rsrc;
   uint32_t voff[kPerWave];  // per-lane byte offsets
   uint32_t kadv;            // bytes to advance per DBK-deep K step
 
@@ -579,7 +579,7 @@ struct DmaOperand {
   __device__ __forceinline__ void init(const uint16_t* p, int64_t ld, int64_t row0, int64_t nrows, int64_t kbeg,
                                        int wave, int lane, int64_t pair = 0) {
     const uint16_t* base = KMAJOR ? p + row0 * ld + kbeg : p + kbeg * ld + row0;
-    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+    rsrc = lz_buffer_rsrc(base);
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
       if constexpr (KMAJOR) {
@@ -599,9 +599,7 @@ struct DmaOperand {
   __device__ __forceinline__ void issue(char* dst, int wave, int kt) const {
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, (__attribute__((address_space(3))) void*)(dst + (wave * kPerWave + q) * 1024), 16, voff[q],
-          (uint32_t)kt * kadv, 0, 0);
+      lz_dma16(rsrc, voff[q], (uint32_t)kt * kadv, dst + (wave * kPerWave + q) * 1024);
   }
 };
 

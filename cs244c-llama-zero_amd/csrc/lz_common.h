@@ -64,6 +64,37 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Raw buffer resource (4 SGPRs) starting at `base`: stride 0, 2^31 - 1
+// bytes addressable, the same flag word as __builtin_amdgcn_make_buffer_rsrc
+// takes.  `base` must be wave-uniform; the words are read from the first
+// active lane so that they live in SGPRs whatever the compiler can prove.
+typedef int lz_v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ lz_v4i lz_buffer_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  lz_v4i r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  r.z = 0x7fffffff;
+  r.w = 0x00020000;
+  return r;
+}
+
+// Direct-to-LDS copy, 16 bytes per lane: buffer_load_dwordx4 ... lds puts
+// the 16 bytes of lane l, at byte offset voff + soff of `rsrc`, at LDS address
+// dst + 16*l (dst wave-uniform; M0 carries it).  Issued from inline assembly
+// so that the compiler does not track these loads: with the intrinsic it
+// makes every later transposed LDS read (ds_read_b64_tr_b16) wait for all of
+// them, so a stage prefetched for the next step stalls the current one.
+// Nothing else waits for them either: every reader of the destination must
+// pass a dma_barrier() (vmcnt(0), then the workgroup barrier) after the copy
+// is issued.
+__device__ __forceinline__ void lz_dma16(lz_v4i rsrc, uint32_t voff, uint32_t soff, void* dst) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst;
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0) : "memory");
+}
+
 // Workgroup barrier that publishes LDS written by this workgroup's
 // global_load_lds (direct-to-LDS) loads: each wave first waits until its own
 // loads have landed (vmcnt(0)), then the barrier orders every wave's reads
@@ -71,7 +102,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // loads: its fence covers stores and LDS instructions only, and the compiler
 // does not always add the wait.
 __device__ __forceinline__ void dma_barrier() {
-  wait_vmcnt<0>();
+  wait_vmcnt<0>();  // the builtin, so the compiler's own count of pending loads restarts from zero too
   __syncthreads();
 }
 
