@@ -207,24 +207,6 @@ struct TileLoader {
   }
 };
 
-// fp32 output of 4 staged values (already scaled by alpha) of row m, columns
-// n..n+3, after beta*C and the residual R.
-__device__ __forceinline__ uint4 finish16(const GemmArgs& go, uint4 v, int64_t m, int64_t n) {
-  {
-    float o[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-    if (go.beta != 0.f) {
-      const float4 c = *reinterpret_cast<const float4*>(static_cast<const float*>(go.C) + m * go.ldc + n);
-      o[0] = fmaf(go.beta, c.x, o[0]); o[1] = fmaf(go.beta, c.y, o[1]);
-      o[2] = fmaf(go.beta, c.z, o[2]); o[3] = fmaf(go.beta, c.w, o[3]);
-    }
-    if (go.R) {
-      const uint2 r = *reinterpret_cast<const uint2*>(go.R + m * go.ldr + n);
-      o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
-    }
-    return make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
-  }
-}
-
 // Chunk swizzle of a staged epilogue row of kRow bytes: rows that share a
 // 256-byte bank window are told apart by the XOR, so 16 lanes writing one
 // chunk of 16 consecutive rows (or reading 16 chunks of a row) hit 16
@@ -279,9 +261,16 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
     }
   }
   // fp32 values staged (fp32 output, or bf16 output with beta / residual,
-  // which are applied before the single rounding): two passes of TM/2 rows
+  // which are applied before the single rounding): two passes of TM/2 rows.
+  // The stores go in blocks of kBlk: each block first issues all of its loads
+  // of C (beta) and R, so that they are in flight together instead of one
+  // load-use round trip per store (C and R may alias the output, so the
+  // compiler cannot hoist them past the stores itself).
   constexpr int kRow = TN * 4, kChunks = kRow / 16;
+  constexpr int kIters = (TM / 2) * kChunks / 64, kBlk = kIters < 4 ? kIters : 4;
   static_assert(kChunks >= 4 && kChunks <= 64, "fp32 rows of 16 to 256 values");
+  static_assert(kIters % kBlk == 0, "store blocks must tile a pass");
+  const bool has_c = go.beta != 0.f, has_r = go.R != nullptr;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
 #pragma unroll
@@ -299,25 +288,53 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
     }
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
-      const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-      const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
-      const int64_t m = mrow0 + p * (TM / 2) + row, n = ncol0 + chunk * 4;
-      if (go.c_f32) {
-        *reinterpret_cast<uint4*>(static_cast<float*>(go.C) + m * go.ldc + n) = finish16(go, v, m, n);
-      } else {
-        float o[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-        uint16_t* cp = static_cast<uint16_t*>(go.C) + m * go.ldc + n;
-        if (go.beta != 0.f) {
-          const uint2 c = *reinterpret_cast<const uint2*>(cp);
-          o[0] = fmaf(go.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, bf2f(c.x >> 16), o[1]);
-          o[2] = fmaf(go.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, bf2f(c.y >> 16), o[3]);
+    for (int t0 = 0; t0 < kIters; t0 += kBlk) {
+      uint4 cpre[kBlk];  // beta's C: fp32 x4, or bf16 x4 in .x/.y
+      uint2 rpre[kBlk];  // residual, bf16 x4
+#pragma unroll
+      for (int u = 0; u < kBlk; ++u) {
+        const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+        const int64_t m = mrow0 + p * (TM / 2) + row, n = ncol0 + chunk * 4;
+        cpre[u] = make_uint4(0u, 0u, 0u, 0u);
+        rpre[u] = make_uint2(0u, 0u);
+        if (has_c) {
+          if (go.c_f32) {
+            cpre[u] = *reinterpret_cast<const uint4*>(static_cast<const float*>(go.C) + m * go.ldc + n);
+          } else {
+            const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(go.C) + m * go.ldc + n);
+            cpre[u].x = c.x;
+            cpre[u].y = c.y;
+          }
         }
-        if (go.R) {
-          const uint2 r = *reinterpret_cast<const uint2*>(go.R + m * go.ldr + n);
+        if (has_r) rpre[u] = *reinterpret_cast<const uint2*>(go.R + m * go.ldr + n);
+      }
+#pragma unroll
+      for (int u = 0; u < kBlk; ++u) {
+        const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+        const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+        const int64_t m = mrow0 + p * (TM / 2) + row, n = ncol0 + chunk * 4;
+        float o[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+        if (has_c) {
+          const uint4 c = cpre[u];
+          if (go.c_f32) {
+            o[0] = fmaf(go.beta, __uint_as_float(c.x), o[0]); o[1] = fmaf(go.beta, __uint_as_float(c.y), o[1]);
+            o[2] = fmaf(go.beta, __uint_as_float(c.z), o[2]); o[3] = fmaf(go.beta, __uint_as_float(c.w), o[3]);
+          } else {
+            o[0] = fmaf(go.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, bf2f(c.x >> 16), o[1]);
+            o[2] = fmaf(go.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, bf2f(c.y >> 16), o[3]);
+          }
+        }
+        if (has_r) {
+          const uint2 r = rpre[u];
           o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
         }
-        *reinterpret_cast<uint2*>(cp) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+        if (go.c_f32) {
+          *reinterpret_cast<uint4*>(static_cast<float*>(go.C) + m * go.ldc + n) = make_uint4(
+              __float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
+        } else {
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(go.C) + m * go.ldc + n) =
+              make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+        }
       }
     }
     asm volatile("" ::: "memory");
@@ -688,14 +705,14 @@ __device__ __forceinline__ void sched_slice() {
 // a multiple of DBK in every split; an M-major A needs M % 8 == 0 (N-major B:
 // N % 8 == 0).
 //
-// Layouts with an M- or N-major operand (input and weight gradients) run a
-// different step (kMid): half of the waves (one per SIMD) issue all stage
-// loads, so the other wave on each SIMD keeps issuing MFMAs while the loads
-// queue, and the barrier sits in the middle of a step, after the last LDS
-// reads of the current stage, so that the MFMAs of its last two slices run
-// while the next stage's first fragments are read.  Measured on the 1B
-// step's shapes: input gradients 1-6 % faster, weight gradients 5-20 %; the
-// K-major x K-major product is unchanged either way and keeps the plain step.
+// With two stages every layout runs the mid-step schedule (kMid): half of the
+// waves (one per SIMD) issue all stage loads, so the other wave on each SIMD
+// keeps issuing MFMAs while the loads queue, and the barrier sits in the
+// middle of a step, after the last LDS reads of the current stage, so that
+// the MFMAs of its last two slices run while the next stage's first
+// fragments are read.  Measured on the 1B step's shapes against the plain
+// step (all waves load, barrier at the step's start): input gradients 3-6 %
+// faster, weight gradients 1-7 %, forward products 4-11 %.
 // Outputs of the fused gate|up projection + SwiGLU: h = silu(gate) * up
 // ([M, F] bf16); the GEMM's own output (gate|up, [M, 2F]) goes to GemmArgs::C
 // when that is not null.
@@ -739,7 +756,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage
   constexpr int kStage = 2 * kOpBytes;
-  constexpr bool kMid = !(AK && BK);
+  constexpr bool kMid = NST == 2;
   constexpr int kLoadWaves = kMid ? kWaves / 2 : kWaves;  // waves that issue the stage loads
   constexpr int kPerWave = kOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
   constexpr int kSlices = DBK / 16;
