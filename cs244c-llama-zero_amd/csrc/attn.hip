@@ -818,14 +818,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
-// Forward on tiles, software-pipelined over key steps: 128 queries per
-// workgroup (32 per wave), 64-key steps.  The score MFMAs of step i+1 are
-// issued before the softmax of step i, so they run on the matrix cores while
-// the VALU computes the row maxima and exponentials.  K and V tiles have
-// separate double buffers: at the barrier that opens step i, K of step i+1
-// and V of step i have landed; then K of step i+2 and V of step i+1 are
-// issued into the slots that steps i and i-1 have finished with.  Each step's
-// arithmetic is the same as attn_fwd_tile_kernel's, so are the results.
+// Forward on tiles: 128 queries per workgroup (32 per wave), 64-key steps,
+// K and V tiles double-buffered in LDS (the next step's tiles are issued
+// right after the barrier that opens a step).
 template <int HD>
 __device__ __forceinline__ void fwd_scores(f32x16_t (&s)[2], const TileOffsets<HD>& to, const char* Kt,
                                            const bf16x8_t (&qf)[HD / 16]) {
@@ -838,6 +833,59 @@ __device__ __forceinline__ void fwd_scores(f32x16_t (&s)[2], const TileOffsets<H
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], s[t], 0, 0, 0);
+}
+
+// Online softmax of one 64-key step and its P.V product.  s: the step's
+// scores (lane = query column, registers = keys t*32 + 8*(r/4) + 4*half +
+// r%4); MASK: keys with index > lim are masked (the diagonal step only, so
+// that the other steps carry no masking instructions).  The running max m is
+// kept in log2 units; l and O are rescaled only when some lane's max moves.
+template <int HD, bool MASK>
+__device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[HD / 32], float& m, float& l,
+                                               const TileOffsets<HD>& to, const char* Vt, float c, int lim, int half) {
+  constexpr int BKV = 64;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if constexpr (MASK) {
+        const int kv = t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (kv > lim) s[t][r] = -INFINITY;
+      }
+      mx = fmaxf(mx, s[t][r]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_step = mx * c;
+  if (__builtin_amdgcn_read_exec() & __ballot(m_step > m)) {  // some lane's max moved
+    const float m_new = fmaxf(m, m_step);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    m = m_new;
+  }
+  const float nm = -m;
+  float rs = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
+      s[t][r] = p;
+      rs += p;
+    }
+  rs += __shfl_xor(rs, 32, 64);
+  l += rs;
+#pragma unroll
+  for (int ks = 0; ks < BKV / 16; ++ks) {
+    const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i)
+      o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Vt, ks, i), pb, o[i], 0, 0, 0);
+  }
 }
 
 template <int HD>
@@ -885,70 +933,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   dma_tile<HD>(kbase, a.ldk, Ks, wave, lane);
   dma_tile<HD>(vbase, a.ldv, Vs, wave, lane);
-  dma_barrier();
-  if (nsteps > 1) dma_tile<HD>(kbase + (int64_t)BKV * a.ldk, a.ldk, Ks + kTile, wave, lane);
-  f32x16_t s[2];
-  fwd_scores<HD>(s, to, Ks, qf);  // step 0 has keys for every wave (kv_end_w > 0)
   for (int it = 0; it < nsteps; ++it) {
-    dma_barrier();  // K of step it+1 and V of step it landed; every wave is done with K(it) and V(it-1)
-    if (it + 2 < nsteps)
-      dma_tile<HD>(kbase + (int64_t)(it + 2) * BKV * a.ldk, a.ldk, Ks + (it & 1) * kTile, wave, lane);
-    if (it + 1 < nsteps)
+    dma_barrier();  // K and V of step it landed; every wave is done with step it-1's slots
+    if (it + 1 < nsteps) {
+      dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, Ks + ((it + 1) & 1) * kTile, wave, lane);
       dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, Vs + ((it + 1) & 1) * kTile, wave, lane);
+    }
     const int k0 = it * BKV;
     if (k0 >= kv_end_w) continue;  // past this wave's diagonal (it only joins the barriers)
-    // step it+1 has keys for this wave only away from the diagonal, where step
-    // it needs no mask
-    const bool next = it + 1 < nsteps && k0 + BKV < kv_end_w;
-    f32x16_t sn[2];
-    if (next) fwd_scores<HD>(sn, to, Ks + ((it + 1) & 1) * kTile, qf);
-    const bool need_mask = k0 + BKV - 1 > qw0;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (need_mask) {
-          const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (kv > qrow) s[t][r] = -INFINITY;
-        }
-        mx = fmaxf(mx, s[t][r]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx * c);
-    const float nm = -m_new;
-    float rs = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
-        s[t][r] = p;
-        rs += p;
-      }
-    rs += __shfl_xor(rs, 32, 64);
-    if (__builtin_amdgcn_read_exec() & __ballot(m_new != m)) {  // some lane's max moved
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-    }
-    l += rs;
-    m = m_new;
+    f32x16_t s[2];
+    fwd_scores<HD>(s, to, Ks + (it & 1) * kTile, qf);
     const char* Vt = Vs + (it & 1) * kTile;
-#pragma unroll
-    for (int ks = 0; ks < BKV / 16; ++ks) {
-      const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
-#pragma unroll
-      for (int i = 0; i < HD / 32; ++i)
-        o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Vt, ks, i), pb, o[i], 0, 0, 0);
-    }
-    if (next) {
-      s[0] = sn[0];
-      s[1] = sn[1];
-    }
+    if (k0 + BKV - 1 > qw0)  // the diagonal step: keys past the query are masked
+      fwd_softmax_pv<HD, true>(s, o, m, l, to, Vt, c, qrow - k0, half);
+    else
+      fwd_softmax_pv<HD, false>(s, o, m, l, to, Vt, c, 0, half);
   }
   if (qrow < S) {
     const float inv_l = 1.0f / l;

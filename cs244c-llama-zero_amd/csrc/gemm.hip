@@ -45,9 +45,27 @@ struct GemmArgs {
   int c_f32;      // output dtype fp32 (else bf16)
   int vec_store;  // N, ldc, ldr multiples of 4 and pointers aligned
   int vec16;      // C rows (and R rows) start 16-byte aligned: row-contiguous 16-byte epilogue
+  int r16;        // R rows 16-byte aligned too: the residual joins the 16-byte bf16 epilogue
   int64_t kper;   // K range of one split (multiple of 64); blockIdx.y is the split
   int64_t slab;   // elements between the fp32 partial slabs of consecutive splits
 };
+
+// Elementwise bf16 sum of two 8-value pieces, rounded once.
+__device__ __forceinline__ uint4 add_bf16x8(const uint4& a, const uint4& b) {
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    o[k] = pack_bf16x2(bf2f((uint16_t)(aw[k] & 0xffff)) + bf2f((uint16_t)(bw[k] & 0xffff)),
+                       bf2f((uint16_t)(aw[k] >> 16)) + bf2f((uint16_t)(bw[k] >> 16)));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// A bf16 output with a residual is rounded twice, as the reference's separate
+// ops are (the nn.Linear output in bf16, then x + y in bf16,
+// model/llama.py:158-159): the product is rounded to bf16 before R is added
+// and the sum is rounded on the store.  fp32 outputs add R unrounded.
+__device__ __forceinline__ float with_residual_bf16(float v, uint32_t r16) { return round_bf(v) + bf2f((uint16_t)r16); }
 
 __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t n, const float (&v)[4]) {
   float o[4] = {v[0] * g.alpha, v[1] * g.alpha, v[2] * g.alpha, v[3] * g.alpha};
@@ -73,7 +91,8 @@ __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t
       }
       if (g.R) {
         uint2 r = *reinterpret_cast<const uint2*>(g.R + m * g.ldr + n);
-        o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+        o[0] = with_residual_bf16(o[0], r.x & 0xffff); o[1] = with_residual_bf16(o[1], r.x >> 16);
+        o[2] = with_residual_bf16(o[2], r.y & 0xffff); o[3] = with_residual_bf16(o[3], r.y >> 16);
       }
       uint2 w;
       w.x = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
@@ -95,7 +114,7 @@ __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t
     } else {
       uint16_t* cp = static_cast<uint16_t*>(g.C) + m * g.ldc + nn;
       if (g.beta != 0.f) val = fmaf(g.beta, bf2f(*cp), val);
-      if (g.R) val += bf2f(g.R[m * g.ldr + nn]);
+      if (g.R) val = with_residual_bf16(val, g.R[m * g.ldr + nn]);
       *cp = f2bf(val);
     }
   }
@@ -236,7 +255,9 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
   if (!go.c_f32) {
     constexpr int kRow = TN * 2, kChunks = kRow / 16;  // bytes and 16-byte chunks per row
     static_assert(kChunks >= 4 && kChunks <= 64, "bf16 rows of 32 to 512 values");
-    const bool plain = go.beta == 0.f && go.R == nullptr;
+    // beta == 0: stage bf16 values (the product rounded once) and store whole
+    // 16-byte row pieces; a residual is added to each piece on the way out
+    const bool plain = go.beta == 0.f && (go.R == nullptr || go.r16);
     if (plain) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -250,12 +271,36 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
                            pack_bf16x2(acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha));
           }
       asm volatile("" ::: "memory");
-      // 64 lanes x 16 bytes per store: whole rows (or 64-chunk row pieces)
+      constexpr int kIters = TM * kChunks / 64;
+      if (go.R == nullptr) {
+        // 64 lanes x 16 bytes per store: whole rows (or 64-chunk row pieces)
 #pragma unroll
-      for (int t = 0; t < TM * kChunks / 64; ++t) {
-        const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-        const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) = v;
+        for (int t = 0; t < kIters; ++t) {
+          const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+          const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) = v;
+        }
+        return;
+      }
+      // with the residual: the R pieces of 8 stores are loaded together (R may
+      // alias the output, so the compiler would not hoist them past the stores)
+      constexpr int kBlk = kIters < 8 ? kIters : 8;
+      static_assert(kIters % kBlk == 0, "store blocks must tile the wave's rows");
+#pragma unroll
+      for (int t0 = 0; t0 < kIters; t0 += kBlk) {
+        uint4 rv[kBlk];
+#pragma unroll
+        for (int u = 0; u < kBlk; ++u) {
+          const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+          rv[u] = *reinterpret_cast<const uint4*>(go.R + (mrow0 + row) * go.ldr + ncol0 + chunk * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < kBlk; ++u) {
+          const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+          const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) =
+              add_bf16x8(v, rv[u]);
+        }
       }
       return;
     }
@@ -326,7 +371,12 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
         }
         if (has_r) {
           const uint2 r = rpre[u];
-          o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+          if (go.c_f32) {
+            o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+          } else {
+            o[0] = with_residual_bf16(o[0], r.x & 0xffff); o[1] = with_residual_bf16(o[1], r.x >> 16);
+            o[2] = with_residual_bf16(o[2], r.y & 0xffff); o[3] = with_residual_bf16(o[3], r.y >> 16);
+          }
         }
         if (go.c_f32) {
           *reinterpret_cast<uint4*>(static_cast<float*>(go.C) + m * go.ldc + n) = make_uint4(
@@ -409,7 +459,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
             }
             if (rrow) {
               const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
-              o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+              o[0] = with_residual_bf16(o[0], r.x & 0xffff); o[1] = with_residual_bf16(o[1], r.x >> 16);
+              o[2] = with_residual_bf16(o[2], r.y & 0xffff); o[3] = with_residual_bf16(o[3], r.y >> 16);
             }
             *cp = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
           }
@@ -1260,6 +1311,7 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
   const int esz = g.c_f32 ? 4 : 2;
   g.vec16 = ((ldc * esz) % 16 == 0) && lz_aligned16(C) &&
             (R == nullptr || ((ldr * 2) % 8 == 0 && (reinterpret_cast<uintptr_t>(R) & 7) == 0));
+  g.r16 = R != nullptr && (ldr * 2) % 16 == 0 && lz_aligned16(R);
   g.vec_store = (N % 4 == 0) && (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & (4 * esz - 1)) == 0) &&
                 (R == nullptr || ((ldr % 4 == 0) && (reinterpret_cast<uintptr_t>(R) & 7) == 0));
   g.kper = K > 0 ? K : 1;
