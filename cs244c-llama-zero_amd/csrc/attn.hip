@@ -693,131 +693,6 @@ struct TileOffsets {
   }
 };
 
-// Forward on tiles: 128 queries per workgroup (32 per wave), 64-key steps.
-template <int HD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_tile_kernel(AttnArgs a) {
-  constexpr int BQ = 128, BKV = 64;
-  constexpr int kTile = BKV * HD * 2;
-  constexpr int kStage = 2 * kTile;  // K, V
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
-
-  const int S = a.S, H = a.H, KV = a.KV;
-  const int nqb = (S + BQ - 1) / BQ;
-  const int bh = a.B * H;
-  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
-  const int rem = blockIdx.x % bh;
-  const int b = rem / H, h = rem % H;
-  const int g = h / (H / KV);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5, l32 = lane & 31;
-  TileOffsets<HD> to;
-  to.init(lane);
-  const int q0 = qb * BQ, qw0 = q0 + 32 * wave;
-  const int qrow = qw0 + l32;
-
-  bf16x8_t qf[HD / 16];
-  {
-    const uint16_t* qp = a.q + ((int64_t)b * S + min(qrow, S - 1)) * a.ldq + (int64_t)h * HD + 8 * half;
-#pragma unroll
-    for (int kk = 0; kk < HD / 16; ++kk) qf[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qp + kk * 16));
-  }
-  f32x16_t o[HD / 32];
-#pragma unroll
-  for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float m = -INFINITY, l = 0.f;
-  const float c = a.scale * kLog2e;
-
-  const int kv_end = min(S, q0 + BQ);  // a multiple of 64
-  const int kv_end_w = min(S, qw0 + 32);
-  const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
-  const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
-  const int nsteps = kv_end / BKV;
-
-  dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
-  dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
-  for (int it = 0; it < nsteps; ++it) {
-    dma_barrier();  // this step's tiles landed (every wave's loads), last step's reads retired
-    if (it + 1 < nsteps) {
-      char* nxt = smem + ((it + 1) & 1) * kStage;
-      dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, nxt, wave, lane);
-      dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, nxt + kTile, wave, lane);
-    }
-    const int k0 = it * BKV;
-    const char* Kt = smem + (it & 1) * kStage;
-    const char* Vt = Kt + kTile;
-    if (k0 < kv_end_w) {
-      f32x16_t s[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < HD / 16; ++kk)
-          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], s[t], 0,
-                                                         0, 0);
-      }
-      const bool need_mask = k0 + BKV - 1 > qw0;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if (need_mask) {
-            const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (kv > qrow) s[t][r] = -INFINITY;
-          }
-          mx = fmaxf(mx, s[t][r]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx * c);
-      const float nm = -m_new;
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
-          s[t][r] = p;
-          rs += p;
-        }
-      rs += __shfl_xor(rs, 32, 64);
-      if (__builtin_amdgcn_read_exec() & __ballot(m_new != m)) {  // some lane's max moved
-        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-        l *= alpha;
-#pragma unroll
-        for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-      }
-      l += rs;
-      m = m_new;
-#pragma unroll
-      for (int ks = 0; ks < BKV / 16; ++ks) {
-        const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
-#pragma unroll
-        for (int i = 0; i < HD / 32; ++i)
-          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Vt, ks, i), pb, o[i], 0, 0, 0);
-      }
-    }
-  }
-  if (qrow < S) {
-    const float inv_l = 1.0f / l;
-    uint16_t* op = a.o + ((int64_t)b * S + qrow) * a.ldo + (int64_t)h * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int hd = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(op + hd, o[i][4 * q4] * inv_l, o[i][4 * q4 + 1] * inv_l, o[i][4 * q4 + 2] * inv_l,
-                     o[i][4 * q4 + 3] * inv_l);
-      }
-    if (half == 0) a.lse[((int64_t)b * H + h) * S + qrow] = (m + log2f(l)) * kLn2;
-  }
-}
-
 // Forward on tiles: 128 queries per workgroup (32 per wave), 64-key steps,
 // K and V tiles double-buffered in LDS (the next step's tiles are issued
 // right after the barrier that opens a step).
@@ -889,7 +764,7 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[H
 }
 
 template <int HD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_pipe_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_tile_kernel(AttnArgs a) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int kTile = BKV * HD * 2;
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];  // K slots 0, 1; V slots 0, 1
@@ -1772,8 +1647,8 @@ LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid = (unsigned)(lz_cdiv(S, 128) * B * H);
-    if (hd == 128) attn_fwd_pipe_kernel<128><<<grid, 256, 0, s>>>(a);
-    else attn_fwd_pipe_kernel<64><<<grid, 256, 0, s>>>(a);
+    if (hd == 128) attn_fwd_tile_kernel<128><<<grid, 256, 0, s>>>(a);
+    else attn_fwd_tile_kernel<64><<<grid, 256, 0, s>>>(a);
     return lz_check_launch("lz_attn_fwd");
   }
   if (mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o)) {
