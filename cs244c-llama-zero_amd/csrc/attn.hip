@@ -118,16 +118,29 @@ __device__ __forceinline__ void store_grad_row(uint16_t* dst, const f32x16_t (&a
       }
     return;
   }
+  // every table value this lane needs is loaded before the first store (the
+  // stores may alias the tables as far as the compiler knows, so it would
+  // otherwise wait for each group's loads in turn)
   constexpr int kHalf = HD / 2, kBlk = HD / 64;
+  uint2 cw[kBlk][4][2], sw[kBlk][4][2];
 #pragma unroll
   for (int i = 0; i < kBlk; ++i)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int c = i * 32 + 8 * q4 + 4 * half;
-      const uint2 c1w = *reinterpret_cast<const uint2*>(cs + c), c2w = *reinterpret_cast<const uint2*>(cs + c + kHalf);
-      const uint2 s1w = *reinterpret_cast<const uint2*>(sn + c), s2w = *reinterpret_cast<const uint2*>(sn + c + kHalf);
-      const uint32_t c1a[2] = {c1w.x, c1w.y}, c2a[2] = {c2w.x, c2w.y}, s1a[2] = {s1w.x, s1w.y},
-                     s2a[2] = {s2w.x, s2w.y};
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        cw[i][q4][hh] = *reinterpret_cast<const uint2*>(cs + c + hh * kHalf);
+        sw[i][q4][hh] = *reinterpret_cast<const uint2*>(sn + c + hh * kHalf);
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < kBlk; ++i)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int c = i * 32 + 8 * q4 + 4 * half;
+      const uint32_t c1a[2] = {cw[i][q4][0].x, cw[i][q4][0].y}, c2a[2] = {cw[i][q4][1].x, cw[i][q4][1].y};
+      const uint32_t s1a[2] = {sw[i][q4][0].x, sw[i][q4][0].y}, s2a[2] = {sw[i][q4][1].x, sw[i][q4][1].y};
       float g1[4], g2[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

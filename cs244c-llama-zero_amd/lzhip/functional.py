@@ -359,8 +359,13 @@ class AttnProjFn(Function):
             qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :], o, do2, lse,
             B, S, H, KV, hd, scale,
             dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :],
-            qt=qt, kt=kt, dot=dot, rope=(cos, sin),  # dq and dk come back through RoPE's backward
+            qt=qt, kt=kt, dot=dot,
         )
+        # RoPE's backward as its own pass over dq|dk: attn_bwd(rope=...) can
+        # fold it into the dQ/dK stores, but in the MFMA output layout each
+        # lane's table reads are 8-byte pieces of 32 different rows, which
+        # cost more than this coalesced pass
+        ops.rope_(dqkv, S, H + KV, hd, cos, sin, backward=True)
         need_w = any(ctx.needs_input_grad[1:4])
         w = fused_weight([wq, wk, wv])
         dh2, dw = _linear_bwd(dqkv, h2, w, ctx.needs_input_grad[0], need_w, [wq, wk, wv])
