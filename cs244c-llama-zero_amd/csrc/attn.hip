@@ -58,6 +58,48 @@ struct AttnArgs {
   float scale;
 };
 
+// Workgroup -> (query block, batch, head), heaviest query blocks first.  The
+// hardware deals workgroup i to XCD i % 8; when the (batch, kv head) pairs
+// split evenly over the 8 XCDs, each XCD gets its own pairs, and all query
+// heads of a pair's group and neighbouring query blocks run on that XCD at
+// about the same time, so the K and V rows they stream are fetched into its
+// L2 once instead of by workgroups spread over every XCD.
+__device__ __forceinline__ void query_block_coords(int bid, int nqb, int B, int H, int KV, int& qb, int& b, int& h) {
+  const int rep = H / KV, npairs = B * KV;
+  if (npairs % 8 == 0) {
+    const int xcd = bid % 8, j = bid / 8;
+    const int per_q = (npairs / 8) * rep;  // workgroups of one query block on one XCD
+    const int qr = j / per_q, rem = j - qr * per_q;
+    const int pair = xcd + 8 * (rem / rep);
+    b = pair / KV;
+    h = (pair % KV) * rep + rem % rep;
+    qb = nqb - 1 - qr;
+  } else {
+    const int bh = B * H;
+    qb = nqb - 1 - bid / bh;
+    b = (bid % bh) / H;
+    h = bid % H;
+  }
+}
+
+// Workgroup -> (key block, batch, kv head), first key blocks (the most
+// queries at or after them) first; pairs split over XCDs as above, so the Q
+// and dO rows a pair's key blocks read share an L2.
+__device__ __forceinline__ void key_block_coords(int bid, int B, int KV, int& kvb, int& b, int& g) {
+  const int npairs = B * KV;
+  int pair;
+  if (npairs % 8 == 0) {
+    const int xcd = bid % 8, j = bid / 8, ppx = npairs / 8;
+    kvb = j / ppx;
+    pair = xcd + 8 * (j - kvb * ppx);
+  } else {
+    kvb = bid / npairs;
+    pair = bid % npairs;
+  }
+  b = pair / KV;
+  g = pair % KV;
+}
+
 // Elements e0..e0+7 of an accumulator -> an 8 x bf16 MFMA operand.
 __device__ __forceinline__ bf16x8_t pack8(const f32x16_t& v, int e0) {
   const uint4 w = make_uint4(pack_bf16x2(v[e0], v[e0 + 1]), pack_bf16x2(v[e0 + 2], v[e0 + 3]),
@@ -212,10 +254,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const int S = a.S, H = a.H, KV = a.KV;
   const int nqb = (S + BQ - 1) / BQ;
-  const int bh = a.B * H;
-  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
-  const int rem = blockIdx.x % bh;
-  const int b = rem / H, h = rem % H;
+  int qb, b, h;
+  query_block_coords(blockIdx.x, nqb, a.B, H, KV, qb, b, h);
   const int g = h / (H / KV);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -376,10 +416,8 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(AttnArgs a) {
   float* Ds = lse2s + BQ;
 
   const int S = a.S, H = a.H, KV = a.KV, rep = H / KV;
-  const int bkv = a.B * KV;
-  const int kvb = blockIdx.x / bkv;
-  const int rem = blockIdx.x % bkv;
-  const int b = rem / KV, g = rem % KV;
+  int kvb, b, g;
+  key_block_coords(blockIdx.x, a.B, KV, kvb, b, g);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
@@ -507,10 +545,8 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(AttnArgs a) {
 
   const int S = a.S, H = a.H, KV = a.KV;
   const int nqb = (S + BQ - 1) / BQ;
-  const int bh = a.B * H;
-  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
-  const int rem = blockIdx.x % bh;
-  const int b = rem / H, h = rem % H;
+  int qb, b, h;
+  query_block_coords(blockIdx.x, nqb, a.B, H, KV, qb, b, h);
   const int g = h / (H / KV);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -786,10 +822,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const int S = a.S, H = a.H, KV = a.KV;
   const int nqb = (S + BQ - 1) / BQ;
-  const int bh = a.B * H;
-  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
-  const int rem = blockIdx.x % bh;
-  const int b = rem / H, h = rem % H;
+  int qb, b, h;
+  query_block_coords(blockIdx.x, nqb, a.B, H, KV, qb, b, h);
   const int g = h / (H / KV);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -903,10 +937,8 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[kVTile + 2 * kStage];
 
   const int S = a.S, H = a.H, KV = a.KV, rep = H / KV;
-  const int bkv = a.B * KV;
-  const int kvb = blockIdx.x / bkv;
-  const int rem = blockIdx.x % bkv;
-  const int b = rem / KV, g = rem % KV;
+  int kvb, b, g;
+  key_block_coords(blockIdx.x, a.B, KV, kvb, b, g);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
@@ -1026,10 +1058,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const int S = a.S, H = a.H, KV = a.KV;
   const int nqb = (S + BQ - 1) / BQ;
-  const int bh = a.B * H;
-  const int qb = nqb - 1 - (int)(blockIdx.x / bh);
-  const int rem = blockIdx.x % bh;
-  const int b = rem / H, h = rem % H;
+  int qb, b, h;
+  query_block_coords(blockIdx.x, nqb, a.B, H, KV, qb, b, h);
   const int g = h / (H / KV);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
