@@ -458,7 +458,8 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
     from oracle import engine as OE
     from oracle import model as OM
 
-    threads = torch.get_num_threads()  # the box's CPU share (OMP_NUM_THREADS), not every host CPU
+    threads = len(os.sched_getaffinity(0))  # every CPU this process may run on
+    torch.set_num_threads(threads)
     ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
                   n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta)
     torch.manual_seed(0)
@@ -485,6 +486,51 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
     }
 
 
+def gemm_sweep(dev: torch.device) -> dict:
+    """The 1B step's GEMM shapes (16384 tokens) one product at a time, with HIP
+    events around 20 launches each: forward x.W^T (with and without the
+    block's residual), input gradient dy.W and weight gradient dy^T.x, next to
+    hipBLASLt (torch.matmul) on the same operands; and the O-projection shape
+    at K = 64 ... 2048, whose intercept is the fixed per-launch cost (prologue,
+    epilogue, launch) and whose slope is the main loop's rate."""
+    from lzhip import ops
+
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    T = 16384
+    out = {"tokens": T, "products_TFLOP/s": {}, "k_sweep_us": {}}
+    for name, (N, K) in {"qkv": (4096, 2048), "gate|up": (11264, 2048), "o": (2048, 2048), "down": (2048, 5632),
+                         "lm_head": (32000, 2048)}.items():
+        x = torch.randn(T, K, device=dev, generator=g).to(bf)
+        w = (0.02 * torch.randn(N, K, device=dev, generator=g)).to(bf)
+        dy = torch.randn(T, N, device=dev, generator=g).to(bf)
+        f = 2.0 * T * N * K / 1e9
+        r = {"forward": f / _time_ms(lambda: ops.gemm(x, w)),
+             "input_grad": f / _time_ms(lambda: ops.gemm(dy, w, b_kmajor=False)),
+             "weight_grad": f / _time_ms(lambda: ops.gemm(dy, x, a_kmajor=False, b_kmajor=False)),
+             "hipblaslt_forward": f / _time_ms(lambda: torch.matmul(x, w.t()))}
+        if N == 2048:
+            res = torch.randn(T, N, device=dev, generator=g).to(bf)
+            r["forward_residual"] = f / _time_ms(lambda: ops.gemm(x, w, residual=res))
+        out["products_TFLOP/s"][name] = {k: round(v, 1) for k, v in r.items()}
+        del x, w, dy
+    N = 2048
+    for K in (64, 128, 256, 512, 1024, 2048):
+        x = torch.randn(T, K, device=dev, generator=g).to(bf)
+        w = torch.randn(N, K, device=dev, generator=g).to(bf)
+        res = torch.randn(T, N, device=dev, generator=g).to(bf)
+        y = torch.empty(T, N, device=dev, dtype=bf)
+        out["k_sweep_us"][K] = {"plain": round(1000 * _time_ms(lambda: ops.gemm(x, w, out=y)), 2),
+                                "residual": round(1000 * _time_ms(lambda: ops.gemm(x, w, out=y, residual=res)), 2)}
+    ks = sorted(out["k_sweep_us"])
+    k0, k1 = ks[-3], ks[-1]
+    t0, t1 = out["k_sweep_us"][k0]["plain"], out["k_sweep_us"][k1]["plain"]
+    slope = (t1 - t0) / (k1 - k0)  # us per unit of K
+    out["fixed_cost_us"] = round(t1 - slope * k1, 2)
+    out["main_loop_TFLOP/s"] = round(2.0 * T * N / (slope * 1e-6) / 1e12, 1)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -499,6 +545,9 @@ def main() -> int:
     ap.add_argument("--skip-plumbing", action="store_true", help="skip the train.py plumbing leg")
     ap.add_argument("--plumbing-only", action="store_true",
                     help="only the train.py plumbing leg (eager and HIP-graph replay); prints its JSON and exits")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="the 1B step's GEMM shapes one product at a time (with hipBLASLt beside them) and a K "
+                         "sweep of the O projection; prints one JSON line and exits")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the 1B ZeRO-3 step (no recompute=False, 125M, AdamW or pointwise legs)")
     args = ap.parse_args()
@@ -525,6 +574,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.fit_sweep:
         print(json.dumps(fit_sweep(dev, args.fit_max_batch)), flush=True)
+        return 0
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": gemm_sweep(dev)}), flush=True)
         return 0
     B, S = 8, 2048
     log("building 1B model + ZeRO-3 engine")

@@ -31,7 +31,7 @@ class GraphedTrainStep:
             raise ValueError("grad_accum must be >= 1")
         self.model, self.opt, self.grads = model, opt, grads
         self.grad_accum, self.max_grad_norm = int(grad_accum), float(max_grad_norm)
-        self.ids = [torch.zeros(tuple(batch_shape), dtype=torch.int64, device=device) for _ in range(grad_accum)]
+        self.ids = [ops.zeros(tuple(batch_shape), torch.int64, device) for _ in range(grad_accum)]
         self.seed = ops.fill_(torch.empty((), dtype=torch.float32, device=device), 1.0 / self.grad_accum)
         self.graph = None
         self.loss = None

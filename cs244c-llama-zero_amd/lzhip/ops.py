@@ -204,9 +204,18 @@ def fill_(x: torch.Tensor, value: float) -> torch.Tensor:
 
 
 def zeros(shape, dtype: torch.dtype, device) -> torch.Tensor:
+    """A zero-filled device tensor written by this library's fill kernel;
+    integer dtypes are filled through a float view of the same width (zero
+    has the same bits)."""
     t = torch.empty(shape, dtype=dtype, device=device)
     if t.numel():
-        fill_(t, 0.0)
+        v = t
+        if not t.is_floating_point():
+            views = {8: torch.float64, 4: torch.float32, 2: torch.bfloat16}
+            if t.element_size() not in views:
+                raise TypeError(f"zeros: no fill for {dtype}")
+            v = t.view(views[t.element_size()])
+        fill_(v, 0.0)
     return t
 
 

@@ -77,7 +77,7 @@ class FusedAdamW(torch.optim.Optimizer):
                     continue
                 dev = next(p.device for p in group["params"] if p.grad is not None)
                 if "step_dev" not in group:
-                    group["step_dev"] = torch.zeros((1,), dtype=torch.int64, device=dev)
+                    group["step_dev"] = ops.zeros((1,), torch.int64, dev)
                     group["hyper_dev"] = ops.zeros((3,), torch.float32, dev)
                 beta1, beta2 = group["betas"]
                 ops.adamw_step_(group["step_dev"], group["lr"], beta1, beta2, group["weight_decay"],
