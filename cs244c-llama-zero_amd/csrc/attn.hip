@@ -1225,9 +1225,26 @@ struct GenArgs {
   int64_t lddq, lddk, lddv;
   int B, S, H, KV, hd;
   float scale;
+  // explicit mask (SDPA's attn_mask; then no causal mask): kind 1 = bool
+  // (bytes, nonzero keeps the score), 2 = fp32, 3 = bf16 (added to the
+  // scaled score); element strides over [B, H, S(query), S(key)], 0 where
+  // the mask broadcasts
+  const void* mask;
+  int mask_kind;
+  int64_t msb, msh, msq, msk;
 };
 
 constexpr int kGenMax = 4;  // head dim up to 64 * kGenMax
+
+// The scaled score of (b, h, query s, key kv) with the explicit mask applied:
+// -inf where a bool mask is false, score + mask for a float mask.
+template <typename T>
+__device__ __forceinline__ float masked_score(const GenArgs<T>& a, float sc, int b, int h, int s, int kv) {
+  const int64_t i = (int64_t)b * a.msb + (int64_t)h * a.msh + (int64_t)s * a.msq + (int64_t)kv * a.msk;
+  if (a.mask_kind == 1) return static_cast<const uint8_t*>(a.mask)[i] ? sc : -INFINITY;
+  if (a.mask_kind == 2) return sc + static_cast<const float*>(a.mask)[i];
+  return sc + bf2f(static_cast<const uint16_t*>(a.mask)[i]);
+}
 
 template <typename T>
 __global__ void __launch_bounds__(256) attn_fwd_generic_kernel(GenArgs<T> a) {
@@ -1248,7 +1265,8 @@ __global__ void __launch_bounds__(256) attn_fwd_generic_kernel(GenArgs<T> a) {
     ov[j] = 0.f;
   }
   float m = -INFINITY, l = 0.f;
-  for (int kv = 0; kv <= s; ++kv) {
+  const int kv_last = a.mask_kind ? a.S - 1 : s;  // an explicit mask replaces the causal one
+  for (int kv = 0; kv <= kv_last; ++kv) {
     const T* kp = a.k + ((int64_t)b * a.S + kv) * a.ldk + (int64_t)g * a.hd;
     const T* vp = a.v + ((int64_t)b * a.S + kv) * a.ldv + (int64_t)g * a.hd;
     float dot = 0.f;
@@ -1257,7 +1275,11 @@ __global__ void __launch_bounds__(256) attn_fwd_generic_kernel(GenArgs<T> a) {
       const int d = lane + 64 * j;
       if (d < a.hd) dot = fmaf(qv[j], Elem<T>::load(kp, d), dot);
     }
-    const float sc = wave_sum(dot) * a.scale;
+    float sc = wave_sum(dot) * a.scale;
+    if (a.mask_kind) {
+      sc = masked_score(a, sc, b, h, s, kv);
+      if (sc == -INFINITY) continue;  // contributes nothing (and keeps m finite once it is)
+    }
     const float m_new = fmaxf(m, sc);
     const float corr = expf(m - m_new), p = expf(sc - m_new);
     l = l * corr + p;
@@ -1299,7 +1321,8 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_generic_kernel(GenArgs<T> a) 
   }
   const float lse = a.lse[((int64_t)b * a.H + h) * a.S + s];
   const float D = a.delta[((int64_t)b * a.H + h) * a.S + s];
-  for (int kv = 0; kv <= s; ++kv) {
+  const int kv_last = a.mask_kind ? a.S - 1 : s;
+  for (int kv = 0; kv <= kv_last; ++kv) {
     const T* kp = a.k + ((int64_t)b * a.S + kv) * a.ldk + (int64_t)g * a.hd;
     const T* vp = a.v + ((int64_t)b * a.S + kv) * a.ldv + (int64_t)g * a.hd;
     float dot = 0.f, dpd = 0.f;
@@ -1311,7 +1334,9 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_generic_kernel(GenArgs<T> a) 
         dpd = fmaf(dov[j], Elem<T>::load(vp, d), dpd);
       }
     }
-    const float p = expf(wave_sum(dot) * a.scale - lse);
+    float sc = wave_sum(dot) * a.scale;
+    if (a.mask_kind) sc = masked_score(a, sc, b, h, s, kv);
+    const float p = expf(sc - lse);
     const float ds = p * (wave_sum(dpd) - D);
 #pragma unroll
     for (int j = 0; j < kGenMax; ++j) {
@@ -1350,7 +1375,7 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_generic_kernel(GenArgs<T> a
   }
   for (int hq = 0; hq < rep; ++hq) {
     const int h = g * rep + hq;
-    for (int s = kv; s < a.S; ++s) {
+    for (int s = a.mask_kind ? 0 : kv; s < a.S; ++s) {
       const T* qp = a.q + ((int64_t)b * a.S + s) * a.ldq + (int64_t)h * a.hd;
       const T* dop = a.dout + ((int64_t)b * a.S + s) * a.lddo + (int64_t)h * a.hd;
       float dot = 0.f, dpd = 0.f;
@@ -1363,7 +1388,9 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_generic_kernel(GenArgs<T> a
         }
       }
       const int64_t li = ((int64_t)b * a.H + h) * a.S + s;
-      const float p = expf(wave_sum(dot) * a.scale - a.lse[li]);
+      float sc = wave_sum(dot) * a.scale;
+      if (a.mask_kind) sc = masked_score(a, sc, b, h, s, kv);
+      const float p = expf(sc - a.lse[li]);
       const float ds = p * (wave_sum(dpd) - a.delta[li]);
 #pragma unroll
       for (int j = 0; j < kGenMax; ++j) {
@@ -1883,3 +1910,94 @@ int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const 
 }
 
 }  // namespace
+
+namespace {
+
+template <typename T>
+int masked_args(GenArgs<T>& a, const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                const void* mask, int mask_kind, const int64_t* mstride, int64_t B, int64_t S, int64_t H, int64_t KV,
+                int64_t hd, float scale) {
+  a.q = (const T*)q; a.k = (const T*)k; a.v = (const T*)v;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv;
+  a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+  a.mask = mask; a.mask_kind = mask_kind;
+  a.msb = mstride[0]; a.msh = mstride[1]; a.msq = mstride[2]; a.msk = mstride[3];
+  return LZ_OK;
+}
+
+int check_mask(const void* mask, int mask_kind, const int64_t* mstride) {
+  LZ_REQUIRE(mask && mstride, "attention mask: null pointer");
+  LZ_REQUIRE(mask_kind >= 1 && mask_kind <= 3, "attention mask: kind %d (1 bool, 2 fp32, 3 bf16)", mask_kind);
+  for (int i = 0; i < 4; ++i) LZ_REQUIRE(mstride[i] >= 0, "attention mask: negative stride");
+  return LZ_OK;
+}
+
+}  // namespace
+
+// Attention with an explicit mask instead of the causal one (SDPA's
+// attn_mask with is_causal=False, model/llama.py:109-117): mask_kind 1 =
+// bool bytes (nonzero: the key takes part), 2 = fp32, 3 = bf16 (added to the
+// scaled scores); mstride = element strides of the mask over [B, H, S
+// (query), S (key)], 0 where it broadcasts.  A row whose keys are all masked
+// gives NaN, as the reference's softmax of an all -inf row does.  One wave
+// per query row (any head dim up to 256, bf16 or fp32).
+LZ_EXPORT int lz_attn_fwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                 const void* mask, int mask_kind, const int64_t* mstride, void* o, int64_t ldo,
+                                 float* lse, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
+                                 int dtype, void* stream) {
+  int rc = check_shape(B, S, H, KV, hd);
+  if (rc) return rc;
+  rc = check_mask(mask, mask_kind, mstride);
+  if (rc) return rc;
+  LZ_REQUIRE(q && k && v && o && lse, "lz_attn_fwd_masked: null pointer");
+  hipStream_t s = lz_stream(stream);
+  const unsigned grid = (unsigned)lz_cdiv(B * H * S, 4);
+  if (dtype == LZ_BF16) {
+    GenArgs<uint16_t> a{};
+    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
+    attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F32) {
+    GenArgs<float> a{};
+    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    a.o = (float*)o; a.ldo = ldo; a.lse = lse;
+    attn_fwd_generic_kernel<float><<<grid, 256, 0, s>>>(a);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_attn_fwd_masked: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_attn_fwd_masked");
+}
+
+// Backward of lz_attn_fwd_masked (same mask); delta from lz_attn_delta.
+LZ_EXPORT int lz_attn_bwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                 const void* dout, int64_t lddo, const float* lse, const float* delta,
+                                 const void* mask, int mask_kind, const int64_t* mstride, void* dq, int64_t lddq,
+                                 void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S, int64_t H,
+                                 int64_t KV, int64_t hd, float scale, int dtype, void* stream) {
+  int rc = check_shape(B, S, H, KV, hd);
+  if (rc) return rc;
+  rc = check_mask(mask, mask_kind, mstride);
+  if (rc) return rc;
+  LZ_REQUIRE(q && k && v && dout && lse && delta && dq && dk && dv, "lz_attn_bwd_masked: null pointer");
+  hipStream_t s = lz_stream(stream);
+  const unsigned grid_q = (unsigned)lz_cdiv(B * H * S, 4);
+  const unsigned grid_kv = (unsigned)lz_cdiv(B * KV * S, 4);
+  if (dtype == LZ_BF16) {
+    GenArgs<uint16_t> a{};
+    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    a.lse = const_cast<float*>(lse); a.dout = (const uint16_t*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F32) {
+    GenArgs<float> a{};
+    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    a.lse = const_cast<float*>(lse); a.dout = (const float*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (float*)dq; a.dk = (float*)dk; a.dv = (float*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    attn_bwd_dq_generic_kernel<float><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_generic_kernel<float><<<grid_kv, 256, 0, s>>>(a);
+  } else {
+    return lz_set_error(LZ_EINVAL, "lz_attn_bwd_masked: bad dtype %d", dtype);
+  }
+  return lz_check_launch("lz_attn_bwd_masked");
+}

@@ -83,6 +83,17 @@ SIGNATURES = {
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     ),
     "lz_attn_delta": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "lz_attn_fwd_masked": (
+        _i32,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
+    ),
+    "lz_attn_bwd_masked": (
+        _i32,
+        [
+            _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
+            _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
+        ],
+    ),
     "lz_attn_bwd": (
         _i32,
         [

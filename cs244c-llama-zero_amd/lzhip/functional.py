@@ -319,7 +319,7 @@ class AttnProjFn(Function):
     [B, S, H*hd] that o_proj consumes."""
 
     @staticmethod
-    def forward(ctx, h, wq, wk, wv, cos, sin, n_heads: int, n_kv: int, scale: float):
+    def forward(ctx, h, wq, wk, wv, cos, sin, n_heads: int, n_kv: int, scale: float, mask=None):
         B, S, d = h.shape
         hd = wq.shape[0] // n_heads
         h2 = _rows(h)
@@ -335,11 +335,15 @@ class AttnProjFn(Function):
         k2 = qkv[:, H * hd : (H + KV) * hd]
         v2 = qkv[:, (H + KV) * hd :]
         ld = qkv.shape[1]
-        vt = None
-        if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, H * hd) == 1:
-            vt = ops.transpose_heads(qkv, B, S, KV, hd, col0=(H + KV) * hd)
-        o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
+        if mask is not None:  # an explicit mask (SDPA attn_mask) replaces the causal one
+            o, lse = ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, scale, mask)
+        else:
+            vt = None
+            if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, H * hd) == 1:
+                vt = ops.transpose_heads(qkv, B, S, KV, hd, col0=(H + KV) * hd)
+            o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
         ctx.save_for_backward(h2, wq, wk, wv, qkv, o, lse, cos, sin)
+        ctx.mask = mask
         ctx.meta = (B, S, H, KV, hd, scale)
         return o.view(B, S, H * hd)
 
@@ -350,17 +354,17 @@ class AttnProjFn(Function):
         do2 = _rows(do)
         ld = qkv.shape[1]
         dqkv = torch.empty_like(qkv)
-        qt = kt = dot = None
-        if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, do2.stride(0)) == 1:
-            qt = ops.transpose_heads(qkv, B, S, H, hd, col0=0)
-            kt = ops.transpose_heads(qkv, B, S, KV, hd, col0=H * hd)
-            dot = ops.transpose_heads(do2, B, S, H, hd, col0=0)
-        ops.attn_bwd(
-            qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :], o, do2, lse,
-            B, S, H, KV, hd, scale,
-            dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :],
-            qt=qt, kt=kt, dot=dot,
-        )
+        q2, k2, v2 = qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :]
+        dq2, dk2, dv2 = dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :]
+        if ctx.mask is not None:
+            ops.attn_bwd_masked(q2, k2, v2, o, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, ctx.mask)
+        else:
+            qt = kt = dot = None
+            if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, do2.stride(0)) == 1:
+                qt = ops.transpose_heads(qkv, B, S, H, hd, col0=0)
+                kt = ops.transpose_heads(qkv, B, S, KV, hd, col0=H * hd)
+                dot = ops.transpose_heads(do2, B, S, H, hd, col0=0)
+            ops.attn_bwd(q2, k2, v2, o, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt=qt, kt=kt, dot=dot)
         # RoPE's backward as its own pass over dq|dk: attn_bwd(rope=...) can
         # fold it into the dQ/dK stores, but in the MFMA output layout each
         # lane's table reads are 8-byte pieces of 32 different rows, which
@@ -374,7 +378,7 @@ class AttnProjFn(Function):
             nq, nk = wq.shape[0], wk.shape[0]
             dwq, dwk, dwv = dw[:nq], dw[nq : nq + nk], dw[nq + nk :]
         dh = dh2.view(B, S, -1) if dh2 is not None else None
-        return dh, dwq, dwk, dwv, None, None, None, None, None
+        return dh, dwq, dwk, dwv, None, None, None, None, None, None
 
 
 class MLPFn(Function):

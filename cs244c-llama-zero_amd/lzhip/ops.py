@@ -859,6 +859,45 @@ def attn_fwd(q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, B: int, S: in
     return o, lse
 
 
+def _attn_mask_args(mask: torch.Tensor, B: int, H: int, S: int):
+    """(kind, strides array) of an attention mask broadcastable to [B, H, S, S]
+    (bool: True keeps the score; fp32/bf16: added to it)."""
+    require_gpu(mask)
+    kinds = {torch.bool: 1, torch.float32: 2, torch.bfloat16: 3}
+    if mask.dtype not in kinds:
+        raise TypeError(f"attention mask must be bool, float32 or bfloat16 (got {mask.dtype})")
+    try:
+        strides = mask.expand(B, H, S, S).stride()
+    except RuntimeError as e:
+        raise ValueError(f"attention mask of shape {tuple(mask.shape)} does not broadcast to {(B, H, S, S)}") from e
+    return kinds[mask.dtype], (ctypes.c_int64 * 4)(*strides)
+
+
+def attn_fwd_masked(q2, k2, v2, B: int, S: int, H: int, KV: int, hd: int, scale: float, mask: torch.Tensor):
+    """attn_fwd with an explicit mask in place of the causal one; returns o,
+    lse."""
+    require_gpu(q2, k2, v2)
+    kind, st = _attn_mask_args(mask, B, H, S)
+    o = torch.empty((B * S, H * hd), dtype=q2.dtype, device=q2.device)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
+    _lib.call("lz_attn_fwd_masked", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
+              _row_stride(v2), mask.data_ptr(), kind, ctypes.addressof(st), o.data_ptr(), H * hd, lse.data_ptr(), B, S,
+              H, KV, hd, float(scale), dtype_code(q2), stream_ptr(q2.device))
+    return o, lse
+
+
+def attn_bwd_masked(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, mask: torch.Tensor) -> None:
+    require_gpu(q2, k2, v2, o2, do2, lse, dq2, dk2, dv2)
+    kind, st = _attn_mask_args(mask, B, H, S)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
+    _lib.call("lz_attn_delta", o2.data_ptr(), _row_stride(o2), do2.data_ptr(), _row_stride(do2), delta.data_ptr(),
+              B, S, H, hd, dtype_code(o2), stream_ptr(q2.device))
+    _lib.call("lz_attn_bwd_masked", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
+              _row_stride(v2), do2.data_ptr(), _row_stride(do2), lse.data_ptr(), delta.data_ptr(), mask.data_ptr(),
+              kind, ctypes.addressof(st), dq2.data_ptr(), _row_stride(dq2), dk2.data_ptr(), _row_stride(dk2),
+              dv2.data_ptr(), _row_stride(dv2), B, S, H, KV, hd, float(scale), dtype_code(q2), stream_ptr(q2.device))
+
+
 def attn_bwd(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt=None, kt=None, dot=None,
              rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
     """dq2/dk2/dv2 = gradients of causal GQA attention.  With rope = (cos,

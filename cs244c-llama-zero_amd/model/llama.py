@@ -157,17 +157,17 @@ class GroupedQueryAttention(nn.Module):
         attention_mask: Optional[torch.Tensor] = None,
         residual: Optional[torch.Tensor] = None,
     ) -> torch.Tensor:
-        """Causal GQA (model/llama.py:95-133); `residual` (optional) is added
-        inside the o_proj GEMM."""
-        if attention_mask is not None:
-            raise NotImplementedError("explicit attention masks are not supported; the HIP kernel is causal")
+        """GQA (model/llama.py:95-133): causal, or with `attention_mask` in its
+        place (SDPA's attn_mask: bool keeps where True, a float mask is added
+        to the scaled scores; broadcastable to [B, H, S, S]); `residual`
+        (optional) is added inside the o_proj GEMM."""
         _no_dropout(self.dropout, self.training, "attention")
         ops.require_gpu(x)
         bsz, seq_len, _ = x.shape
         cos, sin = self.rotary.tables(seq_len, x.device, x.dtype)
         y = LF.AttnProjFn.apply(
             x, self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, cos, sin,
-            self.n_heads, self.n_kv_heads, float(self.scale),
+            self.n_heads, self.n_kv_heads, float(self.scale), attention_mask,
         )
         return self.o_proj(y, residual)
 

@@ -274,6 +274,21 @@ int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_t lddo, fl
  * are returned as the gradients of q and k before RoPE (model/llama.py:35-39
  * backward), folded into the bf16 MFMA kernels' stores or, on the other
  * paths, applied by lz_rope afterwards. */
+/* Attention with an explicit mask in place of the causal one
+ * (model/llama.py:109-117: F.scaled_dot_product_attention(attn_mask=mask,
+ * is_causal=False)): mask_kind 1 = bool bytes (nonzero: the key takes part),
+ * 2 = fp32, 3 = bf16 (added to the scaled scores); mstride = 4 element
+ * strides over [B, H, S(query), S(key)], 0 where the mask broadcasts.  A
+ * query row whose keys are all masked gives NaN, as the reference's softmax
+ * does.  Any head dim up to 256, bf16 or fp32, one wave per row. */
+int lz_attn_fwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                       const void* mask, int mask_kind, const int64_t* mstride, void* o, int64_t ldo, float* lse,
+                       int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale, int dtype, void* stream);
+int lz_attn_bwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                       const void* dout, int64_t lddo, const float* lse, const float* delta, const void* mask,
+                       int mask_kind, const int64_t* mstride, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
+                       int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale, int dtype,
+                       void* stream);
 int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
                 int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
                 void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,

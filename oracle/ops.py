@@ -47,10 +47,14 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     return (x * cos) + (rotate_half(x) * sin)
 
 
-def causal_gqa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+def causal_gqa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
+                         attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
     """model/llama.py:88-117 with is_causal=True: q [B,H,S,hd], k/v [B,KV,S,hd];
     K/V heads repeated (repeat_interleave) to H, softmax(q k^T * scale) v with
-    the upper triangle masked.  Written out explicitly (no fused kernel)."""
+    the upper triangle masked.  Written out explicitly (no fused kernel).
+    With attn_mask (model/llama.py:109-117, is_causal=False): a bool mask
+    keeps the scores where True, a float mask is added to the scaled scores
+    (the reference's fallback branch, llama.py:118-129)."""
     B, H, S, hd = q.shape
     KV = k.shape[1]
     if H != KV:
@@ -58,8 +62,13 @@ def causal_gqa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scal
         v = v.repeat_interleave(H // KV, dim=1)
     scale = hd**-0.5 if scale is None else scale
     scores = torch.matmul(q, k.transpose(-2, -1)) * scale
-    mask = torch.triu(torch.ones(S, S, dtype=torch.bool), diagonal=1)
-    scores = scores.masked_fill(mask, float("-inf"))
+    if attn_mask is None:
+        mask = torch.triu(torch.ones(S, S, dtype=torch.bool), diagonal=1)
+        scores = scores.masked_fill(mask, float("-inf"))
+    elif attn_mask.dtype == torch.bool:
+        scores = scores.masked_fill(~attn_mask, float("-inf"))
+    else:
+        scores = scores + attn_mask.to(scores.dtype)
     probs = torch.softmax(scores, dim=-1)
     return torch.matmul(probs, v)
 

@@ -169,3 +169,49 @@ def test_generate_runs():
     model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
     out = model.generate(torch.zeros(1, 4, dtype=torch.long, device=DEV), max_new_tokens=5, temperature=0.0)
     assert out.shape == (1, 9)
+
+
+@pytest.mark.parametrize("stage3", [False, True])
+def test_model_with_attention_mask(stage3):
+    """The model called with attention_mask (model/llama.py:203-216 ->
+    SDPA attn_mask): an explicit causal mask gives the causal model's loss
+    and gradients (the masked kernels accumulate in another order: bf16
+    bars), a padding mask changes the loss and keeps everything finite; the
+    same through the ZeRO-3 executor, which carries the mask into its
+    recompute."""
+    from zero import ZeROStage3Optimizer
+
+    cfg = ModelConfig(name="mask", vocab_size=1000, max_seq_len=64, dim=256, n_layers=2, n_heads=8, n_kv_heads=4,
+                      ffn_dim=512)
+    torch.manual_seed(5)
+    model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+    B, S = 2, 64
+    ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(1)).to(DEV)
+    causal = ~torch.triu(torch.ones(S, S, dtype=torch.bool, device=DEV), 1)
+    pad = causal.expand(B, 1, S, S).clone()
+    pad[1, :, :, S // 2:] = False
+    pad[..., 0] = True
+    engine = ZeROStage3Optimizer(model=model, lr=1e-3) if stage3 else None
+
+    def run(mask):
+        if engine is not None:
+            engine.zero_grad()
+            engine.prepare_forward()
+        else:
+            model.zero_grad(set_to_none=True)
+        loss = model(input_ids=ids, labels=ids, attention_mask=mask, return_logits=False).loss
+        if engine is not None:
+            engine.backward(loss)
+            g = engine._grad_all.detach().double().cpu().clone()  # every handle's fp32 gradient shard
+        else:
+            loss.backward()
+            g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
+        return float(loss), g
+
+    l0, g0 = run(None)
+    l1, g1 = run(causal)
+    assert abs(l1 - l0) <= 1e-2 * abs(l0)
+    assert float(F.cosine_similarity(g0, g1, dim=0)) >= 0.999
+    l2, g2 = run(pad)
+    assert torch.isfinite(torch.tensor(l2)) and abs(l2 - l0) > 1e-4
+    assert bool(torch.isfinite(g2).all())

@@ -446,6 +446,78 @@ def test_attention_fwd_bwd(B, S, H, KV, hd):
     assert _rel_err(dv, vr.grad) < 2e-2
 
 
+def _attn_masks(kind, B, H, S, g):
+    """Masks of the shapes a caller of the reference's attention passes."""
+    if kind == "bool_padding":  # [B, 1, S, S]: causal, and each batch's last keys padded away
+        causal = ~torch.triu(torch.ones(S, S, dtype=torch.bool), 1)
+        keep = torch.ones(B, 1, S, S, dtype=torch.bool)
+        for b in range(B):
+            keep[b, :, :, S - 3 * (b + 1):] = False
+        m = causal & keep
+        m[..., 0] = True  # every query keeps at least one key
+        return m
+    if kind == "float_2d":  # [S, S] additive: -inf above the diagonal, random biases below
+        m = torch.randn(S, S, generator=g)
+        return m.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    if kind == "bf16_full":  # [B, H, S, S] additive, no -inf (every key of every query)
+        return torch.randn(B, H, S, S, generator=g).to(torch.bfloat16)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["bool_padding", "float_2d", "bf16_full"])
+@pytest.mark.parametrize("B,S,H,KV,hd,dtype", [(2, 64, 4, 2, 64, torch.bfloat16), (1, 48, 4, 4, 32, torch.float32),
+                                               (2, 40, 6, 2, 128, torch.bfloat16)])
+def test_attention_with_explicit_mask_vs_oracle(kind, B, S, H, KV, hd, dtype):
+    """model/llama.py:109-117: SDPA with attn_mask (no causal mask): forward
+    and gradients against the oracle's restatement in float64."""
+    g = _seed(B * S + hd + len(kind))
+    ld = (H + 2 * KV) * hd
+    qkv = torch.randn(B * S, ld, generator=g).to(dtype)
+    mask = _attn_masks(kind, B, H, S, g)
+    d = qkv.to(DEV)
+    q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
+    scale = hd**-0.5
+    o, lse = ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, scale, mask.to(DEV))
+
+    def heads(t, n):
+        return t.double().view(B, S, n, hd).transpose(1, 2).requires_grad_(True)
+
+    qr, kr, vr = heads(qkv[:, : H * hd], H), heads(qkv[:, H * hd : (H + KV) * hd], KV), heads(qkv[:, (H + KV) * hd :], KV)
+    mref = mask if mask.dtype == torch.bool else mask.double()
+    oref = R.causal_gqa_attention(qr, kr, vr, scale, attn_mask=mref)
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-5
+    assert _rel_err(o.cpu().double().view(B, S, H, hd).transpose(1, 2), oref) < tol
+    do = torch.randn(B * S, H * hd, generator=g).to(dtype)
+    dqkv = torch.zeros_like(d)
+    ops.attn_bwd_masked(q2, k2, v2, o, do.to(DEV), lse, B, S, H, KV, hd, scale, dqkv[:, : H * hd],
+                        dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :], mask.to(DEV))
+    oref.backward(do.double().view(B, S, H, hd).transpose(1, 2))
+    dq = dqkv[:, : H * hd].cpu().double().view(B, S, H, hd).transpose(1, 2)
+    dk = dqkv[:, H * hd : (H + KV) * hd].cpu().double().view(B, S, KV, hd).transpose(1, 2)
+    dv = dqkv[:, (H + KV) * hd :].cpu().double().view(B, S, KV, hd).transpose(1, 2)
+    gtol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    assert _grad_err(dq, qr.grad, vr.grad) < gtol
+    assert _grad_err(dk, kr.grad, vr.grad) < gtol
+    assert _rel_err(dv, vr.grad) < gtol
+
+
+def test_attention_explicit_causal_mask_equals_causal():
+    """An explicit causal bool mask reproduces the causal kernels (fp32: to
+    rounding), and a mask that does not broadcast is refused."""
+    g = _seed(77)
+    B, S, H, KV, hd = 2, 96, 4, 2, 64
+    d = torch.randn(B * S, (H + 2 * KV) * hd, generator=g).to(DEV)
+    q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
+    causal = ~torch.triu(torch.ones(S, S, dtype=torch.bool, device=DEV), 1)
+    o1, l1 = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, 0.125, None)
+    o2, l2 = ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, 0.125, causal)
+    assert _rel_err(o2, o1) < 1e-6 and _rel_err(l2, l1) < 1e-6
+    with pytest.raises(ValueError):
+        ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, 0.125, causal[:5])
+    with pytest.raises(TypeError):
+        ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, 0.125, causal.to(torch.int32))
+
+
 @pytest.mark.parametrize("B,S,H,KV,hd,dtype", [(2, 256, 8, 4, 128, torch.bfloat16), (1, 128, 4, 2, 64, torch.bfloat16),
                                                (1, 200, 4, 2, 128, torch.bfloat16), (2, 64, 4, 2, 32, torch.bfloat16),
                                                (1, 96, 4, 2, 64, torch.float32)])

@@ -223,3 +223,24 @@ def test_synthetic_streams():
     assert torch.equal(u1, u2)
     inputs, labels = OD.split_chunk(first)
     assert torch.equal(inputs, labels) and inputs.shape == (2, 8)
+
+
+def test_oracle_masked_attention_matches_sdpa():
+    """The oracle's attn_mask branch against F.scaled_dot_product_attention
+    (the call the reference makes, model/llama.py:109-117) for bool and
+    additive masks, and an explicit causal mask against is_causal."""
+    g = torch.Generator().manual_seed(3)
+    B, H, KV, S, hd = 2, 4, 2, 12, 8
+    q = torch.randn(B, H, S, hd, generator=g, dtype=torch.float64)
+    k = torch.randn(B, KV, S, hd, generator=g, dtype=torch.float64)
+    v = torch.randn(B, KV, S, hd, generator=g, dtype=torch.float64)
+    kk, vv = k.repeat_interleave(H // KV, dim=1), v.repeat_interleave(H // KV, dim=1)
+    bmask = torch.rand(B, 1, S, S, generator=g) > 0.3
+    bmask[..., 0] = True
+    fmask = torch.randn(S, S, generator=g, dtype=torch.float64)
+    for m in (bmask, fmask):
+        ref = F.scaled_dot_product_attention(q, kk, vv, attn_mask=m, is_causal=False)
+        assert torch.allclose(R.causal_gqa_attention(q, k, v, attn_mask=m), ref, atol=1e-12, rtol=1e-10)
+    causal = ~torch.triu(torch.ones(S, S, dtype=torch.bool), 1)
+    assert torch.allclose(R.causal_gqa_attention(q, k, v, attn_mask=causal), R.causal_gqa_attention(q, k, v),
+                          atol=1e-14, rtol=0)
