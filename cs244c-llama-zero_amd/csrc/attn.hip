@@ -1232,7 +1232,21 @@ struct GenArgs {
   const void* mask;
   int mask_kind;
   int64_t msb, msh, msq, msk;
+  // attention dropout (SDPA dropout_p): the probability of (b, h, query s,
+  // key kv) is kept with scale 1/(1-p) when element ((b*H + h)*S + s)*S + kv
+  // of the seed's stream is kept (lz_keep); drop_thresh 0 = no dropout
+  uint32_t drop_thresh;
+  float drop_scale;
+  uint64_t drop_seed;
 };
+
+// Dropout factor of one attention probability (1 without dropout).
+template <typename T>
+__device__ __forceinline__ float drop_factor(const GenArgs<T>& a, int b, int h, int s, int kv) {
+  if (a.drop_thresh == 0) return 1.0f;
+  const uint64_t i = (((uint64_t)b * a.H + h) * a.S + s) * a.S + kv;
+  return lz_keep(a.drop_seed, i, a.drop_thresh) ? a.drop_scale : 0.0f;
+}
 
 constexpr int kGenMax = 4;  // head dim up to 64 * kGenMax
 
@@ -1282,11 +1296,12 @@ __global__ void __launch_bounds__(256) attn_fwd_generic_kernel(GenArgs<T> a) {
     }
     const float m_new = fmaxf(m, sc);
     const float corr = expf(m - m_new), p = expf(sc - m_new);
-    l = l * corr + p;
+    l = l * corr + p;  // the normaliser sums the probabilities before dropout
+    const float pz = p * drop_factor(a, b, h, s, kv);
 #pragma unroll
     for (int j = 0; j < kGenMax; ++j) {
       const int d = lane + 64 * j;
-      if (d < a.hd) ov[j] = ov[j] * corr + p * Elem<T>::load(vp, d);
+      if (d < a.hd) ov[j] = ov[j] * corr + pz * Elem<T>::load(vp, d);
     }
     m = m_new;
   }
@@ -1337,7 +1352,8 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_generic_kernel(GenArgs<T> a) 
     float sc = wave_sum(dot) * a.scale;
     if (a.mask_kind) sc = masked_score(a, sc, b, h, s, kv);
     const float p = expf(sc - lse);
-    const float ds = p * (wave_sum(dpd) - D);
+    // dL/dP = Z * dO.V for the dropped-out P; D = rowsum(dO * O) is unchanged
+    const float ds = p * (drop_factor(a, b, h, s, kv) * wave_sum(dpd) - D);
 #pragma unroll
     for (int j = 0; j < kGenMax; ++j) {
       const int d = lane + 64 * j;
@@ -1391,12 +1407,14 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_generic_kernel(GenArgs<T> a
       float sc = wave_sum(dot) * a.scale;
       if (a.mask_kind) sc = masked_score(a, sc, b, h, s, kv);
       const float p = expf(sc - a.lse[li]);
-      const float ds = p * (wave_sum(dpd) - a.delta[li]);
+      const float z = drop_factor(a, b, h, s, kv);
+      const float ds = p * (z * wave_sum(dpd) - a.delta[li]);
+      const float pz = p * z;
 #pragma unroll
       for (int j = 0; j < kGenMax; ++j) {
         const int d = lane + 64 * j;
         if (d < a.hd) {
-          dva[j] = fmaf(p, Elem<T>::load(dop, d), dva[j]);
+          dva[j] = fmaf(pz, Elem<T>::load(dop, d), dva[j]);
           dka[j] = fmaf(ds, Elem<T>::load(qp, d), dka[j]);
         }
       }
@@ -1914,90 +1932,106 @@ int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const 
 namespace {
 
 template <typename T>
-int masked_args(GenArgs<T>& a, const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
-                const void* mask, int mask_kind, const int64_t* mstride, int64_t B, int64_t S, int64_t H, int64_t KV,
-                int64_t hd, float scale) {
+int general_args(GenArgs<T>& a, const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                 const void* mask, int mask_kind, const int64_t* mstride, float dropout_p, uint64_t seed, int64_t B,
+                 int64_t S, int64_t H, int64_t KV, int64_t hd, float scale) {
   a.q = (const T*)q; a.k = (const T*)k; a.v = (const T*)v;
   a.ldq = ldq; a.ldk = ldk; a.ldv = ldv;
   a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
   a.mask = mask; a.mask_kind = mask_kind;
-  a.msb = mstride[0]; a.msh = mstride[1]; a.msq = mstride[2]; a.msk = mstride[3];
+  if (mask_kind) {
+    a.msb = mstride[0]; a.msh = mstride[1]; a.msq = mstride[2]; a.msk = mstride[3];
+  }
+  a.drop_thresh = (uint32_t)std::min(std::ceil((double)dropout_p * 16777216.0), 16777216.0);
+  a.drop_scale = dropout_p < 1.f ? 1.0f / (1.0f - dropout_p) : 0.f;
+  a.drop_seed = seed;
   return LZ_OK;
 }
 
-int check_mask(const void* mask, int mask_kind, const int64_t* mstride) {
-  LZ_REQUIRE(mask && mstride, "attention mask: null pointer");
-  LZ_REQUIRE(mask_kind >= 1 && mask_kind <= 3, "attention mask: kind %d (1 bool, 2 fp32, 3 bf16)", mask_kind);
-  for (int i = 0; i < 4; ++i) LZ_REQUIRE(mstride[i] >= 0, "attention mask: negative stride");
+int check_general(const void* mask, int mask_kind, const int64_t* mstride, float dropout_p) {
+  LZ_REQUIRE(mask_kind >= 0 && mask_kind <= 3, "attention mask: kind %d (0 causal, 1 bool, 2 fp32, 3 bf16)",
+             mask_kind);
+  if (mask_kind) {
+    LZ_REQUIRE(mask && mstride, "attention mask: null pointer");
+    for (int i = 0; i < 4; ++i) LZ_REQUIRE(mstride[i] >= 0, "attention mask: negative stride");
+  }
+  LZ_REQUIRE(dropout_p >= 0.f && dropout_p <= 1.f, "attention dropout p %g not in [0, 1]", (double)dropout_p);
   return LZ_OK;
 }
 
 }  // namespace
 
-// Attention with an explicit mask instead of the causal one (SDPA's
-// attn_mask with is_causal=False, model/llama.py:109-117): mask_kind 1 =
-// bool bytes (nonzero: the key takes part), 2 = fp32, 3 = bf16 (added to the
-// scaled scores); mstride = element strides of the mask over [B, H, S
-// (query), S (key)], 0 where it broadcasts.  A row whose keys are all masked
-// gives NaN, as the reference's softmax of an all -inf row does.  One wave
-// per query row (any head dim up to 256, bf16 or fp32).
-LZ_EXPORT int lz_attn_fwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
-                                 const void* mask, int mask_kind, const int64_t* mstride, void* o, int64_t ldo,
-                                 float* lse, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
-                                 int dtype, void* stream) {
+// Attention on the one-wave-per-row kernels with the options the tile paths
+// do not take (model/llama.py:109-117, F.scaled_dot_product_attention):
+//   - an explicit mask in place of the causal one (attn_mask with
+//     is_causal=False): mask_kind 1 = bool bytes (nonzero: the key takes
+//     part), 2 = fp32, 3 = bf16 (added to the scaled scores); mstride = its
+//     element strides over [B, H, S(query), S(key)], 0 where it broadcasts;
+//     mask_kind 0 = causal (mask and mstride ignored).  A row whose keys are
+//     all masked gives NaN, as the reference's softmax of an all -inf row does;
+//   - attention dropout (dropout_p): each probability kept with scale
+//     1/(1-p) by element ((b*H + h)*S + s)*S + kv of seed's stream (the
+//     stream lz_dropout uses), the normaliser summing them before dropout.
+// Any head dim up to 256, bf16 or fp32.
+LZ_EXPORT int lz_attn_fwd_general(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                  const void* mask, int mask_kind, const int64_t* mstride, float dropout_p,
+                                  uint64_t seed, void* o, int64_t ldo, float* lse, int64_t B, int64_t S, int64_t H,
+                                  int64_t KV, int64_t hd, float scale, int dtype, void* stream) {
   int rc = check_shape(B, S, H, KV, hd);
   if (rc) return rc;
-  rc = check_mask(mask, mask_kind, mstride);
+  rc = check_general(mask, mask_kind, mstride, dropout_p);
   if (rc) return rc;
-  LZ_REQUIRE(q && k && v && o && lse, "lz_attn_fwd_masked: null pointer");
+  LZ_REQUIRE(q && k && v && o && lse, "lz_attn_fwd_general: null pointer");
   hipStream_t s = lz_stream(stream);
   const unsigned grid = (unsigned)lz_cdiv(B * H * S, 4);
   if (dtype == LZ_BF16) {
     GenArgs<uint16_t> a{};
-    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
     a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
     attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
-    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
     a.o = (float*)o; a.ldo = ldo; a.lse = lse;
     attn_fwd_generic_kernel<float><<<grid, 256, 0, s>>>(a);
   } else {
-    return lz_set_error(LZ_EINVAL, "lz_attn_fwd_masked: bad dtype %d", dtype);
+    return lz_set_error(LZ_EINVAL, "lz_attn_fwd_general: bad dtype %d", dtype);
   }
-  return lz_check_launch("lz_attn_fwd_masked");
+  return lz_check_launch("lz_attn_fwd_general");
 }
 
-// Backward of lz_attn_fwd_masked (same mask); delta from lz_attn_delta.
-LZ_EXPORT int lz_attn_bwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
-                                 const void* dout, int64_t lddo, const float* lse, const float* delta,
-                                 const void* mask, int mask_kind, const int64_t* mstride, void* dq, int64_t lddq,
-                                 void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S, int64_t H,
-                                 int64_t KV, int64_t hd, float scale, int dtype, void* stream) {
+// Backward of lz_attn_fwd_general (same mask, dropout p and seed); delta
+// from lz_attn_delta.
+LZ_EXPORT int lz_attn_bwd_general(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                  const void* dout, int64_t lddo, const float* lse, const float* delta,
+                                  const void* mask, int mask_kind, const int64_t* mstride, float dropout_p,
+                                  uint64_t seed, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
+                                  int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
+                                  int dtype, void* stream) {
   int rc = check_shape(B, S, H, KV, hd);
   if (rc) return rc;
-  rc = check_mask(mask, mask_kind, mstride);
+  rc = check_general(mask, mask_kind, mstride, dropout_p);
   if (rc) return rc;
-  LZ_REQUIRE(q && k && v && dout && lse && delta && dq && dk && dv, "lz_attn_bwd_masked: null pointer");
+  LZ_REQUIRE(q && k && v && dout && lse && delta && dq && dk && dv, "lz_attn_bwd_general: null pointer");
   hipStream_t s = lz_stream(stream);
   const unsigned grid_q = (unsigned)lz_cdiv(B * H * S, 4);
   const unsigned grid_kv = (unsigned)lz_cdiv(B * KV * S, 4);
   if (dtype == LZ_BF16) {
     GenArgs<uint16_t> a{};
-    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
     a.lse = const_cast<float*>(lse); a.dout = (const uint16_t*)dout; a.lddo = lddo; a.delta = delta;
     a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
     attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
     attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
-    masked_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, B, S, H, KV, hd, scale);
+    general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
     a.lse = const_cast<float*>(lse); a.dout = (const float*)dout; a.lddo = lddo; a.delta = delta;
     a.dq = (float*)dq; a.dk = (float*)dk; a.dv = (float*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
     attn_bwd_dq_generic_kernel<float><<<grid_q, 256, 0, s>>>(a);
     attn_bwd_dkdv_generic_kernel<float><<<grid_kv, 256, 0, s>>>(a);
   } else {
-    return lz_set_error(LZ_EINVAL, "lz_attn_bwd_masked: bad dtype %d", dtype);
+    return lz_set_error(LZ_EINVAL, "lz_attn_bwd_general: bad dtype %d", dtype);
   }
-  return lz_check_launch("lz_attn_bwd_masked");
+  return lz_check_launch("lz_attn_bwd_general");
 }

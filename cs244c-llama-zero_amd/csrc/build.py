@@ -21,6 +21,7 @@ OUT_LIB = PKG / "lzhip" / "libllamazero_hip.so"
 
 SOURCES = [
     "runtime.hip",
+    "dropout.hip",
     "optim.hip",
     "norm.hip",
     "rope.hip",

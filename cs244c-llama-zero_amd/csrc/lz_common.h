@@ -106,6 +106,24 @@ __device__ __forceinline__ void dma_barrier() {
   __syncthreads();
 }
 
+// Dropout's counter-based random stream: element i of a stream with seed s
+// is the i-th output of SplitMix64 (Steele, Lea and Flood, "Fast Splittable
+// Pseudorandom Number Generators", OOPSLA 2014) started at s, i.e. its
+// finalizer applied to s + (i + 1) * gamma.  The top 24 bits are a uniform
+// draw u in [0, 2^24); the element is kept when u >= thresh, thresh =
+// ceil(p * 2^24).  Any element's draw is computed on its own, so forward and
+// backward regenerate the same mask from (seed, index) without storing it.
+__device__ __forceinline__ uint64_t lz_splitmix64(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ bool lz_keep(uint64_t seed, uint64_t i, uint32_t thresh) {
+  return (uint32_t)(lz_splitmix64(seed, i) >> 40) >= thresh;
+}
+
 // Rounds a float to the nearest bfloat16 value, kept as float.
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 

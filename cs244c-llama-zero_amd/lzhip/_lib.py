@@ -25,6 +25,7 @@ _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
 _f64 = ctypes.c_double
+_u64 = ctypes.c_uint64
 
 # name -> (restype, argtypes); the order of arguments follows the header.
 SIGNATURES = {
@@ -83,17 +84,22 @@ SIGNATURES = {
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     ),
     "lz_attn_delta": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
-    "lz_attn_fwd_masked": (
-        _i32,
-        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
-    ),
-    "lz_attn_bwd_masked": (
+    "lz_attn_fwd_general": (
         _i32,
         [
-            _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
-            _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
+            _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _f32, _u64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+            _i64, _f32, _i32, _vp,
         ],
     ),
+    "lz_attn_bwd_general": (
+        _i32,
+        [
+            _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _vp, _f32, _u64, _vp, _i64, _vp, _i64,
+            _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
+        ],
+    ),
+    "lz_dropout": (_i32, [_vp, _vp, _i64, _f32, _u64, _i32, _vp]),
+    "lz_dropout_mask": (_i32, [_vp, _i64, _f32, _u64, _vp]),
     "lz_attn_bwd": (
         _i32,
         [

@@ -316,10 +316,13 @@ class AttnProjFn(Function):
     """Fused QKV projection + RoPE + causal GQA flash attention
     (model/llama.py:95-117).  Input h [B, S, d] (the normed residual stream),
     weights Wq [H*hd, d], Wk/Wv [KV*hd, d]; returns the attention output
-    [B, S, H*hd] that o_proj consumes."""
+    [B, S, H*hd] that o_proj consumes.  mask: SDPA's attn_mask in place of
+    the causal mask; dropout_p > 0: attention dropout with the stream key
+    `seed` (both on the one-wave-per-row kernels)."""
 
     @staticmethod
-    def forward(ctx, h, wq, wk, wv, cos, sin, n_heads: int, n_kv: int, scale: float, mask=None):
+    def forward(ctx, h, wq, wk, wv, cos, sin, n_heads: int, n_kv: int, scale: float, mask=None,
+                dropout_p: float = 0.0, seed: int = 0):
         B, S, d = h.shape
         hd = wq.shape[0] // n_heads
         h2 = _rows(h)
@@ -335,8 +338,9 @@ class AttnProjFn(Function):
         k2 = qkv[:, H * hd : (H + KV) * hd]
         v2 = qkv[:, (H + KV) * hd :]
         ld = qkv.shape[1]
-        if mask is not None:  # an explicit mask (SDPA attn_mask) replaces the causal one
-            o, lse = ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, scale, mask)
+        general = mask is not None or dropout_p > 0.0
+        if general:
+            o, lse = ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, scale, mask, dropout_p, seed)
         else:
             vt = None
             if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, H * hd) == 1:
@@ -344,6 +348,7 @@ class AttnProjFn(Function):
             o, lse = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, scale, vt)
         ctx.save_for_backward(h2, wq, wk, wv, qkv, o, lse, cos, sin)
         ctx.mask = mask
+        ctx.general = (general, dropout_p, seed)
         ctx.meta = (B, S, H, KV, hd, scale)
         return o.view(B, S, H * hd)
 
@@ -356,8 +361,10 @@ class AttnProjFn(Function):
         dqkv = torch.empty_like(qkv)
         q2, k2, v2 = qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :]
         dq2, dk2, dv2 = dqkv[:, : H * hd], dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :]
-        if ctx.mask is not None:
-            ops.attn_bwd_masked(q2, k2, v2, o, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, ctx.mask)
+        general, dropout_p, seed = ctx.general
+        if general:
+            ops.attn_bwd_general(q2, k2, v2, o, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, ctx.mask,
+                                 dropout_p, seed)
         else:
             qt = kt = dot = None
             if ops.attn_path(qkv.dtype, S, hd, ld, ld, ld, do2.stride(0)) == 1:
@@ -378,16 +385,18 @@ class AttnProjFn(Function):
             nq, nk = wq.shape[0], wk.shape[0]
             dwq, dwk, dwv = dw[:nq], dw[nq : nq + nk], dw[nq + nk :]
         dh = dh2.view(B, S, -1) if dh2 is not None else None
-        return dh, dwq, dwk, dwv, None, None, None, None, None, None
+        return dh, dwq, dwk, dwv, None, None, None, None, None, None, None, None
 
 
 class MLPFn(Function):
     """SwiGLU MLP (model/llama.py:136-146): down(silu(gate x) * up x), gate and
     up as one GEMM, with an optional residual added in the down projection's
-    epilogue."""
+    epilogue.  dropout_p > 0: the gated activations pass through dropout
+    (model/llama.py:146) with the stream key `seed` before the down
+    projection."""
 
     @staticmethod
-    def forward(ctx, x, wg, wu, wd, residual, grad_wanted=True):
+    def forward(ctx, x, wg, wu, wd, residual, grad_wanted=True, dropout_p: float = 0.0, seed: int = 0):
         x2 = _rows(x)
         F_ = wg.shape[0]
         w = fused_weight([wg, wu])
@@ -399,6 +408,9 @@ class MLPFn(Function):
         else:
             gu = _linear_fwd(x2, w)                 # [T, 2F]
             m = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
+        if dropout_p > 0.0:
+            ops.dropout_(m, dropout_p, seed)  # the saved m is the dropped-out input of down_proj
+        ctx.dropout = (dropout_p, seed)
         r2 = _rows(residual) if residual is not None else None
         y = _linear_fwd(m, wd, r2)
         if grad_wanted:
@@ -413,6 +425,9 @@ class MLPFn(Function):
         F_ = wg.shape[0]
         dy2 = _rows(dy)
         dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3], [wd])
+        dropout_p, seed = ctx.dropout
+        if dropout_p > 0.0:
+            ops.dropout_(dm, dropout_p, seed)  # the forward's keep mask and scale
         dgu = torch.empty_like(gu)
         ops.swiglu_bwd(gu[:, :F_], gu[:, F_:], dm, dgu[:, :F_], dgu[:, F_:])
         w = fused_weight([wg, wu])
@@ -423,7 +438,34 @@ class MLPFn(Function):
             dwg, dwu = dw[:F_], dw[F_:]
         dx = dx2.view(ctx.in_shape) if dx2 is not None else None
         dres = dy if (ctx.has_residual and ctx.needs_input_grad[4]) else None
-        return dx, dwg, dwu, dwd, dres, None
+        return dx, dwg, dwu, dwd, dres, None, None, None
+
+
+class DropoutFn(Function):
+    """nn.Dropout in training mode (model/llama.py:175,213 on the token
+    embeddings): x * keep / (1 - p) with the keep mask of the stream key
+    `seed`; the backward regenerates the mask instead of storing it."""
+
+    @staticmethod
+    def forward(ctx, x, p: float, seed: int):
+        xc = x.contiguous()
+        y = ops.dropout_(xc, p, seed, out=torch.empty_like(xc))
+        ctx.p, ctx.seed = p, seed
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        g = dy.contiguous()
+        return ops.dropout_(g, ctx.p, ctx.seed, out=torch.empty_like(g)), None, None
+
+
+def dropout(x: torch.Tensor, p: float, training: bool = True) -> torch.Tensor:
+    """F.dropout on the HIP kernel (identity when not training or p == 0)."""
+    if not training or p == 0.0:
+        return x
+    if not 0.0 <= p <= 1.0:
+        raise ValueError(f"dropout probability has to be between 0 and 1, but got {p}")
+    return DropoutFn.apply(x, float(p), ops.dropout_seed(x.device))
 
 
 class SwiGLUPointwiseFn(Function):

@@ -873,29 +873,91 @@ def _attn_mask_args(mask: torch.Tensor, B: int, H: int, S: int):
     return kinds[mask.dtype], (ctypes.c_int64 * 4)(*strides)
 
 
-def attn_fwd_masked(q2, k2, v2, B: int, S: int, H: int, KV: int, hd: int, scale: float, mask: torch.Tensor):
-    """attn_fwd with an explicit mask in place of the causal one; returns o,
-    lse."""
+def attn_fwd_general(q2, k2, v2, B: int, S: int, H: int, KV: int, hd: int, scale: float,
+                     mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0, seed: int = 0):
+    """attn_fwd on the one-wave-per-row kernels, with an explicit mask in
+    place of the causal one (mask=None: causal) and/or attention dropout
+    (dropout_p with seed, see dropout_seed); returns o, lse."""
     require_gpu(q2, k2, v2)
-    kind, st = _attn_mask_args(mask, B, H, S)
+    kind, st = _attn_mask_args(mask, B, H, S) if mask is not None else (0, None)
     o = torch.empty((B * S, H * hd), dtype=q2.dtype, device=q2.device)
     lse = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
-    _lib.call("lz_attn_fwd_masked", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
-              _row_stride(v2), mask.data_ptr(), kind, ctypes.addressof(st), o.data_ptr(), H * hd, lse.data_ptr(), B, S,
-              H, KV, hd, float(scale), dtype_code(q2), stream_ptr(q2.device))
+    _lib.call("lz_attn_fwd_general", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
+              _row_stride(v2), _ptr(mask), kind, ctypes.addressof(st) if st is not None else None, float(dropout_p),
+              int(seed), o.data_ptr(), H * hd, lse.data_ptr(), B, S, H, KV, hd, float(scale), dtype_code(q2),
+              stream_ptr(q2.device))
     return o, lse
 
 
-def attn_bwd_masked(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, mask: torch.Tensor) -> None:
+def attn_bwd_general(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2,
+                     mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0, seed: int = 0) -> None:
+    """Backward of attn_fwd_general with the forward's mask, dropout_p and
+    seed."""
     require_gpu(q2, k2, v2, o2, do2, lse, dq2, dk2, dv2)
-    kind, st = _attn_mask_args(mask, B, H, S)
+    kind, st = _attn_mask_args(mask, B, H, S) if mask is not None else (0, None)
     delta = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
     _lib.call("lz_attn_delta", o2.data_ptr(), _row_stride(o2), do2.data_ptr(), _row_stride(do2), delta.data_ptr(),
               B, S, H, hd, dtype_code(o2), stream_ptr(q2.device))
-    _lib.call("lz_attn_bwd_masked", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
-              _row_stride(v2), do2.data_ptr(), _row_stride(do2), lse.data_ptr(), delta.data_ptr(), mask.data_ptr(),
-              kind, ctypes.addressof(st), dq2.data_ptr(), _row_stride(dq2), dk2.data_ptr(), _row_stride(dk2),
-              dv2.data_ptr(), _row_stride(dv2), B, S, H, KV, hd, float(scale), dtype_code(q2), stream_ptr(q2.device))
+    _lib.call("lz_attn_bwd_general", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),
+              _row_stride(v2), do2.data_ptr(), _row_stride(do2), lse.data_ptr(), delta.data_ptr(), _ptr(mask), kind,
+              ctypes.addressof(st) if st is not None else None, float(dropout_p), int(seed), dq2.data_ptr(),
+              _row_stride(dq2), dk2.data_ptr(), _row_stride(dk2), dv2.data_ptr(), _row_stride(dv2), B, S, H, KV, hd,
+              float(scale), dtype_code(q2), stream_ptr(q2.device))
+
+
+_MASK64 = (1 << 64) - 1
+
+
+def _mix64(z: int) -> int:
+    """SplitMix64's output function (Steele, Lea & Flood, OOPSLA 2014)."""
+    z &= _MASK64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _MASK64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _MASK64
+    return z ^ (z >> 31)
+
+
+def dropout_seed(device: torch.device) -> int:
+    """The stream key of one dropout call, drawn from the device's torch
+    generator as torch's own GPU dropout draws its Philox (seed, offset):
+    the key mixes the generator's seed and offset, and the offset advances
+    by 4.  torch.manual_seed, torch.cuda.set_rng_state and the activation
+    checkpoint's RNG replay therefore replay the masks."""
+    if device.type != "cuda":
+        raise RuntimeError(f"lzhip dropout needs a GPU tensor (got device {device})")
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    gen = torch.cuda.default_generators[idx]
+    off = int(gen.get_offset())
+    gen.set_offset(off + 4)
+    return dropout_key(int(gen.initial_seed()), off)
+
+
+def dropout_key(seed: int, offset: int) -> int:
+    return _mix64((seed & _MASK64) ^ _mix64(offset + 0x9E3779B97F4A7C15))
+
+
+def dropout_(x: torch.Tensor, p: float, seed: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = x * keep / (1 - p) (out=None: in place), keep from (seed, flat
+    element index); the same call with the same seed is its backward."""
+    require_gpu(x, out)
+    if not x.is_contiguous():
+        raise ValueError("dropout_: x must be contiguous")
+    y = x if out is None else out
+    if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
+        raise ValueError("dropout_: out must be a contiguous tensor of x's shape and dtype")
+    if not 0.0 <= p <= 1.0:
+        raise ValueError(f"dropout probability has to be between 0 and 1, but got {p}")
+    _lib.call("lz_dropout", x.data_ptr(), y.data_ptr(), x.numel(), float(p), int(seed), dtype_code(x),
+              stream_ptr(x.device))
+    return y
+
+
+def dropout_mask(n: int, p: float, seed: int, device: torch.device) -> torch.Tensor:
+    """The keep mask (uint8, 1 = kept) that dropout_ and attention dropout
+    use for elements 0..n-1 of seed's stream."""
+    keep = torch.empty(n, dtype=torch.uint8, device=device)
+    require_gpu(keep)
+    _lib.call("lz_dropout_mask", keep.data_ptr(), n, float(p), int(seed), stream_ptr(keep.device))
+    return keep
 
 
 def attn_bwd(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt=None, kt=None, dot=None,

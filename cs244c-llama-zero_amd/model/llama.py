@@ -24,13 +24,6 @@ from lzhip import ops
 from .config import ModelConfig
 
 
-def _no_dropout(p: float, training: bool, where: str) -> None:
-    if training and p > 0.0:
-        raise NotImplementedError(
-            f"{where}: dropout {p} in training mode is not implemented by the HIP kernels (use dropout=0.0)"
-        )
-
-
 class HipLinear(nn.Linear):
     """nn.Linear (same parameters, initialisation and state_dict) whose
     forward is the MFMA GEMM; bias is not supported (the model has none)."""
@@ -159,15 +152,17 @@ class GroupedQueryAttention(nn.Module):
     ) -> torch.Tensor:
         """GQA (model/llama.py:95-133): causal, or with `attention_mask` in its
         place (SDPA's attn_mask: bool keeps where True, a float mask is added
-        to the scaled scores; broadcastable to [B, H, S, S]); `residual`
-        (optional) is added inside the o_proj GEMM."""
-        _no_dropout(self.dropout, self.training, "attention")
+        to the scaled scores; broadcastable to [B, H, S, S]); attention
+        dropout with p = cfg.dropout in training mode (model/llama.py:107);
+        `residual` (optional) is added inside the o_proj GEMM."""
         ops.require_gpu(x)
         bsz, seq_len, _ = x.shape
         cos, sin = self.rotary.tables(seq_len, x.device, x.dtype)
+        attn_dropout = float(self.dropout) if self.training else 0.0
+        seed = ops.dropout_seed(x.device) if attn_dropout > 0.0 else 0
         y = LF.AttnProjFn.apply(
             x, self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, cos, sin,
-            self.n_heads, self.n_kv_heads, float(self.scale), attention_mask,
+            self.n_heads, self.n_kv_heads, float(self.scale), attention_mask, attn_dropout, seed,
         )
         return self.o_proj(y, residual)
 
@@ -181,9 +176,11 @@ class SwiGLU(nn.Module):
         self.dropout = nn.Dropout(cfg.dropout)
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
-        _no_dropout(self.dropout.p, self.training, "mlp")
+        ops.require_gpu(x)
+        p = float(self.dropout.p) if self.training else 0.0  # nn.Dropout on the gated activations
+        seed = ops.dropout_seed(x.device) if p > 0.0 else 0
         return LF.MLPFn.apply(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight, residual,
-                              torch.is_grad_enabled())
+                              torch.is_grad_enabled(), p, seed)
 
 
 class TransformerBlock(nn.Module):
@@ -255,7 +252,7 @@ class LlamaForCausalLM(nn.Module):
             raise ValueError(f"input_ids should have shape [batch, seq], got {tuple(input_ids.shape)}")
 
         x = self._call_parametrized_module("tok_embeddings", self.tok_embeddings, input_ids)
-        _no_dropout(self.dropout.p, self.training, "embedding")
+        x = LF.dropout(x, float(self.dropout.p), self.training)
 
         for layer_idx in range(len(self.layers)):
             if self._should_checkpoint_activations(x):

@@ -274,26 +274,44 @@ int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_t lddo, fl
  * are returned as the gradients of q and k before RoPE (model/llama.py:35-39
  * backward), folded into the bf16 MFMA kernels' stores or, on the other
  * paths, applied by lz_rope afterwards. */
-/* Attention with an explicit mask in place of the causal one
- * (model/llama.py:109-117: F.scaled_dot_product_attention(attn_mask=mask,
- * is_causal=False)): mask_kind 1 = bool bytes (nonzero: the key takes part),
- * 2 = fp32, 3 = bf16 (added to the scaled scores); mstride = 4 element
- * strides over [B, H, S(query), S(key)], 0 where the mask broadcasts.  A
- * query row whose keys are all masked gives NaN, as the reference's softmax
- * does.  Any head dim up to 256, bf16 or fp32, one wave per row. */
-int lz_attn_fwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
-                       const void* mask, int mask_kind, const int64_t* mstride, void* o, int64_t ldo, float* lse,
-                       int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale, int dtype, void* stream);
-int lz_attn_bwd_masked(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
-                       const void* dout, int64_t lddo, const float* lse, const float* delta, const void* mask,
-                       int mask_kind, const int64_t* mstride, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv,
-                       int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale, int dtype,
-                       void* stream);
+/* Attention on the one-wave-per-row kernels with the options the MFMA tile
+ * paths do not take (model/llama.py:105-117, F.scaled_dot_product_attention):
+ *  - an explicit mask in place of the causal one (attn_mask with
+ *    is_causal=False): mask_kind 1 = bool bytes (nonzero: the key takes
+ *    part), 2 = fp32, 3 = bf16 (added to the scaled scores); mstride = 4
+ *    element strides over [B, H, S(query), S(key)], 0 where the mask
+ *    broadcasts; mask_kind 0 = causal (mask, mstride ignored).  A query row
+ *    whose keys are all masked gives NaN, as the reference's softmax does;
+ *  - attention dropout (dropout_p, model/llama.py:107,115): probability
+ *    (b, h, s, kv) is kept, scaled by 1/(1-p), when element
+ *    ((b*H + h)*S + s)*S + kv of seed's keep stream (lz_dropout_mask) is 1.
+ * Any head dim up to 256, bf16 or fp32.  The backward takes the forward's
+ * mask, dropout_p and seed; delta from lz_attn_delta. */
+int lz_attn_fwd_general(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                        const void* mask, int mask_kind, const int64_t* mstride, float dropout_p, uint64_t seed,
+                        void* o, int64_t ldo, float* lse, int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd,
+                        float scale, int dtype, void* stream);
+int lz_attn_bwd_general(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                        const void* dout, int64_t lddo, const float* lse, const float* delta, const void* mask,
+                        int mask_kind, const int64_t* mstride, float dropout_p, uint64_t seed, void* dq, int64_t lddq,
+                        void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S, int64_t H, int64_t KV,
+                        int64_t hd, float scale, int dtype, void* stream);
 int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
                 int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
                 void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
                 int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin, int dtype,
                 void* stream);
+
+/* ---- dropout (model/llama.py:142,146 on the MLP's gated activations and
+ * :175,213 on the token embeddings: nn.Dropout in training mode) ----
+ * y = x * keep / (1 - p) over n contiguous elements (x == y allowed).  The
+ * keep mask is not stored: element i is kept when the top 24 bits of
+ * SplitMix64(seed, i) are >= ceil(p * 2^24), so the backward is the same
+ * call on the gradient with the same seed, and a recompute that replays the
+ * seed replays the mask.  p in [0, 1]; p == 1 zeroes y.  dtype LZ_BF16 or
+ * LZ_F32.  lz_dropout_mask writes that keep mask (1 byte per element). */
+int lz_dropout(const void* x, void* y, int64_t n, float p, uint64_t seed, int dtype, void* stream);
+int lz_dropout_mask(uint8_t* keep, int64_t n, float p, uint64_t seed, void* stream);
 
 #ifdef __cplusplus
 }

@@ -127,8 +127,11 @@ def lm_head_weight(P: Dict[str, torch.Tensor], cfg: Cfg) -> torch.Tensor:
     return P["tok_embeddings.weight"] if cfg.tie_word_embeddings else P["lm_head.weight"]
 
 
-def block_forward(P: Dict[str, torch.Tensor], cfg: Cfg, i: int, x: torch.Tensor, attn_impl: str = "sdpa") -> torch.Tensor:
-    """model/llama.py:149-160 with GroupedQueryAttention (:95-133) and SwiGLU (:143-146)."""
+def block_forward(P: Dict[str, torch.Tensor], cfg: Cfg, i: int, x: torch.Tensor, attn_impl: str = "sdpa",
+                  drop: Optional[Dict] = None) -> torch.Tensor:
+    """model/llama.py:149-160 with GroupedQueryAttention (:95-133) and SwiGLU
+    (:143-146).  drop (training-mode dropout given its keep masks): {"p": p,
+    (i, "attn"): keep [B, H, S, S], (i, "mlp"): keep [B, S, ffn]}."""
     p = f"layers.{i}."
     B, S, d = x.shape
     H, KV, hd = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
@@ -139,7 +142,9 @@ def block_forward(P: Dict[str, torch.Tensor], cfg: Cfg, i: int, x: torch.Tensor,
     cos, sin = ops.rope_tables(S, hd, cfg.rope_theta, dtype=q.dtype, angle_dtype=cfg.rope_angle_dtype)
     q = ops.apply_rope(q, cos, sin)
     k = ops.apply_rope(k, cos, sin)
-    if attn_impl == "sdpa":
+    if drop is not None:
+        y = ops.causal_gqa_attention(q, k, v, dropout_keep=drop[(i, "attn")], dropout_p=drop["p"])
+    elif attn_impl == "sdpa":
         if H != KV:
             k = k.repeat_interleave(H // KV, dim=1)
             v = v.repeat_interleave(H // KV, dim=1)
@@ -151,13 +156,21 @@ def block_forward(P: Dict[str, torch.Tensor], cfg: Cfg, i: int, x: torch.Tensor,
     h2 = ops.rmsnorm(x, P[p + "post_attn_norm.weight"], cfg.rms_norm_eps)
     g = h2 @ P[p + "mlp.gate_proj.weight"].t()
     u = h2 @ P[p + "mlp.up_proj.weight"].t()
-    return x + ops.swiglu(g, u) @ P[p + "mlp.down_proj.weight"].t()
+    m = ops.swiglu(g, u)
+    if drop is not None:
+        m = ops.dropout(m, drop[(i, "mlp")], drop["p"])
+    return x + m @ P[p + "mlp.down_proj.weight"].t()
 
 
-def hidden_states(P: Dict[str, torch.Tensor], cfg: Cfg, ids: torch.Tensor, attn_impl: str = "sdpa") -> torch.Tensor:
+def hidden_states(P: Dict[str, torch.Tensor], cfg: Cfg, ids: torch.Tensor, attn_impl: str = "sdpa",
+                  drop: Optional[Dict] = None) -> torch.Tensor:
+    """drop: see block_forward; its "embed" entry ([B, S, dim]) is the token
+    embeddings' dropout (model/llama.py:212-213)."""
     x = P["tok_embeddings.weight"][ids]
+    if drop is not None:
+        x = ops.dropout(x, drop["embed"], drop["p"])
     for i in range(cfg.n_layers):
-        x = block_forward(P, cfg, i, x, attn_impl)
+        x = block_forward(P, cfg, i, x, attn_impl, drop)
     return ops.rmsnorm(x, P["norm.weight"], cfg.rms_norm_eps)
 
 
@@ -166,12 +179,12 @@ def logits(P: Dict[str, torch.Tensor], cfg: Cfg, ids: torch.Tensor, attn_impl: s
 
 
 def loss(P: Dict[str, torch.Tensor], cfg: Cfg, ids: torch.Tensor, labels: Optional[torch.Tensor] = None,
-         chunk_size: int = 0, attn_impl: str = "sdpa") -> torch.Tensor:
+         chunk_size: int = 0, attn_impl: str = "sdpa", drop: Optional[Dict] = None) -> torch.Tensor:
     """Training loss: full mean CE (chunk_size == 0, model/llama.py:273-280) or
     the chunked sum/max(count,1) computed chunk by chunk with F.cross_entropy
     (model/llama.py:282-302)."""
     labels = ids if labels is None else labels
-    x = hidden_states(P, cfg, ids, attn_impl)
+    x = hidden_states(P, cfg, ids, attn_impl, drop)
     W = lm_head_weight(P, cfg)
     S = x.size(1)
     if chunk_size <= 0:

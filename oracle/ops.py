@@ -8,6 +8,7 @@ from __future__ import annotations
 import math
 from typing import Optional, Tuple
 
+import numpy as np
 import torch
 
 
@@ -48,13 +49,16 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 
 
 def causal_gqa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
-                         attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         attn_mask: Optional[torch.Tensor] = None, dropout_keep: Optional[torch.Tensor] = None,
+                         dropout_p: float = 0.0) -> torch.Tensor:
     """model/llama.py:88-117 with is_causal=True: q [B,H,S,hd], k/v [B,KV,S,hd];
     K/V heads repeated (repeat_interleave) to H, softmax(q k^T * scale) v with
     the upper triangle masked.  Written out explicitly (no fused kernel).
     With attn_mask (model/llama.py:109-117, is_causal=False): a bool mask
     keeps the scores where True, a float mask is added to the scaled scores
-    (the reference's fallback branch, llama.py:118-129)."""
+    (the reference's fallback branch, llama.py:118-129).  With dropout_keep
+    ([B, H, S, S], nonzero = kept): probs * keep / (1 - dropout_p) before
+    the product with v (llama.py:115 dropout_p, :129 F.dropout(probs))."""
     B, H, S, hd = q.shape
     KV = k.shape[1]
     if H != KV:
@@ -70,7 +74,43 @@ def causal_gqa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scal
     else:
         scores = scores + attn_mask.to(scores.dtype)
     probs = torch.softmax(scores, dim=-1)
+    if dropout_keep is not None:
+        probs = dropout(probs, dropout_keep, dropout_p)
     return torch.matmul(probs, v)
+
+
+def dropout(x: torch.Tensor, keep: torch.Tensor, p: float) -> torch.Tensor:
+    """nn.Dropout in training mode given its keep mask (model/llama.py:146,
+    :213): x * keep / (1 - p); p == 1 gives zeros."""
+    if p >= 1.0:
+        return x * 0.0
+    return x * keep.to(x.dtype) * (1.0 / (1.0 - p))
+
+
+_GAMMA = 0x9E3779B97F4A7C15
+
+
+def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """Outputs start .. start+n-1 of SplitMix64 with state `seed` (Steele,
+    Lea & Flood, "Fast splittable pseudorandom number generators", OOPSLA
+    2014; the constants of Vigna's public-domain splitmix64.c): output i is
+    mix(seed + (i + 1) * 0x9E3779B97F4A7C15) with mix(z) = z ^ z >> 31 after
+    z = (z ^ z >> 30) * 0xBF58476D1CE4E5B9, z = (z ^ z >> 27) *
+    0x94D049BB133111EB, all modulo 2^64 (numpy uint64 wraps)."""
+    i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & (2**64 - 1)) + i * np.uint64(_GAMMA)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def dropout_keep(seed: int, n: int, p: float) -> np.ndarray:
+    """The keep mask of elements 0..n-1 of the dropout stream with key
+    `seed`: kept when the top 24 bits of SplitMix64 output i are >= ceil(p *
+    2^24), so P(keep) = 1 - p to 2^-24 (bool array)."""
+    thresh = min(math.ceil(p * 16777216.0), 16777216)
+    return (splitmix64(seed, n) >> np.uint64(40)) >= np.uint64(thresh)
 
 
 def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:

@@ -138,6 +138,43 @@ def test_stage3_matches_stage0_training():
 
 
 @pytest.mark.parametrize("recompute", [True, False])
+def test_stage3_matches_stage0_with_dropout(recompute):
+    """zero/tests/test_zero_stages.py:195-271 at world size 1: dropout 0.2,
+    torch.manual_seed before each forward; the stage-3 executor (its
+    recompute restores the RNG state, so the masks replay) trains like
+    stage 0: equal first-step losses, and losses and parameters within the
+    bf16 bar after that."""
+    kw = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01)
+    m0, m3 = _model(4321, dropout=0.2), _model(4321, dropout=0.2)
+    e0 = ZeROStage0DDP(model=m0, **kw)
+    e3 = ZeROStage3Optimizer(model=m3, recompute=recompute, **kw)
+    nodrop = float(m0.eval()(input_ids=_batch(0), labels=_batch(0)).loss)
+    for step in range(2):
+        ids = _batch(step)
+        seed = 10_000 + step * 31
+        losses = []
+        for m, e in ((m0, e0), (m3, e3)):
+            m.train()
+            e.zero_grad()
+            e.prepare_forward()
+            torch.manual_seed(seed)
+            loss = m(input_ids=ids, labels=ids).loss
+            e.backward(loss)
+            e.step()
+            losses.append(float(loss))
+        # step 0 starts from equal weights; after it the engines' updates
+        # differ in rounding (stage 0 sums the tied weight's two gradient
+        # contributions in bf16, stage 3 in fp32)
+        assert abs(losses[0] - losses[1]) <= (1e-6 if step == 0 else 1e-2) * abs(losses[0]), (step, losses)
+        if step == 0:
+            assert nodrop != losses[0]  # dropout was applied
+    p0, p3 = _full_params(e0, m0), _full_params(e3, m3)
+    for n in p0:
+        rel = float((p0[n] - p3[n]).norm() / p0[n].norm())
+        assert rel < 2e-2, (n, rel)
+
+
+@pytest.mark.parametrize("recompute", [True, False])
 def test_stage3_executor_gradients_match_stage0(recompute):
     """The stage-3 executor (_ShardedModuleFunction: no-grad forward, then
     recompute or the kept graph, autograd.grad per module call, bucketed

@@ -9,6 +9,8 @@ buffer.
 """
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -215,3 +217,94 @@ def test_model_with_attention_mask(stage3):
     l2, g2 = run(pad)
     assert torch.isfinite(torch.tensor(l2)) and abs(l2 - l0) > 1e-4
     assert bool(torch.isfinite(g2).all())
+
+
+def _record_dropout_keys(monkeypatch):
+    """Records the stream key of every dropout call the model makes."""
+    from lzhip import ops
+
+    keys = []
+    draw = ops.dropout_seed
+
+    def recording(device):
+        k = draw(device)
+        keys.append(k)
+        return k
+
+    monkeypatch.setattr(ops, "dropout_seed", recording)
+    return keys
+
+
+def _oracle_drop(cfg: ModelConfig, keys, B: int, S: int):
+    """The keep masks the model's dropout calls used, in call order: token
+    embeddings, then per layer attention probabilities and MLP activations."""
+    from lzhip import ops
+
+    p = cfg.dropout
+    assert len(keys) == 1 + 2 * cfg.n_layers
+    mask = lambda k, shape: ops.dropout_mask(math.prod(shape), p, k, DEV).cpu().view(shape).bool()
+    drop = {"p": p, "embed": mask(keys[0], (B, S, cfg.dim))}
+    for i in range(cfg.n_layers):
+        drop[(i, "attn")] = mask(keys[1 + 2 * i], (B, cfg.n_heads, S, S))
+        drop[(i, "mlp")] = mask(keys[2 + 2 * i], (B, S, cfg.ffn_dim))
+    return drop
+
+
+@pytest.mark.parametrize("dim,H,KV,S", [(128, 4, 2, 64), (256, 4, 2, 96)])
+def test_model_dropout_vs_oracle(monkeypatch, dim, H, KV, S):
+    """Training-mode dropout (model/llama.py:107-115 attention, :146 MLP,
+    :213 embeddings) against the float64 oracle given the keep masks the
+    model's calls drew: loss within 1e-2, gradients cosine >= 0.999."""
+    cfg = ModelConfig(name="drop", vocab_size=300, max_seq_len=S, dim=dim, n_layers=2, n_heads=H, n_kv_heads=KV,
+                      ffn_dim=2 * dim, rope_theta=10_000.0, dropout=0.2)
+    torch.manual_seed(dim + S)
+    model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
+    model.train()
+    P = _oracle_params(model)
+    B = 2
+    ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(S))
+    keys = _record_dropout_keys(monkeypatch)
+    out = model(input_ids=ids.to(DEV), labels=ids.to(DEV), return_logits=False)
+    out.loss.backward()
+    drop = _oracle_drop(cfg, keys, B, S)
+    ref = OM.loss(P, _ocfg(cfg), ids, drop=drop)
+    ref.backward()
+    assert abs(float(out.loss) - float(ref)) <= 1e-2 * abs(float(ref))
+    nodrop = OM.loss({k: v.detach() for k, v in P.items()}, _ocfg(cfg), ids)
+    assert abs(float(nodrop) - float(ref)) > 1e-4 * abs(float(ref))  # the masks matter
+    for name, prm in model.named_parameters():
+        cos = float(F.cosine_similarity(prm.grad.detach().double().cpu().view(-1), P[name].grad.view(-1), dim=0))
+        assert cos >= 0.999, (name, cos)
+
+
+def test_model_dropout_replay_and_eval():
+    """torch.manual_seed replays a dropout forward bit for bit, activation
+    checkpointing's recompute replays the masks (same loss bits, gradients
+    as without it), eval mode and dropout=0 skip dropout."""
+    kw = dict(name="drop", vocab_size=256, max_seq_len=128, dim=256, n_layers=3, n_heads=4, n_kv_heads=2,
+              ffn_dim=512, rope_theta=10_000.0)
+    torch.manual_seed(9)
+    m1 = LlamaForCausalLM(ModelConfig(dropout=0.1, **kw)).to(device=DEV, dtype=torch.bfloat16)
+    m2 = LlamaForCausalLM(ModelConfig(dropout=0.1, **kw)).to(device=DEV, dtype=torch.bfloat16)
+    m0 = LlamaForCausalLM(ModelConfig(dropout=0.0, **kw)).to(device=DEV, dtype=torch.bfloat16)
+    m2.load_state_dict(m1.state_dict())
+    m0.load_state_dict(m1.state_dict())
+    m2.set_activation_checkpointing(True)
+    ids = torch.randint(0, 256, (2, 128), generator=torch.Generator().manual_seed(3)).to(DEV)
+    torch.manual_seed(100)
+    l1 = m1(ids, labels=ids).loss
+    torch.manual_seed(100)
+    l2 = m2(ids, labels=ids).loss
+    assert float(l1) == float(l2)
+    l1.backward()
+    l2.backward()
+    for (n, p1), (_, p2) in zip(m1.named_parameters(), m2.named_parameters()):
+        assert torch.allclose(p1.grad.float(), p2.grad.float(), rtol=1e-2, atol=1e-4), n
+    torch.manual_seed(100)
+    again = m1(ids, labels=ids).loss
+    other = m1(ids, labels=ids).loss
+    base = m0(ids, labels=ids).loss
+    m1.eval()
+    ev = m1(ids, labels=ids).loss
+    assert float(again) == float(l1) and float(other) != float(l1)
+    assert float(ev) == float(base) and float(ev) != float(l1)

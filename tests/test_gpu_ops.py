@@ -477,7 +477,7 @@ def test_attention_with_explicit_mask_vs_oracle(kind, B, S, H, KV, hd, dtype):
     d = qkv.to(DEV)
     q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
     scale = hd**-0.5
-    o, lse = ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, scale, mask.to(DEV))
+    o, lse = ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, scale, mask.to(DEV))
 
     def heads(t, n):
         return t.double().view(B, S, n, hd).transpose(1, 2).requires_grad_(True)
@@ -489,7 +489,7 @@ def test_attention_with_explicit_mask_vs_oracle(kind, B, S, H, KV, hd, dtype):
     assert _rel_err(o.cpu().double().view(B, S, H, hd).transpose(1, 2), oref) < tol
     do = torch.randn(B * S, H * hd, generator=g).to(dtype)
     dqkv = torch.zeros_like(d)
-    ops.attn_bwd_masked(q2, k2, v2, o, do.to(DEV), lse, B, S, H, KV, hd, scale, dqkv[:, : H * hd],
+    ops.attn_bwd_general(q2, k2, v2, o, do.to(DEV), lse, B, S, H, KV, hd, scale, dqkv[:, : H * hd],
                         dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :], mask.to(DEV))
     oref.backward(do.double().view(B, S, H, hd).transpose(1, 2))
     dq = dqkv[:, : H * hd].cpu().double().view(B, S, H, hd).transpose(1, 2)
@@ -510,12 +510,113 @@ def test_attention_explicit_causal_mask_equals_causal():
     q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
     causal = ~torch.triu(torch.ones(S, S, dtype=torch.bool, device=DEV), 1)
     o1, l1 = ops.attn_fwd(q2, k2, v2, B, S, H, KV, hd, 0.125, None)
-    o2, l2 = ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, 0.125, causal)
+    o2, l2 = ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, 0.125, causal)
     assert _rel_err(o2, o1) < 1e-6 and _rel_err(l2, l1) < 1e-6
     with pytest.raises(ValueError):
-        ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, 0.125, causal[:5])
+        ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, 0.125, causal[:5])
     with pytest.raises(TypeError):
-        ops.attn_fwd_masked(q2, k2, v2, B, S, H, KV, hd, 0.125, causal.to(torch.int32))
+        ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, 0.125, causal.to(torch.int32))
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20, 1000003])
+@pytest.mark.parametrize("p", [0.0, 0.1, 0.5, 0.97, 1.0])
+def test_dropout_mask_matches_oracle_stream(n, p):
+    """The GPU keep mask is the oracle's SplitMix64 stream, bit for bit."""
+    key = ops.dropout_key(1234 + n, 8)
+    keep = ops.dropout_mask(n, p, key, DEV).cpu().numpy().astype(bool)
+    assert (keep == R.dropout_keep(key, n, p)).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,offset", [(4096 * 8, 0), (4096 * 8 + 5, 0), (777, 1), (1 << 16, 3)])
+@pytest.mark.parametrize("p", [0.1, 0.5, 1.0])
+def test_dropout_op_vs_oracle(dtype, n, offset, p):
+    """y = x * keep / (1 - p) exactly (scale computed in fp32, product
+    rounded once), on the 16-byte and element-wise paths (a view that starts
+    `offset` elements into its buffer is not 16-byte aligned), in place and
+    out of place; the same call on y's gradient applies the same mask."""
+    g = _seed(n + offset)
+    base = torch.randn(n + offset, generator=g).to(dtype)
+    x = base.to(DEV)[offset:]
+    key = ops.dropout_key(77, n)
+    keep = torch.from_numpy(R.dropout_keep(key, n, p))
+    scale = (1.0 / (1.0 - torch.tensor(p, dtype=torch.float32))) if p < 1.0 else torch.tensor(0.0)
+    want = (base[offset:].float() * keep.float() * scale).to(dtype)
+    y = ops.dropout_(x, p, key, out=torch.empty_like(x))
+    assert torch.equal(y.cpu(), want)
+    xi = x.clone()
+    ops.dropout_(xi, p, key)
+    assert torch.equal(xi.cpu(), want)
+    assert torch.equal(x.cpu(), base[offset:])  # out-of-place left x alone
+
+
+def test_dropout_fn_backward_and_seed_draws():
+    """DropoutFn: the backward applies the forward's mask and scale; seeds
+    come from the device generator (torch.manual_seed replays them, each call
+    draws a new one) and the kept fraction is 1 - p."""
+    from lzhip import functional as LF
+
+    x = torch.randn(64, 1024, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    torch.manual_seed(3)
+    y = LF.dropout(x, 0.25)
+    y2 = LF.dropout(x, 0.25)
+    torch.manual_seed(3)
+    y3 = LF.dropout(x, 0.25)
+    assert torch.equal(y, y3) and not torch.equal(y, y2)
+    kept = (y != 0).float().mean().item()
+    assert abs(kept - 0.75) < 0.01
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    keep = (y != 0)
+    want = (dy.float() * keep.float() * (1 / torch.tensor(0.75))).to(torch.bfloat16)
+    assert torch.equal(x.grad, want)
+    assert LF.dropout(x, 0.3, training=False) is x and LF.dropout(x, 0.0) is x
+
+
+@pytest.mark.parametrize("mask_kind", [None, "bool_padding", "float_2d"])
+@pytest.mark.parametrize("B,S,H,KV,hd,dtype,p", [(2, 64, 4, 2, 64, torch.bfloat16, 0.2),
+                                                 (1, 48, 4, 4, 32, torch.float32, 0.5),
+                                                 (2, 40, 6, 2, 128, torch.bfloat16, 0.1)])
+def test_attention_dropout_vs_oracle(mask_kind, B, S, H, KV, hd, dtype, p):
+    """model/llama.py:105-117 in training mode (SDPA dropout_p): forward and
+    gradients of attention with dropout against the oracle in float64 given
+    the kernel's keep mask (element ((b*H + h)*S + s)*S + kv of the stream),
+    causal or with an explicit mask."""
+    g = _seed(B * S + hd + int(p * 10))
+    ld = (H + 2 * KV) * hd
+    qkv = torch.randn(B * S, ld, generator=g).to(dtype)
+    mask = _attn_masks(mask_kind, B, H, S, g) if mask_kind else None
+    d = qkv.to(DEV)
+    q2, k2, v2 = d[:, : H * hd], d[:, H * hd : (H + KV) * hd], d[:, (H + KV) * hd :]
+    scale = hd**-0.5
+    key = ops.dropout_key(2024, B * S)
+    keep = ops.dropout_mask(B * H * S * S, p, key, DEV).cpu().view(B, H, S, S)
+    mdev = mask.to(DEV) if mask is not None else None
+    o, lse = ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, scale, mdev, p, key)
+
+    def heads(t, n):
+        return t.double().view(B, S, n, hd).transpose(1, 2).requires_grad_(True)
+
+    qr, kr, vr = heads(qkv[:, : H * hd], H), heads(qkv[:, H * hd : (H + KV) * hd], KV), heads(qkv[:, (H + KV) * hd :], KV)
+    mref = None if mask is None else (mask if mask.dtype == torch.bool else mask.double())
+    oref = R.causal_gqa_attention(qr, kr, vr, scale, attn_mask=mref, dropout_keep=keep, dropout_p=p)
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-5
+    assert _rel_err(o.cpu().double().view(B, S, H, hd).transpose(1, 2), oref) < tol
+    # the normaliser is the undropped softmax's: lse equals the no-dropout call's
+    _, lse0 = ops.attn_fwd_general(q2, k2, v2, B, S, H, KV, hd, scale, mdev)
+    assert torch.equal(lse, lse0)
+    do = torch.randn(B * S, H * hd, generator=g).to(dtype)
+    dqkv = torch.zeros_like(d)
+    ops.attn_bwd_general(q2, k2, v2, o, do.to(DEV), lse, B, S, H, KV, hd, scale, dqkv[:, : H * hd],
+                         dqkv[:, H * hd : (H + KV) * hd], dqkv[:, (H + KV) * hd :], mdev, p, key)
+    oref.backward(do.double().view(B, S, H, hd).transpose(1, 2))
+    dq = dqkv[:, : H * hd].cpu().double().view(B, S, H, hd).transpose(1, 2)
+    dk = dqkv[:, H * hd : (H + KV) * hd].cpu().double().view(B, S, KV, hd).transpose(1, 2)
+    dv = dqkv[:, (H + KV) * hd :].cpu().double().view(B, S, KV, hd).transpose(1, 2)
+    gtol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    assert _grad_err(dq, qr.grad, vr.grad) < gtol
+    assert _grad_err(dk, kr.grad, vr.grad) < gtol
+    assert _rel_err(dv, vr.grad) < gtol
 
 
 @pytest.mark.parametrize("B,S,H,KV,hd,dtype", [(2, 256, 8, 4, 128, torch.bfloat16), (1, 128, 4, 2, 64, torch.bfloat16),

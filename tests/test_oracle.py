@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -244,3 +245,64 @@ def test_oracle_masked_attention_matches_sdpa():
     causal = ~torch.triu(torch.ones(S, S, dtype=torch.bool), 1)
     assert torch.allclose(R.causal_gqa_attention(q, k, v, attn_mask=causal), R.causal_gqa_attention(q, k, v),
                           atol=1e-14, rtol=0)
+
+
+def test_oracle_splitmix64_known_answers():
+    """The dropout stream is SplitMix64 (Steele, Lea & Flood, OOPSLA 2014):
+    the first five outputs of Vigna's reference splitmix64.c with state
+    1234567, a published known-answer sequence; and the stream's blocks
+    agree with one long draw (output i depends only on (seed, i))."""
+    assert R.splitmix64(1234567, 5).tolist() == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                                                 4593380528125082431, 16408922859458223821]
+    full = R.splitmix64(99, 1000)
+    assert np.array_equal(R.splitmix64(99, 300, start=700), full[700:])
+
+
+@pytest.mark.parametrize("p", [0.0, 0.1, 0.2, 0.5, 0.9, 1.0])
+def test_oracle_dropout_keep_rate(p):
+    """P(keep) = 1 - p: p = 0 keeps all, p = 1 none, otherwise the kept
+    fraction of 2^20 draws is within 5 binomial sigmas of 1 - p, and two keys
+    give different masks."""
+    n = 1 << 20
+    keep = R.dropout_keep(12345, n, p)
+    if p == 0.0:
+        assert keep.all()
+    elif p == 1.0:
+        assert not keep.any()
+    else:
+        sigma = (p * (1 - p) / n) ** 0.5
+        assert abs(keep.mean() - (1 - p)) < 5 * sigma
+        assert (keep != R.dropout_keep(12346, n, p)).any()
+
+
+def test_oracle_dropout_matches_torch_dropout():
+    """oracle dropout(x, keep, p) reproduces F.dropout in training mode when
+    given F.dropout's own keep mask (model/llama.py:146, :213), and the
+    attention-probability dropout of the reference's fallback branch
+    (model/llama.py:127-130: softmax, F.dropout, @ v) with its mask laid out
+    [B, H, S(query), S(key)]."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 7, 33, generator=g, dtype=torch.float64)
+    for p in (0.1, 0.5):
+        torch.manual_seed(11)
+        y = F.dropout(x, p=p, training=True)
+        assert torch.equal(R.dropout(x, y != 0, p), y)
+    B, H, KV, S, hd, p = 2, 4, 2, 10, 8, 0.3
+    q = torch.randn(B, H, S, hd, generator=g, dtype=torch.float64)
+    k = torch.randn(B, KV, S, hd, generator=g, dtype=torch.float64)
+    v = torch.randn(B, KV, S, hd, generator=g, dtype=torch.float64)
+    kk, vv = k.repeat_interleave(H // KV, dim=1), v.repeat_interleave(H // KV, dim=1)
+    scores = (q @ kk.transpose(-2, -1)) * hd**-0.5
+    scores = scores.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    probs = torch.softmax(scores, dim=-1)
+    torch.manual_seed(12)
+    dropped = F.dropout(probs, p=p, training=True)
+    ref = dropped @ vv
+    keep = dropped != 0
+    out = R.causal_gqa_attention(q, k, v, dropout_keep=keep, dropout_p=p)
+    assert torch.allclose(out, ref, atol=1e-12, rtol=1e-12)
+    # the mask changes the result (it is applied), and keep = 1 everywhere is plain attention
+    assert not torch.allclose(out, R.causal_gqa_attention(q, k, v))
+    ones = torch.ones(B, H, S, S, dtype=torch.bool)
+    assert torch.allclose(R.causal_gqa_attention(q, k, v, dropout_keep=ones, dropout_p=0.0),
+                          R.causal_gqa_attention(q, k, v), atol=1e-14, rtol=0)
