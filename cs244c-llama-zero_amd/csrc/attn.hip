@@ -1226,7 +1226,7 @@ struct GenArgs {
   int B, S, H, KV, hd;
   float scale;
   // explicit mask (SDPA's attn_mask; then no causal mask): kind 1 = bool
-  // (bytes, nonzero keeps the score), 2 = fp32, 3 = bf16 (added to the
+  // (bytes, nonzero keeps the score), 2 = fp32, 3 = bf16, 4 = fp16 (added to the
   // scaled score); element strides over [B, H, S(query), S(key)], 0 where
   // the mask broadcasts
   const void* mask;
@@ -1257,7 +1257,8 @@ __device__ __forceinline__ float masked_score(const GenArgs<T>& a, float sc, int
   const int64_t i = (int64_t)b * a.msb + (int64_t)h * a.msh + (int64_t)s * a.msq + (int64_t)kv * a.msk;
   if (a.mask_kind == 1) return static_cast<const uint8_t*>(a.mask)[i] ? sc : -INFINITY;
   if (a.mask_kind == 2) return sc + static_cast<const float*>(a.mask)[i];
-  return sc + bf2f(static_cast<const uint16_t*>(a.mask)[i]);
+  if (a.mask_kind == 3) return sc + bf2f(static_cast<const uint16_t*>(a.mask)[i]);
+  return sc + h2f(static_cast<const uint16_t*>(a.mask)[i]);
 }
 
 template <typename T>
@@ -1759,6 +1760,13 @@ LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
     if (hd == 16 || hd == 32) launch_fwd_small(a, s);
     else attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F16) {
+    GenArgs<_Float16> a{};
+    a.q = (const _Float16*)q; a.k = (const _Float16*)k; a.v = (const _Float16*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.o = (_Float16*)o; a.ldo = ldo; a.lse = lse;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+    if (hd == 16 || hd == 32) launch_fwd_small(a, s);
+    else attn_fwd_generic_kernel<_Float16><<<grid, 256, 0, s>>>(a);
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
     a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
@@ -1791,6 +1799,8 @@ LZ_EXPORT int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_
     attn_delta_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)o, ldo, (const uint16_t*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);
   else if (dtype == LZ_F32)
     attn_delta_kernel<float><<<grid, 256, 0, s>>>((const float*)o, ldo, (const float*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);
+  else if (dtype == LZ_F16)
+    attn_delta_kernel<_Float16><<<grid, 256, 0, s>>>((const _Float16*)o, ldo, (const _Float16*)dout, lddo, delta, (int)B, (int)S, (int)H, (int)hd);
   else
     return lz_set_error(LZ_EINVAL, "lz_attn_delta: bad dtype %d", dtype);
   return lz_check_launch("lz_attn_delta");
@@ -1908,6 +1918,19 @@ int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const 
       attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
       attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
     }
+  } else if (dtype == LZ_F16) {
+    GenArgs<_Float16> a{};
+    a.q = (const _Float16*)q; a.k = (const _Float16*)k; a.v = (const _Float16*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.lse = const_cast<float*>(lse);
+    a.dout = (const _Float16*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (_Float16*)dq; a.dk = (_Float16*)dk; a.dv = (_Float16*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.hd = (int)hd; a.scale = scale;
+    if (hd == 16 || hd == 32) {
+      launch_bwd_small(a, s);
+    } else {
+      attn_bwd_dq_generic_kernel<_Float16><<<grid_q, 256, 0, s>>>(a);
+      attn_bwd_dkdv_generic_kernel<_Float16><<<grid_kv, 256, 0, s>>>(a);
+    }
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
     a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
@@ -1949,7 +1972,7 @@ int general_args(GenArgs<T>& a, const void* q, int64_t ldq, const void* k, int64
 }
 
 int check_general(const void* mask, int mask_kind, const int64_t* mstride, float dropout_p) {
-  LZ_REQUIRE(mask_kind >= 0 && mask_kind <= 3, "attention mask: kind %d (0 causal, 1 bool, 2 fp32, 3 bf16)",
+  LZ_REQUIRE(mask_kind >= 0 && mask_kind <= 4, "attention mask: kind %d (0 causal, 1 bool, 2 fp32, 3 bf16, 4 fp16)",
              mask_kind);
   if (mask_kind) {
     LZ_REQUIRE(mask && mstride, "attention mask: null pointer");
@@ -1965,7 +1988,7 @@ int check_general(const void* mask, int mask_kind, const int64_t* mstride, float
 // do not take (model/llama.py:109-117, F.scaled_dot_product_attention):
 //   - an explicit mask in place of the causal one (attn_mask with
 //     is_causal=False): mask_kind 1 = bool bytes (nonzero: the key takes
-//     part), 2 = fp32, 3 = bf16 (added to the scaled scores); mstride = its
+//     part), 2 = fp32, 3 = bf16, 4 = fp16 (added to the scaled scores); mstride = its
 //     element strides over [B, H, S(query), S(key)], 0 where it broadcasts;
 //     mask_kind 0 = causal (mask and mstride ignored).  A row whose keys are
 //     all masked gives NaN, as the reference's softmax of an all -inf row does;
@@ -1989,6 +2012,11 @@ LZ_EXPORT int lz_attn_fwd_general(const void* q, int64_t ldq, const void* k, int
     general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
     a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
     attn_fwd_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F16) {
+    GenArgs<_Float16> a{};
+    general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
+    a.o = (_Float16*)o; a.ldo = ldo; a.lse = lse;
+    attn_fwd_generic_kernel<_Float16><<<grid, 256, 0, s>>>(a);
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
     general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
@@ -2023,6 +2051,13 @@ LZ_EXPORT int lz_attn_bwd_general(const void* q, int64_t ldq, const void* k, int
     a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
     attn_bwd_dq_generic_kernel<uint16_t><<<grid_q, 256, 0, s>>>(a);
     attn_bwd_dkdv_generic_kernel<uint16_t><<<grid_kv, 256, 0, s>>>(a);
+  } else if (dtype == LZ_F16) {
+    GenArgs<_Float16> a{};
+    general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);
+    a.lse = const_cast<float*>(lse); a.dout = (const _Float16*)dout; a.lddo = lddo; a.delta = delta;
+    a.dq = (_Float16*)dq; a.dk = (_Float16*)dk; a.dv = (_Float16*)dv; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    attn_bwd_dq_generic_kernel<_Float16><<<grid_q, 256, 0, s>>>(a);
+    attn_bwd_dkdv_generic_kernel<_Float16><<<grid_kv, 256, 0, s>>>(a);
   } else if (dtype == LZ_F32) {
     GenArgs<float> a{};
     general_args(a, q, ldq, k, ldk, v, ldv, mask, mask_kind, mstride, dropout_p, seed, B, S, H, KV, hd, scale);

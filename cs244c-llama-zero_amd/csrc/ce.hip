@@ -179,6 +179,8 @@ LZ_EXPORT int lz_ce_fwd(const void* logits, int64_t ld, int64_t rows, int64_t vo
       ce_fwd_kernel<uint16_t, false><<<grid_rows(rows), kThreads, 0, s>>>((const uint16_t*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, row_loss);
   } else if (dtype == LZ_F32) {
     ce_fwd_kernel<float, false><<<grid_rows(rows), kThreads, 0, s>>>((const float*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, row_loss);
+  } else if (dtype == LZ_F16) {
+    ce_fwd_kernel<_Float16, false><<<grid_rows(rows), kThreads, 0, s>>>((const _Float16*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, row_loss);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_ce_fwd: bad dtype %d", dtype);
   }
@@ -210,6 +212,10 @@ LZ_EXPORT int lz_ce_bwd(const void* logits, int64_t ld, int64_t rows, int64_t vo
     ce_bwd_kernel<float, float, false><<<g, kThreads, 0, s>>>((const float*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, grad_loss, count, (float*)dlogits, ldd);
   } else if (dtype == LZ_BF16 && ddtype == LZ_F32) {
     ce_bwd_kernel<uint16_t, float, false><<<g, kThreads, 0, s>>>((const uint16_t*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, grad_loss, count, (float*)dlogits, ldd);
+  } else if (dtype == LZ_F16 && ddtype == LZ_F16) {
+    ce_bwd_kernel<_Float16, _Float16, false><<<g, kThreads, 0, s>>>((const _Float16*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, grad_loss, count, (_Float16*)dlogits, ldd);
+  } else if (dtype == LZ_F16 && ddtype == LZ_F32) {
+    ce_bwd_kernel<_Float16, float, false><<<g, kThreads, 0, s>>>((const _Float16*)logits, ld, rows, vocab, labels, seq, ignore_index, lse, grad_loss, count, (float*)dlogits, ldd);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_ce_bwd: bad dtypes %d->%d", dtype, ddtype);
   }

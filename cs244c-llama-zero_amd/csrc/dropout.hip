@@ -70,6 +70,8 @@ LZ_EXPORT int lz_dropout(const void* x, void* y, int64_t n, float p, uint64_t se
       dropout_bf16x8_kernel<<<grid_for(n / 8), 256, 0, s>>>((const uint16_t*)x, (uint16_t*)y, n / 8, thresh, scale, seed);
     else
       dropout_kernel<uint16_t><<<grid_for(n), 256, 0, s>>>((const uint16_t*)x, (uint16_t*)y, n, thresh, scale, seed);
+  } else if (dtype == LZ_F16) {
+    dropout_kernel<_Float16><<<grid_for(n), 256, 0, s>>>((const _Float16*)x, (_Float16*)y, n, thresh, scale, seed);
   } else if (dtype == LZ_F32) {
     dropout_kernel<float><<<grid_for(n), 256, 0, s>>>((const float*)x, (float*)y, n, thresh, scale, seed);
   } else {

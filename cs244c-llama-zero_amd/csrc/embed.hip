@@ -74,12 +74,12 @@ LZ_EXPORT int lz_embedding_fwd(const int64_t* ids, int64_t ntok, const void* tab
   LZ_REQUIRE(ntok >= 0 && vocab > 0 && dim > 0 && ldo >= dim, "lz_embedding_fwd: bad shape");
   if (ntok == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
-  const int esz = dtype == LZ_BF16 ? 2 : 4;
-  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_embedding_fwd: bad dtype %d", dtype);
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32 || dtype == LZ_F16, "lz_embedding_fwd: bad dtype %d", dtype);
+  const int esz = lz_esize(dtype);
   if ((dim * esz) % 16 == 0 && (ldo * esz) % 16 == 0 && lz_aligned16(table) && lz_aligned16(out)) {
     embed_fwd_vec_kernel<<<grid_cap(ntok), 128, 0, s>>>(ids, ntok, (const uint4*)table, vocab, dim * esz / 16, (uint4*)out,
                                                        ldo * esz / 16, bad_flag);
-  } else if (dtype == LZ_BF16) {
+  } else if (dtype != LZ_F32) {  // a row copy: the 16-bit formats move alike
     embed_fwd_kernel<uint16_t><<<grid_cap(ntok), 128, 0, s>>>(ids, ntok, (const uint16_t*)table, vocab, dim, (uint16_t*)out, ldo, bad_flag);
   } else {
     embed_fwd_kernel<float><<<grid_cap(ntok), 128, 0, s>>>(ids, ntok, (const float*)table, vocab, dim, (float*)out, ldo, bad_flag);
@@ -92,15 +92,17 @@ LZ_EXPORT int lz_embedding_bwd(const int64_t* ids, int64_t ntok, const void* dou
                                void* grad, int accumulate, float* workspace, int dtype, void* stream) {
   LZ_REQUIRE(ntok >= 0 && vocab > 0 && dim > 0 && ldo >= dim, "lz_embedding_bwd: bad shape");
   LZ_REQUIRE(workspace && lz_aligned16(workspace), "lz_embedding_bwd: workspace must be 16-byte aligned");
-  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_embedding_bwd: bad dtype %d", dtype);
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32 || dtype == LZ_F16, "lz_embedding_bwd: bad dtype %d", dtype);
   hipStream_t s = lz_stream(stream);
   const int64_t n = vocab * dim;
   zero_f32_kernel<<<grid_cap(lz_cdiv(n / 4 + 1, 256)), 256, 0, s>>>(workspace, n);
   if (ntok > 0) {
     if (dtype == LZ_BF16) embed_bwd_scatter_kernel<uint16_t><<<grid_cap(ntok), 256, 0, s>>>(ids, ntok, (const uint16_t*)dout, ldo, vocab, dim, workspace);
+    else if (dtype == LZ_F16) embed_bwd_scatter_kernel<_Float16><<<grid_cap(ntok), 256, 0, s>>>(ids, ntok, (const _Float16*)dout, ldo, vocab, dim, workspace);
     else embed_bwd_scatter_kernel<float><<<grid_cap(ntok), 256, 0, s>>>(ids, ntok, (const float*)dout, ldo, vocab, dim, workspace);
   }
   if (dtype == LZ_BF16) embed_bwd_finish_kernel<uint16_t><<<grid_cap(lz_cdiv(n, 256)), 256, 0, s>>>(workspace, (uint16_t*)grad, n, accumulate);
+  else if (dtype == LZ_F16) embed_bwd_finish_kernel<_Float16><<<grid_cap(lz_cdiv(n, 256)), 256, 0, s>>>(workspace, (_Float16*)grad, n, accumulate);
   else embed_bwd_finish_kernel<float><<<grid_cap(lz_cdiv(n, 256)), 256, 0, s>>>(workspace, (float*)grad, n, accumulate);
   return lz_check_launch("lz_embedding_bwd");
 }

@@ -1,4 +1,4 @@
-// bf16 GEMM on CDNA4 matrix cores:
+// bf16 / fp16 GEMM on CDNA4 matrix cores:
 //
 //   C[M,N] = alpha * sum_k A(m,k) B(n,k)  (+ beta * C)  (+ R)
 //
@@ -29,7 +29,19 @@
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// One 32x32x16 MFMA of the operand format F (FmtBF16 or FmtF16).  Fragments
+// travel as bf16x8_t whatever the format: they are 16 raw bytes per lane.
+template <typename F>
+__device__ __forceinline__ f32x16_t mfma16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  if constexpr (F::kDtype == LZ_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 
 constexpr int kBK = 64;                 // K elements per stage
 constexpr int kRowBytes = kBK * 2 + 16; // padded LDS row (144 B)
@@ -42,7 +54,7 @@ struct GemmArgs {
   int64_t lda, ldb, ldc, ldr;
   int64_t M, N, K;
   float alpha, beta;
-  int c_f32;      // output dtype fp32 (else bf16)
+  int c_f32;      // output dtype fp32 (else the operands' 16-bit format)
   int vec_store;  // N, ldc, ldr multiples of 4 and pointers aligned
   int vec16;      // C rows (and R rows) start 16-byte aligned: row-contiguous 16-byte epilogue
   int r16;        // R rows 16-byte aligned too: the residual joins the 16-byte bf16 epilogue
@@ -50,23 +62,25 @@ struct GemmArgs {
   int64_t slab;   // elements between the fp32 partial slabs of consecutive splits
 };
 
-// Elementwise bf16 sum of two 8-value pieces, rounded once.
-__device__ __forceinline__ uint4 add_bf16x8(const uint4& a, const uint4& b) {
+// Elementwise sum of two 8-value 16-bit pieces, rounded once.
+template <typename F>
+__device__ __forceinline__ uint4 add16x8(const uint4& a, const uint4& b) {
   const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
   uint32_t o[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
-    o[k] = pack_bf16x2(bf2f((uint16_t)(aw[k] & 0xffff)) + bf2f((uint16_t)(bw[k] & 0xffff)),
-                       bf2f((uint16_t)(aw[k] >> 16)) + bf2f((uint16_t)(bw[k] >> 16)));
+    o[k] = F::pack2(F::to_f(aw[k] & 0xffff) + F::to_f(bw[k] & 0xffff), F::to_f(aw[k] >> 16) + F::to_f(bw[k] >> 16));
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// A bf16 output with a residual is rounded twice, as the reference's separate
-// ops are (the nn.Linear output in bf16, then x + y in bf16,
-// model/llama.py:158-159): the product is rounded to bf16 before R is added
-// and the sum is rounded on the store.  fp32 outputs add R unrounded.
-__device__ __forceinline__ float with_residual_bf16(float v, uint32_t r16) { return round_bf(v) + bf2f((uint16_t)r16); }
+// A 16-bit output with a residual is rounded twice, as the reference's
+// separate ops are (the nn.Linear output in bf16, then x + y in bf16,
+// model/llama.py:158-159): the product is rounded to the format before R is
+// added and the sum is rounded on the store.  fp32 outputs add R unrounded.
+template <typename F>
+__device__ __forceinline__ float with_residual(float v, uint32_t r16) { return F::round(v) + F::to_f(r16 & 0xffff); }
 
+template <typename F>
 __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t n, const float (&v)[4]) {
   float o[4] = {v[0] * g.alpha, v[1] * g.alpha, v[2] * g.alpha, v[3] * g.alpha};
   if (g.vec_store && n + 3 < g.N) {
@@ -79,24 +93,24 @@ __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t
       }
       if (g.R) {
         uint2 r = *reinterpret_cast<const uint2*>(g.R + m * g.ldr + n);
-        o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+        o[0] += F::to_f(r.x & 0xffff); o[1] += F::to_f(r.x >> 16); o[2] += F::to_f(r.y & 0xffff); o[3] += F::to_f(r.y >> 16);
       }
       *cp = make_float4(o[0], o[1], o[2], o[3]);
     } else {
       uint2* cp = reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.C) + m * g.ldc + n);
       if (g.beta != 0.f) {
         uint2 c = *cp;
-        o[0] = fmaf(g.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(g.beta, bf2f(c.x >> 16), o[1]);
-        o[2] = fmaf(g.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(g.beta, bf2f(c.y >> 16), o[3]);
+        o[0] = fmaf(g.beta, F::to_f(c.x & 0xffff), o[0]); o[1] = fmaf(g.beta, F::to_f(c.x >> 16), o[1]);
+        o[2] = fmaf(g.beta, F::to_f(c.y & 0xffff), o[2]); o[3] = fmaf(g.beta, F::to_f(c.y >> 16), o[3]);
       }
       if (g.R) {
         uint2 r = *reinterpret_cast<const uint2*>(g.R + m * g.ldr + n);
-        o[0] = with_residual_bf16(o[0], r.x & 0xffff); o[1] = with_residual_bf16(o[1], r.x >> 16);
-        o[2] = with_residual_bf16(o[2], r.y & 0xffff); o[3] = with_residual_bf16(o[3], r.y >> 16);
+        o[0] = with_residual<F>(o[0], r.x & 0xffff); o[1] = with_residual<F>(o[1], r.x >> 16);
+        o[2] = with_residual<F>(o[2], r.y & 0xffff); o[3] = with_residual<F>(o[3], r.y >> 16);
       }
       uint2 w;
-      w.x = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
-      w.y = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
+      w.x = (uint32_t)F::from_f(o[0]) | ((uint32_t)F::from_f(o[1]) << 16);
+      w.y = (uint32_t)F::from_f(o[2]) | ((uint32_t)F::from_f(o[3]) << 16);
       *cp = w;
     }
     return;
@@ -109,13 +123,13 @@ __device__ __forceinline__ void store_out4(const GemmArgs& g, int64_t m, int64_t
     if (g.c_f32) {
       float* cp = static_cast<float*>(g.C) + m * g.ldc + nn;
       if (g.beta != 0.f) val = fmaf(g.beta, *cp, val);
-      if (g.R) val += bf2f(g.R[m * g.ldr + nn]);
+      if (g.R) val += F::to_f(g.R[m * g.ldr + nn]);
       *cp = val;
     } else {
       uint16_t* cp = static_cast<uint16_t*>(g.C) + m * g.ldc + nn;
-      if (g.beta != 0.f) val = fmaf(g.beta, bf2f(*cp), val);
-      if (g.R) val = with_residual_bf16(val, g.R[m * g.ldr + nn]);
-      *cp = f2bf(val);
+      if (g.beta != 0.f) val = fmaf(g.beta, F::to_f(*cp), val);
+      if (g.R) val = with_residual<F>(val, g.R[m * g.ldr + nn]);
+      *cp = F::from_f(val);
     }
   }
 }
@@ -243,7 +257,7 @@ __device__ __forceinline__ int epi_swz(int row) {
 // conflicts), then writes whole 16-byte pieces of consecutive row bytes, so a
 // store instruction covers full cache lines.  fp32 output goes in two passes
 // of TM/2 rows.  Needs BM*BN*2 bytes of LDS.
-template <int BM, int BN, int WM, int WN>
+template <typename F, int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
                                              int64_t m0, int64_t n0, char* smem, int lane, int wave) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -267,8 +281,8 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
           for (int q = 0; q < 4; ++q) {
             const int row = i * 32 + frag_row, chunk = j * 4 + q;
             *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
-                make_uint2(pack_bf16x2(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha),
-                           pack_bf16x2(acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha));
+                make_uint2(F::pack2(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha),
+                           F::pack2(acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha));
           }
       asm volatile("" ::: "memory");
       constexpr int kIters = TM * kChunks / 64;
@@ -299,7 +313,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
           const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
           const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
           *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) =
-              add_bf16x8(v, rv[u]);
+              add16x8<F>(v, rv[u]);
         }
       }
       return;
@@ -365,17 +379,17 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
             o[0] = fmaf(go.beta, __uint_as_float(c.x), o[0]); o[1] = fmaf(go.beta, __uint_as_float(c.y), o[1]);
             o[2] = fmaf(go.beta, __uint_as_float(c.z), o[2]); o[3] = fmaf(go.beta, __uint_as_float(c.w), o[3]);
           } else {
-            o[0] = fmaf(go.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, bf2f(c.x >> 16), o[1]);
-            o[2] = fmaf(go.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, bf2f(c.y >> 16), o[3]);
+            o[0] = fmaf(go.beta, F::to_f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, F::to_f(c.x >> 16), o[1]);
+            o[2] = fmaf(go.beta, F::to_f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, F::to_f(c.y >> 16), o[3]);
           }
         }
         if (has_r) {
           const uint2 r = rpre[u];
           if (go.c_f32) {
-            o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16); o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+            o[0] += F::to_f(r.x & 0xffff); o[1] += F::to_f(r.x >> 16); o[2] += F::to_f(r.y & 0xffff); o[3] += F::to_f(r.y >> 16);
           } else {
-            o[0] = with_residual_bf16(o[0], r.x & 0xffff); o[1] = with_residual_bf16(o[1], r.x >> 16);
-            o[2] = with_residual_bf16(o[2], r.y & 0xffff); o[3] = with_residual_bf16(o[3], r.y >> 16);
+            o[0] = with_residual<F>(o[0], r.x & 0xffff); o[1] = with_residual<F>(o[1], r.x >> 16);
+            o[2] = with_residual<F>(o[2], r.y & 0xffff); o[3] = with_residual<F>(o[3], r.y >> 16);
           }
         }
         if (go.c_f32) {
@@ -383,7 +397,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
               __float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
         } else {
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(go.C) + m * go.ldc + n) =
-              make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+              make_uint2(F::pack2(o[0], o[1]), F::pack2(o[2], o[3]));
         }
       }
     }
@@ -400,7 +414,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
 // go through LDS one 32-row band at a time and are written as whole rows with
 // bounds checks, so the accumulators are never indexed dynamically.  `smem` must be free and at
 // least max(WM*WN*32*(BN/WN+4)*4, BM*BN*2) bytes.
-template <int BM, int BN, int WM, int WN>
+template <typename F, int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0,
                                            int64_t n0, char* smem, int lane, int wave) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -408,7 +422,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
   const int frag_row = lane & 31, half = lane >> 5;
   if constexpr (TN <= 64) {  // (wider wave tiles run out of registers in the staged path)
     if (m0 + BM <= go.M && n0 + BN <= go.N && go.vec16) {
-      store_tile16<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+      store_tile16<F, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
       return;
     }
   }
@@ -434,7 +448,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
             }
             if (rrow) {
               const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
-              o.x += bf2f(r.x & 0xffff); o.y += bf2f(r.x >> 16); o.z += bf2f(r.y & 0xffff); o.w += bf2f(r.y >> 16);
+              o.x += F::to_f(r.x & 0xffff); o.y += F::to_f(r.x >> 16); o.z += F::to_f(r.y & 0xffff); o.w += F::to_f(r.y >> 16);
             }
             *cp = o;
           }
@@ -454,15 +468,15 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
             uint2* cp = reinterpret_cast<uint2*>(crow + j * 32 + q * 8);
             if (go.beta != 0.f) {
               const uint2 c = *cp;
-              o[0] = fmaf(go.beta, bf2f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, bf2f(c.x >> 16), o[1]);
-              o[2] = fmaf(go.beta, bf2f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, bf2f(c.y >> 16), o[3]);
+              o[0] = fmaf(go.beta, F::to_f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, F::to_f(c.x >> 16), o[1]);
+              o[2] = fmaf(go.beta, F::to_f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, F::to_f(c.y >> 16), o[3]);
             }
             if (rrow) {
               const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
-              o[0] = with_residual_bf16(o[0], r.x & 0xffff); o[1] = with_residual_bf16(o[1], r.x >> 16);
-              o[2] = with_residual_bf16(o[2], r.y & 0xffff); o[3] = with_residual_bf16(o[3], r.y >> 16);
+              o[0] = with_residual<F>(o[0], r.x & 0xffff); o[1] = with_residual<F>(o[1], r.x >> 16);
+              o[2] = with_residual<F>(o[2], r.y & 0xffff); o[3] = with_residual<F>(o[3], r.y >> 16);
             }
-            *cp = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+            *cp = make_uint2(F::pack2(o[0], o[1]), F::pack2(o[2], o[3]));
           }
       }
     }
@@ -486,7 +500,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
       if (m < go.M && n < go.N) {
         const float4 v4 = *reinterpret_cast<const float4*>(stage + r * kPitch + c4 * 4);
         const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-        store_out4(go, m, n, v);
+        store_out4<F>(go, m, n, v);
       }
     }
     __syncthreads();
@@ -496,7 +510,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
 // Register-staged kernel: any operand layouts.  Global loads for K step k+1
 // are in flight in registers while step k's MFMAs run, then written to the
 // other LDS buffer (transposed on the way for an M/N-major operand).
-template <int BM, int BN, int WM, int WN, bool AK, bool BK>
+template <typename F, int BM, int BN, int WM, int WN, bool AK, bool BK>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   constexpr int kThreads = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave sub-tile
@@ -568,7 +582,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = mfma16<F>(fa[j], fb[i], acc[i][j]);
     }
     if (kt + 1 < ktiles) {
       char* nxt = smem + (cur ^ 1) * kStageBytes;
@@ -580,7 +594,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 
   GemmArgs go = g;  // split-K: this split's fp32 slab
   if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
-  store_tile<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+  store_tile<F, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
 }
 
 // ---------------------------------------------------------------------------
@@ -725,12 +739,12 @@ __device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM, DBK>& fra,
   for (int i = 0; i < FM; ++i) fb[i] = fra.frag(sa, i, kk);
 }
 
-template <int FM, int FN>
+template <typename F, int FM, int FN>
 __device__ __forceinline__ void dma_mfma(f32x16_t (&acc)[FM][FN], const bf16x8_t (&fa)[FN], const bf16x8_t (&fb)[FM]) {
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], fb[i], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<F>(fa[j], fb[i], acc[i][j]);
 }
 
 // Scheduling of one K slice: NM MFMAs, each followed by up to ceil(R/NM) of
@@ -799,7 +813,7 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
 // matching 128 up rows of a [gate; up] weight (o.F rows apart), and the
 // epilogue writes silu(gate) * up.  kEpiRope: the epilogue rotates the tile's
 // columns below r.nrope as RoPE heads of 128.
-template <int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi>
+template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi>
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o, const RopeIn& rope) {
   constexpr bool kSwiGLU = kEpi == kEpiSwiGLU;
   constexpr int BM = 256, BN = 256;
@@ -815,6 +829,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   static_assert(!kMid || (NST == 2 && kSlices == 4), "the mid-step barrier runs two stages of four slices");
   static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
   static_assert(kSlices == 2 || kSlices == 4, "stages hold 2 or 4 K slices");
+  static_assert(kEpi == kEpiPlain || F::kDtype == LZ_BF16, "the fused epilogues are bf16");
 
   __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
 
@@ -866,9 +881,9 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
     for (int kt = 0; kt < ktiles; ++kt) {
       const char* sa = smem + (kt & 1) * kStage;
       const char* sb = sa + kOpBytes;
-      dma_mfma(acc, fa0, fb0);
+      dma_mfma<F>(acc, fa0, fb0);
       dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
-      dma_mfma(acc, fa1, fb1);
+      dma_mfma<F>(acc, fa1, fb1);
       dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
       sched_slice<kReads, FM * FN>();
       sched_slice<kReads, FM * FN>();
@@ -886,9 +901,9 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
       const char* na = smem + ((kt + 1) & 1) * kStage;
       const char* nb = na + kOpBytes;
       bf16x8_t ga0[FN], gb0[FM], ga1[FN], gb1[FM];
-      dma_mfma(acc, fa0, fb0);
+      dma_mfma<F>(acc, fa0, fb0);
       dma_load_frags(fra, frb, na, nb, 0, ga0, gb0);
-      dma_mfma(acc, fa1, fb1);
+      dma_mfma<F>(acc, fa1, fb1);
       dma_load_frags(fra, frb, na, nb, 1, ga1, gb1);
       sched_slice<kReads, FM * FN>();
       sched_slice<kReads, FM * FN>();
@@ -943,14 +958,14 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
       constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);
       dma_load_frags(fra, frb, sa, sb, 0, fa0, fb0);
       dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
-      dma_mfma(acc, fa0, fb0);
+      dma_mfma<F>(acc, fa0, fb0);
       if constexpr (kSlices == 4) {
         dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
-        dma_mfma(acc, fa1, fb1);
+        dma_mfma<F>(acc, fa1, fb1);
         dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
-        dma_mfma(acc, fa0, fb0);
+        dma_mfma<F>(acc, fa0, fb0);
       }
-      dma_mfma(acc, fa1, fb1);
+      dma_mfma<F>(acc, fa1, fb1);
       __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
       for (int q = 0; q < kSlices - 1; ++q) sched_slice<kReads, FM * FN>();
@@ -966,25 +981,25 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   } else {
     GemmArgs go = g;  // split-K: this split's fp32 slab
     if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
-    store_tile<BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+    store_tile<F, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
   }
 }
 
-template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
+template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
-  gemm_dma_tile<WM, WN, AK, BK, DBK, NST, kEpiPlain>(g, SwigluOut{}, RopeIn{});
+  gemm_dma_tile<F, WM, WN, AK, BK, DBK, NST, kEpiPlain>(g, SwigluOut{}, RopeIn{});
 }
 
 // Fused gate|up projection + SwiGLU (both operands K-major): tile (tm, tn)
 // covers rows 256 tm.. of x and gate/up columns 128 tn.. of the [M, F] result.
 __global__ void __launch_bounds__(512) gemm_swiglu_kernel(GemmArgs g, SwigluOut o) {
-  gemm_dma_tile<2, 4, true, true, 64, 2, kEpiSwiGLU>(g, o, RopeIn{});
+  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiSwiGLU>(g, o, RopeIn{});
 }
 
 // Fused QKV projection + RoPE on the q and k heads (both operands K-major,
 // M and N multiples of 256, head dim 128).
 __global__ void __launch_bounds__(512) gemm_rope_kernel(GemmArgs g, RopeIn r) {
-  gemm_dma_tile<2, 4, true, true, 64, 2, kEpiRope>(g, SwigluOut{}, r);
+  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiRope>(g, SwigluOut{}, r);
 }
 
 // SwiGLU epilogue.  Each wave stages its 128x64 tile as bf16 in its own LDS
@@ -1056,7 +1071,7 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   static_assert(WN == 4 && TN == 64, "a head of 128 is two 64-column waves");
   if (n0 >= r.nrope) {
-    store_tile<BM, BN, WM, WN>(g, acc, m0, n0, smem, lane, wave);
+    store_tile<FmtBF16, BM, BN, WM, WN>(g, acc, m0, n0, smem, lane, wave);
     return;
   }
   constexpr int kRow = TN * 2, kChunks = kRow / 16, kWaveBytes = TM * kRow, kHd = 2 * TN;
@@ -1118,6 +1133,7 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
 // Sums the fp32 partial slabs of a split-K product and applies the epilogue
 // (alpha, beta*C, R) to the real output, 4 columns per thread, in a fixed
 // order so results do not depend on scheduling.
+template <typename F>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const float* __restrict__ slabs, int splits) {
   const int64_t n4 = lz_cdiv(g.N, 4);
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1141,7 +1157,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
         if (n + e < g.N) v[e] += row[n + e];
     }
   }
-  store_out4(g, m, n, v);
+  store_out4<F>(g, m, n, v);
 }
 
 // Tile configurations: 0 = 256x256 with 8 waves (128x64 per wave),
@@ -1207,48 +1223,53 @@ inline bool dma_span_fits(bool kmajor, int64_t ld, int64_t kper, int64_t rows = 
   return elems < (1ll << 30);
 }
 
-template <int BM, int BN, int WM, int WN, bool AK, bool BK>
+template <typename F, int BM, int BN, int WM, int WN, bool AK, bool BK>
 int launch(const GemmArgs& g, int splits, hipStream_t s) {
   const int64_t tiles = lz_cdiv(g.M, BM) * lz_cdiv(g.N, BN);
   LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
-  gemm_kernel<BM, BN, WM, WN, AK, BK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  gemm_kernel<F, BM, BN, WM, WN, AK, BK><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
   return lz_check_launch("lz_gemm");
 }
 
 // Explicit instantiations: when the host pass only meets these kernels through
 // the dispatch templates it does not emit the launch stubs of the variants
 // that use ds_read_b64_tr_b16.
-template __global__ void gemm_dma_kernel<2, 4, true, true, 64, 2>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 4, true, false, 64, 2>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 4, false, true, 64, 2>(GemmArgs);
-template __global__ void gemm_dma_kernel<2, 4, false, false, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtBF16, 2, 4, true, true, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtBF16, 2, 4, true, false, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtBF16, 2, 4, false, true, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtBF16, 2, 4, false, false, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtF16, 2, 4, true, true, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtF16, 2, 4, true, false, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtF16, 2, 4, false, true, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_kernel<FmtF16, 2, 4, false, false, 64, 2>(GemmArgs);
 
-template <int WM, int WN, bool AK, bool BK, int DBK, int NST>
+template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST>
 int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
   const int64_t tiles = lz_cdiv(g.M, 256) * lz_cdiv(g.N, 256);
   LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
-  gemm_dma_kernel<WM, WN, AK, BK, DBK, NST><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
+  gemm_dma_kernel<F, WM, WN, AK, BK, DBK, NST><<<dim3((unsigned)tiles, (unsigned)splits), 64 * WM * WN, 0, s>>>(g);
   return lz_check_launch("lz_gemm");
 }
 
-template <bool AK, bool BK>
+template <typename F, bool AK, bool BK>
 int dispatch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
-  if (cfg == 5) return launch_dma<2, 4, AK, BK, 64, 2>(g, splits, s);
+  if (cfg == 5) return launch_dma<F, 2, 4, AK, BK, 64, 2>(g, splits, s);
   switch (cfg) {
     case 0:
-      return launch<256, 256, 2, 4, AK, BK>(g, splits, s);
+      return launch<F, 256, 256, 2, 4, AK, BK>(g, splits, s);
     case 1:
-      return launch<256, 256, 2, 2, AK, BK>(g, splits, s);
+      return launch<F, 256, 256, 2, 2, AK, BK>(g, splits, s);
     default:
-      return launch<128, 128, 2, 2, AK, BK>(g, splits, s);
+      return launch<F, 128, 128, 2, 2, AK, BK>(g, splits, s);
   }
 }
 
+template <typename F>
 int dispatch_layout(const GemmArgs& g, bool ak, bool bk, int cfg, int splits, hipStream_t s) {
-  if (ak && bk) return dispatch<true, true>(g, cfg, splits, s);
-  if (ak) return dispatch<true, false>(g, cfg, splits, s);
-  if (bk) return dispatch<false, true>(g, cfg, splits, s);
-  return dispatch<false, false>(g, cfg, splits, s);
+  if (ak && bk) return dispatch<F, true, true>(g, cfg, splits, s);
+  if (ak) return dispatch<F, true, false>(g, cfg, splits, s);
+  if (bk) return dispatch<F, false, true>(g, cfg, splits, s);
+  return dispatch<F, false, false>(g, cfg, splits, s);
 }
 
 }  // namespace
@@ -1271,15 +1292,15 @@ LZ_EXPORT int lz_gemm_plan(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_
 }
 
 // C = alpha * sum_k A(m,k) B(n,k) (+ beta*C) (+ R), see the top of this file
-// for the operand layouts.  C: [M,N] bf16 or fp32 (ldc), R: optional [M,N]
-// bf16 (ldr).  Requirements: A and B 16-byte aligned, lda and ldb multiples
+// for the operand layouts.  A and B: ab_dtype (LZ_BF16 or LZ_F16); C: [M,N]
+// in ab_dtype or fp32 (c_dtype, ldc); R: optional [M,N] in ab_dtype (ldr).  Requirements: A and B 16-byte aligned, lda and ldb multiples
 // of 8; K % 8 == 0 for a K-major operand; M % 8 == 0 (N % 8 == 0) for an
 // M-major A (N-major B).  `ws` (16-byte aligned, ws_bytes long, may be null)
 // holds the fp32 partial products when K is split; with less workspace than
 // lz_gemm_workspace() reports the product runs unsplit.
-LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb, int b_kmajor, void* C,
-                      int64_t ldc, int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha,
-                      float beta, void* ws, int64_t ws_bytes, void* stream) {
+LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb, int b_kmajor, int ab_dtype,
+                      void* C, int64_t ldc, int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K,
+                      float alpha, float beta, void* ws, int64_t ws_bytes, void* stream) {
   LZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lz_gemm: negative shape");
   if (M == 0 || N == 0) return LZ_OK;
   LZ_REQUIRE(A && B && C, "lz_gemm: null pointer");
@@ -1291,7 +1312,9 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
   LZ_REQUIRE(lz_aligned16(A) && lz_aligned16(B), "lz_gemm: A and B must be 16-byte aligned");
   LZ_REQUIRE(lda >= (a_kmajor ? K : M) && ldb >= (b_kmajor ? K : N) && ldc >= N && (R == nullptr || ldr >= N),
              "lz_gemm: bad leading dimension");
-  LZ_REQUIRE(c_dtype == LZ_BF16 || c_dtype == LZ_F32, "lz_gemm: bad output dtype %d", c_dtype);
+  LZ_REQUIRE(ab_dtype == LZ_BF16 || ab_dtype == LZ_F16, "lz_gemm: bad operand dtype %d", ab_dtype);
+  LZ_REQUIRE(c_dtype == ab_dtype || c_dtype == LZ_F32, "lz_gemm: bad output dtype %d for operands of dtype %d", c_dtype,
+             ab_dtype);
   LZ_REQUIRE(ws_bytes >= 0 && (ws == nullptr || lz_aligned16(ws)), "lz_gemm: workspace must be 16-byte aligned");
   GemmArgs g;
   g.A = (const uint16_t*)A;
@@ -1325,7 +1348,9 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
   }
   if (p.cfg == 5 && !(dma_span_fits(ak, lda, p.kper) && dma_span_fits(bk, ldb, p.kper)))
     p.cfg = ak ? 0 : 1;  // register-staged loads take 64-bit addresses
-  if (p.splits == 1) return dispatch_layout(g, ak, bk, p.cfg, 1, s);
+  const bool f16 = ab_dtype == LZ_F16;
+  if (p.splits == 1)
+    return f16 ? dispatch_layout<FmtF16>(g, ak, bk, p.cfg, 1, s) : dispatch_layout<FmtBF16>(g, ak, bk, p.cfg, 1, s);
   GemmArgs gs = g;  // partial products into fp32 slabs [splits][M][N]
   gs.C = ws;
   gs.ldc = N;
@@ -1337,19 +1362,21 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
   gs.vec16 = N % 4 == 0 && lz_aligned16(ws);
   gs.kper = p.kper;
   gs.slab = M * N;
-  int rc = dispatch_layout(gs, ak, bk, p.cfg, p.splits, s);
+  int rc = f16 ? dispatch_layout<FmtF16>(gs, ak, bk, p.cfg, p.splits, s)
+               : dispatch_layout<FmtBF16>(gs, ak, bk, p.cfg, p.splits, s);
   if (rc) return rc;
-  const int64_t work = M * lz_cdiv(N, 4);
-  splitk_reduce_kernel<<<(unsigned)lz_cdiv(work, 256), 256, 0, s>>>(g, static_cast<const float*>(ws), p.splits);
+  const unsigned grid = (unsigned)lz_cdiv(M * lz_cdiv(N, 4), 256);
+  if (f16) splitk_reduce_kernel<FmtF16><<<grid, 256, 0, s>>>(g, static_cast<const float*>(ws), p.splits);
+  else splitk_reduce_kernel<FmtBF16><<<grid, 256, 0, s>>>(g, static_cast<const float*>(ws), p.splits);
   return lz_check_launch("lz_gemm(split-K reduce)");
 }
 
 // C = alpha * A . B^T (+ beta*C) (+ R) with A: [M,K] and B: [N,K] row-major,
 // never split along K (no workspace).
-LZ_EXPORT int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype,
-                         const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta,
-                         void* stream) {
-  return lz_gemm(A, lda, 1, B, ldb, 1, C, ldc, c_dtype, R, ldr, M, N, K, alpha, beta, nullptr, 0, stream);
+LZ_EXPORT int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int ab_dtype, void* C, int64_t ldc,
+                         int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha,
+                         float beta, void* stream) {
+  return lz_gemm(A, lda, 1, B, ldb, 1, ab_dtype, C, ldc, c_dtype, R, ldr, M, N, K, alpha, beta, nullptr, 0, stream);
 }
 
 // Fused gate|up projection + SwiGLU (reference model/llama.py:136-146, the

@@ -19,6 +19,10 @@
 // dtype codes shared with the Python side.
 #define LZ_F32 0
 #define LZ_BF16 1
+#define LZ_F16 2
+
+// Bytes per element of a dtype code.
+static inline int lz_esize(int dtype) { return dtype == LZ_F32 ? 4 : 2; }
 
 #define LZ_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -127,6 +131,32 @@ __device__ __forceinline__ bool lz_keep(uint64_t seed, uint64_t i, uint32_t thre
 // Rounds a float to the nearest bfloat16 value, kept as float.
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// IEEE binary16 <-> float (v_cvt_f32_f16 / v_cvt_f16_f32: round to nearest
+// even, overflow to infinity, as torch's `.to(torch.float16)`).  Storage is
+// the 16 bits, as for bfloat16.
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) { return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16); }
+__device__ __forceinline__ float round_h(float f) { return (float)(_Float16)f; }
+
+// The two 16-bit float formats as policies over uint16_t storage, for kernels
+// written once for both: to_f / from_f / pack2 (two values, low first) /
+// round (to the format and back).
+struct FmtBF16 {
+  static constexpr int kDtype = LZ_BF16;
+  static __device__ __forceinline__ float to_f(uint32_t h) { return bf2f((uint16_t)h); }
+  static __device__ __forceinline__ uint16_t from_f(float f) { return f2bf(f); }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  static __device__ __forceinline__ float round(float f) { return round_bf(f); }
+};
+struct FmtF16 {
+  static constexpr int kDtype = LZ_F16;
+  static __device__ __forceinline__ float to_f(uint32_t h) { return h2f((uint16_t)h); }
+  static __device__ __forceinline__ uint16_t from_f(float f) { return f2h(f); }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_f16x2(lo, hi); }
+  static __device__ __forceinline__ float round(float f) { return round_h(f); }
+};
+
 // sigmoid(g) = 1 / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal
 // (about 1 ulp in fp32, below the bf16 rounding of every output).
 __device__ __forceinline__ float sigmoid_hw(float g) {
@@ -166,6 +196,14 @@ struct Elem<uint16_t> {
   static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
   static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
   static __device__ __forceinline__ float round(float v) { return round_bf(v); }
+};
+
+// IEEE fp16 storage.
+template <>
+struct Elem<_Float16> {
+  static __device__ __forceinline__ float load(const _Float16* p, int64_t i) { return (float)p[i]; }
+  static __device__ __forceinline__ void store(_Float16* p, int64_t i, float v) { p[i] = (_Float16)v; }
+  static __device__ __forceinline__ float round(float v) { return round_h(v); }
 };
 
 // ---------------------------------------------------------------------------

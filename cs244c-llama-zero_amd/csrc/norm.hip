@@ -21,32 +21,35 @@ constexpr int kThreads = 64 * kRowsPerBlock;
 template <typename T>
 struct Pack8;
 
-template <>
-struct Pack8<uint16_t> {
-  static __device__ __forceinline__ void load(const uint16_t* p, float (&r)[8]) {
-    uint4 v = *reinterpret_cast<const uint4*>(p);
-    r[0] = bf2f(v.x & 0xffff); r[1] = bf2f(v.x >> 16);
-    r[2] = bf2f(v.y & 0xffff); r[3] = bf2f(v.y >> 16);
-    r[4] = bf2f(v.z & 0xffff); r[5] = bf2f(v.z >> 16);
-    r[6] = bf2f(v.w & 0xffff); r[7] = bf2f(v.w >> 16);
+// 16-bit formats: T is the storage type (uint16_t = bf16, _Float16 = fp16),
+// F the format policy.
+template <typename T, typename F>
+struct Pack8H {
+  static __device__ __forceinline__ void unpack(const uint4& v, float (&r)[8]) {
+    r[0] = F::to_f(v.x & 0xffff); r[1] = F::to_f(v.x >> 16);
+    r[2] = F::to_f(v.y & 0xffff); r[3] = F::to_f(v.y >> 16);
+    r[4] = F::to_f(v.z & 0xffff); r[5] = F::to_f(v.z >> 16);
+    r[6] = F::to_f(v.w & 0xffff); r[7] = F::to_f(v.w >> 16);
   }
-  static __device__ __forceinline__ void store(uint16_t* p, const float (&r)[8]) {
-    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]),
-                                              pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7]));
+  static __device__ __forceinline__ void load(const T* p, float (&r)[8]) {
+    unpack(*reinterpret_cast<const uint4*>(p), r);
+  }
+  static __device__ __forceinline__ void store(T* p, const float (&r)[8]) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(F::pack2(r[0], r[1]), F::pack2(r[2], r[3]),
+                                              F::pack2(r[4], r[5]), F::pack2(r[6], r[7]));
   }
   // non-temporal store (streamed output: measured 5% faster for the forward's y)
-  static __device__ __forceinline__ void store_nt(uint16_t* p, const float (&r)[8]) {
+  static __device__ __forceinline__ void store_nt(T* p, const float (&r)[8]) {
     typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
-    const v4u_t t = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7])};
+    const v4u_t t = {F::pack2(r[0], r[1]), F::pack2(r[2], r[3]), F::pack2(r[4], r[5]), F::pack2(r[6], r[7])};
     __builtin_nontemporal_store(t, reinterpret_cast<v4u_t*>(p));
   }
-  static __device__ __forceinline__ void unpack(const uint4& v, float (&r)[8]) {
-    r[0] = bf2f(v.x & 0xffff); r[1] = bf2f(v.x >> 16);
-    r[2] = bf2f(v.y & 0xffff); r[3] = bf2f(v.y >> 16);
-    r[4] = bf2f(v.z & 0xffff); r[5] = bf2f(v.z >> 16);
-    r[6] = bf2f(v.w & 0xffff); r[7] = bf2f(v.w >> 16);
-  }
 };
+
+template <>
+struct Pack8<uint16_t> : Pack8H<uint16_t, FmtBF16> {};
+template <>
+struct Pack8<_Float16> : Pack8H<_Float16, FmtF16> {};
 
 template <>
 struct Pack8<float> {
@@ -103,14 +106,14 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(const T* __restri
   }
 }
 
-// bf16 backward: workgroup b owns rows [b*rpb, (b+1)*rpb), its wave w takes
+// 16-bit backward (T = uint16_t for bf16, _Float16 for fp16): workgroup b owns rows [b*rpb, (b+1)*rpb), its wave w takes
 // rows w, w+4, ... of that range and loads the next one (x, dy and the
 // residual gradient) while it computes the current one.  The 4 waves' dw contributions are summed in LDS (in a fixed
 // order) into one fp32 partial row per workgroup: dw_part[b][cols].
-template <int NC>
-__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ rstd,
-    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ dres, uint16_t* __restrict__ dx,
+template <typename T, int NC>
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd16_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const float* __restrict__ rstd,
+    const T* __restrict__ dy, const T* __restrict__ dres, T* __restrict__ dx,
     float* __restrict__ dw_part, int64_t rows, int64_t rpb, int cols, int64_t ldx, int64_t lddy, int64_t lddx) {
   __shared__ float red[2][NC * 512];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -125,7 +128,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
       dwacc[j][e] = 0.f;
       wv[j][e] = 0.f;
     }
-    if (c < nchunk) Pack8<uint16_t>::load(w + 8 * c, wv[j]);
+    if (c < nchunk) Pack8<T>::load(w + 8 * c, wv[j]);
   }
   const float inv_n = 1.0f / (float)cols;
   uint4 xn[NC], gn[NC], rn[NC] = {};
@@ -157,8 +160,8 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
     for (int j = 0; j < NC; ++j) {
       if (lane + 64 * j < nchunk) {
         float xv[8], gv[8];
-        Pack8<uint16_t>::unpack(xc[j], xv);
-        Pack8<uint16_t>::unpack(gc[j], gv);
+        Pack8<T>::unpack(xc[j], xv);
+        Pack8<T>::unpack(gc[j], gv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           dot = fmaf(gv[e] * wv[j][e], xv[e], dot);
@@ -173,17 +176,17 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_bf16_kernel(
       const int c = lane + 64 * j;
       if (c < nchunk) {
         float xv[8], gv[8], o[8];
-        Pack8<uint16_t>::unpack(xc[j], xv);
-        Pack8<uint16_t>::unpack(gc[j], gv);
+        Pack8<T>::unpack(xc[j], xv);
+        Pack8<T>::unpack(gc[j], gv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = r * wv[j][e] * gv[e] - coef * xv[e];
         if (dres) {
           float rv[8];
-          Pack8<uint16_t>::unpack(rc[j], rv);
+          Pack8<T>::unpack(rc[j], rv);
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[e] += rv[e];
         }
-        Pack8<uint16_t>::store(dx + row * lddx + 8 * c, o);
+        Pack8<T>::store(dx + row * lddx + 8 * c, o);
       }
     }
   }
@@ -441,14 +444,11 @@ int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy
       const int64_t nblk = bwd_blocks(rows, cols), rpb = lz_cdiv(rows, nblk);
       LZ_REQUIRE(ws_bytes >= (nblk + kSlices) * (int64_t)cols * 4, "lz_rmsnorm_bwd: workspace too small (%lld bytes)",
                  (long long)ws_bytes);
-      const uint16_t *x16 = (const uint16_t*)x, *w16 = (const uint16_t*)w, *g16 = (const uint16_t*)dy,
-                     *r16 = (const uint16_t*)dres;
-      uint16_t* dx16 = (uint16_t*)dx;
       const unsigned grid = (unsigned)nblk;
-      if (cols <= 512) rmsnorm_bwd_bf16_kernel<1><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
-      else if (cols <= 1024) rmsnorm_bwd_bf16_kernel<2><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
-      else if (cols <= 2048) rmsnorm_bwd_bf16_kernel<4><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
-      else rmsnorm_bwd_bf16_kernel<8><<<grid, kThreads, 0, s>>>(x16, w16, rstd, g16, r16, dx16, ws, rows, rpb, cols, ldx, lddy, lddx);
+      if (cols <= 512) rmsnorm_bwd16_kernel<T, 1><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else if (cols <= 1024) rmsnorm_bwd16_kernel<T, 2><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else if (cols <= 2048) rmsnorm_bwd16_kernel<T, 4><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, rpb, cols, ldx, lddy, lddx);
+      else rmsnorm_bwd16_kernel<T, 8><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, rpb, cols, ldx, lddy, lddx);
       int rc = lz_check_launch("lz_rmsnorm_bwd");
       if (rc) return rc;
       if (dw) {
@@ -489,6 +489,7 @@ LZ_EXPORT int lz_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,
   if (rows == 0) return LZ_OK;
   if (dtype == LZ_BF16) return fwd_dispatch<uint16_t>(x, w, y, rstd, rows, (int)cols, ldx, ldy, eps, lz_stream(stream));
   if (dtype == LZ_F32) return fwd_dispatch<float>(x, w, y, rstd, rows, (int)cols, ldx, ldy, eps, lz_stream(stream));
+  if (dtype == LZ_F16) return fwd_dispatch<_Float16>(x, w, y, rstd, rows, (int)cols, ldx, ldy, eps, lz_stream(stream));
   return lz_set_error(LZ_EINVAL, "lz_rmsnorm_fwd: bad dtype %d", dtype);
 }
 
@@ -510,6 +511,9 @@ LZ_EXPORT int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, co
   if (dtype == LZ_F32)
     return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (float*)workspace, workspace_bytes, rows,
                                (int)cols, ldx, lddy, lddx, lz_stream(stream));
+  if (dtype == LZ_F16)
+    return bwd_dispatch<_Float16>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, (float*)workspace, workspace_bytes,
+                                  rows, (int)cols, ldx, lddy, lddx, lz_stream(stream));
   return lz_set_error(LZ_EINVAL, "lz_rmsnorm_bwd: bad dtype %d", dtype);
 }
 

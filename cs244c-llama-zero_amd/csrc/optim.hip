@@ -13,6 +13,7 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kFillF64 = 3;  // lz_fill's code for float64 (the norm accumulators)
 
 inline int stream_grid(int64_t work_items) {
   int64_t blocks = lz_cdiv(work_items, kThreads);
@@ -102,6 +103,17 @@ struct Vec4<uint16_t> {
   static __device__ __forceinline__ void store(uint16_t* p, int64_t i, const float (&r)[4]) {
     const u32x2_t x = {(uint32_t)f2bf(r[0]) | ((uint32_t)f2bf(r[1]) << 16),
                        (uint32_t)f2bf(r[2]) | ((uint32_t)f2bf(r[3]) << 16)};
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x2_t*>(p + i));
+  }
+};
+template <>
+struct Vec4<_Float16> {
+  static __device__ __forceinline__ void load(const _Float16* p, int64_t i, float (&r)[4]) {
+    const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p + i));
+    r[0] = h2f(x[0] & 0xffff); r[1] = h2f(x[0] >> 16); r[2] = h2f(x[1] & 0xffff); r[3] = h2f(x[1] >> 16);
+  }
+  static __device__ __forceinline__ void store(_Float16* p, int64_t i, const float (&r)[4]) {
+    const u32x2_t x = {pack_f16x2(r[0], r[1]), pack_f16x2(r[2], r[3])};
     __builtin_nontemporal_store(x, reinterpret_cast<u32x2_t*>(p + i));
   }
 };
@@ -210,14 +222,16 @@ __global__ void sumsq_vec4_f32_kernel(const float* __restrict__ x, int64_t n, do
 // norm = sqrt(sum of squares) rounded to fp32 (the reference reads an fp32
 // norm with .item()); scale = max/(norm + 1e-6) when clipping applies, else 1
 // (zero/stage0_ddp.py:66-71).
-__global__ void clip_finalize_kernel(const double* __restrict__ acc, float max_norm, float* __restrict__ norm_out,
-                                     float* __restrict__ scale_out) {
+__global__ void clip_finalize_kernel(const double* __restrict__ acc, float max_norm, float inv_grad_scale,
+                                     float* __restrict__ norm_out, float* __restrict__ scale_out) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    const float norm = (float)sqrt(*acc);
+    // the gradients carry a loss scale: their norm divided by it is the true
+    // norm, and the factor handed to AdamW unscales them as well as clipping
+    const float norm = (float)(sqrt(*acc) * (double)inv_grad_scale);
     float scale = 1.0f;
     if (max_norm > 0.0f && norm > max_norm) scale = (float)((double)max_norm / ((double)norm + 1e-6));
     if (norm_out) *norm_out = norm;
-    if (scale_out) *scale_out = scale;
+    if (scale_out) *scale_out = scale * inv_grad_scale;
   }
 }
 
@@ -278,6 +292,22 @@ struct Vec8<uint16_t> {
   }
   static __device__ __forceinline__ void store(uint16_t* p, const float (&r)[8]) {
     *reinterpret_cast<uint4*>(p) = make_uint4(pack(r[0], r[1]), pack(r[2], r[3]), pack(r[4], r[5]), pack(r[6], r[7]));
+  }
+};
+template <>
+struct Vec8<_Float16> {
+  static __device__ __forceinline__ void load(const _Float16* p, float (&r)[8]) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r[2 * k] = h2f(w[k] & 0xffff);
+      r[2 * k + 1] = h2f(w[k] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void store(_Float16* p, const float (&r)[8]) {
+    *reinterpret_cast<uint4*>(p) =
+        make_uint4(pack_f16x2(r[0], r[1]), pack_f16x2(r[2], r[3]), pack_f16x2(r[4], r[5]), pack_f16x2(r[6], r[7]));
   }
 };
 
@@ -629,6 +659,28 @@ __global__ void __launch_bounds__(kThreads) sumsq_multi_kernel(const MultiSegs t
   }
 }
 
+// Calls f with a value of the storage type of `dtype` (float, uint16_t for
+// bf16, _Float16 for fp16).
+template <typename Fn>
+int with_elem(int dtype, Fn&& f) {
+  if (dtype == LZ_F32) return f(float{});
+  if (dtype == LZ_BF16) return f(uint16_t{});
+  return f(_Float16{});
+}
+
+template <typename S, typename D>
+int cast_typed(const void* src, void* dst, int64_t n, hipStream_t s) {
+  if (lz_aligned16(src) && lz_aligned16(dst) && n >= 8) {
+    const int64_t n8 = n / 8, done = 8 * n8;
+    cast_vec8_kernel<S, D><<<vec_grid(n8), kThreads, 0, s>>>((const S*)src, (D*)dst, n8);
+    int rc = lz_check_launch("lz_cast");
+    if (rc || done == n) return rc;
+    return cast_typed<S, D>(static_cast<const S*>(src) + done, static_cast<D*>(dst) + done, n - done, s);
+  }
+  cast_kernel<S, D><<<stream_grid(n), kThreads, 0, s>>>((const S*)src, (D*)dst, n);
+  return lz_check_launch("lz_cast");
+}
+
 // ===========================================================================
 // Exported entry points.
 // ===========================================================================
@@ -658,8 +710,14 @@ int adamw_entry(float* p, float* m, float* v, const void* g, int g_dtype, void* 
   a.eps = (float)eps;
   a.neg_step = (float)(-(lr / bc1));
   hipStream_t s = lz_stream(stream);
-  const bool gb = g_dtype == LZ_BF16;
-  LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32, "lz_adamw: bad grad dtype %d", g_dtype);
+  const bool gb = g_dtype == LZ_BF16, gh = g_dtype == LZ_F16;
+  LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32 || g_dtype == LZ_F16, "lz_adamw: bad grad dtype %d", g_dtype);
+  if (gh) {  // fp16 models: fp16 gradients, fp16 (or no) parameter copy
+    if (p_out == nullptr || p_out_dtype == LZ_F32)
+      return launch_adamw<_Float16, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+    LZ_REQUIRE(p_out_dtype == LZ_F16, "lz_adamw: bad output dtype %d for fp16 gradients", p_out_dtype);
+    return launch_adamw<_Float16, _Float16>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+  }
   if (p_out == nullptr || p_out_dtype == LZ_F32) {
     return gb ? launch_adamw<uint16_t, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s)
               : launch_adamw<float, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
@@ -718,6 +776,8 @@ LZ_EXPORT int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* s
     else sumsq_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((const float*)x, n, acc);
   } else if (dtype == LZ_BF16) {
     sumsq_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((const uint16_t*)x, n, acc);
+  } else if (dtype == LZ_F16) {
+    sumsq_kernel<_Float16><<<stream_grid(n), kThreads, 0, s>>>((const _Float16*)x, n, acc);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_sumsq: bad dtype %d", dtype);
   }
@@ -765,8 +825,12 @@ LZ_EXPORT int lz_adamw_multi(const int64_t* table, int nseg, int g_dtype, int p_
                              const float* grad_scale, void* stream) {
   LZ_REQUIRE(table && nseg >= 0, "lz_adamw_multi: bad table");
   LZ_REQUIRE(hyper || step >= 1, "lz_adamw_multi: step must be >= 1");
-  LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32, "lz_adamw_multi: bad grad dtype %d", g_dtype);
-  LZ_REQUIRE(p_out_dtype == LZ_BF16 || p_out_dtype == LZ_F32, "lz_adamw_multi: bad output dtype %d", p_out_dtype);
+  LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32 || g_dtype == LZ_F16, "lz_adamw_multi: bad grad dtype %d",
+             g_dtype);
+  LZ_REQUIRE(p_out_dtype == LZ_BF16 || p_out_dtype == LZ_F32 || p_out_dtype == LZ_F16,
+             "lz_adamw_multi: bad output dtype %d", p_out_dtype);
+  LZ_REQUIRE((g_dtype == LZ_F16) == (p_out_dtype == LZ_F16) || p_out_dtype == LZ_F32,
+             "lz_adamw_multi: fp16 gradients go with fp16 (or fp32) parameters (%d, %d)", g_dtype, p_out_dtype);
   for (int r = 0; r < nseg; ++r) {
     const int64_t* row = table + (int64_t)r * 6;
     LZ_REQUIRE(row[5] >= 0, "lz_adamw_multi: negative size in row %d", r);
@@ -785,14 +849,16 @@ LZ_EXPORT int lz_adamw_multi(const int64_t* table, int nseg, int g_dtype, int p_
   a.eps = (float)eps;
   a.neg_step = (float)(-(lr / bc1));
   hipStream_t s = lz_stream(stream);
-  const bool gb = g_dtype == LZ_BF16, ob = p_out_dtype == LZ_BF16;
+  const bool gb = g_dtype == LZ_BF16, ob = p_out_dtype == LZ_BF16, gh = g_dtype == LZ_F16, oh = p_out_dtype == LZ_F16;
   for (int r0 = 0; r0 < nseg; r0 += kMultiSegs) {
     MultiSegs t;
     const int64_t chunks = fill_multi(t, table, 6, r0, min(nseg, r0 + kMultiSegs));
     if (chunks == 0) continue;
     LZ_REQUIRE(chunks < (1ll << 31), "lz_adamw_multi: too many chunks");
     const unsigned grid = (unsigned)chunks;
-    if (gb && ob) adamw_multi_kernel<uint16_t, uint16_t><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    if (gh && oh) adamw_multi_kernel<_Float16, _Float16><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    else if (gh) adamw_multi_kernel<_Float16, float><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
+    else if (gb && ob) adamw_multi_kernel<uint16_t, uint16_t><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
     else if (gb) adamw_multi_kernel<uint16_t, float><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
     else if (ob) adamw_multi_kernel<float, uint16_t><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
     else adamw_multi_kernel<float, float><<<grid, kThreads, 0, s>>>(t, a, grad_scale, hyper);
@@ -806,7 +872,7 @@ LZ_EXPORT int lz_adamw_multi(const int64_t* table, int nseg, int g_dtype, int p_
 // one launch per 24 tensors.
 LZ_EXPORT int lz_sumsq_multi(const int64_t* table, int nseg, int dtype, double* acc, void* stream) {
   LZ_REQUIRE(table && nseg >= 0 && acc, "lz_sumsq_multi: bad arguments");
-  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_sumsq_multi: bad dtype %d", dtype);
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32 || dtype == LZ_F16, "lz_sumsq_multi: bad dtype %d", dtype);
   for (int r = 0; r < nseg; ++r)
     LZ_REQUIRE(table[2 * r + 1] >= 0 && (table[2 * r + 1] == 0 || table[2 * r]), "lz_sumsq_multi: bad row %d", r);
   hipStream_t s = lz_stream(stream);
@@ -816,6 +882,7 @@ LZ_EXPORT int lz_sumsq_multi(const int64_t* table, int nseg, int dtype, double* 
     if (chunks == 0) continue;
     LZ_REQUIRE(chunks < (1ll << 31), "lz_sumsq_multi: too many chunks");
     if (dtype == LZ_BF16) sumsq_multi_kernel<uint16_t><<<(unsigned)chunks, kThreads, 0, s>>>(t, acc);
+    else if (dtype == LZ_F16) sumsq_multi_kernel<_Float16><<<(unsigned)chunks, kThreads, 0, s>>>(t, acc);
     else sumsq_multi_kernel<float><<<(unsigned)chunks, kThreads, 0, s>>>(t, acc);
     int rc = lz_check_launch("lz_sumsq_multi");
     if (rc) return rc;
@@ -823,9 +890,11 @@ LZ_EXPORT int lz_sumsq_multi(const int64_t* table, int nseg, int dtype, double* 
   return LZ_OK;
 }
 
-LZ_EXPORT int lz_clip_finalize(const double* acc, float max_norm, float* norm_out, float* scale_out, void* stream) {
+LZ_EXPORT int lz_clip_finalize(const double* acc, float max_norm, float inv_grad_scale, float* norm_out,
+                               float* scale_out, void* stream) {
   LZ_REQUIRE(acc, "lz_clip_finalize: null accumulator");
-  clip_finalize_kernel<<<1, 64, 0, lz_stream(stream)>>>(acc, max_norm, norm_out, scale_out);
+  LZ_REQUIRE(inv_grad_scale > 0.f, "lz_clip_finalize: inverse loss scale must be positive");
+  clip_finalize_kernel<<<1, 64, 0, lz_stream(stream)>>>(acc, max_norm, inv_grad_scale, norm_out, scale_out);
   return lz_check_launch("lz_clip_finalize");
 }
 
@@ -851,7 +920,16 @@ LZ_EXPORT int lz_fill(void* x, int dtype, int64_t n, double value, void* stream)
     } else {
       fill_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, h);
     }
-  } else if (dtype == 2) {  // float64 (accumulators)
+  } else if (dtype == LZ_F16) {
+    const _Float16 h = (_Float16)value;  // host conversion, round to nearest even
+    const uint16_t hb = __builtin_bit_cast(uint16_t, h);
+    if (lz_aligned16(x) && n % 8 == 0) {
+      const uint32_t w = (uint32_t)hb | ((uint32_t)hb << 16);
+      fill16_kernel<<<flat_grid(n / 8), kThreads, 0, s>>>((uint4*)x, n / 8, make_uint4(w, w, w, w));
+    } else {
+      fill_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, hb);
+    }
+  } else if (dtype == kFillF64) {  // float64 (accumulators)
     fill_kernel<double><<<stream_grid(n), kThreads, 0, s>>>((double*)x, n, value);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_fill: bad dtype %d", dtype);
@@ -861,29 +939,16 @@ LZ_EXPORT int lz_fill(void* x, int dtype, int64_t n, double value, void* stream)
 
 LZ_EXPORT int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream) {
   LZ_REQUIRE(n >= 0, "lz_cast: negative n");
+  LZ_REQUIRE(src_dtype >= LZ_F32 && src_dtype <= LZ_F16 && dst_dtype >= LZ_F32 && dst_dtype <= LZ_F16,
+             "lz_cast: bad dtypes %d->%d", src_dtype, dst_dtype);
   if (n == 0) return LZ_OK;
-  hipStream_t s = lz_stream(stream);
-  if ((src_dtype == LZ_F32 || src_dtype == LZ_BF16) && (dst_dtype == LZ_F32 || dst_dtype == LZ_BF16) &&
-      lz_aligned16(src) && lz_aligned16(dst) && n >= 8) {
-    const int64_t n8 = n / 8, done = 8 * n8;
-    const unsigned g8 = vec_grid(n8);
-    if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) cast_vec8_kernel<float, uint16_t><<<g8, kThreads, 0, s>>>((const float*)src, (uint16_t*)dst, n8);
-    else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) cast_vec8_kernel<uint16_t, float><<<g8, kThreads, 0, s>>>((const uint16_t*)src, (float*)dst, n8);
-    else if (src_dtype == LZ_F32) cast_vec8_kernel<float, float><<<g8, kThreads, 0, s>>>((const float*)src, (float*)dst, n8);
-    else cast_vec8_kernel<uint16_t, uint16_t><<<g8, kThreads, 0, s>>>((const uint16_t*)src, (uint16_t*)dst, n8);
-    int rc = lz_check_launch("lz_cast");
-    if (rc || done == n) return rc;
-    const size_t ss = src_dtype == LZ_F32 ? 4 : 2, ds = dst_dtype == LZ_F32 ? 4 : 2;
-    return lz_cast(static_cast<const char*>(src) + done * ss, src_dtype, static_cast<char*>(dst) + done * ds, dst_dtype,
-                   n - done, stream);
-  }
-  const int g = stream_grid(n);
-  if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) cast_kernel<float, uint16_t><<<g, kThreads, 0, s>>>((const float*)src, (uint16_t*)dst, n);
-  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) cast_kernel<uint16_t, float><<<g, kThreads, 0, s>>>((const uint16_t*)src, (float*)dst, n);
-  else if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) cast_kernel<float, float><<<g, kThreads, 0, s>>>((const float*)src, (float*)dst, n);
-  else if (src_dtype == LZ_BF16 && dst_dtype == LZ_BF16) cast_kernel<uint16_t, uint16_t><<<g, kThreads, 0, s>>>((const uint16_t*)src, (uint16_t*)dst, n);
-  else return lz_set_error(LZ_EINVAL, "lz_cast: bad dtypes %d->%d", src_dtype, dst_dtype);
-  return lz_check_launch("lz_cast");
+  return with_elem(src_dtype, [&](auto s0) {
+    using S = decltype(s0);
+    return with_elem(dst_dtype, [&](auto d0) {
+      using D = decltype(d0);
+      return cast_typed<S, D>(src, dst, n, lz_stream(stream));
+    });
+  });
 }
 
 LZ_EXPORT int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n, float alpha, void* stream) {
@@ -901,6 +966,7 @@ LZ_EXPORT int lz_axpy_f32(float* dst, const void* src, int src_dtype, int64_t n,
                        n - done, alpha, stream);
   }
   if (src_dtype == LZ_BF16) axpy_f32_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>(dst, (const uint16_t*)src, n, alpha, unit);
+  else if (src_dtype == LZ_F16) axpy_f32_kernel<_Float16><<<stream_grid(n), kThreads, 0, s>>>(dst, (const _Float16*)src, n, alpha, unit);
   else if (src_dtype == LZ_F32) axpy_f32_kernel<float><<<stream_grid(n), kThreads, 0, s>>>(dst, (const float*)src, n, alpha, unit);
   else return lz_set_error(LZ_EINVAL, "lz_axpy_f32: bad dtype %d", src_dtype);
   return lz_check_launch("lz_axpy_f32");
@@ -911,6 +977,7 @@ LZ_EXPORT int lz_scale_dev(void* x, int dtype, int64_t n, const float* scale, vo
   if (n == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   if (dtype == LZ_BF16) scale_dev_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, scale);
+  else if (dtype == LZ_F16) scale_dev_kernel<_Float16><<<stream_grid(n), kThreads, 0, s>>>((_Float16*)x, n, scale);
   else if (dtype == LZ_F32) scale_dev_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)x, n, scale);
   else return lz_set_error(LZ_EINVAL, "lz_scale_dev: bad dtype %d", dtype);
   return lz_check_launch("lz_scale_dev");
@@ -921,6 +988,7 @@ LZ_EXPORT int lz_add_inplace(void* dst, const void* src, int dtype, int64_t n, v
   if (n == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   if (dtype == LZ_BF16) add_inplace_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)dst, (const uint16_t*)src, n);
+  else if (dtype == LZ_F16) add_inplace_kernel<_Float16><<<stream_grid(n), kThreads, 0, s>>>((_Float16*)dst, (const _Float16*)src, n);
   else if (dtype == LZ_F32) add_inplace_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)dst, (const float*)src, n);
   else return lz_set_error(LZ_EINVAL, "lz_add_inplace: bad dtype %d", dtype);
   return lz_check_launch("lz_add_inplace");
@@ -931,6 +999,7 @@ LZ_EXPORT int lz_scale_inplace(void* x, int dtype, int64_t n, float alpha, void*
   if (n == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   if (dtype == LZ_BF16) scale_kernel<uint16_t><<<stream_grid(n), kThreads, 0, s>>>((uint16_t*)x, n, alpha);
+  else if (dtype == LZ_F16) scale_kernel<_Float16><<<stream_grid(n), kThreads, 0, s>>>((_Float16*)x, n, alpha);
   else if (dtype == LZ_F32) scale_kernel<float><<<stream_grid(n), kThreads, 0, s>>>((float*)x, n, alpha);
   else return lz_set_error(LZ_EINVAL, "lz_scale_inplace: bad dtype %d", dtype);
   return lz_check_launch("lz_scale_inplace");

@@ -167,18 +167,26 @@ LZ_EXPORT int lz_rope_table(void* cos_t, void* sin_t, int dtype, int64_t seq, in
   if (seq == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
   const int g = grid_for(seq * hd / 2);
-  const int key = dtype * 2 + freq_dtype;
+  LZ_REQUIRE(dtype >= LZ_F32 && dtype <= LZ_F16 && freq_dtype >= LZ_F32 && freq_dtype <= LZ_F16,
+             "lz_rope_table: bad dtypes %d/%d", dtype, freq_dtype);
+  const int key = dtype * 3 + freq_dtype;
   switch (key) {
-    case LZ_BF16 * 2 + LZ_BF16:
+    case LZ_F16 * 3 + LZ_F16:
+      rope_table_kernel<_Float16, _Float16><<<g, 256, 0, s>>>((_Float16*)cos_t, (_Float16*)sin_t, seq, (int)hd, (const _Float16*)inv_freq);
+      break;
+    case LZ_F16 * 3 + LZ_F32:
+      rope_table_kernel<_Float16, float><<<g, 256, 0, s>>>((_Float16*)cos_t, (_Float16*)sin_t, seq, (int)hd, (const float*)inv_freq);
+      break;
+    case LZ_BF16 * 3 + LZ_BF16:
       rope_table_kernel<uint16_t, uint16_t><<<g, 256, 0, s>>>((uint16_t*)cos_t, (uint16_t*)sin_t, seq, (int)hd, (const uint16_t*)inv_freq);
       break;
-    case LZ_BF16 * 2 + LZ_F32:
+    case LZ_BF16 * 3 + LZ_F32:
       rope_table_kernel<uint16_t, float><<<g, 256, 0, s>>>((uint16_t*)cos_t, (uint16_t*)sin_t, seq, (int)hd, (const float*)inv_freq);
       break;
-    case LZ_F32 * 2 + LZ_F32:
+    case LZ_F32 * 3 + LZ_F32:
       rope_table_kernel<float, float><<<g, 256, 0, s>>>((float*)cos_t, (float*)sin_t, seq, (int)hd, (const float*)inv_freq);
       break;
-    case LZ_F32 * 2 + LZ_BF16:
+    case LZ_F32 * 3 + LZ_BF16:
       rope_table_kernel<float, uint16_t><<<g, 256, 0, s>>>((float*)cos_t, (float*)sin_t, seq, (int)hd, (const uint16_t*)inv_freq);
       break;
     default:
@@ -195,8 +203,11 @@ LZ_EXPORT int lz_rope(void* x, int dtype, int64_t ld, int64_t rows, int64_t seq,
   LZ_REQUIRE(ld >= nheads * hd, "lz_rope: leading dimension %lld < %lld", (long long)ld, (long long)(nheads * hd));
   if (rows == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
-  const int esz = dtype == LZ_BF16 ? 2 : 4, vec = 16 / esz;
-  if ((dtype == LZ_BF16 || dtype == LZ_F32) && (hd / 2) % vec == 0 && (ld * esz) % 16 == 0 && lz_aligned16(x) &&
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32 || dtype == LZ_F16, "lz_rope: bad dtype %d", dtype);
+  const int esz = lz_esize(dtype), vec = 16 / esz;
+  // (fp16 takes the element-wise kernel: the vector kernel's fp16 instance
+  // does not compile with this file's flags)
+  if (dtype != LZ_F16 && (hd / 2) % vec == 0 && (ld * esz) % 16 == 0 && lz_aligned16(x) &&
       lz_aligned16(cos_t) && lz_aligned16(sin_t)) {
     const int64_t work = rows * (hd / 2 / vec) * ((nheads + 3) / 4);
     LZ_REQUIRE(work < (1ll << 31) && seq < (1ll << 31), "lz_rope: too many rows");
@@ -218,6 +229,9 @@ LZ_EXPORT int lz_rope(void* x, int dtype, int64_t ld, int64_t rows, int64_t seq,
   } else if (dtype == LZ_F32) {
     if (backward) rope_kernel<float, true><<<g, 256, 0, s>>>((float*)x, ld, rows, seq, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
     else rope_kernel<float, false><<<g, 256, 0, s>>>((float*)x, ld, rows, seq, (int)nheads, (int)hd, (const float*)cos_t, (const float*)sin_t, pos_offset);
+  } else if (dtype == LZ_F16) {
+    if (backward) rope_kernel<_Float16, true><<<g, 256, 0, s>>>((_Float16*)x, ld, rows, seq, (int)nheads, (int)hd, (const _Float16*)cos_t, (const _Float16*)sin_t, pos_offset);
+    else rope_kernel<_Float16, false><<<g, 256, 0, s>>>((_Float16*)x, ld, rows, seq, (int)nheads, (int)hd, (const _Float16*)cos_t, (const _Float16*)sin_t, pos_offset);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_rope: bad dtype %d", dtype);
   }

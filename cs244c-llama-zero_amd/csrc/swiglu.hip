@@ -143,6 +143,8 @@ LZ_EXPORT int lz_swiglu_fwd(const void* g, int64_t ldg, const void* u, int64_t l
       swiglu_fwd_kernel<uint16_t><<<grid_for(rows * cols), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)h, ldh, rows, cols);
   } else if (dtype == LZ_F32) {
     swiglu_fwd_kernel<float><<<grid_for(rows * cols), 256, 0, s>>>((const float*)g, ldg, (const float*)u, ldu, (float*)h, ldh, rows, cols);
+  } else if (dtype == LZ_F16) {
+    swiglu_fwd_kernel<_Float16><<<grid_for(rows * cols), 256, 0, s>>>((const _Float16*)g, ldg, (const _Float16*)u, ldu, (_Float16*)h, ldh, rows, cols);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_swiglu_fwd: bad dtype %d", dtype);
   }
@@ -164,6 +166,8 @@ LZ_EXPORT int lz_swiglu_bwd(const void* g, int64_t ldg, const void* u, int64_t l
       swiglu_bwd_kernel<uint16_t><<<grid_for(rows * cols), 256, 0, s>>>((const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (const uint16_t*)dh, lddh, (uint16_t*)dg, lddg, (uint16_t*)du, lddu, rows, cols);
   } else if (dtype == LZ_F32) {
     swiglu_bwd_kernel<float><<<grid_for(rows * cols), 256, 0, s>>>((const float*)g, ldg, (const float*)u, ldu, (const float*)dh, lddh, (float*)dg, lddg, (float*)du, lddu, rows, cols);
+  } else if (dtype == LZ_F16) {
+    swiglu_bwd_kernel<_Float16><<<grid_for(rows * cols), 256, 0, s>>>((const _Float16*)g, ldg, (const _Float16*)u, ldu, (const _Float16*)dh, lddh, (_Float16*)dg, lddg, (_Float16*)du, lddu, rows, cols);
   } else {
     return lz_set_error(LZ_EINVAL, "lz_swiglu_bwd: bad dtype %d", dtype);
   }

@@ -66,8 +66,9 @@ LZ_EXPORT int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, in
   LZ_REQUIRE(rows >= 0 && cols >= 0 && lds >= cols && ldd >= cols, "lz_copy2d: bad shape");
   if (rows == 0 || cols == 0) return LZ_OK;
   hipStream_t s = lz_stream(stream);
-  const int64_t esz = dtype == LZ_BF16 ? 2 : 4;
-  if ((dtype == LZ_BF16 || dtype == LZ_F32) && lz_aligned16(src) && lz_aligned16(dst) && (cols * esz) % 16 == 0 &&
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32 || dtype == LZ_F16, "lz_copy2d: bad dtype %d", dtype);
+  const int64_t esz = lz_esize(dtype);  // a copy: the 16-bit formats move alike
+  if (lz_aligned16(src) && lz_aligned16(dst) && (cols * esz) % 16 == 0 &&
       (lds * esz) % 16 == 0 && (ldd * esz) % 16 == 0) {
     int64_t vr = rows, vc = cols * esz / 16, vls = lds * esz / 16, vld = ldd * esz / 16;
     if (vls == vc && vld == vc) {  // both contiguous: one long row
@@ -80,9 +81,8 @@ LZ_EXPORT int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, in
     return lz_check_launch("lz_copy2d");
   }
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(lz_cdiv(rows * cols, 256), (int64_t)lz_num_cus() * 16));
-  if (dtype == LZ_BF16) copy2d_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols);
-  else if (dtype == LZ_F32) copy2d_kernel<float><<<grid, 256, 0, s>>>((const float*)src, lds, (float*)dst, ldd, rows, cols);
-  else return lz_set_error(LZ_EINVAL, "lz_copy2d: bad dtype %d", dtype);
+  if (dtype == LZ_F32) copy2d_kernel<float><<<grid, 256, 0, s>>>((const float*)src, lds, (float*)dst, ldd, rows, cols);
+  else copy2d_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols);
   return lz_check_launch("lz_copy2d");
 }
 
@@ -95,7 +95,7 @@ LZ_EXPORT int lz_transpose(const void* src, void* dst, int dtype, int64_t nb1, i
   LZ_REQUIRE(lz_cdiv(rows, kTile) < 65536, "lz_transpose: too many rows");
   dim3 grid((unsigned)lz_cdiv(cols, kTile), (unsigned)lz_cdiv(rows, kTile), (unsigned)(nb1 * nb2));
   hipStream_t s = lz_stream(stream);
-  if (dtype == LZ_BF16)
+  if (dtype == LZ_BF16 || dtype == LZ_F16)  // a permutation: the 16-bit formats move alike
     transpose_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)src, (uint16_t*)dst, nb2, rows, cols, lds, sb1s, sb2s,
                                                      ldd, sb1d, sb2d);
   else if (dtype == LZ_F32)

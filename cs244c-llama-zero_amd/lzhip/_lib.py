@@ -19,6 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 F32 = 0
 BF16 = 1
+F16 = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -38,7 +39,7 @@ SIGNATURES = {
     "lz_sumsq": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "lz_adamw_multi": (_i32, [_vp, _i32, _i32, _i32, _f64, _f64, _f64, _f64, _f64, _i64, _vp, _vp, _vp]),
     "lz_sumsq_multi": (_i32, [_vp, _i32, _i32, _vp, _vp]),
-    "lz_clip_finalize": (_i32, [_vp, _f32, _vp, _vp, _vp]),
+    "lz_clip_finalize": (_i32, [_vp, _f32, _f32, _vp, _vp, _vp]),
     "lz_mt_gather": (_i32, [_vp, _i32, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),
     "lz_mt_scatter": (_i32, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp]),
     "lz_mt_gather_host": (_i32, [_vp, _i32, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),
@@ -67,11 +68,11 @@ SIGNATURES = {
     "lz_ce_bwd": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "lz_transpose": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "lz_copy2d": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp]),
-    "lz_gemm_nt": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
+    "lz_gemm_nt": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
     "lz_gemm_swiglu": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "lz_gemm_rope": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
-    "lz_gemm": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp,
-                       _i64, _vp]),
+    "lz_gemm": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32,
+                       _vp, _i64, _vp]),
     "lz_gemm_f32": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32,
                            _f32, _vp, _i64, _vp]),
     "lz_gemm_f32_workspace": (_i64, [_i64, _i64, _i64]),

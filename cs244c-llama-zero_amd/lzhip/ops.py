@@ -14,16 +14,18 @@ from typing import Dict, Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from ._lib import BF16, F32
+from ._lib import BF16, F16, F32
 
-_DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+# 16-bit float formats (the MFMA GEMM and attention operands)
+HALF_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def dtype_code(t: torch.Tensor) -> int:
     try:
         return _DTYPES[t.dtype]
     except KeyError:
-        raise TypeError(f"llama-zero HIP kernels support float32 and bfloat16 tensors, got {t.dtype}") from None
+        raise TypeError(f"llama-zero HIP kernels support float32, bfloat16 and float16 tensors, got {t.dtype}") from None
 
 
 def require_gpu(*tensors: Optional[torch.Tensor]) -> None:
@@ -186,11 +188,14 @@ def adamw_multi_(ps, ms, vs, gs, p_outs, lr: float, beta1: float, beta2: float, 
               float(weight_decay), int(step), _ptr(hyper), _ptr(grad_scale), stream_ptr(ps[0].device))
 
 
-def clip_finalize(acc: torch.Tensor, max_norm: float, norm_out: torch.Tensor, scale_out: torch.Tensor) -> None:
+def clip_finalize(acc: torch.Tensor, max_norm: float, norm_out: torch.Tensor, scale_out: torch.Tensor,
+                  inv_grad_scale: float = 1.0) -> None:
+    """norm_out = sqrt(acc) * inv_grad_scale (the true norm of gradients that
+    carry a loss scale); scale_out = inv_grad_scale * the clip factor."""
     require_gpu(acc, norm_out, scale_out)
     _lib.call(
-        "lz_clip_finalize", acc.data_ptr(), float(max_norm), norm_out.data_ptr(), scale_out.data_ptr(),
-        stream_ptr(acc.device),
+        "lz_clip_finalize", acc.data_ptr(), float(max_norm), float(inv_grad_scale), norm_out.data_ptr(),
+        scale_out.data_ptr(), stream_ptr(acc.device),
     )
 
 
@@ -198,7 +203,7 @@ def fill_(x: torch.Tensor, value: float) -> torch.Tensor:
     require_gpu(x)
     if not x.is_contiguous():
         raise ValueError("fill_ needs a contiguous tensor")
-    code = 2 if x.dtype == torch.float64 else dtype_code(x)
+    code = 3 if x.dtype == torch.float64 else dtype_code(x)
     _lib.call("lz_fill", x.data_ptr(), code, x.numel(), float(value), stream_ptr(x.device))
     return x
 
@@ -628,17 +633,18 @@ def _gemm_operand(t: torch.Tensor, kmajor: bool) -> Tuple[torch.Tensor, bool]:
 def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool = True,
          out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
          residual: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
-    """out[M,N] = alpha * sum_k A(m,k) B(n,k) (+ beta*out) (+ residual), bf16
-    operands, fp32 accumulation.  `a` is [M,K] when a_kmajor else [K,M];
+    """out[M,N] = alpha * sum_k A(m,k) B(n,k) (+ beta*out) (+ residual), two
+    bf16, two fp16 or two fp32 operands, fp32 accumulation, the output in
+    the operands' dtype or fp32.  `a` is [M,K] when a_kmajor else [K,M];
     `b` is [N,K] when b_kmajor else [K,N].  So x.W^T is gemm(x, W),
     dy.W is gemm(dy, W, b_kmajor=False) and dy^T.x is
     gemm(dy, x, a_kmajor=False, b_kmajor=False)."""
     require_gpu(a, b, out, residual)
     if a.dtype == torch.float32 and b.dtype == torch.float32:
         return _gemm_f32(a, b, a_kmajor, b_kmajor, out, out_dtype, residual, alpha, beta)
-    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+    if a.dtype != b.dtype or a.dtype not in HALF_DTYPES:
         raise TypeError(
-            f"the MFMA GEMM takes two bfloat16 or two float32 operands (got {a.dtype}, {b.dtype})"
+            f"the MFMA GEMM takes two bfloat16, two float16 or two float32 operands (got {a.dtype}, {b.dtype})"
         )
     M, K = a.shape if a_kmajor else (a.shape[1], a.shape[0])
     N, K2 = b.shape if b_kmajor else (b.shape[1], b.shape[0])
@@ -655,8 +661,8 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
     Kp = _round8(K) if (a_kmajor or b_kmajor) else K
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype or a.dtype, device=a.device)
-    if residual is not None and (residual.dtype != torch.bfloat16 or tuple(residual.shape) != (M, N)):
-        raise ValueError("residual must be a bf16 [M, N] view")
+    if residual is not None and (residual.dtype != a.dtype or tuple(residual.shape) != (M, N)):
+        raise ValueError(f"residual must be a {a.dtype} [M, N] view")
     lib = _lib.load()
     ws_bytes = int(lib.lz_gemm_workspace(M, N, Kp, int(a_kmajor), int(b_kmajor)))
     ws = torch.empty(((ws_bytes + 15) // 16) * 4, dtype=torch.float32, device=a.device) if ws_bytes else None
@@ -666,7 +672,7 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
         end = torch.cuda.Event(enable_timing=True)
         start.record()
     _lib.call("lz_gemm", a.data_ptr(), _row_stride(a), int(a_kmajor), b.data_ptr(), _row_stride(b), int(b_kmajor),
-              out.data_ptr(), _row_stride(out), dtype_code(out), _ptr(residual),
+              dtype_code(a), out.data_ptr(), _row_stride(out), dtype_code(out), _ptr(residual),
               _row_stride(residual) if residual is not None else 0, M, N, Kp, float(alpha), float(beta), _ptr(ws),
               ws_bytes if ws is not None else 0, stream_ptr(a.device))
     if probe is not None:
@@ -863,9 +869,9 @@ def _attn_mask_args(mask: torch.Tensor, B: int, H: int, S: int):
     """(kind, strides array) of an attention mask broadcastable to [B, H, S, S]
     (bool: True keeps the score; fp32/bf16: added to it)."""
     require_gpu(mask)
-    kinds = {torch.bool: 1, torch.float32: 2, torch.bfloat16: 3}
+    kinds = {torch.bool: 1, torch.float32: 2, torch.bfloat16: 3, torch.float16: 4}
     if mask.dtype not in kinds:
-        raise TypeError(f"attention mask must be bool, float32 or bfloat16 (got {mask.dtype})")
+        raise TypeError(f"attention mask must be bool, float32, bfloat16 or float16 (got {mask.dtype})")
     try:
         strides = mask.expand(B, H, S, S).stride()
     except RuntimeError as e:

@@ -9,9 +9,16 @@ low-precision dtype get an fp32 master copy and fp32 moments; the kernel writes
 the rounded parameter back.  clip_grad_norm_() computes the global gradient
 norm and the clip factor on the device; the factor is folded into the next
 step() instead of rescaling every gradient in a separate pass.
+
+LossScaler is torch.cuda.amp.GradScaler's dynamic loss scaling for fp16
+training (reference train.py:213-214,254-269) over FusedAdamW: the backward
+is seeded with the scale instead of multiplying the loss, unscaling rides on
+clip_grad_norm_'s factor, and a step whose gradients hold an inf or NaN is
+skipped and halves the scale.
 """
 from __future__ import annotations
 
+import math
 from typing import Iterable, Optional
 
 import torch
@@ -42,9 +49,11 @@ class FusedAdamW(torch.optim.Optimizer):
                     yield group, p
 
     @torch.no_grad()
-    def clip_grad_norm_(self, max_norm: float) -> torch.Tensor:
+    def clip_grad_norm_(self, max_norm: float, inv_grad_scale: float = 1.0) -> torch.Tensor:
         """Returns the global L2 norm of all gradients (a device scalar) and
-        arms the clip factor max/(norm+1e-6) (when norm > max) for step()."""
+        arms the clip factor max/(norm+1e-6) (when norm > max) for step().
+        With inv_grad_scale (1 / a loss scale the gradients carry) the norm
+        returned is the unscaled one, and the armed factor also unscales."""
         dev = None
         for _, p in self._params_with_grad():
             dev = p.grad.device
@@ -60,9 +69,13 @@ class FusedAdamW(torch.optim.Optimizer):
             ops.sumsq_multi_(grads, acc)
         norm = torch.empty((1,), dtype=torch.float32, device=dev)
         scale = torch.empty((1,), dtype=torch.float32, device=dev)
-        ops.clip_finalize(acc, float(max_norm), norm, scale)
-        self._grad_scale = scale if max_norm > 0 else None
+        ops.clip_finalize(acc, float(max_norm), norm, scale, inv_grad_scale)
+        self._grad_scale = scale if (max_norm > 0 or inv_grad_scale != 1.0) else None
         return norm.view(())
+
+    def discard_step(self) -> None:
+        """Drops the factor armed by clip_grad_norm_ when step() is skipped."""
+        self._grad_scale = None
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -126,3 +139,86 @@ class FusedAdamW(torch.optim.Optimizer):
                              hyper=hypers.get(id(group)))
         self._grad_scale = None
         return loss
+
+
+class LossScaler:
+    """Dynamic loss scaling with torch.cuda.amp.GradScaler's schedule and
+    defaults (reference train.py:213-214,254-269): gradients are computed for
+    loss * scale; a step whose gradients hold an inf or NaN is skipped and
+    the scale multiplied by backoff_factor; after growth_interval finite steps
+    in a row it is multiplied by growth_factor.  Disabled, it is the
+    identity.  Use with FusedAdamW:
+
+        seed = scaler.scale_value() / accum_steps     # backward's seed
+        ...backward of every micro-batch...
+        norm = scaler.unscale_(optimizer, max_norm)  # true norm, clip armed
+        scaler.step(optimizer, float(norm))          # skipped if not finite
+        scaler.update()
+    """
+
+    def __init__(self, init_scale: float = 2.0 ** 16, growth_factor: float = 2.0, backoff_factor: float = 0.5,
+                 growth_interval: int = 2000, enabled: bool = True) -> None:
+        if not (growth_factor > 1.0 and 0.0 < backoff_factor < 1.0 and growth_interval > 0 and init_scale > 0):
+            raise ValueError("invalid loss scaler settings")
+        self._enabled = bool(enabled)
+        self._scale = float(init_scale)
+        self.growth_factor = float(growth_factor)
+        self.backoff_factor = float(backoff_factor)
+        self.growth_interval = int(growth_interval)
+        self._growth_tracker = 0
+        self._found_inf: Optional[bool] = None
+
+    def is_enabled(self) -> bool:
+        return self._enabled
+
+    def scale_value(self) -> float:
+        """The current scale (1.0 when disabled)."""
+        return self._scale if self._enabled else 1.0
+
+    def get_scale(self) -> float:
+        return self.scale_value()
+
+    def unscale_(self, optimizer: FusedAdamW, max_norm: float = 0.0) -> torch.Tensor:
+        """The global norm of the unscaled gradients (device scalar; inf or
+        NaN when they overflowed), with optimizer's next step armed to unscale
+        and, when max_norm > 0, clip them."""
+        return optimizer.clip_grad_norm_(max_norm, 1.0 / self.scale_value())
+
+    def step(self, optimizer: FusedAdamW, grad_norm: float) -> bool:
+        """optimizer.step() unless grad_norm is inf or NaN; returns whether
+        the step ran."""
+        finite = math.isfinite(grad_norm)
+        self._found_inf = not finite
+        if finite or not self._enabled:
+            optimizer.step()
+            return True
+        optimizer.discard_step()
+        return False
+
+    def update(self) -> None:
+        if not self._enabled or self._found_inf is None:
+            return
+        if self._found_inf:
+            self._scale *= self.backoff_factor
+            self._growth_tracker = 0
+        else:
+            self._growth_tracker += 1
+            if self._growth_tracker == self.growth_interval:
+                self._scale *= self.growth_factor
+                self._growth_tracker = 0
+        self._found_inf = None
+
+    def state_dict(self) -> dict:
+        if not self._enabled:
+            return {}
+        return {"scale": self._scale, "growth_factor": self.growth_factor, "backoff_factor": self.backoff_factor,
+                "growth_interval": self.growth_interval, "_growth_tracker": self._growth_tracker}
+
+    def load_state_dict(self, state: dict) -> None:
+        if not state:
+            return
+        self._scale = float(state["scale"])
+        self.growth_factor = float(state["growth_factor"])
+        self.backoff_factor = float(state["backoff_factor"])
+        self.growth_interval = int(state["growth_interval"])
+        self._growth_tracker = int(state["_growth_tracker"])

@@ -267,7 +267,10 @@ class LlamaForCausalLM(nn.Module):
         x = self._call_parametrized_module("norm", self.norm, x)
         logits = None
         chunked = self._should_chunk_training_loss(input_ids)
-        if labels is not None and not return_logits and self.fused_lm_head_loss:
+        # fp16 takes the unfused loss: the fused one forms the logit gradient
+        # for a unit loss gradient before the (loss-scaled) gradient arrives,
+        # and (softmax - onehot) / count underflows fp16's range
+        if labels is not None and not return_logits and self.fused_lm_head_loss and x.dtype != torch.float16:
             if labels.shape != input_ids.shape:
                 raise ValueError(
                     f"labels should have same shape as input_ids; got {tuple(labels.shape)} vs {tuple(input_ids.shape)}"

@@ -31,7 +31,7 @@ from data import (
 )
 from lzhip.functional import GradSink, pack_parameters_
 from lzhip.ops import fill_
-from lzhip.optim import FusedAdamW
+from lzhip.optim import FusedAdamW, LossScaler
 from model import MODEL_SIZES, LlamaForCausalLM, build_config, estimate_num_parameters, human_readable_count
 
 DATA_MODES = ["fineweb", "synthetic", "synthetic-uniform"]
@@ -150,8 +150,6 @@ def save_checkpoint(save_dir: str, step: int, model: LlamaForCausalLM, optimizer
 def train(args: argparse.Namespace) -> None:
     set_seed(args.seed)
     device = choose_device(args.device)
-    if args.dtype == "float16":
-        raise NotImplementedError("float16 training (GradScaler) is not supported by the HIP kernels; use bfloat16")
 
     base_vocab = args.synthetic_vocab_size
     cfg = build_config(size=args.model_size, vocab_size=base_vocab, max_seq_len=args.seq_len)
@@ -172,6 +170,8 @@ def train(args: argparse.Namespace) -> None:
     model.set_activation_checkpointing(args.activation_checkpointing)
     optimizer = FusedAdamW(model.parameters(), lr=args.learning_rate, betas=(args.beta1, args.beta2),
                            weight_decay=args.weight_decay)
+    # fp16: dynamic loss scaling (the reference's torch.cuda.amp.GradScaler)
+    scaler = LossScaler(enabled=device.type == "cuda" and args.dtype == "float16")
     # the backward kernels write and accumulate the parameter gradients
     # themselves (no autograd accumulation kernels between micro-batches)
     grads = GradSink(model)
@@ -193,6 +193,8 @@ def train(args: argparse.Namespace) -> None:
     for step in range(1, args.max_steps + 1):
         model.train()
         grads.begin_step()  # in place of optimizer.zero_grad(set_to_none=True)
+        if scaler.is_enabled():  # d(scale * loss / GA) / d(loss)
+            fill_(seed, scaler.scale_value() / args.grad_accum_steps)
         t0 = time.perf_counter()
         micro_losses = []
         for _ in range(args.grad_accum_steps):
@@ -212,7 +214,14 @@ def train(args: argparse.Namespace) -> None:
             micro_losses.append(loss.detach().float().item())
             loss.backward(gradient=seed.to(loss.dtype) if loss.dtype != seed.dtype else seed)
         grads.finish()
-        if args.max_grad_norm > 0:
+        if scaler.is_enabled():
+            # unscale (and clip) folded into the step; a step whose gradients
+            # overflowed is skipped and the scale backed off
+            norm_value = float(scaler.unscale_(optimizer, max(args.max_grad_norm, 0.0)).item())
+            scaler.step(optimizer, norm_value)
+            scaler.update()
+            grad_norm_value = norm_value if args.max_grad_norm > 0 else math.nan
+        elif args.max_grad_norm > 0:
             norm = optimizer.clip_grad_norm_(args.max_grad_norm)
             optimizer.step()
             grad_norm_value = float(norm.item())

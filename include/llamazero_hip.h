@@ -12,7 +12,8 @@
  *     message;
  *   - nothing allocates device memory: every buffer, including workspaces, is
  *     passed in by the caller;
- *   - dtype codes: LZ_F32 = 0, LZ_BF16 = 1 (bf16 stored as uint16 bits).
+ *   - dtype codes: LZ_F32 = 0, LZ_BF16 = 1, LZ_F16 = 2 (16-bit formats stored
+ *     as uint16 bits).  Entry points that do not list LZ_F16 refuse it.
  *
  * The reference (dannyadkins/cs244c-llama-zero) is pure PyTorch and has no
  * FFI; each declaration names the reference code whose computation it
@@ -29,6 +30,7 @@ extern "C" {
 
 #define LZ_F32 0
 #define LZ_BF16 1
+#define LZ_F16 2
 
 /* ---- library ------------------------------------------------------------ */
 const char* lz_last_error(void);
@@ -79,9 +81,13 @@ int lz_adamw_multi(const int64_t* table, int nseg, int g_dtype, int p_out_dtype,
                    void* stream);
 int lz_sumsq_multi(const int64_t* table, int nseg, int dtype, double* acc, void* stream);
 
-/* norm = sqrt(*acc); scale = max/(norm+1e-6) if 0 < max < norm else 1.
- * Replaces the clip decision of zero/stage0_ddp.py:66-71 (and stage1/2/3). */
-int lz_clip_finalize(const double* acc, float max_norm, float* norm_out, float* scale_out, void* stream);
+/* norm = sqrt(*acc) * inv_grad_scale; scale = inv_grad_scale * (max/(norm+1e-6)
+ * if 0 < max < norm else 1).  Replaces the clip decision of
+ * zero/stage0_ddp.py:66-71 (and stage1/2/3) and, with inv_grad_scale = 1 /
+ * the loss scale, GradScaler.unscale_ before clip_grad_norm_
+ * (train.py:254-262): the gradients stay scaled and AdamW applies `scale`. */
+int lz_clip_finalize(const double* acc, float max_norm, float inv_grad_scale, float* norm_out, float* scale_out,
+                     void* stream);
 
 /* Multi-tensor gather: dst[i-begin] = src_seg[i-off] for flat i in [begin,end).
  * table: device int64 records {ptr, numel, flat_offset} sorted by offset; a
@@ -123,7 +129,7 @@ int lz_scale_dev(void* x, int dtype, int64_t n, const float* scale, void* stream
 
 /* Fill / cast.  Replace torch.zeros(...) for gradient buffers
  * (zero/stage2_optimizer.py:88-89) and dtype casts (.to()).  lz_fill also
- * takes dtype 2 (float64) for the norm accumulators. */
+ * takes dtype 3 (float64) for the norm accumulators. */
 int lz_fill(void* x, int dtype, int64_t n, double value, void* stream);
 int lz_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
 
@@ -205,9 +211,11 @@ int lz_transpose(const void* src, void* dst, int dtype, int64_t nb1, int64_t nb2
 int lz_copy2d(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows, int64_t cols, int dtype,
               void* stream);
 
-/* bf16 MFMA GEMM C[M,N] = alpha * sum_k A(m,k) B(n,k) (+beta*C) (+R): the
- * nn.Linear products of model/llama.py:81-84,133,139-141,178 and their
- * gradients, fp32 accumulation, C bf16 or fp32, R an optional bf16 residual.
+/* bf16 / fp16 MFMA GEMM C[M,N] = alpha * sum_k A(m,k) B(n,k) (+beta*C) (+R):
+ * the nn.Linear products of model/llama.py:81-84,133,139-141,178 and their
+ * gradients (bf16 models, and fp16 ones: train.py --dtype float16).  A and B
+ * in ab_dtype (LZ_BF16 or LZ_F16), fp32 accumulation, C in ab_dtype or fp32,
+ * R an optional residual in ab_dtype.
  *   a_kmajor = 1: A(m,k) = A[m*lda + k]   a_kmajor = 0: A(m,k) = A[k*lda + m]
  *   b_kmajor = 1: B(n,k) = B[n*ldb + k]   b_kmajor = 0: B(n,k) = B[k*ldb + n]
  * so y = x.W^T is (1,1), dx = dy.W is (1,0) and dW = dy^T.x is (0,0).
@@ -223,12 +231,12 @@ int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_k
  * Diagnostic only (used to attribute timings to kernels); no reference
  * counterpart. */
 int lz_gemm_plan(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor);
-int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb, int b_kmajor, void* C, int64_t ldc,
-            int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* ws,
-            int64_t ws_bytes, void* stream);
+int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb, int b_kmajor, int ab_dtype, void* C,
+            int64_t ldc, int c_dtype, const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha,
+            float beta, void* ws, int64_t ws_bytes, void* stream);
 /* lz_gemm with both operands K-major and no workspace. */
-int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int c_dtype, const void* R,
-               int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* stream);
+int lz_gemm_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int ab_dtype, void* C, int64_t ldc, int c_dtype,
+               const void* R, int64_t ldr, int64_t M, int64_t N, int64_t K, float alpha, float beta, void* stream);
 /* fp32 MFMA GEMM with lz_gemm's operand layouts and epilogue: the nn.Linear
  * products when the model is kept in float32 (train.py:148-160 and
  * train_zero.py:74,150-164 with --dtype float32).  fp32 operands, fp32
@@ -278,7 +286,7 @@ int lz_attn_delta(const void* o, int64_t ldo, const void* dout, int64_t lddo, fl
  * paths do not take (model/llama.py:105-117, F.scaled_dot_product_attention):
  *  - an explicit mask in place of the causal one (attn_mask with
  *    is_causal=False): mask_kind 1 = bool bytes (nonzero: the key takes
- *    part), 2 = fp32, 3 = bf16 (added to the scaled scores); mstride = 4
+ *    part), 2 = fp32, 3 = bf16, 4 = fp16 (added to the scaled scores); mstride = 4
  *    element strides over [B, H, S(query), S(key)], 0 where the mask
  *    broadcasts; mask_kind 0 = causal (mask, mstride ignored).  A query row
  *    whose keys are all masked gives NaN, as the reference's softmax does;

@@ -160,8 +160,8 @@ def test_activation_checkpointing_matches_plain():
 def test_unsupported_dtype_is_refused_clearly():
     cfg = ModelConfig(name="t", vocab_size=64, max_seq_len=16, dim=64, n_layers=1, n_heads=2, n_kv_heads=1,
                       ffn_dim=128)
-    model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.float16)
-    with pytest.raises(TypeError, match="float32 and bfloat16"):
+    model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.float64)
+    with pytest.raises(TypeError, match="float32, bfloat16 and float16"):
         model(torch.zeros(1, 16, dtype=torch.long, device=DEV))
 
 

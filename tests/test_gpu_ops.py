@@ -159,7 +159,7 @@ def test_gemm_split_k_workspace_and_determinism():
     assert torch.equal(c1, c2)
     # without a workspace the same product runs unsplit (same values up to summation order)
     c3 = torch.empty_like(c1)
-    ops._lib.call("lz_gemm", a.data_ptr(), M, 0, b.data_ptr(), N, 0, c3.data_ptr(), N, 0, 0, 0, M, N, K, 1.0, 0.0,
+    ops._lib.call("lz_gemm", a.data_ptr(), M, 0, b.data_ptr(), N, 0, 1, c3.data_ptr(), N, 0, 0, 0, M, N, K, 1.0, 0.0,
                   0, 0, ops.stream_ptr(a.device))
     assert torch.allclose(c1, c3, rtol=1e-4, atol=1e-3)
 

@@ -385,3 +385,51 @@ def test_gemm_plan_codes_and_workspace():
     assert int(lib.lz_gemm_plan(768, 768, 16384, 0, 0)) % 64 > 8  # the 125M weight gradient splits widely
     assert int(lib.lz_gemm_plan(16384, 4096, 2048, 1, 1)) % 64 == 1
     assert int(lib.lz_gemm_plan(0, 10, 10, 1, 1)) == 0
+
+
+def test_loss_scaler_follows_torch_grad_scaler():
+    """lzhip.optim.LossScaler's schedule (reference train.py:213-214,254-269:
+    torch.cuda.amp.GradScaler) against torch.amp.GradScaler itself on the
+    CPU: the same scale after every step for a pattern of overflowing and
+    finite steps, the same steps skipped, growth after growth_interval
+    finite steps, backoff on overflow; disabled it is the identity."""
+    from lzhip.optim import LossScaler
+
+    class _Opt:
+        def __init__(self):
+            self.steps = 0
+            self.discarded = 0
+
+        def step(self):
+            self.steps += 1
+
+        def discard_step(self):
+            self.discarded += 1
+
+    pattern = [False, True, False, False, False, True, True, False, False, False, False, False]
+    p = torch.nn.Parameter(torch.zeros(3))
+    topt = torch.optim.SGD([p], lr=1.0)
+    ts = torch.amp.GradScaler("cpu", init_scale=1024.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=3)
+    ls = LossScaler(init_scale=1024.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=3)
+    fake = _Opt()
+    torch_steps = 0
+    ts.scale(torch.ones(()))  # torch's scaler creates its scale on first use
+    for overflow in pattern:
+        topt.zero_grad()
+        p.grad = torch.full((3,), float("inf") if overflow else 1.0)
+        before = p.detach().clone()
+        ts.step(topt)
+        ts.update()
+        torch_steps += int(not torch.equal(before, p.detach()))
+        ls.step(fake, float("inf") if overflow else 1.0)
+        ls.update()
+        assert ls.scale_value() == ts.get_scale()
+    assert fake.steps == torch_steps == pattern.count(False)
+    assert fake.discarded == pattern.count(True)
+    restored = LossScaler()
+    restored.load_state_dict(ls.state_dict())
+    assert restored.scale_value() == ls.scale_value() and restored.state_dict() == ls.state_dict()
+    off = LossScaler(enabled=False)
+    off.step(fake, float("nan"))  # disabled: the step runs whatever the norm
+    off.update()
+    assert off.scale_value() == 1.0 and fake.steps == torch_steps + 1 and off.state_dict() == {}
