@@ -585,7 +585,8 @@ class LaunchProbe:
 
 
 def gemm_kernel_name(key) -> str:
-    """Kernel name (as profilers print it) of a LaunchProbe key."""
+    """Kernel name (as profilers print it, namespaces dropped) of a
+    LaunchProbe key of a bf16 product."""
     ak, bk, code = key
     if code == "swiglu":
         return "gemm_swiglu_kernel"
@@ -596,10 +597,10 @@ def gemm_kernel_name(key) -> str:
     cfg, splits = code // 64, code % 64
     tf = lambda b: "true" if b else "false"
     if cfg == 5:
-        name = f"gemm_dma_kernel<2, 4, {tf(ak)}, {tf(bk)}, 64, 2>"
+        name = f"gemm_dma_kernel<FmtBF16, 2, 4, {tf(ak)}, {tf(bk)}, 64, 2>"
     else:
         bm, wn = (128, 2) if cfg == 2 else (256, 4 if cfg == 0 else 2)
-        name = f"gemm_kernel<{bm}, {bm}, 2, {wn}, {tf(ak)}, {tf(bk)}>"
+        name = f"gemm_kernel<FmtBF16, {bm}, {bm}, 2, {wn}, {tf(ak)}, {tf(bk)}>"
     return name + (f" split-K x{splits} (+ splitk_reduce_kernel)" if splits > 1 else "")
 
 
