@@ -848,29 +848,41 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const float c = a.scale * kLog2e;
 
   const int kv_end = min(S, q0 + BQ);  // a multiple of 64
-  const int kv_end_w = min(S, qw0 + 32);
+  const int kv_end_w = qw0 < S ? min(S, qw0 + 32) : 0;  // a wave past the sequence computes nothing
   const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
   const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
   const int nsteps = kv_end / BKV;
 
-  dma_tile<HD>(kbase, a.ldk, Ks, wave, lane);
-  dma_tile<HD>(vbase, a.ldv, Vs, wave, lane);
-  for (int it = 0; it < nsteps; ++it) {
-    dma_barrier();  // K and V of step it landed; every wave is done with step it-1's slots
+  // Step it: wait for its K/V (and every wave's reads of step it-1), then
+  // issue step it+1's tiles into the other slot.
+  auto open_step = [&](int it) {
+    dma_barrier();
     if (it + 1 < nsteps) {
       dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, Ks + ((it + 1) & 1) * kTile, wave, lane);
       dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, Vs + ((it + 1) & 1) * kTile, wave, lane);
     }
-    const int k0 = it * BKV;
-    if (k0 >= kv_end_w) continue;  // past this wave's diagonal (it only joins the barriers)
+  };
+  // This wave's last step holds its diagonal (the only step with masked
+  // keys: 32 queries starting at a multiple of 32 against 64-key steps);
+  // the loop before it has no branch, so the accumulators stay in place.
+  const int last_w = kv_end_w > 0 ? (kv_end_w - 1) / BKV : -1;
+  dma_tile<HD>(kbase, a.ldk, Ks, wave, lane);
+  dma_tile<HD>(vbase, a.ldv, Vs, wave, lane);
+  int it = 0;
+  for (; it < last_w; ++it) {
+    open_step(it);
     f32x16_t s[2];
     fwd_scores<HD>(s, to, Ks + (it & 1) * kTile, qf);
-    const char* Vt = Vs + (it & 1) * kTile;
-    if (k0 + BKV - 1 > qw0)  // the diagonal step: keys past the query are masked
-      fwd_softmax_pv<HD, true>(s, o, m, l, to, Vt, c, qrow - k0, half);
-    else
-      fwd_softmax_pv<HD, false>(s, o, m, l, to, Vt, c, 0, half);
+    fwd_softmax_pv<HD, false>(s, o, m, l, to, Vs + (it & 1) * kTile, c, 0, half);
   }
+  if (last_w >= 0) {
+    open_step(it);
+    f32x16_t s[2];
+    fwd_scores<HD>(s, to, Ks + (it & 1) * kTile, qf);
+    fwd_softmax_pv<HD, true>(s, o, m, l, to, Vs + (it & 1) * kTile, c, qrow - it * BKV, half);
+    ++it;
+  }
+  for (; it < nsteps; ++it) open_step(it);  // past this wave's diagonal: it only joins the barriers
   if (qrow < S) {
     const float inv_l = 1.0f / l;
     uint16_t* op = a.o + ((int64_t)b * S + qrow) * a.ldo + (int64_t)h * HD;
@@ -928,6 +940,66 @@ __device__ __forceinline__ void dkdv8_issue(const AttnArgs& a, int step, int nqs
 // group from the diagonal on: S^T = K Q^T and dP^T = V dO^T per 32-query
 // half, P = exp(S*scale - lse), dS = P (dP - delta), then dV += P^T dO and
 // dK += dS^T Q from transposed LDS reads.
+// One 64-query step of the 8-wave dK/dV kernel for this wave's 32 keys:
+// S^T and dP^T, P and dS, then dV += P^T dO and dK += dS^T Q.  MASK: the
+// step crosses this wave's diagonal, so pairs with key > query are dropped
+// (the other steps carry no masking instructions).
+template <int HD, bool MASK>
+__device__ __forceinline__ void dkdv_step(f32x16_t (&dk)[HD / 32], f32x16_t (&dv)[HD / 32], const TileOffsets<HD>& to,
+                                          const char* Qt, const char* Vt, const bf16x8_t (&kf)[HD / 16], float c,
+                                          int q0, int kvrow, int wave, int half) {
+  constexpr int kTile = 64 * HD * 2;
+  const char* dOt = Qt + kTile;
+  const float* lse_s = reinterpret_cast<const float*>(Qt + 2 * kTile);
+  const float* D_s = lse_s + 64;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    f32x16_t sc, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sc[r] = 0.f;
+      dp[r] = 0.f;
+    }
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Qt, t, kk), kf[kk], sc, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(dOt, t, kk), to.frag(Vt, wave, kk), dp, 0, 0, 0);
+      // keeps the fragment reads next to their MFMAs: two waves per SIMD
+      // hide the latency, and the register budget is 256
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // lane holds key column kvrow; query rows t*32 + 8*(r/4) + 4*half + r%4
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int qlb = t * 32 + 8 * r4 + 4 * half;
+      const float4 l4 = *reinterpret_cast<const float4*>(lse_s + qlb);
+      const float4 d4 = *reinterpret_cast<const float4*>(D_s + qlb);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dvv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * r4 + e;
+        float p = __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lv[e] * kLog2e));
+        if constexpr (MASK) p = kvrow <= q0 + qlb + e ? p : 0.f;
+        dp[r] = p * (dp[r] - dvv[e]);
+        sc[r] = p;
+      }
+    }
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      const int ks = 2 * t + kh;
+      const bf16x8_t pb = pack8(sc, 8 * kh);
+      const bf16x8_t dsb = pack8(dp, 8 * kh);
+#pragma unroll
+      for (int i = 0; i < HD / 32; ++i) {
+        dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(dOt, ks, i), pb, dv[i], 0, 0, 0);
+        dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Qt, ks, i), dsb, dk[i], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+}
+
 template <int HD>
 __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   constexpr int BKV = 256, BQ = 64;
@@ -979,63 +1051,31 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   const int qstart = (k0 / BQ) * BQ;
   const int nqs = (S - qstart) / BQ;
   const int nsteps = rep * nqs;
-  dkdv8_issue<HD>(a, 0, nqs, qstart, b, g, rep, stages, wave, lane);
-  for (int step = 0; step < nsteps; ++step) {
+  auto open_step = [&](int step) {
     dma_barrier();  // this step's tiles (and the V tile) landed, last step's reads retired
     if (step + 1 < nsteps)
       dkdv8_issue<HD>(a, step + 1, nqs, qstart, b, g, rep, stages + ((step + 1) & 1) * kStage, wave, lane);
-    const int hq = step / nqs, q0 = qstart + (step - hq * nqs) * BQ;
-    const char* Qt = stages + (step & 1) * kStage;
-    const char* dOt = Qt + kTile;
-    const float* lse_s = reinterpret_cast<const float*>(Qt + 2 * kTile);
-    const float* D_s = lse_s + BQ;
-    if (q0 + BQ - 1 >= kw0 && kw0 < S) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        f32x16_t sc, dp;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sc[r] = 0.f;
-          dp[r] = 0.f;
-        }
-#pragma unroll
-        for (int kk = 0; kk < HD / 16; ++kk) {
-          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Qt, t, kk), kf[kk], sc, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(dOt, t, kk), to.frag(Vt, wave, kk), dp, 0, 0, 0);
-          // keeps the fragment reads next to their MFMAs: two waves per SIMD
-          // hide the latency, and the register budget is 256
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        // lane holds key column kvrow; query rows t*32 + 8*(r/4) + 4*half + r%4
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int qlb = t * 32 + 8 * r4 + 4 * half;
-          const float4 l4 = *reinterpret_cast<const float4*>(lse_s + qlb);
-          const float4 d4 = *reinterpret_cast<const float4*>(D_s + qlb);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-          const float dvv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * r4 + e;
-            const bool ok = kvrow <= q0 + qlb + e && kvrow < S;
-            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lv[e] * kLog2e)) : 0.f;
-            dp[r] = p * (dp[r] - dvv[e]);
-            sc[r] = p;
-          }
-        }
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const int ks = 2 * t + kh;
-          const bf16x8_t pb = pack8(sc, 8 * kh);
-          const bf16x8_t dsb = pack8(dp, 8 * kh);
-#pragma unroll
-          for (int i = 0; i < HD / 32; ++i) {
-            dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(dOt, ks, i), pb, dv[i], 0, 0, 0);
-            dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Qt, ks, i), dsb, dk[i], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-        }
-      }
+  };
+  // Per query head, the 64-query blocks j = 0 .. nqs-1 (queries qstart + 64j
+  // on) fall into three runs for this wave's keys kw0 .. kw0+31 (kw0 a
+  // multiple of 32): blocks wholly before the keys (no work), blocks across
+  // the diagonal (masked), blocks wholly after it (unmasked).  Every wave
+  // opens every step, so the barriers match.
+  const int rel = kw0 - qstart;  // 0 .. 224
+  const int j_first = kw0 < S ? min(nqs, rel / BQ) : nqs;
+  const int j_unmasked = kw0 < S ? min(nqs, (rel + 32 + BQ - 1) / BQ) : nqs;
+  dkdv8_issue<HD>(a, 0, nqs, qstart, b, g, rep, stages, wave, lane);
+  int step = 0;
+  for (int hq = 0; hq < rep; ++hq) {
+    int j = 0;
+    for (; j < j_first; ++j, ++step) open_step(step);
+    for (; j < j_unmasked; ++j, ++step) {
+      open_step(step);
+      dkdv_step<HD, true>(dk, dv, to, stages + (step & 1) * kStage, Vt, kf, c, qstart + j * BQ, kvrow, wave, half);
+    }
+    for (; j < nqs; ++j, ++step) {
+      open_step(step);
+      dkdv_step<HD, false>(dk, dv, to, stages + (step & 1) * kStage, Vt, kf, c, qstart + j * BQ, kvrow, wave, half);
     }
   }
   if (kvrow < S) {
@@ -1045,6 +1085,48 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
     store_grad_row<HD>(dkp, dk, a.scale, half, rope ? a.rcos + (int64_t)kvrow * HD : nullptr,
                        rope ? a.rsin + (int64_t)kvrow * HD : nullptr);
     store_grad_row<HD>(dvp, dv, 1.0f, half, nullptr, nullptr);
+  }
+}
+
+// One 64-key step of the dQ kernel for this wave's 32 queries: S and dP, dS,
+// then dQ += dS K.  MASK: the step holds this wave's diagonal, so keys past
+// the query are dropped (the other steps carry no masking instructions).
+template <int HD, bool MASK>
+__device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffsets<HD>& to, const char* Kt,
+                                        const bf16x8_t (&qf)[HD / 16], const bf16x8_t (&df)[HD / 16], float c, float nl2,
+                                        float Dq, int k0, int qrow, int half) {
+  constexpr int kTile = 64 * HD * 2;
+  const char* Vt = Kt + kTile;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    f32x16_t st, dpt;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      st[r] = 0.f;
+      dpt[r] = 0.f;
+    }
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], st, 0, 0, 0);
+      dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Vt, t, kk), df[kk], dpt, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = __builtin_amdgcn_exp2f(fmaf(st[r], c, nl2));
+      if constexpr (MASK) {
+        const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        p = kv <= qrow ? p : 0.f;
+      }
+      dpt[r] = p * (dpt[r] - Dq);
+    }
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      const int ks = 2 * t + kh;
+      const bf16x8_t dsb = pack8(dpt, 8 * kh);
+#pragma unroll
+      for (int i = 0; i < HD / 32; ++i)
+        dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Kt, ks, i), dsb, dq[i], 0, 0, 0);
+    }
   }
 }
 
@@ -1090,56 +1172,35 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
 
   const int kv_end = min(S, q0 + BQ);
-  const int kv_end_w = min(S, qw0 + 32);
+  const int kv_end_w = qw0 < S ? min(S, qw0 + 32) : 0;  // a wave past the sequence computes nothing
   const uint16_t* kbase = a.k + (int64_t)b * S * a.ldk + (int64_t)g * HD;
   const uint16_t* vbase = a.v + (int64_t)b * S * a.ldv + (int64_t)g * HD;
   const int nsteps = kv_end / BKV;
 
-  dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
-  dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
-  for (int it = 0; it < nsteps; ++it) {
+  auto open_step = [&](int it) {
     dma_barrier();  // this step's tiles landed (every wave's loads), last step's reads retired
     if (it + 1 < nsteps) {
       char* nxt = smem + ((it + 1) & 1) * kStage;
       dma_tile<HD>(kbase + (int64_t)(it + 1) * BKV * a.ldk, a.ldk, nxt, wave, lane);
       dma_tile<HD>(vbase + (int64_t)(it + 1) * BKV * a.ldv, a.ldv, nxt + kTile, wave, lane);
     }
-    const int k0 = it * BKV;
-    const char* Kt = smem + (it & 1) * kStage;
-    const char* Vt = Kt + kTile;
-    if (k0 < kv_end_w) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        f32x16_t st, dpt;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          st[r] = 0.f;
-          dpt[r] = 0.f;
-        }
-#pragma unroll
-        for (int kk = 0; kk < HD / 16; ++kk) {
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], st, 0, 0, 0);
-          dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Vt, t, kk), df[kk], dpt, 0,
-                                                        0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kv = k0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const bool ok = kv <= qrow && qrow < S;
-          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, nl2)) : 0.f;
-          dpt[r] = p * (dpt[r] - Dq);
-        }
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const int ks = 2 * t + kh;
-          const bf16x8_t dsb = pack8(dpt, 8 * kh);
-#pragma unroll
-          for (int i = 0; i < HD / 32; ++i)
-            dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Kt, ks, i), dsb, dq[i], 0, 0, 0);
-        }
-      }
-    }
+  };
+  // This wave's last step holds its diagonal (the only masked step); the
+  // steps after it only join the barriers.
+  const int last_w = kv_end_w > 0 ? (kv_end_w - 1) / BKV : -1;
+  dma_tile<HD>(kbase, a.ldk, smem, wave, lane);
+  dma_tile<HD>(vbase, a.ldv, smem + kTile, wave, lane);
+  int it = 0;
+  for (; it < last_w; ++it) {
+    open_step(it);
+    dq_step<HD, false>(dq, to, smem + (it & 1) * kStage, qf, df, c, nl2, Dq, it * BKV, qrow, half);
   }
+  if (last_w >= 0) {
+    open_step(it);
+    dq_step<HD, true>(dq, to, smem + (it & 1) * kStage, qf, df, c, nl2, Dq, it * BKV, qrow, half);
+    ++it;
+  }
+  for (; it < nsteps; ++it) open_step(it);
   if (qrow < S) {
     uint16_t* dqp = a.dq + ((int64_t)b * S + qrow) * a.lddq + (int64_t)h * HD;
     const bool rope = a.rcos != nullptr;
