@@ -24,6 +24,17 @@ from lzhip import ops
 from .config import ModelConfig
 
 
+def _next_token(logits: torch.Tensor, temperature: float, top_k: Optional[int]) -> torch.Tensor:
+    """One token per row of [B, V] logits (see LlamaForCausalLM.generate)."""
+    if temperature <= 0:
+        return logits.argmax(dim=-1)
+    scaled = logits / temperature
+    if top_k is not None:
+        kth = torch.topk(scaled, min(top_k, scaled.size(-1))).values[:, -1:]
+        scaled = scaled.masked_fill(scaled < kth, float("-inf"))
+    return torch.multinomial(torch.softmax(scaled, dim=-1), num_samples=1).squeeze(-1)
+
+
 class HipLinear(nn.Linear):
     """nn.Linear (same parameters, initialisation and state_dict) whose
     forward is the MFMA GEMM; bias is not supported (the model has none)."""
@@ -334,6 +345,7 @@ class LlamaForCausalLM(nn.Module):
         return executor.call_module(module_name, module, *args)
 
     @torch.no_grad()
+    @torch.no_grad()
     def generate(
         self,
         input_ids: torch.Tensor,
@@ -341,20 +353,18 @@ class LlamaForCausalLM(nn.Module):
         temperature: float = 1.0,
         top_k: Optional[int] = None,
     ) -> torch.Tensor:
-        """Sampling loop (model/llama.py:310-335): full forward per new token."""
+        """Autoregressive sampling with the reference's semantics
+        (model/llama.py:311-335): each new token takes a full forward over the
+        last max_seq_len tokens; temperature <= 0 picks the arg-max, otherwise
+        the logits / temperature, cut to their top_k largest, are sampled.
+        The sequence grows in one preallocated buffer."""
         self.eval()
-        for _ in range(max_new_tokens):
-            input_slice = input_ids[:, -self.cfg.max_seq_len :]
-            out = self(input_slice)
-            next_logits = out.logits[:, -1, :].float()
-            if temperature <= 0:
-                next_token = torch.argmax(next_logits, dim=-1, keepdim=True)
-            else:
-                next_logits = next_logits / temperature
-                if top_k is not None:
-                    values, _ = torch.topk(next_logits, min(top_k, next_logits.size(-1)))
-                    next_logits[next_logits < values[:, [-1]]] = float("-inf")
-                probs = torch.softmax(next_logits, dim=-1)
-                next_token = torch.multinomial(probs, num_samples=1)
-            input_ids = torch.cat([input_ids, next_token], dim=1)
-        return input_ids
+        bsz, t0 = input_ids.shape
+        seq = input_ids.new_empty((bsz, t0 + max_new_tokens))
+        seq[:, :t0] = input_ids
+        window = self.cfg.max_seq_len
+        for t in range(t0, t0 + max_new_tokens):
+            context = seq[:, max(0, t - window) : t].contiguous()
+            last = self(context).logits[:, -1, :].float()
+            seq[:, t] = _next_token(last, temperature, top_k)
+        return seq

@@ -166,11 +166,27 @@ def test_unsupported_dtype_is_refused_clearly():
 
 
 def test_generate_runs():
+    """generate (model/llama.py:311-335): greedy tokens are the arg-max of the
+    model's last logits over the last max_seq_len tokens (the window slides
+    once the sequence outgrows it); top_k=1 sampling is greedy; a seeded
+    sampling run repeats."""
     cfg = ModelConfig(name="t", vocab_size=64, max_seq_len=32, dim=128, n_layers=1, n_heads=2, n_kv_heads=1,
                       ffn_dim=256, rope_theta=10_000.0)
+    torch.manual_seed(0)
     model = LlamaForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16)
-    out = model.generate(torch.zeros(1, 4, dtype=torch.long, device=DEV), max_new_tokens=5, temperature=0.0)
-    assert out.shape == (1, 9)
+    prompt = torch.randint(0, 64, (2, 29), generator=torch.Generator().manual_seed(1)).to(DEV)
+    out = model.generate(prompt, max_new_tokens=6, temperature=0.0)
+    assert out.shape == (2, 35) and torch.equal(out[:, :29], prompt)
+    with torch.no_grad():
+        for t in range(29, 35):
+            ctx = out[:, max(0, t - 32) : t].contiguous()
+            assert torch.equal(out[:, t], model(ctx).logits[:, -1, :].float().argmax(dim=-1))
+    assert torch.equal(model.generate(prompt, 6, temperature=0.7, top_k=1), out)
+    torch.manual_seed(5)
+    s1 = model.generate(prompt, 4, temperature=1.0, top_k=10)
+    torch.manual_seed(5)
+    s2 = model.generate(prompt, 4, temperature=1.0, top_k=10)
+    assert torch.equal(s1, s2) and s1.shape == (2, 33)
 
 
 @pytest.mark.parametrize("stage3", [False, True])
