@@ -100,11 +100,25 @@ __device__ __forceinline__ void key_block_coords(int bid, int B, int KV, int& kv
   g = pair % KV;
 }
 
-// Elements e0..e0+7 of an accumulator -> an 8 x bf16 MFMA operand.
+// Elements e0..e0+7 of an accumulator -> an 8-element MFMA operand of the
+// 16-bit format F (fragments travel as bf16x8_t: 16 raw bytes per lane).
+template <typename F = FmtBF16>
 __device__ __forceinline__ bf16x8_t pack8(const f32x16_t& v, int e0) {
-  const uint4 w = make_uint4(pack_bf16x2(v[e0], v[e0 + 1]), pack_bf16x2(v[e0 + 2], v[e0 + 3]),
-                             pack_bf16x2(v[e0 + 4], v[e0 + 5]), pack_bf16x2(v[e0 + 6], v[e0 + 7]));
+  const uint4 w = make_uint4(F::pack2(v[e0], v[e0 + 1]), F::pack2(v[e0 + 2], v[e0 + 3]),
+                             F::pack2(v[e0 + 4], v[e0 + 5]), F::pack2(v[e0 + 6], v[e0 + 7]));
   return __builtin_bit_cast(bf16x8_t, w);
+}
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// One 32x32x16 MFMA on operands of the format F.
+template <typename F>
+__device__ __forceinline__ f32x16_t mfma16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  if constexpr (F::kDtype == LZ_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ bf16x8_t lds_frag16(const char* p) {
@@ -130,23 +144,24 @@ __device__ __forceinline__ uint4 load8(const uint16_t* row, int64_t idx, int64_t
                     (uint32_t)t[4] | ((uint32_t)t[5] << 16), (uint32_t)t[6] | ((uint32_t)t[7] << 16));
 }
 
+template <typename F = FmtBF16>
 __device__ __forceinline__ void store_bf16x4(uint16_t* p, float a, float b, float c, float d) {
   uint2 w;
-  w.x = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
-  w.y = (uint32_t)f2bf(c) | ((uint32_t)f2bf(d) << 16);
+  w.x = (uint32_t)F::from_f(a) | ((uint32_t)F::from_f(b) << 16);
+  w.y = (uint32_t)F::from_f(c) | ((uint32_t)F::from_f(d) << 16);
   *reinterpret_cast<uint2*>(p) = w;
 }
 
 // One lane's row of a dQ or dK accumulator set (columns 32*i + 8*q4 +
 // 4*half + e, the MFMA output layout), times `scale`, stored as bf16 at dst.
 // With RoPE tables (cs/sn: the row's position, HD values each) the stored row
-// is the gradient of the un-rotated input: the bf16 gradient pair (d1, d2) of
-// columns (c, c + HD/2) becomes g1 = r(r(d1*c1) + r(d2*s2)) and
-// g2 = r(r(d2*c2) - r(d1*s1)), rounding each product and sum to bf16 as the
+// is the gradient of the un-rotated input: the gradient pair (d1, d2) of
+// columns (c, c + HD/2) in the format F becomes g1 = r(r(d1*c1) + r(d2*s2)) and
+// g2 = r(r(d2*c2) - r(d1*s1)), rounding each product and sum to F as the
 // separate RoPE backward pass (and the reference's bf16 autograd of
 // x*cos + rotate_half(x)*sin, model/llama.py:35-39) does.  Columns c and
 // c + HD/2 sit in accumulator blocks i and i + HD/64 of the same lane.
-template <int HD>
+template <int HD, typename F = FmtBF16>
 __device__ __forceinline__ void store_grad_row(uint16_t* dst, const f32x16_t (&acc)[HD / 32], float scale, int half,
                                                const uint16_t* cs, const uint16_t* sn) {
   if (cs == nullptr) {
@@ -155,7 +170,7 @@ __device__ __forceinline__ void store_grad_row(uint16_t* dst, const f32x16_t (&a
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int c = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(dst + c, acc[i][4 * q4] * scale, acc[i][4 * q4 + 1] * scale, acc[i][4 * q4 + 2] * scale,
+        store_bf16x4<F>(dst + c, acc[i][4 * q4] * scale, acc[i][4 * q4 + 1] * scale, acc[i][4 * q4 + 2] * scale,
                      acc[i][4 * q4 + 3] * scale);
       }
     return;
@@ -187,14 +202,14 @@ __device__ __forceinline__ void store_grad_row(uint16_t* dst, const f32x16_t (&a
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int sh = (e & 1) * 16;
-        const float c1 = bf2f((uint16_t)(c1a[e >> 1] >> sh)), c2 = bf2f((uint16_t)(c2a[e >> 1] >> sh));
-        const float s1 = bf2f((uint16_t)(s1a[e >> 1] >> sh)), s2 = bf2f((uint16_t)(s2a[e >> 1] >> sh));
-        const float d1 = round_bf(acc[i][4 * q4 + e] * scale), d2 = round_bf(acc[i + kBlk][4 * q4 + e] * scale);
-        g1[e] = __fadd_rn(round_bf(__fmul_rn(d1, c1)), round_bf(__fmul_rn(d2, s2)));
-        g2[e] = __fadd_rn(round_bf(__fmul_rn(d2, c2)), -round_bf(__fmul_rn(d1, s1)));
+        const float c1 = F::to_f((uint16_t)(c1a[e >> 1] >> sh)), c2 = F::to_f((uint16_t)(c2a[e >> 1] >> sh));
+        const float s1 = F::to_f((uint16_t)(s1a[e >> 1] >> sh)), s2 = F::to_f((uint16_t)(s2a[e >> 1] >> sh));
+        const float d1 = F::round(acc[i][4 * q4 + e] * scale), d2 = F::round(acc[i + kBlk][4 * q4 + e] * scale);
+        g1[e] = __fadd_rn(F::round(__fmul_rn(d1, c1)), F::round(__fmul_rn(d2, s2)));
+        g2[e] = __fadd_rn(F::round(__fmul_rn(d2, c2)), -F::round(__fmul_rn(d1, s1)));
       }
-      store_bf16x4(dst + c, g1[0], g1[1], g1[2], g1[3]);
-      store_bf16x4(dst + c + kHalf, g2[0], g2[1], g2[2], g2[3]);
+      store_bf16x4<F>(dst + c, g1[0], g1[1], g1[2], g1[3]);
+      store_bf16x4<F>(dst + c + kHalf, g2[0], g2[1], g2[2], g2[3]);
     }
 }
 
@@ -745,7 +760,7 @@ struct TileOffsets {
 // Forward on tiles: 128 queries per workgroup (32 per wave), 64-key steps,
 // K and V tiles double-buffered in LDS (the next step's tiles are issued
 // right after the barrier that opens a step).
-template <int HD>
+template <int HD, typename F>
 __device__ __forceinline__ void fwd_scores(f32x16_t (&s)[2], const TileOffsets<HD>& to, const char* Kt,
                                            const bf16x8_t (&qf)[HD / 16]) {
 #pragma unroll
@@ -756,7 +771,7 @@ __device__ __forceinline__ void fwd_scores(f32x16_t (&s)[2], const TileOffsets<H
   for (int kk = 0; kk < HD / 16; ++kk)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], s[t], 0, 0, 0);
+      s[t] = mfma16<F>(to.frag(Kt, t, kk), qf[kk], s[t]);
 }
 
 // Online softmax of one 64-key step and its P.V product.  s: the step's
@@ -764,7 +779,7 @@ __device__ __forceinline__ void fwd_scores(f32x16_t (&s)[2], const TileOffsets<H
 // r%4); MASK: keys with index > lim are masked (the diagonal step only, so
 // that the other steps carry no masking instructions).  The running max m is
 // kept in log2 units; l and O are rescaled only when some lane's max moves.
-template <int HD, bool MASK>
+template <int HD, bool MASK, typename F>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[HD / 32], float& m, float& l,
                                                const TileOffsets<HD>& to, const char* Vt, float c, int lim, int half) {
   constexpr int BKV = 64;
@@ -805,14 +820,14 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[H
   l += rs;
 #pragma unroll
   for (int ks = 0; ks < BKV / 16; ++ks) {
-    const bf16x8_t pb = pack8(s[ks >> 1], 8 * (ks & 1));
+    const bf16x8_t pb = pack8<F>(s[ks >> 1], 8 * (ks & 1));
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i)
-      o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Vt, ks, i), pb, o[i], 0, 0, 0);
+      o[i] = mfma16<F>(to.frag_t(Vt, ks, i), pb, o[i]);
   }
 }
 
-template <int HD>
+template <int HD, typename F>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_tile_kernel(AttnArgs a) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int kTile = BKV * HD * 2;
@@ -872,14 +887,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   for (; it < last_w; ++it) {
     open_step(it);
     f32x16_t s[2];
-    fwd_scores<HD>(s, to, Ks + (it & 1) * kTile, qf);
-    fwd_softmax_pv<HD, false>(s, o, m, l, to, Vs + (it & 1) * kTile, c, 0, half);
+    fwd_scores<HD, F>(s, to, Ks + (it & 1) * kTile, qf);
+    fwd_softmax_pv<HD, false, F>(s, o, m, l, to, Vs + (it & 1) * kTile, c, 0, half);
   }
   if (last_w >= 0) {
     open_step(it);
     f32x16_t s[2];
-    fwd_scores<HD>(s, to, Ks + (it & 1) * kTile, qf);
-    fwd_softmax_pv<HD, true>(s, o, m, l, to, Vs + (it & 1) * kTile, c, qrow - it * BKV, half);
+    fwd_scores<HD, F>(s, to, Ks + (it & 1) * kTile, qf);
+    fwd_softmax_pv<HD, true, F>(s, o, m, l, to, Vs + (it & 1) * kTile, c, qrow - it * BKV, half);
     ++it;
   }
   for (; it < nsteps; ++it) open_step(it);  // past this wave's diagonal: it only joins the barriers
@@ -891,7 +906,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int hd = i * 32 + 8 * q4 + 4 * half;
-        store_bf16x4(op + hd, o[i][4 * q4] * inv_l, o[i][4 * q4 + 1] * inv_l, o[i][4 * q4 + 2] * inv_l,
+        store_bf16x4<F>(op + hd, o[i][4 * q4] * inv_l, o[i][4 * q4 + 1] * inv_l, o[i][4 * q4 + 2] * inv_l,
                      o[i][4 * q4 + 3] * inv_l);
       }
     if (half == 0) a.lse[((int64_t)b * H + h) * S + qrow] = (m + log2f(l)) * kLn2;
@@ -944,7 +959,7 @@ __device__ __forceinline__ void dkdv8_issue(const AttnArgs& a, int step, int nqs
 // S^T and dP^T, P and dS, then dV += P^T dO and dK += dS^T Q.  MASK: the
 // step crosses this wave's diagonal, so pairs with key > query are dropped
 // (the other steps carry no masking instructions).
-template <int HD, bool MASK>
+template <int HD, bool MASK, typename F>
 __device__ __forceinline__ void dkdv_step(f32x16_t (&dk)[HD / 32], f32x16_t (&dv)[HD / 32], const TileOffsets<HD>& to,
                                           const char* Qt, const char* Vt, const bf16x8_t (&kf)[HD / 16], float c,
                                           int q0, int kvrow, int wave, int half) {
@@ -962,8 +977,8 @@ __device__ __forceinline__ void dkdv_step(f32x16_t (&dk)[HD / 32], f32x16_t (&dv
     }
 #pragma unroll
     for (int kk = 0; kk < HD / 16; ++kk) {
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Qt, t, kk), kf[kk], sc, 0, 0, 0);
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(dOt, t, kk), to.frag(Vt, wave, kk), dp, 0, 0, 0);
+      sc = mfma16<F>(to.frag(Qt, t, kk), kf[kk], sc);
+      dp = mfma16<F>(to.frag(dOt, t, kk), to.frag(Vt, wave, kk), dp);
       // keeps the fragment reads next to their MFMAs: two waves per SIMD
       // hide the latency, and the register budget is 256
       __builtin_amdgcn_sched_barrier(0);
@@ -988,19 +1003,19 @@ __device__ __forceinline__ void dkdv_step(f32x16_t (&dk)[HD / 32], f32x16_t (&dv
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       const int ks = 2 * t + kh;
-      const bf16x8_t pb = pack8(sc, 8 * kh);
-      const bf16x8_t dsb = pack8(dp, 8 * kh);
+      const bf16x8_t pb = pack8<F>(sc, 8 * kh);
+      const bf16x8_t dsb = pack8<F>(dp, 8 * kh);
 #pragma unroll
       for (int i = 0; i < HD / 32; ++i) {
-        dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(dOt, ks, i), pb, dv[i], 0, 0, 0);
-        dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Qt, ks, i), dsb, dk[i], 0, 0, 0);
+        dv[i] = mfma16<F>(to.frag_t(dOt, ks, i), pb, dv[i]);
+        dk[i] = mfma16<F>(to.frag_t(Qt, ks, i), dsb, dk[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
 }
 
-template <int HD>
+template <int HD, typename F>
 __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
   constexpr int BKV = 256, BQ = 64;
   constexpr int kTile = BQ * HD * 2;
@@ -1071,27 +1086,27 @@ __global__ void __launch_bounds__(512) attn_bwd_dkdv_wide_kernel(AttnArgs a) {
     for (; j < j_first; ++j, ++step) open_step(step);
     for (; j < j_unmasked; ++j, ++step) {
       open_step(step);
-      dkdv_step<HD, true>(dk, dv, to, stages + (step & 1) * kStage, Vt, kf, c, qstart + j * BQ, kvrow, wave, half);
+      dkdv_step<HD, true, F>(dk, dv, to, stages + (step & 1) * kStage, Vt, kf, c, qstart + j * BQ, kvrow, wave, half);
     }
     for (; j < nqs; ++j, ++step) {
       open_step(step);
-      dkdv_step<HD, false>(dk, dv, to, stages + (step & 1) * kStage, Vt, kf, c, qstart + j * BQ, kvrow, wave, half);
+      dkdv_step<HD, false, F>(dk, dv, to, stages + (step & 1) * kStage, Vt, kf, c, qstart + j * BQ, kvrow, wave, half);
     }
   }
   if (kvrow < S) {
     uint16_t* dkp = a.dk + ((int64_t)b * S + kvrow) * a.lddk + (int64_t)g * HD;
     uint16_t* dvp = a.dv + ((int64_t)b * S + kvrow) * a.lddv + (int64_t)g * HD;
     const bool rope = a.rcos != nullptr;
-    store_grad_row<HD>(dkp, dk, a.scale, half, rope ? a.rcos + (int64_t)kvrow * HD : nullptr,
+    store_grad_row<HD, F>(dkp, dk, a.scale, half, rope ? a.rcos + (int64_t)kvrow * HD : nullptr,
                        rope ? a.rsin + (int64_t)kvrow * HD : nullptr);
-    store_grad_row<HD>(dvp, dv, 1.0f, half, nullptr, nullptr);
+    store_grad_row<HD, F>(dvp, dv, 1.0f, half, nullptr, nullptr);
   }
 }
 
 // One 64-key step of the dQ kernel for this wave's 32 queries: S and dP, dS,
 // then dQ += dS K.  MASK: the step holds this wave's diagonal, so keys past
 // the query are dropped (the other steps carry no masking instructions).
-template <int HD, bool MASK>
+template <int HD, bool MASK, typename F>
 __device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffsets<HD>& to, const char* Kt,
                                         const bf16x8_t (&qf)[HD / 16], const bf16x8_t (&df)[HD / 16], float c, float nl2,
                                         float Dq, int k0, int qrow, int half) {
@@ -1107,8 +1122,8 @@ __device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffse
     }
 #pragma unroll
     for (int kk = 0; kk < HD / 16; ++kk) {
-      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Kt, t, kk), qf[kk], st, 0, 0, 0);
-      dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag(Vt, t, kk), df[kk], dpt, 0, 0, 0);
+      st = mfma16<F>(to.frag(Kt, t, kk), qf[kk], st);
+      dpt = mfma16<F>(to.frag(Vt, t, kk), df[kk], dpt);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -1122,16 +1137,16 @@ __device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffse
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       const int ks = 2 * t + kh;
-      const bf16x8_t dsb = pack8(dpt, 8 * kh);
+      const bf16x8_t dsb = pack8<F>(dpt, 8 * kh);
 #pragma unroll
       for (int i = 0; i < HD / 32; ++i)
-        dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(to.frag_t(Kt, ks, i), dsb, dq[i], 0, 0, 0);
+        dq[i] = mfma16<F>(to.frag_t(Kt, ks, i), dsb, dq[i]);
     }
   }
 }
 
 // dQ on tiles: 128 queries per workgroup, 64-key steps up to the diagonal.
-template <int HD>
+template <int HD, typename F>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_bwd_dq_tile_kernel(AttnArgs a) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int kTile = BKV * HD * 2;
@@ -1193,18 +1208,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   int it = 0;
   for (; it < last_w; ++it) {
     open_step(it);
-    dq_step<HD, false>(dq, to, smem + (it & 1) * kStage, qf, df, c, nl2, Dq, it * BKV, qrow, half);
+    dq_step<HD, false, F>(dq, to, smem + (it & 1) * kStage, qf, df, c, nl2, Dq, it * BKV, qrow, half);
   }
   if (last_w >= 0) {
     open_step(it);
-    dq_step<HD, true>(dq, to, smem + (it & 1) * kStage, qf, df, c, nl2, Dq, it * BKV, qrow, half);
+    dq_step<HD, true, F>(dq, to, smem + (it & 1) * kStage, qf, df, c, nl2, Dq, it * BKV, qrow, half);
     ++it;
   }
   for (; it < nsteps; ++it) open_step(it);
   if (qrow < S) {
     uint16_t* dqp = a.dq + ((int64_t)b * S + qrow) * a.lddq + (int64_t)h * HD;
     const bool rope = a.rcos != nullptr;
-    store_grad_row<HD>(dqp, dq, a.scale, half, rope ? a.rcos + (int64_t)qrow * HD : nullptr,
+    store_grad_row<HD, F>(dqp, dq, a.scale, half, rope ? a.rcos + (int64_t)qrow * HD : nullptr,
                        rope ? a.rsin + (int64_t)qrow * HD : nullptr);
   }
 }
@@ -1759,7 +1774,7 @@ bool strides_ok(int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
 
 bool mfma_ok(int dtype, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, const void* q, const void* k,
              const void* v, const void* o) {
-  return dtype == LZ_BF16 && (hd == 64 || hd == 128) && strides_ok(ldq, ldk, ldv, ldo) &&
+  return (dtype == LZ_BF16 || dtype == LZ_F16) && (hd == 64 || hd == 128) && strides_ok(ldq, ldk, ldv, ldo) &&
          lz_aligned16(q) && lz_aligned16(k) && lz_aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7) == 0;
 }
 
@@ -1776,9 +1791,10 @@ int check_shape(int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd) {
 // Which path lz_attn_fwd/bwd take for these arguments: 2 = MFMA on LDS tiles
 // (S a multiple of 64; no transposed buffers), 1 = MFMA with the transposed
 // operand buffers (V^T for the forward; Q^T, K^T, dO^T for the backward),
-// 0 = generic.
+// 0 = generic.  fp16 takes the tile path or the generic one.
 LZ_EXPORT int lz_attn_path(int dtype, int64_t S, int64_t hd, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo) {
-  const bool mfma = dtype == LZ_BF16 && (hd == 64 || hd == 128) && strides_ok(ldq, ldk, ldv, ldo);
+  const bool mfma = (dtype == LZ_BF16 || (dtype == LZ_F16 && S % 64 == 0)) && (hd == 64 || hd == 128) &&
+                    strides_ok(ldq, ldk, ldv, ldo);
   return mfma ? (S % 64 == 0 ? 2 : 1) : 0;
 }
 
@@ -1797,11 +1813,16 @@ LZ_EXPORT int lz_attn_fwd(const void* q, int64_t ldq, const void* k, int64_t ldk
     a.o = (uint16_t*)o; a.ldo = ldo; a.lse = lse;
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid = (unsigned)(lz_cdiv(S, 128) * B * H);
-    if (hd == 128) attn_fwd_tile_kernel<128><<<grid, 256, 0, s>>>(a);
-    else attn_fwd_tile_kernel<64><<<grid, 256, 0, s>>>(a);
+    if (dtype == LZ_F16) {
+      if (hd == 128) attn_fwd_tile_kernel<128, FmtF16><<<grid, 256, 0, s>>>(a);
+      else attn_fwd_tile_kernel<64, FmtF16><<<grid, 256, 0, s>>>(a);
+    } else {
+      if (hd == 128) attn_fwd_tile_kernel<128, FmtBF16><<<grid, 256, 0, s>>>(a);
+      else attn_fwd_tile_kernel<64, FmtBF16><<<grid, 256, 0, s>>>(a);
+    }
     return lz_check_launch("lz_attn_fwd");
   }
-  if (mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o)) {
+  if (dtype == LZ_BF16 && mfma_ok(dtype, hd, ldq, ldk, ldv, ldo, q, k, v, o)) {
     LZ_REQUIRE(vt && lz_aligned16(vt), "lz_attn_fwd: MFMA path needs an aligned V^T buffer");
     AttnArgs a{};
     a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
@@ -1931,16 +1952,24 @@ int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const 
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid_kv = (unsigned)(lz_cdiv(S, 256) * B * KV);
     const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
-    if (hd == 128) {
-      attn_bwd_dkdv_wide_kernel<128><<<grid_kv, 512, 0, s>>>(a);
-      attn_bwd_dq_tile_kernel<128><<<grid_q, 256, 0, s>>>(a);
+    if (dtype == LZ_F16) {
+      if (hd == 128) {
+        attn_bwd_dkdv_wide_kernel<128, FmtF16><<<grid_kv, 512, 0, s>>>(a);
+        attn_bwd_dq_tile_kernel<128, FmtF16><<<grid_q, 256, 0, s>>>(a);
+      } else {
+        attn_bwd_dkdv_wide_kernel<64, FmtF16><<<grid_kv, 512, 0, s>>>(a);
+        attn_bwd_dq_tile_kernel<64, FmtF16><<<grid_q, 256, 0, s>>>(a);
+      }
+    } else if (hd == 128) {
+      attn_bwd_dkdv_wide_kernel<128, FmtBF16><<<grid_kv, 512, 0, s>>>(a);
+      attn_bwd_dq_tile_kernel<128, FmtBF16><<<grid_q, 256, 0, s>>>(a);
     } else {
-      attn_bwd_dkdv_wide_kernel<64><<<grid_kv, 512, 0, s>>>(a);
-      attn_bwd_dq_tile_kernel<64><<<grid_q, 256, 0, s>>>(a);
+      attn_bwd_dkdv_wide_kernel<64, FmtBF16><<<grid_kv, 512, 0, s>>>(a);
+      attn_bwd_dq_tile_kernel<64, FmtBF16><<<grid_q, 256, 0, s>>>(a);
     }
     return lz_check_launch("lz_attn_bwd");
   }
-  if (mfma) {
+  if (mfma && dtype == LZ_BF16) {
     LZ_REQUIRE(qt && kt && dot, "lz_attn_bwd: MFMA path needs the transposed Q, K and dO buffers");
     AttnArgs a{};
     a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
