@@ -1048,6 +1048,7 @@ LZ_EXPORT int lz_mt_gather_host(const int64_t* host_table, int nseg, int src_dty
   if (src_dtype == LZ_BF16 && dst_dtype == LZ_F32) return run_host_table<uint16_t, float>(0, host_table, nseg, dst, begin, end, accumulate, s);
   if (src_dtype == LZ_F32 && dst_dtype == LZ_F32) return run_host_table<float, float>(0, host_table, nseg, dst, begin, end, accumulate, s);
   if (src_dtype == LZ_F32 && dst_dtype == LZ_BF16) return run_host_table<float, uint16_t>(0, host_table, nseg, dst, begin, end, 0, s);
+  if (src_dtype == LZ_F16 && dst_dtype == LZ_F32) return run_host_table<_Float16, float>(0, host_table, nseg, dst, begin, end, accumulate, s);
   return lz_set_error(LZ_EINVAL, "lz_mt_gather_host: bad dtypes");
 }
 

@@ -163,6 +163,16 @@ class _Stage3ParamHandle:
             grads.append(g)
         table = self.meta.segment_table(grads)
         src_dtype = next((g.dtype for g in grads if g is not None), self.param_dtype)
+        if self.collectives.is_identity and self.world_size == 1:
+            # One rank: the reduce-scatter returns the bucket unchanged, so the
+            # gradients go straight into the fp32 shard in one launch, written
+            # on the step's first contribution and added afterwards.  Same
+            # values as the bucket path (16-bit -> fp32 is exact, the add is
+            # the same fp32 add), without the bucket's write and read.
+            ops.mt_gather_host(table, src_dtype, self.grad_shard, 0, self.meta.total_numel,
+                               accumulate=not self.grad_fresh)
+            self.grad_fresh = False
+            return 0.0
         comm_ms = 0.0
         for b0, b1 in bucket_ranges(0, self.meta.total_numel, self.engine.grad_bucket_numel):
             bucket = self.engine._bucket_buffer(b1 - b0, self.param_dtype)
