@@ -1181,8 +1181,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
   Plan p{big_cfg, 1, K};
   if (ak && bk) {
     // 128x128 tiles (two per CU) win when they fill the chip in fewer rounds.
-    // Relative speeds measured on MI355X: 0.85 and 0.75.
-    const double c256 = (double)lz_cdiv(big, cus) * 4.0 / 0.85;
+    // Relative speeds per tile measured on MI355X: 1.0 for the direct-to-LDS
+    // 256x256 kernel and 0.75 for the 128x128 one (at the 125M QKV shape,
+    // 16384x1280x768, the 256x256 kernel's two rounds beat three 128x128 ones).
+    const double c256 = (double)lz_cdiv(big, cus) * 4.0 / (big_cfg == 5 ? 1.0 : 0.85);
     const double c128 = (double)lz_cdiv(small, 2 * cus) * 2.0 / 0.75;
     if (c128 < c256) p.cfg = 2;
   }
