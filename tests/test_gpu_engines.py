@@ -116,7 +116,7 @@ def _train(engine, model, steps, max_norm=0.0):
         engine.zero_grad()
         engine.prepare_forward()
         loss = model(input_ids=ids, labels=ids).loss
-        losses.append(float(loss))
+        losses.append(float(loss.detach()))
         engine.backward(loss)
         engine.step(max_grad_norm=max_norm)
     return losses
@@ -161,7 +161,7 @@ def test_stage3_matches_stage0_with_dropout(recompute):
             loss = m(input_ids=ids, labels=ids).loss
             e.backward(loss)
             e.step()
-            losses.append(float(loss))
+            losses.append(float(loss.detach()))
         # step 0 starts from equal weights; after it the engines' updates
         # differ in rounding (stage 0 sums the tied weight's two gradient
         # contributions in bf16, stage 3 in fp32)

@@ -76,7 +76,7 @@ def _plumbing_run(oracle_param_dtype, angle_dtype):
         for _ in range(GA):
             ids = next(chunks)[:, :-1].contiguous().to(DEV)
             loss = model(input_ids=ids, labels=ids, return_logits=False).loss
-            losses.append(float(loss))
+            losses.append(float(loss.detach()))
             (loss / GA).backward()
         g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
         opt.clip_grad_norm_(1.0)
@@ -336,7 +336,7 @@ def test_packed_parameters_train_bit_identically():
             loss.backward()
             o.clip_grad_norm_(1.0)
             o.step()
-            losses.append(float(loss))
+            losses.append(float(loss.detach()))
         return losses, {k: v.float().cpu() for k, v in m.state_dict().items()}
 
     la, sa = run(False)
