@@ -797,7 +797,19 @@ struct RopeIn {
   int64_t nrope;
 };
 
-enum { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
+// The fused SwiGLU backward on the down projection's input gradient: the
+// GEMM's product dm = dy . W_down ([M, F]) meets gate and up in gu ([M, 2F]:
+// gate columns [0, F), up columns [F, 2F)) and the epilogue writes dgate and
+// dup to the same columns of dgu.
+struct SwigluBwdIn {
+  const uint16_t* gu;
+  int64_t ldgu;
+  uint16_t* dgu;
+  int64_t lddgu;
+  int64_t F;
+};
+
+enum { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2, kEpiSwiGLUBwd = 3 };
 
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
@@ -807,14 +819,20 @@ template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
                                            f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t n0,
                                            char* smem, int lane, int wave);
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
+                                                 int64_t m0, int64_t n0, char* smem, int lane, int wave);
 
 // One workgroup's 256x256 tile of the direct-to-LDS GEMM (main loop, then the
 // epilogue).  kEpiSwiGLU: the tile's 256 B rows are 128 gate rows and the
 // matching 128 up rows of a [gate; up] weight (o.F rows apart), and the
 // epilogue writes silu(gate) * up.  kEpiRope: the epilogue rotates the tile's
-// columns below r.nrope as RoPE heads of 128.
+// columns below r.nrope as RoPE heads of 128.  kEpiSwiGLUBwd: the product is
+// the down projection's input gradient and the epilogue runs SwiGLU's
+// backward on it (sb).
 template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi>
-__device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o, const RopeIn& rope) {
+__device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o, const RopeIn& rope,
+                                              const SwigluBwdIn& sb) {
   constexpr bool kSwiGLU = kEpi == kEpiSwiGLU;
   constexpr int BM = 256, BN = 256;
   constexpr int kWaves = WM * WN;
@@ -978,6 +996,8 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
     store_swiglu<BM, BN, WM, WN>(g, o, acc, m0, tn, smem, lane, wave);
   } else if constexpr (kEpi == kEpiRope) {
     store_rope<BM, BN, WM, WN>(g, rope, acc, m0, n0, smem, lane, wave);
+  } else if constexpr (kEpi == kEpiSwiGLUBwd) {
+    store_swiglu_bwd<BM, BN, WM, WN>(sb, acc, m0, n0, smem, lane, wave);
   } else {
     GemmArgs go = g;  // split-K: this split's fp32 slab
     if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
@@ -987,19 +1007,78 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
 
 template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
-  gemm_dma_tile<F, WM, WN, AK, BK, DBK, NST, kEpiPlain>(g, SwigluOut{}, RopeIn{});
+  gemm_dma_tile<F, WM, WN, AK, BK, DBK, NST, kEpiPlain>(g, SwigluOut{}, RopeIn{}, SwigluBwdIn{});
 }
 
 // Fused gate|up projection + SwiGLU (both operands K-major): tile (tm, tn)
 // covers rows 256 tm.. of x and gate/up columns 128 tn.. of the [M, F] result.
 __global__ void __launch_bounds__(512) gemm_swiglu_kernel(GemmArgs g, SwigluOut o) {
-  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiSwiGLU>(g, o, RopeIn{});
+  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiSwiGLU>(g, o, RopeIn{}, SwigluBwdIn{});
 }
 
 // Fused QKV projection + RoPE on the q and k heads (both operands K-major,
 // M and N multiples of 256, head dim 128).
 __global__ void __launch_bounds__(512) gemm_rope_kernel(GemmArgs g, RopeIn r) {
-  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiRope>(g, SwigluOut{}, r);
+  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiRope>(g, SwigluOut{}, r, SwigluBwdIn{});
+}
+
+// Down projection input gradient + SwiGLU backward (dy K-major, W_down read
+// N-major; M and F multiples of 256).
+__global__ void __launch_bounds__(512) gemm_swiglu_bwd_kernel(GemmArgs g, SwigluBwdIn sb) {
+  gemm_dma_tile<FmtBF16, 2, 4, true, false, 64, 2, kEpiSwiGLUBwd>(g, SwigluOut{}, RopeIn{}, sb);
+}
+
+// SwiGLU backward epilogue.  Each wave parks its 128x64 tile of dm, rounded
+// to bf16 as the GEMM's own output would be, in its LDS region (the layout
+// store_tile16 uses), then walks it in 16-byte row pieces: with the gate and
+// up pieces at the same row and columns it forms dgate and dup exactly as the
+// unfused SwiGLU backward kernel does (the same element routine) and writes
+// them as whole 16-byte pieces.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
+                                                 int64_t m0, int64_t n0, char* smem, int lane, int wave) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int kRow = TN * 2, kChunks = kRow / 16;
+  const int wm = wave / WN, wn = wave % WN;
+  const int frag_row = lane & 31, half = lane >> 5;
+  const int64_t mrow0 = m0 + wm * TM, ncol0 = n0 + wn * TN;
+  char* st = smem + wave * (TM * TN * 2);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = i * 32 + frag_row, chunk = j * 4 + q;
+        *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
+            make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                       pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
+      }
+  asm volatile("" ::: "memory");
+  constexpr int kIters = TM * kChunks / 64;
+  constexpr int kBlk = 4;  // gate and up pieces of four stores loaded together
+  static_assert(kIters % kBlk == 0, "store blocks must tile the wave's rows");
+#pragma unroll
+  for (int t0 = 0; t0 < kIters; t0 += kBlk) {
+    uint4 gv[kBlk], uv[kBlk];
+#pragma unroll
+    for (int u = 0; u < kBlk; ++u) {
+      const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+      const uint16_t* gp = sb.gu + (mrow0 + row) * sb.ldgu + ncol0 + chunk * 8;
+      gv[u] = *reinterpret_cast<const uint4*>(gp);
+      uv[u] = *reinterpret_cast<const uint4*>(gp + sb.F);
+    }
+#pragma unroll
+    for (int u = 0; u < kBlk; ++u) {
+      const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
+      const uint4 hv = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+      uint4 dg, du;
+      swiglu_bwd8(gv[u], uv[u], hv, dg, du);
+      uint16_t* dp = sb.dgu + (mrow0 + row) * sb.lddgu + ncol0 + chunk * 8;
+      *reinterpret_cast<uint4*>(dp) = dg;
+      *reinterpret_cast<uint4*>(dp + sb.F) = du;
+    }
+  }
 }
 
 // SwiGLU epilogue.  Each wave stages its 128x64 tile as bf16 in its own LDS
@@ -1423,6 +1502,52 @@ LZ_EXPORT int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t 
   g.slab = 0;
   gemm_swiglu_kernel<<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(g, SwigluOut{(uint16_t*)h, ldh, F});
   return lz_check_launch("lz_gemm_swiglu");
+}
+
+// Down projection input gradient fused with SwiGLU's backward (reference
+// model/llama.py:136-146: autograd of down_proj(silu(gate_proj x) * up_proj
+// x) in bf16): dm = dy . W_down (dy [M, K], W_down [K, F] row-major, so the
+// product reads it N-major) and, with gu = [gate | up] ([M, 2F]), writes
+// dgate and dup to columns [0, F) and [F, 2F) of dgu.  Every value equals
+// lz_gemm (bf16 output) followed by lz_swiglu_bwd; dm itself is not stored.
+// Needs M % 256 == 0, F % 256 == 0, K % 64 == 0 and 16-byte aligned rows.
+LZ_EXPORT int lz_gemm_swiglu_bwd(const void* dy, int64_t lddy, const void* w, int64_t ldw, const void* gu,
+                                 int64_t ldgu, void* dgu, int64_t lddgu, int64_t M, int64_t F, int64_t K,
+                                 void* stream) {
+  LZ_REQUIRE(dy && w && gu && dgu, "lz_gemm_swiglu_bwd: null pointer");
+  LZ_REQUIRE(M > 0 && F > 0 && K > 0 && M % 256 == 0 && F % 256 == 0 && K % 64 == 0,
+             "lz_gemm_swiglu_bwd: needs M %% 256, F %% 256 and K %% 64 == 0 (M %lld, F %lld, K %lld)",
+             (long long)M, (long long)F, (long long)K);
+  LZ_REQUIRE(lddy >= K && ldw >= F && ldgu >= 2 * F && lddgu >= 2 * F, "lz_gemm_swiglu_bwd: bad leading dimension");
+  LZ_REQUIRE(lz_aligned16(dy) && lz_aligned16(w) && lz_aligned16(gu) && lz_aligned16(dgu) && lddy % 8 == 0 &&
+                 ldw % 8 == 0 && ldgu % 8 == 0 && lddgu % 8 == 0,
+             "lz_gemm_swiglu_bwd: rows must be 16-byte aligned");
+  LZ_REQUIRE(dgu != gu, "lz_gemm_swiglu_bwd: dgu must not be gu");
+  const int64_t tiles = (M / 256) * (F / 256);
+  LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm_swiglu_bwd: too many tiles");
+  LZ_REQUIRE(dma_span_fits(true, lddy, K) && dma_span_fits(false, ldw, K), "lz_gemm_swiglu_bwd: operands too large");
+  GemmArgs g{};
+  g.A = (const uint16_t*)dy;
+  g.B = (const uint16_t*)w;
+  g.C = nullptr;
+  g.R = nullptr;
+  g.lda = lddy;
+  g.ldb = ldw;
+  g.ldc = 0;
+  g.ldr = 0;
+  g.M = M;
+  g.N = F;
+  g.K = K;
+  g.alpha = 1.f;
+  g.beta = 0.f;
+  g.c_f32 = 0;
+  g.vec_store = 1;
+  g.vec16 = 1;
+  g.kper = K;
+  g.slab = 0;
+  gemm_swiglu_bwd_kernel<<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(
+      g, SwigluBwdIn{(const uint16_t*)gu, ldgu, (uint16_t*)dgu, lddgu, F});
+  return lz_check_launch("lz_gemm_swiglu_bwd");
 }
 
 // Fused QKV projection + RoPE (reference model/llama.py:95-103: the q/k/v

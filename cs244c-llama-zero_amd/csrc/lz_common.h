@@ -180,6 +180,35 @@ __device__ __forceinline__ uint4 swiglu_fwd8(const uint4& gv, const uint4& uv) {
   return make_uint4(ow[0], ow[1], ow[2], ow[3]);
 }
 
+// SwiGLU backward on 8 bf16 triples (16 bytes each of gate, up and dh) with
+// the reference's bf16 roundings (autograd of F.silu(g) * u in bf16):
+//   ds = r(dh * u),  du = r(dh * r(silu(g))),
+//   dg = r(ds * sigmoid(g) * (1 + g * (1 - sigmoid(g)))).
+__device__ __forceinline__ void swiglu_bwd8(const uint4& gv, const uint4& uv, const uint4& hv, uint4& dgv, uint4& duv) {
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+  uint32_t ga[4], ua[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float dg[2], du[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float gx = bf2f((uint16_t)(gw[k] >> (16 * e))), ux = bf2f((uint16_t)(uw[k] >> (16 * e)));
+      const float dx = bf2f((uint16_t)(hw[k] >> (16 * e)));
+      const float sig = sigmoid_hw(gx);
+      const float sl = round_bf(gx * sig);
+      const float ds = round_bf(dx * ux);
+      du[e] = dx * sl;
+      dg[e] = ds * sig * (1.0f + gx * (1.0f - sig));
+    }
+    ga[k] = pack_bf16x2(dg[0], dg[1]);
+    ua[k] = pack_bf16x2(du[0], du[1]);
+  }
+  dgv = make_uint4(ga[0], ga[1], ga[2], ga[3]);
+  duv = make_uint4(ua[0], ua[1], ua[2], ua[3]);
+}
+
 template <typename T>
 struct Elem;
 

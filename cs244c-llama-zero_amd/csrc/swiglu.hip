@@ -86,28 +86,10 @@ __global__ void __launch_bounds__(256) swiglu_bwd_bf16x8_kernel(
     const uint4 gv = ntl16(g + r * ldg + c);
     const uint4 uv = ntl16(u + r * ldu + c);
     const uint4 hv = ntl16(dh + r * lddh + c);
-    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
-    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-    uint32_t ga[4], ua[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float dgv[2], duv[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float gx = bf2f((uint16_t)(gw[k] >> (16 * e))), ux = bf2f((uint16_t)(uw[k] >> (16 * e)));
-        const float dx = bf2f((uint16_t)(hw[k] >> (16 * e)));
-        const float sig = sigmoid_hw(gx);
-        const float sl = round_bf(gx * sig);
-        const float ds = round_bf(dx * ux);
-        duv[e] = dx * sl;
-        dgv[e] = ds * sig * (1.0f + gx * (1.0f - sig));
-      }
-      ga[k] = pack_bf16x2(dgv[0], dgv[1]);
-      ua[k] = pack_bf16x2(duv[0], duv[1]);
-    }
-    *reinterpret_cast<uint4*>(dg + r * lddg + c) = make_uint4(ga[0], ga[1], ga[2], ga[3]);
-    *reinterpret_cast<uint4*>(du + r * lddu + c) = make_uint4(ua[0], ua[1], ua[2], ua[3]);
+    uint4 gav, uav;
+    swiglu_bwd8(gv, uv, hv, gav, uav);
+    *reinterpret_cast<uint4*>(dg + r * lddg + c) = gav;
+    *reinterpret_cast<uint4*>(du + r * lddu + c) = uav;
   }
 }
 

@@ -424,12 +424,18 @@ class MLPFn(Function):
         x2, wg, wu, wd, gu, m = ctx.saved_tensors
         F_ = wg.shape[0]
         dy2 = _rows(dy)
-        dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3], [wd])
         dropout_p, seed = ctx.dropout
-        if dropout_p > 0.0:
-            ops.dropout_(dm, dropout_p, seed)  # the forward's keep mask and scale
-        dgu = torch.empty_like(gu)
-        ops.swiglu_bwd(gu[:, :F_], gu[:, F_:], dm, dgu[:, :F_], dgu[:, F_:])
+        if dropout_p == 0.0 and ops.swiglu_bwd_fusable(dy2, wd, gu):
+            # dm = dy . W_down goes straight into SwiGLU's backward in the
+            # GEMM's epilogue (same bits as the two kernels, dm never stored)
+            dgu = ops.gemm_swiglu_bwd(dy2, wd, gu)
+            _, dwd = _linear_bwd(dy2, m, wd, False, ctx.needs_input_grad[3], [wd])
+        else:
+            dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3], [wd])
+            if dropout_p > 0.0:
+                ops.dropout_(dm, dropout_p, seed)  # the forward's keep mask and scale
+            dgu = torch.empty_like(gu)
+            ops.swiglu_bwd(gu[:, :F_], gu[:, F_:], dm, dgu[:, :F_], dgu[:, F_:])
         w = fused_weight([wg, wu])
         need_w = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
         dx2, dw = _linear_bwd(dgu, x2, w, ctx.needs_input_grad[0], need_w, [wg, wu])

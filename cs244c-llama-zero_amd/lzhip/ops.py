@@ -592,6 +592,8 @@ def gemm_kernel_name(key) -> str:
         return "gemm_swiglu_kernel"
     if code == "rope":
         return "gemm_rope_kernel"
+    if code == "swiglu_bwd":
+        return "gemm_swiglu_bwd_kernel"
     if code == "f32":
         return f"gemm_f32_kernel<{'true' if ak else 'false'}, {'true' if bk else 'false'}>"
     cfg, splits = code // 64, code % 64
@@ -762,6 +764,51 @@ def gemm_swiglu(x2: torch.Tensor, w: torch.Tensor, gu: Optional[torch.Tensor] = 
         end.record()
         probe.add(2.0 * M * 2 * F * K, start, end, (True, True, "swiglu"))
     return h
+
+
+def swiglu_bwd_fusable(dy2: torch.Tensor, wd: torch.Tensor, gu: torch.Tensor) -> bool:
+    """Whether gemm_swiglu_bwd takes dy2 [M, K], the down weight wd [K, F] and
+    gu [M, 2F]: M % 256, F % 256 and K % 64 == 0, bf16, unit column stride
+    and 16-byte aligned rows."""
+    if dy2.dim() != 2 or wd.dim() != 2 or gu.dim() != 2:
+        return False
+    if any(t.dtype != torch.bfloat16 for t in (dy2, wd, gu)):
+        return False
+    M, K = dy2.shape
+    k2, F = wd.shape
+    if k2 != K or tuple(gu.shape) != (M, 2 * F) or M % 256 or F % 256 or K % 64 or M == 0:
+        return False
+    return all(t.stride(1) == 1 and _row_stride(t) % 8 == 0 and t.data_ptr() % 16 == 0 for t in (dy2, wd, gu))
+
+
+def gemm_swiglu_bwd(dy2: torch.Tensor, wd: torch.Tensor, gu: torch.Tensor,
+                    dgu: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[dgate | dup] ([M, 2F] bf16) of SwiGLU's backward on dm = dy2 . wd
+    (the down projection's input gradient) with gu = [gate | up], in one
+    kernel that never stores dm.  Bit-identical to gemm(dy2, wd,
+    b_kmajor=False) followed by swiglu_bwd."""
+    require_gpu(dy2, wd, gu, dgu)
+    if not swiglu_bwd_fusable(dy2, wd, gu):
+        raise ValueError(f"gemm_swiglu_bwd: unsupported shapes/layout dy {tuple(dy2.shape)}, w {tuple(wd.shape)}, "
+                         f"gu {tuple(gu.shape)}")
+    M, K = dy2.shape
+    F = wd.shape[1]
+    if dgu is None:
+        dgu = torch.empty((M, 2 * F), dtype=torch.bfloat16, device=dy2.device)
+    elif (tuple(dgu.shape) != (M, 2 * F) or dgu.dtype != torch.bfloat16 or dgu.stride(1) != 1
+          or _row_stride(dgu) % 8 or dgu.data_ptr() % 16):
+        raise ValueError("dgu must be an aligned bf16 [M, 2F] view")
+    probe = _gemm_probe
+    if probe is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+    _lib.call("lz_gemm_swiglu_bwd", dy2.data_ptr(), _row_stride(dy2), wd.data_ptr(), _row_stride(wd), gu.data_ptr(),
+              _row_stride(gu), dgu.data_ptr(), _row_stride(dgu), M, F, K, stream_ptr(dy2.device))
+    if probe is not None:
+        end.record()
+        probe.add(2.0 * M * F * K, start, end, (True, False, "swiglu_bwd"))
+    return dgu
 
 
 def rope_fusable(x2: torch.Tensor, w: torch.Tensor, nrope: int, hd: int, cos: torch.Tensor) -> bool:

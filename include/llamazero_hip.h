@@ -265,10 +265,19 @@ int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, void*
  * 256, K % 64 == 0 and 16-byte aligned rows. */
 int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo, const void* cos_t,
                  const void* sin_t, int64_t S, int64_t nrope, int64_t M, int64_t N, int64_t K, void* stream);
+/* Down projection input gradient fused with SwiGLU's backward
+ * (model/llama.py:136-146: autograd of down_proj(silu(gate_proj x) *
+ * up_proj x)): dm = dy.W_down (dy [M, K], W_down [K, F] row-major) meets
+ * gu = [gate | up] ([M, 2F]) and dgate, dup go to columns [0, F) and [F, 2F)
+ * of dgu; dm is never stored.  Bit-identical to lz_gemm (bf16 out, W_down
+ * read N-major) followed by lz_swiglu_bwd.  Needs M % 256 == 0,
+ * F % 256 == 0, K % 64 == 0 and 16-byte aligned rows; dgu != gu. */
+int lz_gemm_swiglu_bwd(const void* dy, int64_t lddy, const void* w, int64_t ldw, const void* gu, int64_t ldgu,
+                       void* dgu, int64_t lddgu, int64_t M, int64_t F, int64_t K, void* stream);
 
 /* Causal GQA flash attention (model/llama.py:88-117: repeat_kv +
  * F.scaled_dot_product_attention(is_causal=True)).  lz_attn_path reports the
- * path lz_attn_fwd/bwd take: 2 = MFMA on LDS tiles (bf16, hd 64 or 128, S a
+ * path lz_attn_fwd/bwd take: 2 = MFMA on LDS tiles (bf16 or fp16, hd 64 or 128, S a
  * multiple of 64; the transposed-operand arguments may be NULL), 1 = MFMA
  * with the transposed operand buffers (vt for the forward; qt, kt, dot for the
  * backward, each [B, heads, hd, S]), 0 = generic. */

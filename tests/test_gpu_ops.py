@@ -357,6 +357,38 @@ def test_gemm_swiglu_fused_matches_unfused(M, F_, K):
     assert float(diff.max()) <= 2 ** -6 * float(want.abs().max() + 1)
 
 
+@pytest.mark.parametrize("M,F_,K,pad", [(256, 256, 64, 0), (512, 768, 192, 8), (768, 512, 960, 0)])
+def test_gemm_swiglu_bwd_fused_matches_unfused(M, F_, K, pad):
+    """The down projection's input gradient with SwiGLU's backward in its
+    epilogue equals gemm (W_down read N-major) followed by the SwiGLU backward
+    kernel bit for bit, also on padded row strides, and the gradients stay
+    within bf16 rounding of float64 autograd on the same bf16 operands.  (The
+    fused kernel never splits K; K stays below 1024 here so that the unfused
+    product is not split either and sums K in the same order.)"""
+    g = _seed(M + F_ + K + pad)
+    dy = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    wd = (0.05 * torch.randn(K, F_, generator=g)).to(torch.bfloat16)
+    gu = torch.randn(M, 2 * F_ + pad, generator=g).to(torch.bfloat16)
+    dyd, wdd, gud = dy.to(DEV), wd.to(DEV), gu.to(DEV)[:, : 2 * F_]
+    dm = ops.gemm(dyd, wdd, b_kmajor=False)
+    ref = torch.empty((M, 2 * F_), dtype=torch.bfloat16, device=DEV)
+    ops.swiglu_bwd(gud[:, :F_], gud[:, F_:], dm, ref[:, :F_], ref[:, F_:])
+    assert ops.swiglu_bwd_fusable(dyd, wdd, gud)
+    out = torch.full((M, 2 * F_ + pad), 7.0, dtype=torch.bfloat16, device=DEV)
+    got = ops.gemm_swiglu_bwd(dyd, wdd, gud, dgu=out[:, : 2 * F_])
+    assert torch.equal(got.cpu(), ref.cpu())
+    if pad:
+        assert bool((out[:, 2 * F_:] == 7.0).all())
+    assert torch.equal(ops.gemm_swiglu_bwd(dyd, wdd, gud).cpu(), ref.cpu())
+    gate = gu[:, :F_].double().requires_grad_(True)
+    up = gu[:, F_ : 2 * F_].double().requires_grad_(True)
+    R.swiglu(gate, up).backward(dy.double() @ wd.double())
+    assert _rel_err(got[:, :F_], gate.grad) < 1e-2
+    assert _rel_err(got[:, F_:], up.grad) < 1e-2
+    with pytest.raises(ValueError):
+        ops.gemm_swiglu_bwd(dyd[:128], wdd, gud[:128])  # M not a multiple of 256
+
+
 @pytest.mark.parametrize("M,N,nrope,K,S", [(256, 512, 256, 64, 256), (512, 1024, 768, 192, 128), (768, 512, 512, 2048, 384)])
 def test_gemm_rope_fused_matches_unfused(M, N, nrope, K, S):
     """The fused QKV GEMM + RoPE equals gemm followed by the RoPE kernel bit
