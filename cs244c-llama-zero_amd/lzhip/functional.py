@@ -586,7 +586,9 @@ class LMHeadCEFn(Function):
             if need_x:
                 dx = torch.empty((T, d), dtype=x.dtype, device=dev)
             if need_w:
-                dw32 = ops.zeros((V, d), torch.float32, dev)
+                # written by the first chunk's product (beta 0), accumulated by later ones
+                dw32 = (torch.empty((V, d), dtype=torch.float32, device=dev) if T > 0
+                        else ops.zeros((V, d), torch.float32, dev))
         for r0 in range(0, T, rows_per):
             r1 = min(T, r0 + rows_per)
             lg = buf[: r1 - r0]
@@ -597,7 +599,7 @@ class LMHeadCEFn(Function):
                 if need_x:
                     ops.gemm(lg, weight, b_kmajor=False, out=dx[r0:r1])
                 if need_w:
-                    ops.gemm(lg, x2[r0:r1], a_kmajor=False, b_kmajor=False, out=dw32, beta=1.0)
+                    ops.gemm(lg, x2[r0:r1], a_kmajor=False, b_kmajor=False, out=dw32, beta=1.0 if r0 > 0 else 0.0)
         loss, _ = ops.ce_reduce(row_loss, lab, T, S, V, clamp)
         ctx.save_for_backward(dx, dw32)
         ctx.x_shape, ctx.w_dtype = x.shape, weight.dtype
