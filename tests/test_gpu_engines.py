@@ -148,7 +148,7 @@ def test_stage3_matches_stage0_with_dropout(recompute):
     m0, m3 = _model(4321, dropout=0.2), _model(4321, dropout=0.2)
     e0 = ZeROStage0DDP(model=m0, **kw)
     e3 = ZeROStage3Optimizer(model=m3, recompute=recompute, **kw)
-    nodrop = float(m0.eval()(input_ids=_batch(0), labels=_batch(0)).loss)
+    nodrop = float(m0.eval()(input_ids=_batch(0), labels=_batch(0)).loss.detach())
     for step in range(2):
         ids = _batch(step)
         seed = 10_000 + step * 31
