@@ -467,18 +467,45 @@ __global__ void __launch_bounds__(kThreads) mt_gather_args_kernel(const SegArgs 
       if (ptr && ((lo - off) & 7) == 0 && ((lo - dst_base) & 7) == 0 &&
           ((reinterpret_cast<uintptr_t>(ptr) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
         const int64_t nv = (hi - lo) >> 3;
-        for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
+        const S* sp = ptr + (lo - off);
+        const int64_t dofs = lo - dst_base;
+        const int64_t bd = blockDim.x;
+        int64_t v = threadIdx.x;
+        // four groups per thread at a time, their loads issued together (one
+        // group per round trip left too few bytes in flight to reach the
+        // copy rate)
+        for (; v + 3 * bd < nv; v += 4 * bd) {
+          float r[4][8];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) Vec8<S>::load(sp + 8 * (v + u * bd), r[u]);
+          if (mode == 1) {
+            float* dp = reinterpret_cast<float*>(dst) + dofs;
+            float d[4][8];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) Vec8<float>::load(dp + 8 * (v + u * bd), d[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) d[u][e] += r[u][e];
+              Vec8<float>::store(dp + 8 * (v + u * bd), d[u]);
+            }
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) Vec8<D>::store(dst + dofs + 8 * (v + u * bd), r[u]);
+          }
+        }
+        for (; v < nv; v += bd) {
           float r[8];
-          Vec8<S>::load(ptr + (lo - off) + 8 * v, r);
+          Vec8<S>::load(sp + 8 * v, r);
           if (mode == 1) {
             float d[8];
-            float* dp = reinterpret_cast<float*>(dst) + (lo - dst_base) + 8 * v;
+            float* dp = reinterpret_cast<float*>(dst) + dofs + 8 * v;
             Vec8<float>::load(dp, d);
 #pragma unroll
             for (int e = 0; e < 8; ++e) d[e] += r[e];
             Vec8<float>::store(dp, d);
           } else {
-            Vec8<D>::store(dst + (lo - dst_base) + 8 * v, r);
+            Vec8<D>::store(dst + dofs + 8 * v, r);
           }
         }
         i0 = lo + 8 * nv;
