@@ -47,9 +47,38 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_kernel(const T* __restrict__ 
       // base-2 domain: u = x log2(e), s = sum 2^(u - m) with the hardware
       // exp2 (libm expf made this pass ALU-bound); converted back below
       const int64_t nchunk = vocab >> 3;
-      for (int64_t c = threadIdx.x; c < nchunk; c += kThreads) {
+      // four 16-byte chunks per thread at a time, their loads issued
+      // together, so enough bytes are in flight to stream the row at the
+      // copy rate; the running max moves once per group of 32 values
+      const uint4* xv = reinterpret_cast<const uint4*>(x);
+      int64_t c = threadIdx.x;
+      for (; c + 3 * kThreads < nchunk; c += 4 * kThreads) {
+        uint4 raw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) raw[u] = xv[c + u * kThreads];
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            v[8 * u + 2 * k] = bf2f(w[k] & 0xffff) * kLog2E;
+            v[8 * u + 2 * k + 1] = bf2f(w[k] >> 16) * kLog2E;
+          }
+        }
+        float cm = v[0];
+#pragma unroll
+        for (int k = 1; k < 32; ++k) cm = fmaxf(cm, v[k]);
+        if (cm > m) {
+          s = s * __builtin_amdgcn_exp2f(m - cm);
+          m = cm;
+        }
+#pragma unroll
+        for (int k = 0; k < 32; ++k) s += __builtin_amdgcn_exp2f(v[k] - m);
+      }
+      for (; c < nchunk; c += kThreads) {
         float v[8];
-        const uint4 raw = reinterpret_cast<const uint4*>(x)[c];
+        const uint4 raw = xv[c];
         const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
