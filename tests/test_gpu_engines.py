@@ -232,7 +232,7 @@ def test_stage3_recompute_off_matches_recompute_on():
         for s in range(2):  # two micro-batches accumulate into the fp32 shard
             loss = m(input_ids=_batch(s), labels=_batch(s)).loss
             e.backward(loss)
-        e._last_loss = float(loss)
+        e._last_loss = float(loss.detach())
     assert ea._last_loss == eb._last_loss
     ea._finish_grads()
     eb._finish_grads()
