@@ -166,8 +166,9 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(const T* logits, int64
     const float l = lse[r];
     if (kVec) {
       const int64_t nchunk = vocab >> 3;
-      for (int64_t c = threadIdx.x; c < nchunk; c += kThreads) {
-        const uint4 raw = reinterpret_cast<const uint4*>(x)[c];
+      // 8 logits -> 8 gradients (d may alias x: every chunk is read before
+      // it is written, by the same thread)
+      auto grad8 = [&](const uint4& raw, int64_t c) {
         const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
         uint32_t o[4];
 #pragma unroll
@@ -180,8 +181,18 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(const T* logits, int64
           }
           o[k] = (uint32_t)f2bf(g0) | ((uint32_t)f2bf(g1) << 16);
         }
-        reinterpret_cast<uint4*>(d)[c] = make_uint4(o[0], o[1], o[2], o[3]);
+        return make_uint4(o[0], o[1], o[2], o[3]);
+      };
+      // four chunks per thread at a time, their loads issued together
+      int64_t c = threadIdx.x;
+      for (; c + 3 * kThreads < nchunk; c += 4 * kThreads) {
+        uint4 raw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) raw[u] = reinterpret_cast<const uint4*>(x)[c + u * kThreads];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) reinterpret_cast<uint4*>(d)[c + u * kThreads] = grad8(raw[u], c + u * kThreads);
       }
+      for (; c < nchunk; c += kThreads) reinterpret_cast<uint4*>(d)[c] = grad8(reinterpret_cast<const uint4*>(x)[c], c);
     } else {
       for (int64_t c = threadIdx.x; c < vocab; c += kThreads) {
         float g = 0.f;
