@@ -202,7 +202,7 @@ def test_loss_scaled_training_vs_oracle():
             for i in range(GA):
                 ids = batches[(step - 1) * GA + i][:, :-1].contiguous().to(DEV)
                 l = model(input_ids=ids, labels=ids, return_logits=False).loss
-                losses.append(float(l))
+                losses.append(float(l.detach()))
                 l.backward(gradient=seed)
             norm = float(scaler.unscale_(opt, 1.0))
             if math.isfinite(norm):
