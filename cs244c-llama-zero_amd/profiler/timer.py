@@ -31,13 +31,10 @@ class TimerSummary:
 
 
 def _quantile(sorted_ms: List[float], q: float) -> float:
-    """Linear interpolation between the two samples that bracket rank
-    q*(n-1) of the sorted samples."""
-    pos = q * (len(sorted_ms) - 1)
-    lo = math.floor(pos)
-    hi = min(lo + 1, len(sorted_ms) - 1)
-    frac = pos - lo
-    return sorted_ms[lo] * (1.0 - frac) + sorted_ms[hi] * frac
+    """Nearest-rank quantile, as the reference's summary takes it
+    (profiler/timer.py:62-64): the sample at index round(q*(n-1)) of the
+    sorted samples, with Python's round() (ties to even)."""
+    return float(sorted_ms[int(round((len(sorted_ms) - 1) * q))])
 
 
 def _on_gpu(device: Optional[torch.device]) -> bool:

@@ -232,6 +232,14 @@ def test_profiler_helpers():
     s = reg.timer("sleep").summary()
     assert s.count == 5 and s.min_ms == 1.0 and s.max_ms >= 10.0
     assert s.p50_ms == 3.0 and abs(s.mean_ms - s.total_ms / 5) < 1e-12
+    # nearest rank with round() (reference profiler/timer.py:62-64), not interpolation:
+    # two samples give p50 = the first (round(0.5) == 0); p95 of 20 is sample 18 (round(18.05))
+    two = reg.timer("two")
+    two._done_ms.extend([1.0, 2.0])
+    assert two.summary().p50_ms == 1.0 and two.summary().p95_ms == 2.0
+    twenty = reg.timer("twenty")
+    twenty._done_ms.extend([float(i * i) for i in range(20)])
+    assert twenty.summary().p95_ms == 18.0 * 18.0 and twenty.summary().p50_ms == 10.0 * 10.0
     mt = MemoryTracker(device=None)
     mt.record("before")
     mt.record("after")
