@@ -229,7 +229,7 @@ def bench_plumbing_graph(cfg, dtype, ids_all, B: int, S: int, GA: int, steps: in
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     return {"hip_graph_tokens_per_s": B * S * GA * steps / el, "hip_graph_ms_per_step": el * 1000 / steps,
-            "hip_graph_final_loss": float(loss)}
+            "hip_graph_final_loss": float(loss.detach())}
 
 
 def bench_plumbing_eager(cfg, dtype, ids_all, B: int, S: int, GA: int, steps: int, dev: torch.device) -> dict:
@@ -269,7 +269,7 @@ def bench_plumbing_eager(cfg, dtype, ids_all, B: int, S: int, GA: int, steps: in
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     return {"hip_tokens_per_s": B * S * GA * steps / el, "hip_ms_per_step": el * 1000 / steps,
-            "hip_final_loss": float(loss)}
+            "hip_final_loss": float(loss.detach())}
 
 
 def bench_plumbing(dev: torch.device, cpu: bool, steps: int = 100, cpu_steps: int = 3):

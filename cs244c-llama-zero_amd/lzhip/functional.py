@@ -65,8 +65,8 @@ class GradSink:
     autograd Functions return no gradient for the parameter.  So autograd
     neither adds the micro-batches' gradients nor sums the tied weight's two
     contributions with its own kernels.  Call begin_step() where the
-    reference calls optimizer.zero_grad(); finish() zeroes the gradients of
-    parameters no backward reached.  Engines that read gradients through
+    reference calls optimizer.zero_grad(); finish() sets the gradients of
+    parameters no backward reached to None.  Engines that read gradients through
     autograd hooks (ZeRO stage 2) must not be combined with a sink."""
 
     def __init__(self, module: torch.nn.Module) -> None:
@@ -108,10 +108,13 @@ class GradSink:
         return self._views[id(prm)], not fresh
 
     def finish(self) -> None:
+        """Leaves .grad None on parameters that no backward of the step
+        reached, as zero_grad(set_to_none=True) followed by backward does
+        (reference train.py:231), so optimizers skip them: no weight decay and
+        no moment decay for a parameter the step did not use."""
         for prm in self.params:
             if self._fresh[id(prm)]:
-                ops.fill_(self._views[id(prm)], 0.0)
-                self._fresh[id(prm)] = False
+                prm.grad = None
 
     def detach(self) -> None:
         for prm in self.params:

@@ -345,7 +345,6 @@ class LlamaForCausalLM(nn.Module):
         return executor.call_module(module_name, module, *args)
 
     @torch.no_grad()
-    @torch.no_grad()
     def generate(
         self,
         input_ids: torch.Tensor,

@@ -240,6 +240,48 @@ def test_grad_sink_matches_autograd_accumulation():
         sink.detach()
 
 
+def test_grad_sink_leaves_an_unused_parameter_untouched():
+    """A parameter that no backward reaches keeps .grad None after
+    GradSink.finish() (zero_grad(set_to_none=True) then backward, reference
+    train.py:231), so FusedAdamW skips it as torch.optim.AdamW does: no
+    weight decay, no moments, bit-identical after several steps, while the
+    used parameters move exactly as without the unused one."""
+    from lzhip.functional import GradSink
+
+    cfg = ModelConfig(name="unused", vocab_size=512, max_seq_len=64, dim=128, n_layers=1, n_heads=4, n_kv_heads=2,
+                      ffn_dim=256, rope_theta=10_000.0)
+
+    def build(extra: bool):
+        torch.manual_seed(0)
+        m = LlamaForCausalLM(cfg)
+        if extra:
+            m.unused = torch.nn.Parameter(torch.randn(3, 40))  # registered, never called
+        return m.to(device=DEV, dtype=torch.bfloat16)
+
+    plain, with_extra = build(False), build(True)
+    before = with_extra.unused.detach().clone()
+    runs = []
+    for m in (plain, with_extra):
+        sink = GradSink(m)
+        opt = FusedAdamW(m.parameters(), lr=1e-2, betas=(0.9, 0.95), weight_decay=0.1)
+        gen = torch.Generator().manual_seed(5)
+        for _ in range(3):
+            ids = torch.randint(0, cfg.vocab_size, (2, 64), generator=gen).to(DEV)
+            sink.begin_step()
+            m(input_ids=ids, labels=ids, return_logits=False).loss.backward()
+            sink.finish()
+            opt.clip_grad_norm_(1.0)
+            opt.step()
+        runs.append((m, opt))
+        sink.detach()
+    m, opt = runs[1]
+    assert m.unused.grad is None and m.unused not in opt.state
+    assert torch.equal(m.unused.detach(), before)
+    used = dict(m.named_parameters())
+    for n, a in runs[0][0].named_parameters():
+        assert torch.equal(a.detach(), used[n].detach()), n
+
+
 def test_capturable_adamw_refuses_a_late_parameter():
     """With capturable=True the step count lives on the device per parameter
     group, so a parameter whose first gradient arrives after the group's
