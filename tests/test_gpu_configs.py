@@ -152,6 +152,47 @@ def test_1b_layout_zero3_vs_oracle(recompute):
     _run_teacher_forced(cfg, make, B=1, S=2048, GA=2, steps=3, max_norm=1.0)
 
 
+def _gemm_plans_of_step(run) -> set:
+    """The GEMM kernel keys (layouts and lz_gemm_plan codes, or the fused
+    kernels' names) that `run()` launches."""
+    probe = ops.LaunchProbe()
+    ops.set_gemm_probe(probe)
+    try:
+        run()
+        torch.cuda.synchronize()
+    finally:
+        ops.set_gemm_probe(None)
+    return {r[3] for r in probe.records}
+
+
+def test_1b_layout_full_micro_batch_zero3_vs_oracle():
+    """The benchmark step's micro-batch (B=8, S=2048: 16,384 tokens) on 2
+    layers of the 1B layout through stage 3 with recompute, one step with
+    clip 1.0, teacher-forced against the oracle with the bars above.  At this
+    token count the weight-gradient products run at K = 16384 (split along K
+    by the plans the benchmark uses), the LM head's weight gradient over its
+    1000 output tiles, and the fused SwiGLU-backward GEMM over 16,384 rows.
+    The set of GEMM plans launched must equal the set one step of the
+    16-layer benchmark model launches, so every plan the benchmark times is
+    compared with the oracle here."""
+    cfg = ModelConfig(name="1b_2layer", max_seq_len=2048, n_layers=2, **LAYOUT_1B)
+
+    def make(model):
+        return ZeROStage3Optimizer(model=model, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                                   recompute=True)
+
+    tested = _gemm_plans_of_step(lambda: _run_teacher_forced(cfg, make, B=8, S=2048, GA=1, steps=1, max_norm=1.0))
+    _release()
+    cfg16, model = _device_model("1b", 2048)
+    eng = make(model)
+    ids = torch.randint(0, 32000, (8, 2048), device=DEV, generator=torch.Generator(device=DEV).manual_seed(0))
+    bench = _gemm_plans_of_step(lambda: _step(model, eng, ids))
+    del model, eng
+    print("plans:", sorted(map(str, tested)))
+    assert tested == bench, (tested ^ bench)
+    assert any(not ak and not bk and isinstance(c, int) and c % 64 > 1 for ak, bk, c in tested), "no split-K plan"
+
+
 def test_125m_zero1_vs_oracle():
     cfg = build_config("125m", vocab_size=32000, max_seq_len=1024)
     assert (cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.ffn_dim) == (768, 12, 12, 4, 2048)
