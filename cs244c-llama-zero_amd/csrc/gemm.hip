@@ -43,6 +43,53 @@ __device__ __forceinline__ f32x16_t mfma16(const bf16x8_t& a, const bf16x8_t& b,
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// One 16x16x32 MFMA of the operand format F.  The direct-to-LDS kernels use
+// this shape: on MI355X a stream of independent 16x16x32 MFMAs (128
+// accumulator registers per wave, two waves per SIMD, as in these kernels)
+// runs at about 2.39 GHz and 2.46 PFLOP/s, the same work as 32x32x16 MFMAs at
+// about 2.14 GHz and 2.19 PFLOP/s: the same issue efficiency per clock, a
+// higher clock under the power limit.  At the 256x256 tile, under sustained
+// load, the forward product went from 1.23 to 1.31 PFLOP/s (O projection)
+// and from 1.30 to 1.37 (gate|up); the gradient layouts, whose transposed
+// LDS reads (ds_read_b64_tr_b16, about 150 bytes per clock per CU against
+// about 220 for ds_read_b128) keep them near the LDS bound, by 1-2 %.
+template <typename F>
+__device__ __forceinline__ f32x4_t mfma_k32(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
+  if constexpr (F::kDtype == LZ_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Accumulator fragments of an MI x MI MFMA tile (MI = 32: 32x32x16, 16 floats
+// per lane; MI = 16: 16x16x32, 4 floats per lane).  The products are computed
+// as D = B_tile . A_tile^T, so every lane holds groups of 4 consecutive output
+// columns of one output row: group g (floats 4g..4g+3) of fragment (i, j) is
+// row acc_row(i), columns acc_col(j, g) .. +3 of the wave's tile.
+template <int MI>
+struct Acc;
+template <>
+struct Acc<32> {
+  typedef f32x16_t T;
+  static constexpr int kGroups = 4;
+};
+template <>
+struct Acc<16> {
+  typedef f32x4_t T;
+  static constexpr int kGroups = 1;
+};
+template <int MI>
+__device__ __forceinline__ int acc_row(int i, int lane) {
+  return i * MI + (lane & (MI - 1));
+}
+template <int MI>
+__device__ __forceinline__ int acc_col(int j, int g, int lane) {
+  return MI == 32 ? j * 32 + 8 * g + 4 * (lane >> 5) : j * 16 + 4 * (lane >> 4);
+}
+
 constexpr int kBK = 64;                 // K elements per stage
 constexpr int kRowBytes = kBK * 2 + 16; // padded LDS row (144 B)
 
@@ -257,13 +304,31 @@ __device__ __forceinline__ int epi_swz(int row) {
 // conflicts), then writes whole 16-byte pieces of consecutive row bytes, so a
 // store instruction covers full cache lines.  fp32 output goes in two passes
 // of TM/2 rows.  Needs BM*BN*2 bytes of LDS.
-template <typename F, int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
+// Parks a wave's TM x TN accumulator tile in its LDS region as 16-bit values
+// (scaled by alpha, rounded once): rows of TN values (kRow = 2*TN bytes),
+// 16-byte chunks XOR-swizzled by epi_swz, so that the accumulator-layout
+// writes and the row-wise reads are free of bank conflicts.
+template <typename F, int MI, int FM, int FN, int kRow>
+__device__ __forceinline__ void park16(const typename Acc<MI>::T (&acc)[FM][FN], char* st, int lane, float alpha) {
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < Acc<MI>::kGroups; ++q) {
+        const int row = acc_row<MI>(i, lane), byte = 2 * acc_col<MI>(j, q, lane);
+        *reinterpret_cast<uint2*>(st + row * kRow + (((byte >> 4) ^ epi_swz<kRow>(row)) << 4) + (byte & 15)) =
+            make_uint2(F::pack2(acc[i][j][4 * q] * alpha, acc[i][j][4 * q + 1] * alpha),
+                       F::pack2(acc[i][j][4 * q + 2] * alpha, acc[i][j][4 * q + 3] * alpha));
+      }
+}
+
+template <typename F, int MI, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI>::T (&acc)[BM / WM / MI][BN / WN / MI],
                                              int64_t m0, int64_t n0, char* smem, int lane, int wave) {
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MI, FN = TN / MI;
   static_assert(FM % 2 == 0, "fp32 output is staged in two halves");
   const int wm = wave / WN, wn = wave % WN;
-  const int frag_row = lane & 31, half = lane >> 5;
   const int64_t mrow0 = m0 + wm * TM, ncol0 = n0 + wn * TN;
   char* st = smem + wave * (TM * TN * 2);
   if (!go.c_f32) {
@@ -273,17 +338,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
     // 16-byte row pieces; a residual is added to each piece on the way out
     const bool plain = go.beta == 0.f && (go.R == nullptr || go.r16);
     if (plain) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int row = i * 32 + frag_row, chunk = j * 4 + q;
-            *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
-                make_uint2(F::pack2(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha),
-                           F::pack2(acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha));
-          }
+      park16<F, MI, FM, FN, kRow>(acc, st, lane, go.alpha);
       asm volatile("" ::: "memory");
       constexpr int kIters = TM * kChunks / 64;
       if (go.R == nullptr) {
@@ -338,8 +393,8 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = ii * 32 + frag_row, chunk = j * 8 + q * 2 + half;
+        for (int q = 0; q < Acc<MI>::kGroups; ++q) {
+          const int row = acc_row<MI>(ii, lane), chunk = acc_col<MI>(j, q, lane) >> 2;
           *reinterpret_cast<float4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4)) =
               make_float4(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
                           acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha);
@@ -405,49 +460,48 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, f32x16_t (&acc)
   }
 }
 
-// Writes a workgroup's BM x BN accumulator tile.  Lane layout of the
-// accumulators: output row m = lane % 32 of each 32x32 tile, columns
-// n = 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Interior tiles with 16-byte
-// aligned rows and wave tiles up to 64 wide take store_tile16; other interior
-// tiles store each lane's 4-column groups straight from the accumulators (8
-// or 16 bytes) with the row address formed once per 32-row band; edge tiles
-// go through LDS one 32-row band at a time and are written as whole rows with
-// bounds checks, so the accumulators are never indexed dynamically.  `smem` must be free and at
-// least max(WM*WN*32*(BN/WN+4)*4, BM*BN*2) bytes.
-template <typename F, int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0,
-                                           int64_t n0, char* smem, int lane, int wave) {
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+// Writes a workgroup's BM x BN accumulator tile (layout: Acc<MI>).
+// Interior tiles with 16-byte aligned rows and wave tiles up to 64 wide take
+// store_tile16; other interior tiles store each lane's 4-column groups
+// straight from the accumulators (8 or 16 bytes) with the row address formed
+// once per fragment row band; edge tiles go through LDS one MI-row band at a
+// time and are written as whole rows with bounds checks, so the accumulators
+// are never indexed dynamically.  `smem` must be free and at least
+// max(WM*WN*MI*(BN/WN+4)*4, BM*BN*2) bytes.
+template <typename F, int MI, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_tile(const GemmArgs& go, typename Acc<MI>::T (&acc)[BM / WM / MI][BN / WN / MI],
+                                           int64_t m0, int64_t n0, char* smem, int lane, int wave) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MI, FN = TN / MI, G = Acc<MI>::kGroups;
   const int wm = wave / WN, wn = wave % WN;
-  const int frag_row = lane & 31, half = lane >> 5;
   if constexpr (TN <= 64) {  // (wider wave tiles run out of registers in the staged path)
     if (m0 + BM <= go.M && n0 + BN <= go.N && go.vec16) {
-      store_tile16<F, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+      store_tile16<F, MI, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
       return;
     }
   }
   if (m0 + BM <= go.M && n0 + BN <= go.N && go.vec_store) {
-    const int64_t ncol0 = n0 + wn * TN + half * 4;
+    const int64_t ncol0 = n0 + wn * TN;
     if (go.c_f32) {
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const int64_t m = m0 + wm * TM + i * 32 + frag_row;
+        const int64_t m = m0 + wm * TM + acc_row<MI>(i, lane);
         float* crow = static_cast<float*>(go.C) + m * go.ldc + ncol0;
         const uint16_t* rrow = go.R ? go.R + m * go.ldr + ncol0 : nullptr;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
+          for (int q = 0; q < G; ++q) {
+            const int c = acc_col<MI>(j, q, lane);
             float4 o = make_float4(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
                                    acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha);
-            float4* cp = reinterpret_cast<float4*>(crow + j * 32 + q * 8);
+            float4* cp = reinterpret_cast<float4*>(crow + c);
             if (go.beta != 0.f) {
-              const float4 c = *cp;
-              o.x = fmaf(go.beta, c.x, o.x); o.y = fmaf(go.beta, c.y, o.y);
-              o.z = fmaf(go.beta, c.z, o.z); o.w = fmaf(go.beta, c.w, o.w);
+              const float4 cv = *cp;
+              o.x = fmaf(go.beta, cv.x, o.x); o.y = fmaf(go.beta, cv.y, o.y);
+              o.z = fmaf(go.beta, cv.z, o.z); o.w = fmaf(go.beta, cv.w, o.w);
             }
             if (rrow) {
-              const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
+              const uint2 r = *reinterpret_cast<const uint2*>(rrow + c);
               o.x += F::to_f(r.x & 0xffff); o.y += F::to_f(r.x >> 16); o.z += F::to_f(r.y & 0xffff); o.w += F::to_f(r.y >> 16);
             }
             *cp = o;
@@ -456,23 +510,24 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
     } else {
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const int64_t m = m0 + wm * TM + i * 32 + frag_row;
+        const int64_t m = m0 + wm * TM + acc_row<MI>(i, lane);
         uint16_t* crow = static_cast<uint16_t*>(go.C) + m * go.ldc + ncol0;
         const uint16_t* rrow = go.R ? go.R + m * go.ldr + ncol0 : nullptr;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
+          for (int q = 0; q < G; ++q) {
+            const int c = acc_col<MI>(j, q, lane);
             float o[4] = {acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
                           acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha};
-            uint2* cp = reinterpret_cast<uint2*>(crow + j * 32 + q * 8);
+            uint2* cp = reinterpret_cast<uint2*>(crow + c);
             if (go.beta != 0.f) {
-              const uint2 c = *cp;
-              o[0] = fmaf(go.beta, F::to_f(c.x & 0xffff), o[0]); o[1] = fmaf(go.beta, F::to_f(c.x >> 16), o[1]);
-              o[2] = fmaf(go.beta, F::to_f(c.y & 0xffff), o[2]); o[3] = fmaf(go.beta, F::to_f(c.y >> 16), o[3]);
+              const uint2 cv = *cp;
+              o[0] = fmaf(go.beta, F::to_f(cv.x & 0xffff), o[0]); o[1] = fmaf(go.beta, F::to_f(cv.x >> 16), o[1]);
+              o[2] = fmaf(go.beta, F::to_f(cv.y & 0xffff), o[2]); o[3] = fmaf(go.beta, F::to_f(cv.y >> 16), o[3]);
             }
             if (rrow) {
-              const uint2 r = *reinterpret_cast<const uint2*>(rrow + j * 32 + q * 8);
+              const uint2 r = *reinterpret_cast<const uint2*>(rrow + c);
               o[0] = with_residual<F>(o[0], r.x & 0xffff); o[1] = with_residual<F>(o[1], r.x >> 16);
               o[2] = with_residual<F>(o[2], r.y & 0xffff); o[3] = with_residual<F>(o[3], r.y >> 16);
             }
@@ -483,18 +538,18 @@ __device__ __forceinline__ void store_tile(const GemmArgs& go, f32x16_t (&acc)[B
     return;
   }
   constexpr int kPitch = TN + 4;  // floats; 16-byte aligned, staggers the banks of consecutive rows
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
+  float* stage = reinterpret_cast<float*>(smem) + wave * MI * kPitch;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float4*>(stage + frag_row * kPitch + j * 32 + q * 8 + half * 4) =
+      for (int q = 0; q < G; ++q)
+        *reinterpret_cast<float4*>(stage + acc_row<MI>(0, lane) * kPitch + acc_col<MI>(j, q, lane)) =
             make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
     __syncthreads();
-    const int64_t mband = m0 + wm * TM + i * 32, nband = n0 + wn * TN;
-    for (int it = lane; it < 32 * (TN / 4); it += 64) {
+    const int64_t mband = m0 + wm * TM + i * MI, nband = n0 + wn * TN;
+    for (int it = lane; it < MI * (TN / 4); it += 64) {
       const int r = it / (TN / 4), c4 = it % (TN / 4);
       const int64_t m = mband + r, n = nband + c4 * 4;
       if (m < go.M && n < go.N) {
@@ -594,7 +649,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 
   GemmArgs go = g;  // split-K: this split's fp32 slab
   if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
-  store_tile<F, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+  store_tile<F, 32, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
 }
 
 // ---------------------------------------------------------------------------
@@ -685,33 +740,46 @@ struct DmaOperand {
   }
 };
 
-// Per-lane LDS offsets of this wave's NF fragments (32-row blocks blk0 ..
-// blk0+NF-1 of the operand) for the DBK/16 16-deep slices of a stage.
-template <bool KMAJOR, int NF, int DBK>
+// Per-lane LDS offsets of this wave's NF 16-row fragments (16-row blocks
+// blk0 .. blk0+NF-1 of the operand) for the two 32-deep K slices of a 64-deep
+// stage, in the operand layout of the 16x16x32 MFMA: lane l supplies row
+// l % 16 of the fragment and K values 8*(l/16) .. +7 of the slice.
+template <bool KMAJOR, int NF>
 struct DmaFrags {
-  int off[KMAJOR ? NF : 1][DBK / 16];  // K-major
+  int off[KMAJOR ? NF : 1][2];  // K-major
   int base[2], ioff[KMAJOR ? 1 : NF];  // M/N-major
 
   __device__ __forceinline__ void init(int blk0, int lane) {
     if constexpr (KMAJOR) {
+      // a K-major stage row is 64 K (8 chunks of 8, swizzled by swz<8>); chunk
+      // 4*kk + l/16 of row r.  8 consecutive lanes read 8 rows of one logical
+      // chunk: distinct banks under swz<8>.
 #pragma unroll
       for (int f = 0; f < NF; ++f)
 #pragma unroll
-        for (int kk = 0; kk < DBK / 16; ++kk) {
-          const int r = (blk0 + f) * 32 + (lane & 31);
-          off[f][kk] = r * (2 * DBK) + (((2 * kk + (lane >> 5)) ^ (DBK == 64 ? swz<8>(r) : swz_k4(r))) << 4);
+        for (int kk = 0; kk < 2; ++kk) {
+          const int r = (blk0 + f) * 16 + (lane & 15);
+          off[f][kk] = r * 128 + (((4 * kk + (lane >> 4)) ^ swz<8>(r)) << 4);
         }
     } else {
-      // lane 4j+q of 16-lane group G reads row 8*(G/2) + j (+4), columns
-      // 16*(G%2) + 4q .. +3 of the 32-column block, and receives column
-      // 16*(G%2) + (lane%16) at 4 consecutive rows
-      const int p = lane & 15, h = lane >> 5, cg = (lane >> 4) & 1;
-      const int x = 2 * cg + ((p & 3) >> 1);
+      // An M/N-major stage holds 64 K rows of 256 M/N values (512 bytes, 32
+      // chunks swizzled by swz_mn).  ds_read_b64_tr_b16 lets the 16 lanes of
+      // group G = l/16 load a 4 (K) x 16 (M/N) block, lane p = 4j + q reading
+      // K row j, columns 4q .. 4q+3, and gives lane p column p at the 4 K
+      // rows.  Two reads per fragment cover K rows 32*kk + 8G + 4*rd + 0..3
+      // (rd = 0, 1) of column block blk: lane p then holds column 16*blk + p
+      // at K 8G .. 8G+7 of the slice, the MFMA's operand layout.
+      //   chunk of (row r, column 16*blk + 4q) = (2*blk + q/2) ^ swz_mn(r),
+      //   swz_mn(r) = 4j + 2*(G%2) + rd for these rows, so the chunk splits
+      //   into (2*blk ^ (4j + 2*(G%2))) (per fragment: ioff) and (q/2 ^ rd)
+      //   (per read: base).  Each group's 8 chunks of 4 rows hit distinct
+      //   16-byte bank groups, as do the two groups of a half-wave.
+      const int p = lane & 15, grp = lane >> 4, j = p >> 2, q = p & 3;
 #pragma unroll
       for (int rd = 0; rd < 2; ++rd)
-        base[rd] = (8 * h + (p >> 2) + 4 * rd) * 512 + ((x ^ ((2 * h + rd) & 3)) << 4) + (p & 1) * 8;
+        base[rd] = (8 * grp + 4 * rd + j) * 512 + (((q >> 1) ^ rd) << 4) + (q & 1) * 8;
 #pragma unroll
-      for (int f = 0; f < NF; ++f) ioff[f] = ((blk0 + f) ^ (p >> 2)) << 6;
+      for (int f = 0; f < NF; ++f) ioff[f] = ((2 * (blk0 + f)) ^ (4 * j + 2 * (grp & 1))) << 4;
     }
   }
 
@@ -719,7 +787,7 @@ struct DmaFrags {
     if constexpr (KMAJOR) {
       return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(op + off[f][kk]));
     } else {
-      const char* blk = op + kk * 16 * 512 + ioff[f];
+      const char* blk = op + kk * 32 * 512 + ioff[f];
       const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[0]));
       const v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[1]));
       const uint2 xw = __builtin_bit_cast(uint2, x), yw = __builtin_bit_cast(uint2, y);
@@ -728,10 +796,10 @@ struct DmaFrags {
   }
 };
 
-// Fragments of one 16-deep K slice: fa (B operand, FN of them) and fb (A
+// Fragments of one 32-deep K slice: fa (B operand, FN of them) and fb (A
 // operand, FM), read from the LDS stage at (sa, sb).
-template <bool AK, bool BK, int FM, int FN, int DBK>
-__device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM, DBK>& fra, const DmaFrags<BK, FN, DBK>& frb, const char* sa,
+template <bool AK, bool BK, int FM, int FN>
+__device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM>& fra, const DmaFrags<BK, FN>& frb, const char* sa,
                                                const char* sb, int kk, bf16x8_t (&fa)[FN], bf16x8_t (&fb)[FM]) {
 #pragma unroll
   for (int j = 0; j < FN; ++j) fa[j] = frb.frag(sb, j, kk);
@@ -740,11 +808,11 @@ __device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM, DBK>& fra,
 }
 
 template <typename F, int FM, int FN>
-__device__ __forceinline__ void dma_mfma(f32x16_t (&acc)[FM][FN], const bf16x8_t (&fa)[FN], const bf16x8_t (&fb)[FM]) {
+__device__ __forceinline__ void dma_mfma(f32x4_t (&acc)[FM][FN], const bf16x8_t (&fa)[FN], const bf16x8_t (&fb)[FM]) {
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<F>(fa[j], fb[i], acc[i][j]);
+    for (int j = 0; j < FN; ++j) acc[i][j] = mfma_k32<F>(fa[j], fb[i], acc[i][j]);
 }
 
 // Scheduling of one K slice: NM MFMAs, each followed by up to ceil(R/NM) of
@@ -762,22 +830,20 @@ __device__ __forceinline__ void sched_slice() {
 }
 
 
-// Direct-to-LDS kernel, any operand layouts: 256x256 tile, DBK-deep K steps
-// over NST LDS stages of 2 x 512 x DBK bytes.  NST == 2: one stage loads while
-// the other is read, and the barrier's fence waits for all loads.  NST > 2:
-// NST-1 stages are in flight; each step waits (vmcnt) only for the oldest
-// stage's loads and then syncs the workgroup with a bare barrier.  K must be
-// a multiple of DBK in every split; an M-major A needs M % 8 == 0 (N-major B:
+// Direct-to-LDS kernel, any operand layouts: 256x256 tile, 64-deep K steps
+// over two LDS stages of 2 x 512 x 64 bytes; 8 waves of 128x64, each an 8x4
+// grid of 16x16x32 MFMA tiles (two 32-deep slices per stage).  K must be a
+// multiple of 64 in every split; an M-major A needs M % 8 == 0 (N-major B:
 // N % 8 == 0).
 //
-// With two stages every layout runs the mid-step schedule (kMid): half of the
-// waves (one per SIMD) issue all stage loads, so the other wave on each SIMD
-// keeps issuing MFMAs while the loads queue, and the barrier sits in the
-// middle of a step, after the last LDS reads of the current stage, so that
-// the MFMAs of its last two slices run while the next stage's first
-// fragments are read.  Measured on the 1B step's shapes against the plain
-// step (all waves load, barrier at the step's start): input gradients 3-6 %
-// faster, weight gradients 1-7 %, forward products 4-11 %.
+// Schedule (the mid-step barrier): half of the waves (one per SIMD) issue all
+// stage loads, so the other wave on each SIMD keeps issuing MFMAs while the
+// loads queue, and the barrier sits in the middle of a step, after the last
+// LDS reads of the current stage, so that the MFMAs of its second slice run
+// while the next stage's first fragments are read.  Measured on the 1B step's
+// shapes against the plain step (all waves load, barrier at the step's
+// start): input gradients 3-6 % faster, weight gradients 1-7 %, forward
+// products 4-11 %.
 // Outputs of the fused gate|up projection + SwiGLU: h = silu(gate) * up
 // ([M, F] bf16); the GEMM's own output (gate|up, [M, 2F]) goes to GemmArgs::C
 // when that is not null.
@@ -813,14 +879,14 @@ enum { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2, kEpiSwiGLUBwd = 3 };
 
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
-                                             f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t tn,
+                                             f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t tn,
                                              char* smem, int lane, int wave);
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
-                                           f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t n0,
+                                           f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t n0,
                                            char* smem, int lane, int wave);
 template <int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
+__device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t (&acc)[BM / WM / 16][BN / WN / 16],
                                                  int64_t m0, int64_t n0, char* smem, int lane, int wave);
 
 // One workgroup's 256x256 tile of the direct-to-LDS GEMM (main loop, then the
@@ -834,19 +900,16 @@ template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST, int kE
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o, const RopeIn& rope,
                                               const SwigluBwdIn& sb) {
   constexpr bool kSwiGLU = kEpi == kEpiSwiGLU;
-  constexpr int BM = 256, BN = 256;
+  constexpr int BM = 256, BN = 256, MI = 16;
   constexpr int kWaves = WM * WN;
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MI, FN = TN / MI;
   constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage
   constexpr int kStage = 2 * kOpBytes;
-  constexpr bool kMid = NST == 2;
-  constexpr int kLoadWaves = kMid ? kWaves / 2 : kWaves;  // waves that issue the stage loads
+  constexpr int kLoadWaves = kWaves / 2;               // waves that issue the stage loads
   constexpr int kPerWave = kOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
-  constexpr int kSlices = DBK / 16;
+  static_assert(DBK == 64 && NST == 2, "two LDS stages of 64 K: two 32-deep slices each");
   static_assert(kPerWave * kLoadWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
-  static_assert(!kMid || (NST == 2 && kSlices == 4), "the mid-step barrier runs two stages of four slices");
-  static_assert(kWaves * 32 * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
-  static_assert(kSlices == 2 || kSlices == 4, "stages hold 2 or 4 K slices");
+  static_assert(kWaves * MI * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
   static_assert(kEpi == kEpiPlain || F::kDtype == LZ_BF16, "the fused epilogues are bf16");
 
   __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
@@ -868,127 +931,54 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   la.init(g.A, g.lda, m0, g.M, kbeg, lwave, lane);
   if constexpr (kSwiGLU) lb.init(g.B, g.ldb, tn * 128, g.N, kbeg, lwave, lane, o.F);
   else lb.init(g.B, g.ldb, n0, g.N, kbeg, lwave, lane);
-  DmaFrags<AK, FM, DBK> fra;
-  DmaFrags<BK, FN, DBK> frb;
+  DmaFrags<AK, FM> fra;
+  DmaFrags<BK, FN> frb;
   fra.init(wm * FM, lane);
   frb.init(wn * FN, lane);
 
-  f32x16_t acc[FM][FN];
+  f32x4_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
 
-  if constexpr (kMid) {
-    constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);
-    if (ktiles > 0 && loader) {
-      la.issue(smem, lwave, 0);
-      lb.issue(smem + kOpBytes, lwave, 0);
-    }
+  constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);  // LDS read instructions per slice
+  if (ktiles > 0 && loader) {
+    la.issue(smem, lwave, 0);
+    lb.issue(smem + kOpBytes, lwave, 0);
+  }
+  dma_barrier();
+  if (ktiles > 1 && loader) {
+    la.issue(smem + kStage, lwave, 1);
+    lb.issue(smem + kStage + kOpBytes, lwave, 1);
+  }
+  // slice 0 of stage kt is in registers when step kt begins
+  bf16x8_t fa0[FN], fb0[FM];
+  dma_load_frags(fra, frb, smem, smem + kOpBytes, 0, fa0, fb0);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const char* sa = smem + (kt & 1) * kStage;
+    const char* sb = sa + kOpBytes;
+    bf16x8_t fa1[FN], fb1[FM];
+    dma_mfma<F>(acc, fa0, fb0);
+    dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
+    sched_slice<kReads, FM * FN>();
+    // this wave's loads of stage kt+1 and its reads of stage kt are done;
+    // past the barrier stage kt+1 is complete and no wave reads stage kt's
+    // slot any more, so stage kt+2 may refill it
     dma_barrier();
-    if (ktiles > 1 && loader) {
-      la.issue(smem + kStage, lwave, 1);
-      lb.issue(smem + kStage + kOpBytes, lwave, 1);
+    if (kt + 2 < ktiles && loader) {
+      char* nxt = smem + (kt & 1) * kStage;
+      la.issue(nxt, lwave, kt + 2);
+      lb.issue(nxt + kOpBytes, lwave, kt + 2);
     }
-    // slices 0 and 1 of stage kt are in registers when step kt begins
-    bf16x8_t fa0[FN], fb0[FM], fa1[FN], fb1[FM];
-    dma_load_frags(fra, frb, smem, smem + kOpBytes, 0, fa0, fb0);
-    dma_load_frags(fra, frb, smem, smem + kOpBytes, 1, fa1, fb1);
-    for (int kt = 0; kt < ktiles; ++kt) {
-      const char* sa = smem + (kt & 1) * kStage;
-      const char* sb = sa + kOpBytes;
-      dma_mfma<F>(acc, fa0, fb0);
-      dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
-      dma_mfma<F>(acc, fa1, fb1);
-      dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
-      sched_slice<kReads, FM * FN>();
-      sched_slice<kReads, FM * FN>();
-      // this wave's loads of stage kt+1 and its reads of stage kt are done;
-      // past the barrier stage kt+1 is complete and no wave reads stage kt's
-      // slot any more, so stage kt+2 may refill it
-      dma_barrier();
-      if (kt + 2 < ktiles && loader) {
-        char* nxt = smem + (kt & 1) * kStage;
-        la.issue(nxt, lwave, kt + 2);
-        lb.issue(nxt + kOpBytes, lwave, kt + 2);
-      }
-      // slices 0 and 1 of stage kt+1 (after the last step: unused reads of
-      // the other slot) while the MFMAs of slices 2 and 3 run
-      const char* na = smem + ((kt + 1) & 1) * kStage;
-      const char* nb = na + kOpBytes;
-      bf16x8_t ga0[FN], gb0[FM], ga1[FN], gb1[FM];
-      dma_mfma<F>(acc, fa0, fb0);
-      dma_load_frags(fra, frb, na, nb, 0, ga0, gb0);
-      dma_mfma<F>(acc, fa1, fb1);
-      dma_load_frags(fra, frb, na, nb, 1, ga1, gb1);
-      sched_slice<kReads, FM * FN>();
-      sched_slice<kReads, FM * FN>();
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        fa0[j] = ga0[j];
-        fa1[j] = ga1[j];
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        fb0[i] = gb0[i];
-        fb1[i] = gb1[i];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int st = 0; st < NST - 1; ++st)
-      if (st < ktiles) {
-        la.issue(smem + st * kStage, lwave, st);
-        lb.issue(smem + st * kStage + kOpBytes, lwave, st);
-      }
-    for (int kt = 0; kt < ktiles; ++kt) {
-      if constexpr (NST == 2) {
-        // only stage kt's loads are in flight here: wait for them, then the
-        // barrier publishes every wave's part and retires the reads of stage
-        // kt-1, whose slot is refilled next
-        dma_barrier();
-      } else {
-        // stage kt's loads are this wave's oldest: let the (up to NST-2) later
-        // stages stay in flight, then the barrier publishes every wave's part
-        // and retires the reads of stage kt-1, whose slot is refilled next
-        static_assert(NST == 4, "the wait ladder below covers four stages");
-        constexpr int kLoads = 2 * kPerWave;  // DMA instructions per wave per stage
-        const int ahead = ktiles - 1 - kt;
-        asm volatile("" ::: "memory");
-        if (ahead >= 2) wait_vmcnt<2 * kLoads>();
-        else if (ahead == 1) wait_vmcnt<kLoads>();
-        else wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-      }
-      if (kt + NST - 1 < ktiles) {
-        char* nxt = smem + ((kt + NST - 1) % NST) * kStage;
-        la.issue(nxt, lwave, kt + NST - 1);
-        lb.issue(nxt + kOpBytes, lwave, kt + NST - 1);
-      }
-      const char* sa = smem + (kt % NST) * kStage;
-      const char* sb = sa + kOpBytes;
-      // fragments double-buffered in registers: slice kk+1 is read while the
-      // MFMAs of slice kk run
-      bf16x8_t fa0[FN], fb0[FM], fa1[FN], fb1[FM];
-      constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);
-      dma_load_frags(fra, frb, sa, sb, 0, fa0, fb0);
-      dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
-      dma_mfma<F>(acc, fa0, fb0);
-      if constexpr (kSlices == 4) {
-        dma_load_frags(fra, frb, sa, sb, 2, fa0, fb0);
-        dma_mfma<F>(acc, fa1, fb1);
-        dma_load_frags(fra, frb, sa, sb, 3, fa1, fb1);
-        dma_mfma<F>(acc, fa0, fb0);
-      }
-      dma_mfma<F>(acc, fa1, fb1);
-      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
-#pragma unroll
-      for (int q = 0; q < kSlices - 1; ++q) sched_slice<kReads, FM * FN>();
-      sched_slice<0, FM * FN>();
-    }
+    // slice 0 of stage kt+1 (after the last step: unused reads of the other
+    // slot) while the MFMAs of slice 1 run
+    const char* na = smem + ((kt + 1) & 1) * kStage;
+    dma_mfma<F>(acc, fa1, fb1);
+    dma_load_frags(fra, frb, na, na + kOpBytes, 0, fa0, fb0);
+    sched_slice<kReads, FM * FN>();
   }
   __syncthreads();  // every wave is done with the stages before the epilogue may reuse LDS
 
@@ -1001,7 +991,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   } else {
     GemmArgs go = g;  // split-K: this split's fp32 slab
     if (g.slab) go.C = static_cast<float*>(g.C) + (int64_t)blockIdx.y * g.slab;
-    store_tile<F, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
+    store_tile<F, MI, BM, BN, WM, WN>(go, acc, m0, n0, smem, lane, wave);
   }
 }
 
@@ -1035,25 +1025,14 @@ __global__ void __launch_bounds__(512) gemm_swiglu_bwd_kernel(GemmArgs g, Swiglu
 // unfused SwiGLU backward kernel does (the same element routine) and writes
 // them as whole 16-byte pieces.
 template <int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x16_t (&acc)[BM / WM / 32][BN / WN / 32],
+__device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t (&acc)[BM / WM / 16][BN / WN / 16],
                                                  int64_t m0, int64_t n0, char* smem, int lane, int wave) {
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
   constexpr int kRow = TN * 2, kChunks = kRow / 16;
   const int wm = wave / WN, wn = wave % WN;
-  const int frag_row = lane & 31, half = lane >> 5;
   const int64_t mrow0 = m0 + wm * TM, ncol0 = n0 + wn * TN;
   char* st = smem + wave * (TM * TN * 2);
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = i * 32 + frag_row, chunk = j * 4 + q;
-        *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
-            make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                       pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
-      }
+  park16<FmtBF16, 16, FM, FN, kRow>(acc, st, lane, 1.0f);
   asm volatile("" ::: "memory");
   constexpr int kIters = TM * kChunks / 64;
   constexpr int kBlk = 4;  // gate and up pieces of four stores loaded together
@@ -1089,27 +1068,16 @@ __device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x16_t
 // from the stored gate|up, and written as whole 128-byte rows.
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
-                                             f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t tn,
+                                             f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t tn,
                                              char* smem, int lane, int wave) {
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
   static_assert(WN == 4 && TN == 64, "gate and up are two 64-column waves each");
   constexpr int kRow = TN * 2, kChunks = kRow / 16, kWaveBytes = TM * kRow;
   const int wm = wave / WN, wn = wave % WN;
-  const int frag_row = lane & 31, half = lane >> 5;
   const int64_t mrow0 = m0 + wm * TM;
   const int64_t col = tn * 128 + (wn & 1) * 64;  // gate (and up) column of this wave's tile
   char* st = smem + wave * kWaveBytes;
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = i * 32 + frag_row, chunk = j * 4 + q;
-        *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
-            make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                       pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
-      }
+  park16<FmtBF16, 16, FM, FN, kRow>(acc, st, lane, 1.0f);
   if (g.C) {
     asm volatile("" ::: "memory");
     uint16_t* gu = static_cast<uint16_t*>(g.C) + (wn < 2 ? 0 : o.F) + col;
@@ -1145,30 +1113,19 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
 // per-op rounding, as the RoPE kernel computes it.
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
-                                           f32x16_t (&acc)[BM / WM / 32][BN / WN / 32], int64_t m0, int64_t n0,
+                                           f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t n0,
                                            char* smem, int lane, int wave) {
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
   static_assert(WN == 4 && TN == 64, "a head of 128 is two 64-column waves");
   if (n0 >= r.nrope) {
-    store_tile<FmtBF16, BM, BN, WM, WN>(g, acc, m0, n0, smem, lane, wave);
+    store_tile<FmtBF16, 16, BM, BN, WM, WN>(g, acc, m0, n0, smem, lane, wave);
     return;
   }
   constexpr int kRow = TN * 2, kChunks = kRow / 16, kWaveBytes = TM * kRow, kHd = 2 * TN;
   const int wm = wave / WN, wn = wave % WN;
-  const int frag_row = lane & 31, half = lane >> 5;
   const int64_t mrow0 = m0 + wm * TM;
   char* st = smem + wave * kWaveBytes;
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = i * 32 + frag_row, chunk = j * 4 + q;
-        *reinterpret_cast<uint2*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4) + half * 8) =
-            make_uint2(pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                       pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
-      }
+  park16<FmtBF16, 16, FM, FN, kRow>(acc, st, lane, 1.0f);
   __syncthreads();
   const int xw = wave & ~1;  // the wave holding x1 of this head
   const char* s1 = smem + xw * kWaveBytes;
