@@ -58,6 +58,7 @@ def train_reference(
     loss_chunk_size: int = 128,
     on_step: Optional[Callable[[int, float, float, Dict[str, torch.Tensor]], None]] = None,
     param_dtype: torch.dtype = torch.float32,
+    low_precision_state: bool = False,
 ) -> Dict[str, List[float]]:
     """Runs the train.py loop on CPU tensors (P is updated in place).  Returns
     per-step mean micro-batch loss, pre-clip grad norm and step seconds.
@@ -68,8 +69,20 @@ def train_reference(
     param_dtype=torch.bfloat16 gives the reference's bf16-parameter semantics
     (train_zero.py:150-153 with an fp32 master, zero/stage0_ddp.py:44-47): the
     forward and backward see the fp32 master rounded to bf16, the update is
-    applied to the fp32 master.  The arithmetic itself stays fp32."""
-    params = {k: v.detach().clone().requires_grad_(True) for k, v in P.items()}
+    applied to the fp32 master.  The arithmetic itself stays fp32.
+
+    low_precision_state=True (with param_dtype bf16 or fp16) gives the
+    reference train.py's own semantics at --dtype bfloat16 (train.py:157-160
+    builds the model in that dtype, :206-211 hands its parameters to
+    torch.optim.AdamW, :259-271 clips): no fp32 master; the parameters, their
+    gradients and AdamW's exp_avg / exp_avg_sq are all in param_dtype, so
+    clip_grad_norm_ and every op of the update round to it.  The forward and
+    backward still run in fp32 arithmetic on the parameters' values, and each
+    gradient is rounded to param_dtype once."""
+    if low_precision_state and param_dtype == torch.float32:
+        raise ValueError("low_precision_state needs a 16-bit param_dtype")
+    store = param_dtype if low_precision_state else torch.float32
+    params = {k: v.detach().to(store).clone().requires_grad_(True) for k, v in P.items()}
     opt = torch.optim.AdamW(list(params.values()), lr=lr, betas=betas, weight_decay=weight_decay)
     out = {"loss": [], "grad_norm": [], "seconds": []}
     for step in range(1, steps + 1):
@@ -88,15 +101,15 @@ def train_reference(
             (loss / grad_accum_steps).backward()
         if work is not params:
             for k, v in params.items():
-                v.grad = work[k].grad
+                v.grad = work[k].grad.to(store)
         if max_grad_norm > 0:
             gn = float(torch.nn.utils.clip_grad_norm_(list(params.values()), max_norm=max_grad_norm).item())
         else:
             gn = math.nan
         if on_step is not None:
-            grads = {k: v.grad.detach().clone() for k, v in params.items()}
+            grads = {k: v.grad.detach().to(torch.float32, copy=True) for k, v in params.items()}
             if on_step.__code__.co_argcount >= 5:
-                on_step(step, sum(losses) / len(losses), gn, grads, {k: v.detach() for k, v in params.items()})
+                on_step(step, sum(losses) / len(losses), gn, grads, {k: v.detach().float() for k, v in params.items()})
             else:
                 on_step(step, sum(losses) / len(losses), gn, grads)
         opt.step()
@@ -105,5 +118,5 @@ def train_reference(
         out["seconds"].append(time.perf_counter() - t0)
     with torch.no_grad():
         for k in P:
-            P[k].copy_(params[k])
+            P[k].copy_(params[k].to(P[k].dtype))
     return out

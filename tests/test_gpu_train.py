@@ -282,6 +282,48 @@ def test_grad_sink_leaves_an_unused_parameter_untouched():
         assert torch.equal(a.detach(), used[n].detach()), n
 
 
+def test_train_py_bf16_vs_reference_bf16_adamw(tmp_path):
+    """`train.py --dtype bfloat16` (the reference's default) for 100 steps of
+    the plumbing workload, run as the CLI, against the oracle trainer with the
+    reference train.py's own optimizer semantics: torch.optim.AdamW on the
+    bf16 parameters, bf16 exp_avg / exp_avg_sq and clip_grad_norm_ on bf16
+    gradients (train.py:157-160,206-211,259-271).  This build's train.py keeps
+    an fp32 master and fp32 moments for bf16 parameters instead; the bar is
+    the bf16 training tolerance, loss within 1e-2 relative at every step."""
+    from data.fineweb import SyntheticUniformDataset
+
+    steps, B, S, GA = 100, 4, 128, 2
+    out = _run(["train.py", "--model-size", "plumbing", "--dtype", "bfloat16", "--data-mode", "synthetic-uniform",
+                "--synthetic-vocab-size", "32000", "--seq-len", str(S), "--batch-size", str(B), "--grad-accum-steps",
+                str(GA), "--max-steps", str(steps), "--seed", "0", "--log-interval", "1", "--checkpoint-interval", "0",
+                "--save-dir", str(tmp_path)])
+    hip = {int(m.group(1)): float(m.group(2)) for m in STEP_RE.finditer(out)}
+    assert sorted(hip) == list(range(1, steps + 1)), out[-2000:]
+    # the oracle's stream is the CLI's: the dataset's per-sequence draws, batched
+    ds = iter(SyntheticUniformDataset(seq_len=S, vocab_size=32000, seed=0))
+    oc = OD.uniform_chunks(S, 32000, B, seed=0)
+    for _ in range(3):
+        assert torch.equal(next(oc), torch.stack([next(ds) for _ in range(B)]))
+    cfg = build_config("plumbing", vocab_size=32000, max_seq_len=S)
+    torch.manual_seed(0)  # train.py's set_seed(0) before building the model
+    P = {k: v.detach().clone() for k, v in LlamaForCausalLM(cfg).state_dict().items() if k != "lm_head.weight"}
+    ocfg = OM.Cfg(vocab_size=cfg.vocab_size, dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads,
+                  n_kv_heads=cfg.n_kv_heads, ffn_dim=cfg.ffn_dim, rope_theta=cfg.rope_theta,
+                  rope_angle_dtype=torch.bfloat16)
+    runs = {}
+    for name, low in (("bf16 state", True), ("fp32 master", False)):
+        runs[name] = OE.train_reference(ocfg, {k: v.clone() for k, v in P.items()},
+                                        OD.uniform_chunks(S, 32000, B, seed=0), steps=steps, grad_accum_steps=GA,
+                                        lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, max_grad_norm=1.0,
+                                        loss_chunk_size=128, param_dtype=torch.bfloat16,
+                                        low_precision_state=low)["loss"]
+    rel = {name: [abs(hip[i + 1] - l) / abs(l) for i, l in enumerate(ref)] for name, ref in runs.items()}
+    for name, r in rel.items():
+        print(f"train.py bf16 vs oracle ({name}): max loss rel diff {max(r):.2e} (step {r.index(max(r)) + 1}), "
+              f"oracle loss {runs[name][0]:.4f} -> {runs[name][-1]:.4f}, train.py {hip[1]:.4f} -> {hip[steps]:.4f}")
+    assert max(rel["bf16 state"]) <= 1e-2
+
+
 def test_capturable_adamw_refuses_a_late_parameter():
     """With capturable=True the step count lives on the device per parameter
     group, so a parameter whose first gradient arrives after the group's

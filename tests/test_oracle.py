@@ -166,6 +166,32 @@ def test_engine_update_matches_torch_adamw(max_norm):
     assert eng.step_count == 6
 
 
+def test_train_reference_low_precision_state():
+    """The train.py leg with the reference's bf16 optimizer state
+    (low_precision_state): after training, every parameter is a bf16 value
+    (no fp32 master behind it), the parameters moved, and they differ from
+    the fp32-master leg run on the same stream; a fp32 param_dtype is
+    refused."""
+    cfg = OM.Cfg(vocab_size=256, dim=64, n_layers=1, n_heads=4, n_kv_heads=2, ffn_dim=128, rope_theta=10_000.0,
+                 rope_angle_dtype=torch.bfloat16)
+    torch.manual_seed(0)
+    P0 = OM.init_params(cfg)
+    out = {}
+    for low in (True, False):
+        P = {k: v.clone() for k, v in P0.items()}
+        OE.train_reference(cfg, P, OD.uniform_chunks(32, 256, 2, seed=1), steps=3, grad_accum_steps=1, lr=1e-2,
+                           param_dtype=torch.bfloat16, low_precision_state=low)
+        out[low] = P
+    for k, v in out[True].items():
+        assert torch.equal(v, v.to(torch.bfloat16).float()), k
+    assert any(not torch.equal(v, v.to(torch.bfloat16).float()) for v in out[False].values())
+    assert all(not torch.equal(out[True][k], P0[k].to(torch.bfloat16).float()) for k in P0 if P0[k].dim() == 2)
+    assert any(not torch.equal(out[True][k], out[False][k].to(torch.bfloat16).float()) for k in P0)
+    with pytest.raises(ValueError):
+        OE.train_reference(cfg, dict(P0), OD.uniform_chunks(32, 256, 2, seed=1), steps=1, grad_accum_steps=1,
+                           low_precision_state=True)
+
+
 BASELINE_COUNTS = {
     # (dim, layers, heads, kv, ffn) -> tied parameter count (BASELINE workloads)
     (256, 4, 8, 4, 688): 11_094_272,
