@@ -746,21 +746,22 @@ struct DmaOperand {
 // l % 16 of the fragment and K values 8*(l/16) .. +7 of the slice.
 template <bool KMAJOR, int NF>
 struct DmaFrags {
-  int off[KMAJOR ? NF : 1][2];  // K-major
+  int kb[KMAJOR ? 2 : 1];              // K-major
   int base[2], ioff[KMAJOR ? 1 : NF];  // M/N-major
 
   __device__ __forceinline__ void init(int blk0, int lane) {
     if constexpr (KMAJOR) {
       // a K-major stage row is 64 K (8 chunks of 8, swizzled by swz<8>); chunk
-      // 4*kk + l/16 of row r.  8 consecutive lanes read 8 rows of one logical
-      // chunk: distinct banks under swz<8>.
+      // 4*kk + l/16 of row r = 16*(blk0 + f) + l%16.  swz<8>(r) depends only
+      // on r % 16, so fragment f sits at a constant offset f*16*128 from
+      // fragment 0 (two offset registers per operand, not two per fragment).
+      // 8 consecutive lanes read 8 rows of one logical chunk: distinct banks
+      // under swz<8>.
 #pragma unroll
-      for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int r = (blk0 + f) * 16 + (lane & 15);
-          off[f][kk] = r * 128 + (((4 * kk + (lane >> 4)) ^ swz<8>(r)) << 4);
-        }
+      for (int kk = 0; kk < 2; ++kk) {
+        const int r = blk0 * 16 + (lane & 15);
+        kb[kk] = r * 128 + (((4 * kk + (lane >> 4)) ^ swz<8>(r)) << 4);
+      }
     } else {
       // An M/N-major stage holds 64 K rows of 256 M/N values (512 bytes, 32
       // chunks swizzled by swz_mn).  ds_read_b64_tr_b16 lets the 16 lanes of
@@ -785,7 +786,7 @@ struct DmaFrags {
 
   __device__ __forceinline__ bf16x8_t frag(const char* op, int f, int kk) const {
     if constexpr (KMAJOR) {
-      return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(op + off[f][kk]));
+      return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(op + f * 16 * 128 + kb[kk]));
     } else {
       const char* blk = op + kk * 32 * 512 + ioff[f];
       const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[0]));
