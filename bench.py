@@ -82,6 +82,42 @@ def run_steps(model, engine, batches, steps: int, warmup: int):
     return time.perf_counter() - t0, losses
 
 
+def bench_125m(dev: torch.device, steps: int, warmup: int, per_plan: bool = False) -> dict:
+    """The 125M model (d768, 12 layers, 12 q / 4 kv heads of 64, ffn 2048,
+    vocab 32000) through the ZeRO-1 engine at B=16, S=1024; with per_plan,
+    each GEMM launch plan's share of the step (HIP events on the launch
+    stream, as for the headline)."""
+    from lzhip import ops
+    from profiler import estimate_transformer_train_flops
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    cfg, model, eng = make_engine("125m", 1, 16, 1024, dev)
+    batches = [torch.randint(0, 32000, (16, 1024), device=dev, generator=gen) for _ in range(4)]
+    k = max(steps, 5)
+    probe = ops.LaunchProbe() if per_plan else None
+    run_steps(model, eng, batches, steps=0, warmup=warmup)
+    if probe is not None:
+        ops.set_gemm_probe(probe)
+    try:
+        el, _ = run_steps(model, eng, batches, steps=k, warmup=0)
+    finally:
+        ops.set_gemm_probe(None)
+    f = estimate_transformer_train_flops(cfg, 16, 1024, stage=0)
+    out = {"tokens_per_s": 16 * 1024 * k / el, "ms_per_step": el * 1000 / k,
+           "mfma_util": f * k / el / 1e12 / PEAK_BF16_TFLOPS, "model_tflop_per_step": f / 1e12,
+           "workload": "125m ZeRO-1 (d768 L12 12q/4kv ffn2048 V32000), B=16 S=1024"}
+    if probe is not None:
+        n, fl, ms = probe.summary()
+        out["gemm_all_launches"] = {"ms_per_step": ms / k, "TFLOP/s": fl / (ms * 1e-3) / 1e12}
+        out["gemm_kernels"] = sorted(
+            ({"kernel": ops.gemm_kernel_name(key), "launches": v[0], "ms_per_step": v[2] / k,
+              "TFLOP/s": v[1] / (v[2] * 1e-3) / 1e12} for key, v in probe.by_key().items()),
+            key=lambda d: -d["ms_per_step"])
+    del model, eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_adamw(dev: torch.device, ceilings=None, n: int = 124_000_000, iters: int = 10):
     from lzhip import ops
 
@@ -550,6 +586,9 @@ def main() -> int:
                          "sweep of the O projection; prints one JSON line and exits")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the 1B ZeRO-3 step (no recompute=False, 125M, AdamW or pointwise legs)")
+    ap.add_argument("--125m-only", dest="only_125m", action="store_true",
+                    help="only the 125M ZeRO-1 step (B=16, S=1024), with its GEMM launches timed per plan; prints "
+                         "one JSON line and exits")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's engines run at world_size 1 (got --gpus {args.gpus})",
@@ -577,6 +616,9 @@ def main() -> int:
         return 0
     if args.gemm_sweep:
         print(json.dumps({"gemm_sweep": gemm_sweep(dev)}), flush=True)
+        return 0
+    if args.only_125m:
+        print(json.dumps({"llama_125m_zero1": bench_125m(dev, args.steps, args.warmup, per_plan=True)}), flush=True)
         return 0
     B, S = 8, 2048
     log("building 1B model + ZeRO-3 engine")
@@ -623,16 +665,7 @@ def main() -> int:
     res_125m = None
     if not args.skip_125m:
         log("125M ZeRO-1")
-        cfg2, m2, e2 = make_engine("125m", 1, 16, 1024, dev)
-        b2 = [torch.randint(0, 32000, (16, 1024), device=dev, generator=gen) for _ in range(4)]
-        el2, l2 = run_steps(m2, e2, b2, steps=max(args.steps, 5), warmup=args.warmup)
-        k2 = max(args.steps, 5)
-        f2 = estimate_transformer_train_flops(cfg2, 16, 1024, stage=0)
-        res_125m = {"tokens_per_s": 16 * 1024 * k2 / el2, "ms_per_step": el2 * 1000 / k2,
-                    "mfma_util": f2 * k2 / el2 / 1e12 / PEAK_BF16_TFLOPS, "model_tflop_per_step": f2 / 1e12,
-                    "workload": "125m ZeRO-1 (d768 L12 12q/4kv ffn2048 V32000), B=16 S=1024"}
-        del m2, e2
-        torch.cuda.empty_cache()
+        res_125m = bench_125m(dev, args.steps, args.warmup)
     plumbing = ceilings = None
     if not args.headline_only and not args.skip_plumbing:
         log("plumbing workload (train.py config)")
