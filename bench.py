@@ -5,8 +5,10 @@ Headline (`value`): training tokens/s of the 1B-class model (d2048, 16 layers,
 ZeRO-3 engine at world_size 1, micro-batch 8 x 2048 tokens, bf16 compute with
 an fp32 flat master, synthetic uniform token ids (seed 0) already resident in
 HBM, random-init weights (seed 0).  One step = zero_grad, prepare_forward,
-forward + loss, backward (with ZeRO-3's recomputation and 25M-element
-gradient buckets), step_with_stats (norm + fused AdamW).
+forward + loss, backward (with ZeRO-3's recomputation; at one rank the
+reduce-scatter of the flattened gradients is the identity, so each module's
+bf16 gradients are gathered straight into the fp32 gradient shard instead of
+through 25M-element bf16 buckets), step_with_stats (norm + fused AdamW).
 
 Also reported: MFMA utilisation of that step (model FLOPs, 3x forward, over
 2.5 PFLOP/s), the same step with the engine's recompute=False, the
@@ -137,8 +139,24 @@ def bench_adamw(dev: torch.device, ceilings=None, n: int = 124_000_000, iters: i
     ms = start.elapsed_time(end) / iters
     gbs = 28.0 * n / (ms * 1e-3) / 1e9
     out = {"elements": n, "bytes_per_elem": 28, "ms": ms, "GB/s": gbs, "frac_of_8TBs": gbs / PEAK_HBM_GBS}
+    # the form the ZeRO-3 step launches: the clip factor read from device
+    # memory and the bf16 parameters written beside the fp32 master (30 B per
+    # element)
+    p16 = ops.cast(p, torch.bfloat16)
+    scale = torch.ones((1,), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    start.record()
+    for t in range(iters):
+        ops.adamw_(p, m, v, grad, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=t + 12,
+                   grad_scale=scale, p_out=p16)
+    end.record()
+    torch.cuda.synchronize()
+    ms2 = start.elapsed_time(end) / iters
+    gbs2 = 30.0 * n / (ms2 * 1e-3) / 1e9
+    out["in_step_form"] = {"bytes_per_elem": 30, "ms": ms2, "GB/s": gbs2, "frac_of_8TBs": gbs2 / PEAK_HBM_GBS}
     if ceilings:
         out["frac_of_measured_copy"] = gbs / ceilings["copy_GB/s"]
+        out["in_step_form"]["frac_of_measured_copy"] = gbs2 / ceilings["copy_GB/s"]
     return out
 
 
@@ -487,10 +505,11 @@ def bench_pointwise(dev: torch.device, ceilings=None, rows: int = 16384, dim: in
     return out
 
 
-def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
+def cpu_baseline(cfg, tokens: int = 2048, seq: int = 2048, warmup: int = 1):
     """The CPU oracle (a port of the reference math) on a bounded sample of the
-    same workload: one forward+backward over `tokens` tokens of the 1B model
-    and one AdamW update of all its parameters, in fp32 on the host."""
+    same workload: forward+backward over `tokens` tokens (sequences of the
+    headline's length) of the 1B model and one AdamW update of all its
+    parameters, in fp32 on the host, timed after `warmup` untimed steps."""
     from oracle import engine as OE
     from oracle import model as OM
 
@@ -501,13 +520,19 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
     torch.manual_seed(0)
     P = {k: v.requires_grad_(True) for k, v in OM.init_params(ocfg).items()}
     ids = torch.randint(0, cfg.vocab_size, (tokens // seq, seq), generator=torch.Generator().manual_seed(0))
+    eng = OE.EngineRef(torch.cat([p.detach().reshape(-1) for p in P.values()]), lr=3e-4)
+
+    def step():
+        for p in P.values():
+            p.grad = None
+        loss = OM.loss(P, ocfg, ids, chunk_size=128)
+        loss.backward()
+        eng.step(torch.cat([p.grad.reshape(-1) for p in P.values()]))
+
+    for _ in range(warmup):
+        step()
     t0 = time.perf_counter()
-    loss = OM.loss(P, ocfg, ids, chunk_size=128)
-    loss.backward()
-    flat_g = torch.cat([p.grad.reshape(-1) for p in P.values()])
-    master = torch.cat([p.detach().reshape(-1) for p in P.values()])
-    eng = OE.EngineRef(master, lr=3e-4)
-    eng.step(flat_g)
+    step()
     sec = time.perf_counter() - t0
     return {
         "value": tokens / sec,
@@ -516,9 +541,9 @@ def cpu_baseline(cfg, tokens: int = 512, seq: int = 256):
         "host_cpu_count": os.cpu_count(),
         "affinity_cpus": len(os.sched_getaffinity(0)),
         "kind": "port",
-        "sample": f"1 step of the same 1B workload on {tokens} tokens ({tokens // seq}x{seq}) in fp32: forward, "
-                  f"backward and the AdamW update of all {sum(p.numel() for p in P.values()):,} parameters "
-                  f"({sec:.1f} s)",
+        "sample": f"1 step of the same 1B workload on {tokens} tokens ({tokens // seq}x{seq}) in fp32 after "
+                  f"{warmup} untimed step: forward, backward and the AdamW update of all "
+                  f"{sum(p.numel() for p in P.values()):,} parameters ({sec:.1f} s)",
     }
 
 
@@ -702,7 +727,9 @@ def main() -> int:
         "data": "synthetic uniform token ids (seed 0) resident in HBM; random-init weights (seed 0)",
         "config": {
             "workload": "llama-1b ZeRO-3 train step at world_size 1 (d2048 L16 16q/8kv hd128 ffn5632 V32000 tied, "
-                        "820,578,304 params), bf16 + fp32 master, 25M-element grad buckets",
+                        "820,578,304 params), bf16 + fp32 master; at one rank each module's bf16 gradients are "
+                        "gathered straight into the fp32 gradient shard (the reduce-scatter of 25M-element buckets "
+                        "is the identity there)",
             "global_batch": B,
             "seq_len": S,
             "zero_stage": 3,
