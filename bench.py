@@ -98,12 +98,15 @@ def bench_125m(dev: torch.device, steps: int, warmup: int, per_plan: bool = Fals
     k = max(steps, 5)
     probe = ops.LaunchProbe() if per_plan else None
     run_steps(model, eng, batches, steps=0, warmup=warmup)
+    el, _ = run_steps(model, eng, batches, steps=k, warmup=0)
     if probe is not None:
+        # per-plan shares from k more steps: the events add host time per
+        # launch, so the step time above comes from the steps without them
         ops.set_gemm_probe(probe)
-    try:
-        el, _ = run_steps(model, eng, batches, steps=k, warmup=0)
-    finally:
-        ops.set_gemm_probe(None)
+        try:
+            run_steps(model, eng, batches, steps=k, warmup=0)
+        finally:
+            ops.set_gemm_probe(None)
     f = estimate_transformer_train_flops(cfg, 16, 1024, stage=0)
     out = {"tokens_per_s": 16 * 1024 * k / el, "ms_per_step": el * 1000 / k,
            "mfma_util": f * k / el / 1e12 / PEAK_BF16_TFLOPS, "model_tflop_per_step": f / 1e12,

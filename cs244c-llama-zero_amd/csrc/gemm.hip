@@ -24,6 +24,7 @@
 // Global loads for step k+1 are in flight while step k's MFMAs run.
 // Workgroup ids are remapped so that consecutive tiles of one M-band land on
 // the same XCD (its L2 then serves the shared operand rows).
+#include <cmath>
 #include "lz_common.h"
 
 namespace {
@@ -298,12 +299,38 @@ __device__ __forceinline__ int epi_swz(int row) {
   return (row / kPer256) & kMask;
 }
 
+// Staged epilogue rows of kRow bytes: a power-of-two number of 16-byte chunks
+// is XOR-swizzled in place (epi_swz); other widths (the 48-wide wave tiles of
+// 192-wide tiles: 6 bf16 or 12 fp32 chunks) are padded by one chunk instead,
+// an odd pitch in chunks that staggers consecutive rows over the bank groups.
+template <int kRow>
+constexpr bool epi_pow2() {
+  return ((kRow / 16) & (kRow / 16 - 1)) == 0;
+}
+template <int kRow>
+constexpr int epi_pitch() {
+  return epi_pow2<kRow>() ? kRow : kRow + 16;
+}
+template <int kRow>
+__device__ __forceinline__ int epi_off(int row, int chunk) {
+  if constexpr (epi_pow2<kRow>()) return row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4);
+  else return row * epi_pitch<kRow>() + (chunk << 4);
+}
+// LDS bytes one wave's region of store_tile16 takes: TM bf16 rows or TM/2 fp32
+// rows of TN values.
+template <int TM, int TN>
+constexpr int epi_wave_bytes() {
+  return TM * epi_pitch<TN * 2>() > (TM / 2) * epi_pitch<TN * 4>() ? TM * epi_pitch<TN * 2>()
+                                                                    : (TM / 2) * epi_pitch<TN * 4>();
+}
+
 // Interior tiles, 16-byte path: each wave parks its TM x TN sub-tile in a
 // private LDS region (rows of TN values, 16-byte chunks XOR-swizzled so that
 // both the accumulator-layout writes and the row-wise reads are free of bank
 // conflicts), then writes whole 16-byte pieces of consecutive row bytes, so a
 // store instruction covers full cache lines.  fp32 output goes in two passes
-// of TM/2 rows.  Needs BM*BN*2 bytes of LDS.
+// of TM/2 rows.  Needs WM*WN*epi_wave_bytes<TM, TN>() bytes of LDS (BM*BN*2
+// for power-of-two wave tile widths).
 // Parks a wave's TM x TN accumulator tile in its LDS region as 16-bit values
 // (scaled by alpha, rounded once): rows of TN values (kRow = 2*TN bytes),
 // 16-byte chunks XOR-swizzled by epi_swz, so that the accumulator-layout
@@ -317,7 +344,7 @@ __device__ __forceinline__ void park16(const typename Acc<MI>::T (&acc)[FM][FN],
 #pragma unroll
       for (int q = 0; q < Acc<MI>::kGroups; ++q) {
         const int row = acc_row<MI>(i, lane), byte = 2 * acc_col<MI>(j, q, lane);
-        *reinterpret_cast<uint2*>(st + row * kRow + (((byte >> 4) ^ epi_swz<kRow>(row)) << 4) + (byte & 15)) =
+        *reinterpret_cast<uint2*>(st + epi_off<kRow>(row, byte >> 4) + (byte & 15)) =
             make_uint2(F::pack2(acc[i][j][4 * q] * alpha, acc[i][j][4 * q + 1] * alpha),
                        F::pack2(acc[i][j][4 * q + 2] * alpha, acc[i][j][4 * q + 3] * alpha));
       }
@@ -330,7 +357,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
   static_assert(FM % 2 == 0, "fp32 output is staged in two halves");
   const int wm = wave / WN, wn = wave % WN;
   const int64_t mrow0 = m0 + wm * TM, ncol0 = n0 + wn * TN;
-  char* st = smem + wave * (TM * TN * 2);
+  char* st = smem + wave * epi_wave_bytes<TM, TN>();
   if (!go.c_f32) {
     constexpr int kRow = TN * 2, kChunks = kRow / 16;  // bytes and 16-byte chunks per row
     static_assert(kChunks >= 4 && kChunks <= 64, "bf16 rows of 32 to 512 values");
@@ -346,14 +373,14 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
 #pragma unroll
         for (int t = 0; t < kIters; ++t) {
           const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-          const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+          const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
           *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) = v;
         }
         return;
       }
       // with the residual: the R pieces of 8 stores are loaded together (R may
       // alias the output, so the compiler would not hoist them past the stores)
-      constexpr int kBlk = kIters < 8 ? kIters : 8;
+      constexpr int kBlk = kIters < 8 ? kIters : kIters % 8 == 0 ? 8 : kIters % 6 == 0 ? 6 : 4;
       static_assert(kIters % kBlk == 0, "store blocks must tile the wave's rows");
 #pragma unroll
       for (int t0 = 0; t0 < kIters; t0 += kBlk) {
@@ -366,7 +393,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
 #pragma unroll
         for (int u = 0; u < kBlk; ++u) {
           const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-          const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+          const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
           *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) =
               add16x8<F>(v, rv[u]);
         }
@@ -395,7 +422,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
 #pragma unroll
         for (int q = 0; q < Acc<MI>::kGroups; ++q) {
           const int row = acc_row<MI>(ii, lane), chunk = acc_col<MI>(j, q, lane) >> 2;
-          *reinterpret_cast<float4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4)) =
+          *reinterpret_cast<float4*>(st + epi_off<kRow>(row, chunk)) =
               make_float4(acc[i][j][4 * q] * go.alpha, acc[i][j][4 * q + 1] * go.alpha,
                           acc[i][j][4 * q + 2] * go.alpha, acc[i][j][4 * q + 3] * go.alpha);
         }
@@ -425,7 +452,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
 #pragma unroll
       for (int u = 0; u < kBlk; ++u) {
         const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-        const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+        const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
         const int64_t m = mrow0 + p * (TM / 2) + row, n = ncol0 + chunk * 4;
         float o[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
         if (has_c) {
@@ -684,6 +711,14 @@ __device__ __forceinline__ int swz_mn(int r) { return ((r & 3) << 2) | ((r >> 2)
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
 
+// Swizzle of the 16-byte chunks of an M/N-major stage row of 192 M/N values
+// (384 bytes, 24 chunks; consecutive rows start 128 bytes apart modulo the
+// 256-byte bank window, so even and odd rows use opposite halves of it): an
+// even XOR below 8 keeps chunk pairs together and inside their row, and gives
+// the 8 rows r = 8G + 4rd + j (G = 0, 1; j = 0..3) that one half-wave of
+// ds_read_b64_tr_b16 reads distinct 32-byte bank groups.
+__device__ __forceinline__ int swz_mn192(int r) { return 2 * (((r >> 1) & 1) | (((r >> 3) & 1) << 1)); }
+
 // Swizzle of the 16-byte chunks of a K-major stage row of 32 K (64 bytes,
 // 4 chunks): the 16 lanes of a ds_read_b128 quarter-wave (16 consecutive rows,
 // one logical chunk) land on 16 distinct 16-byte bank groups.
@@ -694,12 +729,13 @@ __device__ __forceinline__ int swz_k4(int r) { return (r >> 2) & 3; }
 //   K-major: 256 rows of DBK K values (2*DBK bytes: 8 chunks swizzled by
 //            swz<8> for DBK 64, 4 chunks swizzled by swz_k4 for DBK 32);
 //            fragments are plain 16-byte reads.
-//   M/N-major: DBK rows of 256 M/N values (512 bytes, 32 chunks, swizzled by
-//            swz_mn); fragments are two ds_read_b64_tr_b16 (k-slots 0-3 and
-//            4-7 of the 32x32x16 operand: rows 16*kk + 8*(lane/32) + 0..3 and
-//            + 4..7).
-template <bool KMAJOR, int kPerWave, int DBK>
+//   M/N-major: DBK rows of kCols M/N values (256: 512 bytes, 32 chunks,
+//            swizzled by swz_mn; 192: 384 bytes, 24 chunks, swizzled by
+//            swz_mn192); fragments are two ds_read_b64_tr_b16 each.
+// A K-major stage of kCols rows is the same code with fewer wave loads.
+template <bool KMAJOR, int kPerWave, int DBK, int kCols = 256>
 struct DmaOperand {
+  static_assert(kCols == 256 || kCols == 192, "stages of 256 or 192 M/N values");
   static constexpr int kChunksK = DBK / 8;        // 16-byte chunks per K-major row
   static constexpr int kRowsK = 64 / kChunksK;    // K-major rows per wave load
   // Raw buffer starting at the tile's origin (row0, kbeg): the loads are
@@ -724,6 +760,12 @@ struct DmaOperand {
         const int c = (lane % kChunksK) ^ (DBK == 64 ? swz<8>(r) : swz_k4(r));
         const int64_t gr = pair > 0 ? (r & 127) + (r >> 7) * pair : min(row0 + r, nrows - 1) - row0;
         voff[q] = (uint32_t)((gr * ld + c * 8) * 2);
+      } else if constexpr (kCols == 192) {
+        // a wave load's 1 KB spans 2 2/3 rows: the row and the chunk slot
+        // follow from the 16-byte slot's position in the stage
+        const int pos = (wave * kPerWave + q) * 64 + lane;
+        const int r = pos / 24, c = (pos % 24) ^ swz_mn192(r);
+        voff[q] = (uint32_t)((r * ld + (min(row0 + c * 8, nrows - 8) - row0)) * 2);
       } else {
         const int r = (wave * kPerWave + q) * 2 + (lane >> 5);
         const int c = (lane & 31) ^ swz_mn(r);
@@ -744,8 +786,9 @@ struct DmaOperand {
 // blk0 .. blk0+NF-1 of the operand) for the two 32-deep K slices of a 64-deep
 // stage, in the operand layout of the 16x16x32 MFMA: lane l supplies row
 // l % 16 of the fragment and K values 8*(l/16) .. +7 of the slice.
-template <bool KMAJOR, int NF>
+template <bool KMAJOR, int NF, int kCols = 256>
 struct DmaFrags {
+  static constexpr int kRowBytes = kCols * 2;  // M/N-major stage row
   int kb[KMAJOR ? 2 : 1];              // K-major
   int base[2], ioff[KMAJOR ? 1 : NF];  // M/N-major
 
@@ -762,6 +805,16 @@ struct DmaFrags {
         const int r = blk0 * 16 + (lane & 15);
         kb[kk] = r * 128 + (((4 * kk + (lane >> 4)) ^ swz<8>(r)) << 4);
       }
+    } else if constexpr (kCols == 192) {
+      // The same reads on 384-byte rows: row r = 32*kk + 8G + 4*rd + j has
+      // swz_mn192(r) = 2*((j >> 1) | ((G % 2) << 1)) for either rd, an even
+      // value, so chunk (2*blk + q/2) ^ swz sits at slot (2*blk ^ swz) + q/2.
+      const int p = lane & 15, grp = lane >> 4, j = p >> 2, q = p & 3;
+      const int t = 2 * ((j >> 1) | ((grp & 1) << 1));
+#pragma unroll
+      for (int rd = 0; rd < 2; ++rd) base[rd] = (8 * grp + 4 * rd + j) * kRowBytes + ((q >> 1) << 4) + (q & 1) * 8;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) ioff[f] = ((2 * (blk0 + f)) ^ t) << 4;
     } else {
       // An M/N-major stage holds 64 K rows of 256 M/N values (512 bytes, 32
       // chunks swizzled by swz_mn).  ds_read_b64_tr_b16 lets the 16 lanes of
@@ -788,7 +841,7 @@ struct DmaFrags {
     if constexpr (KMAJOR) {
       return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(op + f * 16 * 128 + kb[kk]));
     } else {
-      const char* blk = op + kk * 32 * 512 + ioff[f];
+      const char* blk = op + kk * 32 * kRowBytes + ioff[f];
       const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[0]));
       const v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(blk + base[1]));
       const uint2 xw = __builtin_bit_cast(uint2, x), yw = __builtin_bit_cast(uint2, y);
@@ -799,8 +852,8 @@ struct DmaFrags {
 
 // Fragments of one 32-deep K slice: fa (B operand, FN of them) and fb (A
 // operand, FM), read from the LDS stage at (sa, sb).
-template <bool AK, bool BK, int FM, int FN>
-__device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM>& fra, const DmaFrags<BK, FN>& frb, const char* sa,
+template <bool AK, bool BK, int FM, int FN, int kColsB>
+__device__ __forceinline__ void dma_load_frags(const DmaFrags<AK, FM>& fra, const DmaFrags<BK, FN, kColsB>& frb, const char* sa,
                                                const char* sb, int kk, bf16x8_t (&fa)[FN], bf16x8_t (&fb)[FM]) {
 #pragma unroll
   for (int j = 0; j < FN; ++j) fa[j] = frb.frag(sb, j, kk);
@@ -890,27 +943,31 @@ template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t (&acc)[BM / WM / 16][BN / WN / 16],
                                                  int64_t m0, int64_t n0, char* smem, int lane, int wave);
 
-// One workgroup's 256x256 tile of the direct-to-LDS GEMM (main loop, then the
-// epilogue).  kEpiSwiGLU: the tile's 256 B rows are 128 gate rows and the
+// One workgroup's 256 x BN tile of the direct-to-LDS GEMM (main loop, then
+// the epilogue).  kEpiSwiGLU: the tile's 256 B rows are 128 gate rows and the
 // matching 128 up rows of a [gate; up] weight (o.F rows apart), and the
 // epilogue writes silu(gate) * up.  kEpiRope: the epilogue rotates the tile's
 // columns below r.nrope as RoPE heads of 128.  kEpiSwiGLUBwd: the product is
 // the down projection's input gradient and the epilogue runs SwiGLU's
-// backward on it (sb).
-template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi>
+// backward on it (sb).  BN = 192 (plain epilogue only): waves of 128x48.
+template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi, int BN = 256>
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut& o, const RopeIn& rope,
                                               const SwigluBwdIn& sb) {
   constexpr bool kSwiGLU = kEpi == kEpiSwiGLU;
-  constexpr int BM = 256, BN = 256, MI = 16;
+  constexpr int BM = 256, MI = 16;
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MI, FN = TN / MI;
-  constexpr int kOpBytes = BM * DBK * 2;              // one operand, one stage
-  constexpr int kStage = 2 * kOpBytes;
-  constexpr int kLoadWaves = kWaves / 2;               // waves that issue the stage loads
-  constexpr int kPerWave = kOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
+  constexpr int kAOpBytes = BM * DBK * 2, kBOpBytes = BN * DBK * 2;  // one operand, one stage
+  constexpr int kStage = kAOpBytes + kBOpBytes;
+  constexpr int kLoadWaves = kWaves / 2;                // waves that issue the stage loads
+  constexpr int kPerWaveA = kAOpBytes / 1024 / kLoadWaves;  // wave loads per operand per stage
+  constexpr int kPerWaveB = kBOpBytes / 1024 / kLoadWaves;
   static_assert(DBK == 64 && NST == 2, "two LDS stages of 64 K: two 32-deep slices each");
-  static_assert(kPerWave * kLoadWaves * 1024 == kOpBytes, "operand stage must split evenly over the waves");
+  static_assert(BN == 256 || (BN == 192 && kEpi == kEpiPlain), "256-wide tiles, or 192-wide with the plain epilogue");
+  static_assert(kPerWaveA * kLoadWaves * 1024 == kAOpBytes && kPerWaveB * kLoadWaves * 1024 == kBOpBytes,
+                "operand stages must split evenly over the waves");
   static_assert(kWaves * MI * (TN + 4) * 4 <= NST * kStage, "epilogue staging does not fit");
+  static_assert(kWaves * epi_wave_bytes<TM, TN>() <= NST * kStage, "epilogue staging does not fit");
   static_assert(kEpi == kEpiPlain || F::kDtype == LZ_BF16, "the fused epilogues are bf16");
 
   __shared__ __attribute__((aligned(1024))) char smem[NST * kStage];
@@ -925,15 +982,15 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   const int64_t kbeg = (int64_t)blockIdx.y * g.kper, kend = min(g.K, kbeg + g.kper);
   const int ktiles = kend > kbeg ? (int)((kend - kbeg) / DBK) : 0;
 
-  DmaOperand<AK, kPerWave, DBK> la;
-  DmaOperand<BK, kPerWave, DBK> lb;
+  DmaOperand<AK, kPerWaveA, DBK> la;
+  DmaOperand<BK, kPerWaveB, DBK, BN> lb;
   const int lwave = wave % kLoadWaves;     // this wave's part of a stage
   const bool loader = wave < kLoadWaves;  // wave-uniform
   la.init(g.A, g.lda, m0, g.M, kbeg, lwave, lane);
   if constexpr (kSwiGLU) lb.init(g.B, g.ldb, tn * 128, g.N, kbeg, lwave, lane, o.F);
   else lb.init(g.B, g.ldb, n0, g.N, kbeg, lwave, lane);
   DmaFrags<AK, FM> fra;
-  DmaFrags<BK, FN> frb;
+  DmaFrags<BK, FN, BN> frb;
   fra.init(wm * FM, lane);
   frb.init(wn * FN, lane);
 
@@ -948,19 +1005,19 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
   constexpr int kReads = FN * (BK ? 1 : 2) + FM * (AK ? 1 : 2);  // LDS read instructions per slice
   if (ktiles > 0 && loader) {
     la.issue(smem, lwave, 0);
-    lb.issue(smem + kOpBytes, lwave, 0);
+    lb.issue(smem + kAOpBytes, lwave, 0);
   }
   dma_barrier();
   if (ktiles > 1 && loader) {
     la.issue(smem + kStage, lwave, 1);
-    lb.issue(smem + kStage + kOpBytes, lwave, 1);
+    lb.issue(smem + kStage + kAOpBytes, lwave, 1);
   }
   // slice 0 of stage kt is in registers when step kt begins
   bf16x8_t fa0[FN], fb0[FM];
-  dma_load_frags(fra, frb, smem, smem + kOpBytes, 0, fa0, fb0);
+  dma_load_frags(fra, frb, smem, smem + kAOpBytes, 0, fa0, fb0);
   for (int kt = 0; kt < ktiles; ++kt) {
     const char* sa = smem + (kt & 1) * kStage;
-    const char* sb = sa + kOpBytes;
+    const char* sb = sa + kAOpBytes;
     bf16x8_t fa1[FN], fb1[FM];
     dma_mfma<F>(acc, fa0, fb0);
     dma_load_frags(fra, frb, sa, sb, 1, fa1, fb1);
@@ -972,13 +1029,13 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
     if (kt + 2 < ktiles && loader) {
       char* nxt = smem + (kt & 1) * kStage;
       la.issue(nxt, lwave, kt + 2);
-      lb.issue(nxt + kOpBytes, lwave, kt + 2);
+      lb.issue(nxt + kAOpBytes, lwave, kt + 2);
     }
     // slice 0 of stage kt+1 (after the last step: unused reads of the other
     // slot) while the MFMAs of slice 1 run
     const char* na = smem + ((kt + 1) & 1) * kStage;
     dma_mfma<F>(acc, fa1, fb1);
-    dma_load_frags(fra, frb, na, na + kOpBytes, 0, fa0, fb0);
+    dma_load_frags(fra, frb, na, na + kAOpBytes, 0, fa0, fb0);
     sched_slice<kReads, FM * FN>();
   }
   __syncthreads();  // every wave is done with the stages before the epilogue may reuse LDS
@@ -999,6 +1056,14 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
 template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_dma_kernel(GemmArgs g) {
   gemm_dma_tile<F, WM, WN, AK, BK, DBK, NST, kEpiPlain>(g, SwigluOut{}, RopeIn{}, SwigluBwdIn{});
+}
+
+// 256x192 tiles (A K-major; B either layout; plain epilogue): for products
+// whose 256-wide tiles would leave CUs idle, e.g. N = 768 over 16384 rows,
+// where 4 column tiles of 192 make 256 workgroups and 3 of 256 only 192.
+template <typename F, bool BK>
+__global__ void __launch_bounds__(512) gemm_dma_n192_kernel(GemmArgs g) {
+  gemm_dma_tile<F, 2, 4, true, BK, 64, 2, kEpiPlain, 192>(g, SwigluOut{}, RopeIn{}, SwigluBwdIn{});
 }
 
 // Fused gate|up projection + SwiGLU (both operands K-major): tile (tm, tn)
@@ -1051,7 +1116,7 @@ __device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t 
 #pragma unroll
     for (int u = 0; u < kBlk; ++u) {
       const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-      const uint4 hv = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+      const uint4 hv = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
       uint4 dg, du;
       swiglu_bwd8(gv[u], uv[u], hv, dg, du);
       uint16_t* dp = sb.dgu + (mrow0 + row) * sb.lddgu + ncol0 + chunk * 8;
@@ -1085,7 +1150,7 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
 #pragma unroll
     for (int t = 0; t < TM * kChunks / 64; ++t) {
       const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
-      const uint4 v = *reinterpret_cast<const uint4*>(st + row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4));
+      const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
       *reinterpret_cast<uint4*>(gu + (mrow0 + row) * g.ldc + chunk * 8) = v;
     }
   }
@@ -1097,7 +1162,7 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
 #pragma unroll
   for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
     const int idx = t * 64 + lane, row = r0 + idx / kChunks, chunk = idx % kChunks;
-    const int off = row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4);
+    const int off = epi_off<kRow>(row, chunk);
     const uint4 gv = *reinterpret_cast<const uint4*>(sg + off);
     const uint4 uv = *reinterpret_cast<const uint4*>(su + off);
     *reinterpret_cast<uint4*>(o.h + (mrow0 + row) * o.ldh + col + chunk * 8) = swiglu_fwd8(gv, uv);
@@ -1136,7 +1201,7 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
 #pragma unroll
   for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
     const int idx = t * 64 + lane, row = r0 + idx / kChunks, chunk = idx % kChunks;
-    const int off = row * kRow + ((chunk ^ epi_swz<kRow>(row)) << 4);
+    const int off = epi_off<kRow>(row, chunk);
     const uint4 av = *reinterpret_cast<const uint4*>(s1 + off);
     const uint4 bv = *reinterpret_cast<const uint4*>(s2 + off);
     const int64_t m = mrow0 + row;
@@ -1200,39 +1265,60 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
 // Tile configurations: 0 = 256x256 with 8 waves (128x64 per wave),
 // 1 = 256x256 with 4 waves (128x128 per wave, accumulators in AGPRs),
 // 2 = 128x128 with 4 waves; 5 = the direct-to-LDS kernel (any layouts,
-// 8 waves, two stages of 64 K).
+// 8 waves, two stages of 64 K); 6 = the direct-to-LDS kernel on 256x192
+// tiles (K-major A, unsplit).
 struct Plan {
   int cfg;
   int splits;
   int64_t kper;
 };
 
+// Main-loop time of a 256x192 tile relative to a 256x256 one (its MFMAs are
+// three quarters, its A stage the same).
+constexpr double kTile192 = 0.8;
+
+// Rounds of `tiles` workgroups over the CUs with a partial last round counted
+// by the square root of its fill: tiles of a short last round run faster than
+// those of a full one.  Measured on MI355X: at 16384x1280x768, 320 tiles of
+// 256x256 (1.25 rounds) beat 448 of 256x192 (1.75) by 5 %; at 16384x768xK,
+// 256 tiles of 256x192 beat 192 of 256x256 by 2-8 % (K = 768 ... 4096).
+inline double fill_rounds(int64_t tiles, int cus) {
+  return (double)(tiles / cus) + std::sqrt((double)(tiles % cus) / (double)cus);
+}
+
 Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
   const int cus = lz_num_cus();
   const int64_t big = lz_cdiv(M, 256) * lz_cdiv(N, 256);
   const int64_t small = lz_cdiv(M, 128) * lz_cdiv(N, 128);
+  const int64_t mid = lz_cdiv(M, 256) * lz_cdiv(N, 192);
   // 256x256 tiles: the direct-to-LDS kernel whenever every split is a whole
   // number of 64-deep K steps; otherwise the register-staged kernel (8 waves
   // for a K-major A, 4 waves when both operands are transposed in registers).
   const int big_cfg = K % 64 == 0 ? 5 : (ak ? 0 : 1);
   Plan p{big_cfg, 1, K};
+  // Cost of an unsplit product in units of one 64-deep K step of one 256x256
+  // tile on one CU (about 2 us): the grid's rounds over the CUs times the
+  // steps of a tile plus 2 for its prologue and epilogue.
+  const double steps = (double)lz_cdiv(K, 64);
+  const double c256 = (double)lz_cdiv(big, cus) * (steps + 2.0);
+  double cost_cur = c256;  // of the plan so far
   if (ak && bk) {
     // 128x128 tiles (two per CU) win when they fill the chip in fewer rounds.
     // Relative speeds per tile measured on MI355X: 1.0 for the direct-to-LDS
     // 256x256 kernel and 0.75 for the 128x128 one (at the 125M QKV shape,
     // 16384x1280x768, the 256x256 kernel's two rounds beat three 128x128 ones).
-    const double c256 = (double)lz_cdiv(big, cus) * 4.0 / (big_cfg == 5 ? 1.0 : 0.85);
-    const double c128 = (double)lz_cdiv(small, 2 * cus) * 2.0 / 0.75;
-    if (c128 < c256) p.cfg = 2;
+    const double c128 = (double)lz_cdiv(small, 2 * cus) * (steps + 2.0) * 0.5 / 0.75 * (big_cfg == 5 ? 1.0 : 0.85);
+    if (c128 < c256) {
+      p.cfg = 2;
+      cost_cur = c128;
+    }
   }
   if (p.cfg != 2 && K >= 1024) {
-    // Long K: split it when that fills the chip better.  Cost in units of one
-    // 64-deep K step of one 256x256 tile on one CU (about 2 us): the grid's
-    // rounds over the CUs times the steps of one split plus 2 for a tile's
-    // prologue and epilogue; a split product also pays its fp32 slabs' round
-    // trip through HBM (written, then read by the reduce) and its output
-    // write, at about 10 MB per unit, plus 3 units for the reduce launch.
-    // Splits are whole multiples of 64 in K and at least 256 deep.
+    // Long K: split it when that fills the chip better.  Same unit; a split
+    // product also pays its fp32 slabs' round trip through HBM (written, then
+    // read by the reduce) and its output write, at about 10 MB per unit, plus
+    // 3 units for the reduce launch.  Splits are whole multiples of 64 in K
+    // and at least 256 deep.
     const double mn = (double)M * (double)N;
     double best = 1e30;
     for (int sp = 1; sp <= 32; ++sp) {
@@ -1246,6 +1332,21 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
         p.splits = sp;
         p.kper = kper;
       }
+    }
+    cost_cur = best;
+  }
+  if (big_cfg == 5 && ak) {  // the plan so far: 256x256 or 128x128 tiles
+    // Unsplit 256x192 tiles when they take fewer tile-steps than the plan so
+    // far: N = 768 over 16384 rows is one full round of 256 tiles instead of
+    // three quarters of one, each tile a quarter narrower.  Against an
+    // unsplit 256x256 plan both count partial rounds by fill_rounds.
+    const bool plain = p.cfg == 5 && p.splits == 1;
+    const double c192 = (plain ? fill_rounds(mid, cus) : (double)lz_cdiv(mid, cus)) * (kTile192 * steps + 2.0);
+    if (plain) cost_cur = fill_rounds(big, cus) * (steps + 2.0);
+    if (c192 < 0.97 * cost_cur) {
+      p.cfg = 6;
+      p.splits = 1;
+      p.kper = K;
     }
   }
   return p;
@@ -1281,6 +1382,10 @@ template __global__ void gemm_dma_kernel<FmtF16, 2, 4, true, true, 64, 2>(GemmAr
 template __global__ void gemm_dma_kernel<FmtF16, 2, 4, true, false, 64, 2>(GemmArgs);
 template __global__ void gemm_dma_kernel<FmtF16, 2, 4, false, true, 64, 2>(GemmArgs);
 template __global__ void gemm_dma_kernel<FmtF16, 2, 4, false, false, 64, 2>(GemmArgs);
+template __global__ void gemm_dma_n192_kernel<FmtBF16, true>(GemmArgs);
+template __global__ void gemm_dma_n192_kernel<FmtBF16, false>(GemmArgs);
+template __global__ void gemm_dma_n192_kernel<FmtF16, true>(GemmArgs);
+template __global__ void gemm_dma_n192_kernel<FmtF16, false>(GemmArgs);
 
 template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST>
 int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
@@ -1290,9 +1395,20 @@ int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
   return lz_check_launch("lz_gemm");
 }
 
+template <typename F, bool BK>
+int launch_dma192(const GemmArgs& g, int splits, hipStream_t s) {
+  const int64_t tiles = lz_cdiv(g.M, 256) * lz_cdiv(g.N, 192);
+  LZ_REQUIRE(tiles < (1ll << 31), "lz_gemm: too many tiles");
+  gemm_dma_n192_kernel<F, BK><<<dim3((unsigned)tiles, (unsigned)splits), 512, 0, s>>>(g);
+  return lz_check_launch("lz_gemm");
+}
+
 template <typename F, bool AK, bool BK>
 int dispatch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   if (cfg == 5) return launch_dma<F, 2, 4, AK, BK, 64, 2>(g, splits, s);
+  if constexpr (AK) {
+    if (cfg == 6) return launch_dma192<F, BK>(g, splits, s);
+  }
   switch (cfg) {
     case 0:
       return launch<F, 256, 256, 2, 4, AK, BK>(g, splits, s);
@@ -1322,6 +1438,7 @@ LZ_EXPORT int64_t lz_gemm_workspace(int64_t M, int64_t N, int64_t K, int a_kmajo
 
 // The kernel lz_gemm launches for this shape and layout, encoded as
 // 64 * cfg + splits: cfg 5 = direct-to-LDS 256x256 tile with 8 waves,
+// 6 = direct-to-LDS 256x192 tile with 8 waves (unsplit),
 // 0 / 1 = register-staged 256x256 with 8 / 4 waves, 2 = 128x128 with 4 waves;
 // splits = number of K slices (1 = unsplit; more need the workspace).
 LZ_EXPORT int lz_gemm_plan(int64_t M, int64_t N, int64_t K, int a_kmajor, int b_kmajor) {
@@ -1385,7 +1502,7 @@ LZ_EXPORT int lz_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, i
     p.splits = 1;
     p.kper = g.kper;
   }
-  if (p.cfg == 5 && !(dma_span_fits(ak, lda, p.kper) && dma_span_fits(bk, ldb, p.kper)))
+  if ((p.cfg == 5 || p.cfg == 6) && !(dma_span_fits(ak, lda, p.kper) && dma_span_fits(bk, ldb, p.kper)))
     p.cfg = ak ? 0 : 1;  // register-staged loads take 64-bit addresses
   const bool f16 = ab_dtype == LZ_F16;
   if (p.splits == 1)

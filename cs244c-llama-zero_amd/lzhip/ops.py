@@ -600,6 +600,8 @@ def gemm_kernel_name(key) -> str:
     tf = lambda b: "true" if b else "false"
     if cfg == 5:
         name = f"gemm_dma_kernel<FmtBF16, 2, 4, {tf(ak)}, {tf(bk)}, 64, 2>"
+    elif cfg == 6:
+        name = f"gemm_dma_n192_kernel<FmtBF16, {tf(bk)}>"
     else:
         bm, wn = (128, 2) if cfg == 2 else (256, 4 if cfg == 0 else 2)
         name = f"gemm_kernel<FmtBF16, {bm}, {bm}, 2, {wn}, {tf(ak)}, {tf(bk)}>"

@@ -123,6 +123,8 @@ def _layout_operand(t, kmajor):
 @pytest.mark.parametrize(
     "M,N,K",
     [(64, 64, 64), (520, 264, 200), (1000, 1000, 520), (1000, 1000, 512), (2048, 1024, 1536),
+     # one full round of 256x256 tiles (the 256x192 tiling would take two)
+     (4096, 4096, 128),
      # few output tiles, long K: split along K (K not a multiple of 64 in the last case)
      (512, 384, 8192), (1024, 768, 8200)],
 )
@@ -144,6 +146,47 @@ def test_gemm_layouts(M, N, K, a_kmajor, b_kmajor):
     ops.gemm(A, B, a_kmajor, b_kmajor, out=acc, alpha=0.5, beta=1.0, residual=r.to(DEV))
     want = 0.5 * ref + c0.double() + r.double()
     assert float((acc.cpu().double() - want).abs().max()) <= 0.5 * tol + 1e-5 * float(want.abs().max())
+
+
+@pytest.mark.parametrize("b_kmajor", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "M,N,K",
+    [(16384, 768, 768),  # 64 x 4 interior tiles: one full round on 256 CUs
+     (4096, 3072, 768),  # 16 x 16 interior tiles
+     (4000, 2904, 1024)],  # edge tiles in M (last 160 rows) and N (last 24 columns)
+)
+def test_gemm_n192_tiles(M, N, K, dtype, b_kmajor):
+    """The 256x192 direct-to-LDS tiles (plan code 6) on every epilogue path:
+    fp32 output, bf16 / fp16 output rounded once, with a residual (rounded
+    twice, as the reference's Linear output + x), and alpha / beta
+    accumulation into fp32 and 16-bit outputs."""
+    lib = _lib.load()
+    assert int(lib.lz_gemm_plan(M, N, K, 1, int(b_kmajor))) == 6 * 64 + 1
+    g = _seed(M + 7 * N + K + b_kmajor)
+    a = torch.randn(M, K, generator=g).to(dtype)
+    b = torch.randn(N, K, generator=g).to(dtype)
+    ref = a.double() @ b.double().t()
+    A, B = a.to(DEV), _layout_operand(b, b_kmajor)
+    tol = 1e-5 * math.sqrt(K) * float(a.float().abs().max() * b.float().abs().max()) * 4
+    c32 = ops.gemm(A, B, True, b_kmajor, out_dtype=torch.float32).cpu()
+    assert float((c32.double() - ref).abs().max()) <= tol
+    eps = 2 ** -8 if dtype == torch.bfloat16 else 2 ** -11
+    c16 = ops.gemm(A, B, True, b_kmajor).cpu()
+    assert c16.dtype == dtype
+    assert torch.equal(c16, c32.to(dtype))  # the fp32 sum rounded once
+    r = torch.randn(M, N, generator=g).to(dtype)
+    cr = ops.gemm(A, B, True, b_kmajor, residual=r.to(DEV)).cpu()
+    assert torch.equal(cr, (c16.float() + r.float()).to(dtype))
+    c0 = torch.randn(M, N, generator=g)
+    acc = c0.to(DEV)
+    ops.gemm(A, B, True, b_kmajor, out=acc, alpha=0.5, beta=1.0)
+    assert float((acc.cpu().double() - (0.5 * ref + c0.double())).abs().max()) <= 0.5 * tol + 1e-5 * float(c0.abs().max())
+    h0 = torch.randn(M, N, generator=g).to(dtype)
+    acc16 = h0.to(DEV)
+    ops.gemm(A, B, True, b_kmajor, out=acc16, alpha=0.5, beta=1.0)
+    want = 0.5 * ref + h0.double()
+    assert bool(((acc16.cpu().double() - want).abs() <= eps * want.abs() + 0.5 * tol + 1e-6).all())
 
 
 def test_gemm_split_k_workspace_and_determinism():

@@ -380,18 +380,29 @@ def test_gemm_plan_codes_and_workspace():
         pytest.skip("libllamazero_hip.so not built (run __graft_entry__.build())")
     lib = L.load()
     shapes = [(4096, 2048, 16384, 0, 0), (768, 768, 16384, 0, 0), (32000, 768, 16384, 0, 0),
-              (16384, 2048, 5632, 1, 0), (16384, 4096, 2048, 1, 1), (16384, 1280, 768, 1, 1), (1000, 1000, 520, 0, 1)]
+              (16384, 2048, 5632, 1, 0), (16384, 4096, 2048, 1, 1), (16384, 1280, 768, 1, 1), (1000, 1000, 520, 0, 1),
+              (16384, 768, 768, 1, 1), (16384, 768, 4096, 1, 0), (16384, 768, 32000, 1, 0)]
+    prefix = {5: "gemm_dma_kernel<", 6: "gemm_dma_n192_kernel<"}
     for M, N, K, ak, bk in shapes:
         code = int(lib.lz_gemm_plan(M, N, K, ak, bk))
         cfg, splits = code // 64, code % 64
-        assert cfg in (0, 1, 2, 5) and 1 <= splits <= 32, (M, N, K, code)
+        assert cfg in (0, 1, 2, 5, 6) and 1 <= splits <= 32, (M, N, K, code)
+        assert cfg != 6 or (ak and splits == 1), (M, N, K, code)  # 256x192 tiles: K-major A, unsplit
         ws = int(lib.lz_gemm_workspace(M, N, K, ak, bk))
         assert ws == (splits * M * N * 4 if splits > 1 else 0), (M, N, K, splits, ws)
         name = ops.gemm_kernel_name((bool(ak), bool(bk), code))
-        assert name.startswith("gemm_dma_kernel<" if cfg == 5 else "gemm_kernel<")
+        assert name.startswith(prefix.get(cfg, "gemm_kernel<"))
         assert ("split-K x%d" % splits in name) == (splits > 1)
     assert int(lib.lz_gemm_plan(768, 768, 16384, 0, 0)) % 64 > 8  # the 125M weight gradient splits widely
-    assert int(lib.lz_gemm_plan(16384, 4096, 2048, 1, 1)) % 64 == 1
+    assert int(lib.lz_gemm_plan(16384, 4096, 2048, 1, 1)) == 5 * 64 + 1
+    # at 16384 rows, N = 768 fills 256 CUs with 256x192 tiles (3 x 64 tiles of 256 would leave 64 idle); N = 1280
+    # keeps 256x256 (a short second round of 64 tiles beats a 3/4-full one of 192), and so do the 1B model's
+    # N = 2048 products (512 tiles: two full rounds)
+    for N, K, bk in ((768, 768, 1), (768, 2048, 1), (768, 768, 0), (768, 1280, 0), (768, 4096, 0), (768, 32000, 0)):
+        assert int(lib.lz_gemm_plan(16384, N, K, 1, bk)) == 6 * 64 + 1, (N, K, bk)
+    for N, K, bk in ((1280, 768, 1), (2048, 2048, 1), (2048, 5632, 1), (32000, 2048, 1), (32000, 768, 1),
+                     (2048, 2048, 0), (2048, 32000, 0)):
+        assert int(lib.lz_gemm_plan(16384, N, K, 1, bk)) // 64 == 5, (N, K, bk)
     assert int(lib.lz_gemm_plan(0, 10, 10, 1, 1)) == 0
 
 
