@@ -24,6 +24,7 @@
 // Global loads for step k+1 are in flight while step k's MFMAs run.
 // Workgroup ids are remapped so that consecutive tiles of one M-band land on
 // the same XCD (its L2 then serves the shared operand rows).
+#include <algorithm>
 #include <cmath>
 #include "lz_common.h"
 
@@ -1313,6 +1314,20 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
       cost_cur = c128;
     }
   }
+  // The direct-to-LDS kernel adds each K step to 32-bit buffer offsets from
+  // the tile's origin (a per-step base would need a scalar written by a
+  // vector instruction right before the loads), so an M/N-major operand's
+  // split, K rows of ld >= M (N) elements, must stay under 2^30 elements:
+  // a longer K is split at least this many ways (the 7B model's weight
+  // gradients over 131072 tokens: 11008 x 131072 elements, two splits).
+  int min_splits = 1;
+  if (big_cfg == 5) {
+    const int64_t wide = std::max(ak ? (int64_t)0 : M, bk ? (int64_t)0 : N);
+    if (wide > 0) {
+      const int64_t kmax = (((1ll << 30) - 256) / wide) / 64 * 64;
+      min_splits = kmax >= 64 ? (int)std::min<int64_t>(lz_cdiv(K, kmax), 64) : 64;
+    }
+  }
   if (p.cfg != 2 && K >= 1024) {
     // Long K: split it when that fills the chip better.  Same unit; a split
     // product also pays its fp32 slabs' round trip through HBM (written, then
@@ -1324,7 +1339,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
     for (int sp = 1; sp <= 32; ++sp) {
       const int64_t kper = lz_cdiv(lz_cdiv(K, sp), 64) * 64;
       if (sp > 1 && kper < 256) break;
-      if (lz_cdiv(K, kper) != sp) continue;
+      if (lz_cdiv(K, kper) != sp || sp < min_splits) continue;
       double cost = (double)lz_cdiv(big * sp, cus) * (double)(kper / 64 + 2);
       if (sp > 1) cost += (2.0 * sp * mn * 4.0 + mn * 4.0) / 10e6 + 3.0;
       if (cost < best - 1e-9) {
@@ -1333,9 +1348,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
         p.kper = kper;
       }
     }
-    cost_cur = best;
+    if (best < 1e30) cost_cur = best;
   }
-  if (big_cfg == 5 && ak) {  // the plan so far: 256x256 or 128x128 tiles
+  if (big_cfg == 5 && ak && min_splits == 1) {  // the plan so far: 256x256 or 128x128 tiles
     // Unsplit 256x192 tiles when they take fewer tile-steps than the plan so
     // far: N = 768 over 16384 rows is one full round of 256 tiles instead of
     // three quarters of one, each tile a quarter narrower.  Against an

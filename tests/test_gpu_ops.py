@@ -189,6 +189,23 @@ def test_gemm_n192_tiles(M, N, K, dtype, b_kmajor):
     assert bool(((acc16.cpu().double() - want).abs() <= eps * want.abs() + 0.5 * tol + 1e-6).all())
 
 
+def test_gemm_long_k_over_a_wide_mn_major_operand_splits():
+    """A K range whose M-major rows span more than 2^30 elements (8192 x
+    262144) is split so that each split's buffer offsets fit; the product
+    matches a float32 one."""
+    lib = _lib.load()
+    M, N, K = 8192, 512, 262144
+    code = int(lib.lz_gemm_plan(M, N, K, 0, 0))
+    assert code // 64 == 5 and code % 64 >= 3
+    g = torch.Generator(device=DEV).manual_seed(3)
+    a = torch.randn(K, M, device=DEV, generator=g).to(torch.bfloat16)
+    b = torch.randn(K, N, device=DEV, generator=g).to(torch.bfloat16)
+    c = ops.gemm(a, b, False, False, out_dtype=torch.float32)
+    ref = torch.matmul(a.float().t(), b.float())
+    del a, b
+    assert float((c - ref).abs().max()) <= 1e-5 * math.sqrt(K) * 4.0 * 25.0
+
+
 def test_gemm_split_k_workspace_and_determinism():
     lib = ops._lib.load()
     M, N, K = 512, 384, 8192

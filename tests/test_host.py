@@ -403,6 +403,14 @@ def test_gemm_plan_codes_and_workspace():
     for N, K, bk in ((1280, 768, 1), (2048, 2048, 1), (2048, 5632, 1), (32000, 2048, 1), (32000, 768, 1),
                      (2048, 2048, 0), (2048, 32000, 0)):
         assert int(lib.lz_gemm_plan(16384, N, K, 1, bk)) // 64 == 5, (N, K, bk)
+    # an M/N-major operand's split (K rows of ld >= M or N) stays under 2^30 elements: the 7B model's weight
+    # gradients over 64 and 128 sequences of 2048 split at least 2-6 ways
+    for M, N, K, least in ((22016, 4096, 131072, 3), (4096, 11008, 131072, 2), (22016, 4096, 262144, 6),
+                           (4096, 11008, 262144, 3), (8192, 512, 262144, 3)):
+        code = int(lib.lz_gemm_plan(M, N, K, 0, 0))
+        assert code // 64 == 5 and code % 64 >= least, (M, N, K, code)
+        kper = -(-(-(-K // (code % 64))) // 64) * 64
+        assert kper * max(M, N) + 256 < 1 << 30, (M, N, K, code)
     assert int(lib.lz_gemm_plan(0, 10, 10, 1, 1)) == 0
 
 
