@@ -556,31 +556,39 @@ int scratch_for_device(float** out) {
 
 }  // namespace
 
-// lz_rmsnorm_bwd with the library's own scratch instead of a workspace:
-// same arguments without workspace/workspace_bytes, same results bit for
-// bit.  Shapes whose workspace (lz_rmsnorm_bwd_workspace for the path taken)
-// exceeds the scratch are refused; bf16 rows of up to 4096 columns fit at
-// any row count.
-LZ_EXPORT int lz_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, const void* dres,
-                                     void* dx, void* dw, int dw_accumulate, int dtype, int64_t rows, int64_t cols,
-                                     int64_t ldx, int64_t lddy, int64_t lddx, void* stream) {
-  LZ_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30), "lz_rmsnorm_bwd_noalloc: bad shape");
-  LZ_REQUIRE(ldx >= cols && lddy >= cols && lddx >= cols, "lz_rmsnorm_bwd_noalloc: bad leading dimension");
-  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32, "lz_rmsnorm_bwd_noalloc: bad dtype %d", dtype);
-  if (rows == 0) return LZ_OK;
-  const int64_t need = dtype == LZ_BF16
-      ? bwd_bytes<uint16_t>(bwd_vec<uint16_t>(x, w, dy, dres, dx, cols, ldx, lddy, lddx), rows, cols)
-      : bwd_bytes<float>(bwd_vec<float>(x, w, dy, dres, dx, cols, ldx, lddy, lddx), rows, cols);
+namespace {
+
+template <typename T>
+int bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx, void* dw,
+                int dw_accumulate, int64_t rows, int64_t cols, int64_t ldx, int64_t lddy, int64_t lddx, void* stream) {
+  const int64_t need = bwd_bytes<T>(bwd_vec<T>(x, w, dy, dres, dx, cols, ldx, lddy, lddx), rows, cols);
   LZ_REQUIRE(need <= kScratchBytes,
              "lz_rmsnorm_bwd_noalloc: rows %lld x cols %lld need %lld bytes of scratch, more than its %lld",
              (long long)rows, (long long)cols, (long long)need, (long long)kScratchBytes);
   float* ws = nullptr;
   const int rc = scratch_for_device(&ws);
   if (rc) return rc;
-  hipStream_t s = lz_stream(stream);
+  return bwd_dispatch<T>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, ws, kScratchBytes, rows, (int)cols, ldx, lddy,
+                         lddx, lz_stream(stream));
+}
+
+}  // namespace
+
+// lz_rmsnorm_bwd with the library's own scratch instead of a workspace:
+// same arguments without workspace/workspace_bytes, same dtypes (bf16, fp32,
+// fp16), same results bit for bit.  Shapes whose workspace
+// (lz_rmsnorm_bwd_workspace for the path taken) exceeds the scratch are
+// refused; 16-bit rows of up to 4096 columns fit at any row count.
+LZ_EXPORT int lz_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, const void* dres,
+                                     void* dx, void* dw, int dw_accumulate, int dtype, int64_t rows, int64_t cols,
+                                     int64_t ldx, int64_t lddy, int64_t lddx, void* stream) {
+  LZ_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30), "lz_rmsnorm_bwd_noalloc: bad shape");
+  LZ_REQUIRE(ldx >= cols && lddy >= cols && lddx >= cols, "lz_rmsnorm_bwd_noalloc: bad leading dimension");
+  LZ_REQUIRE(dtype == LZ_BF16 || dtype == LZ_F32 || dtype == LZ_F16, "lz_rmsnorm_bwd_noalloc: bad dtype %d", dtype);
+  if (rows == 0) return LZ_OK;
   if (dtype == LZ_BF16)
-    return bwd_dispatch<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, ws, kScratchBytes, rows, (int)cols, ldx,
-                                  lddy, lddx, s);
-  return bwd_dispatch<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, ws, kScratchBytes, rows, (int)cols, ldx,
-                             lddy, lddx, s);
+    return bwd_noalloc<uint16_t>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, rows, cols, ldx, lddy, lddx, stream);
+  if (dtype == LZ_F16)
+    return bwd_noalloc<_Float16>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, rows, cols, ldx, lddy, lddx, stream);
+  return bwd_noalloc<float>(x, w, rstd, dy, dres, dx, dw, dw_accumulate, rows, cols, ldx, lddy, lddx, stream);
 }

@@ -154,7 +154,7 @@ int lz_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
  * graph capture, tight serving loops, harnesses that forbid allocation).  The
  * dw partial rows live in the library's own 8 MiB device array,
  * one per device, held until the process ends; shapes that need more are
- * refused (bf16 rows of up to 4096 columns fit at any row count).  Same
+ * refused (bf16 or fp16 rows of up to 4096 columns fit at any row count).  Same
  * results as lz_rmsnorm_bwd bit for bit.  Every call on a device shares that
  * array: calls that overlap in time on one device race. */
 int lz_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,
