@@ -375,7 +375,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
         for (int t = 0; t < kIters; ++t) {
           const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
           const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) = v;
+          st_nt16(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8, v);
         }
         return;
       }
@@ -395,8 +395,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
         for (int u = 0; u < kBlk; ++u) {
           const int idx = (t0 + u) * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
           const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8) =
-              add16x8<F>(v, rv[u]);
+          st_nt16(static_cast<uint16_t*>(go.C) + (mrow0 + row) * go.ldc + ncol0 + chunk * 8, add16x8<F>(v, rv[u]));
         }
       }
       return;
@@ -1121,8 +1120,8 @@ __device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t 
       uint4 dg, du;
       swiglu_bwd8(gv[u], uv[u], hv, dg, du);
       uint16_t* dp = sb.dgu + (mrow0 + row) * sb.lddgu + ncol0 + chunk * 8;
-      *reinterpret_cast<uint4*>(dp) = dg;
-      *reinterpret_cast<uint4*>(dp + sb.F) = du;
+      st_nt16(dp, dg);
+      st_nt16(dp + sb.F, du);
     }
   }
 }
@@ -1152,7 +1151,7 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
     for (int t = 0; t < TM * kChunks / 64; ++t) {
       const int idx = t * 64 + lane, row = idx / kChunks, chunk = idx % kChunks;
       const uint4 v = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
-      *reinterpret_cast<uint4*>(gu + (mrow0 + row) * g.ldc + chunk * 8) = v;
+      st_nt16(gu + (mrow0 + row) * g.ldc + chunk * 8, v);
     }
   }
   __syncthreads();
@@ -1166,7 +1165,7 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
     const int off = epi_off<kRow>(row, chunk);
     const uint4 gv = *reinterpret_cast<const uint4*>(sg + off);
     const uint4 uv = *reinterpret_cast<const uint4*>(su + off);
-    *reinterpret_cast<uint4*>(o.h + (mrow0 + row) * o.ldh + col + chunk * 8) = swiglu_fwd8(gv, uv);
+    st_nt16(o.h + (mrow0 + row) * o.ldh + col + chunk * 8, swiglu_fwd8(gv, uv));
   }
 }
 
@@ -1228,8 +1227,8 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
       y2[k] = pack_bf16x2(o2[0], o2[1]);
     }
     uint16_t* dst = out + m * g.ldc + chunk * 8;
-    *reinterpret_cast<uint4*>(dst) = make_uint4(y1[0], y1[1], y1[2], y1[3]);
-    *reinterpret_cast<uint4*>(dst + TN) = make_uint4(y2[0], y2[1], y2[2], y2[3]);
+    st_nt16(dst, make_uint4(y1[0], y1[1], y1[2], y1[3]));
+    st_nt16(dst + TN, make_uint4(y2[0], y2[1], y2[2], y2[3]));
   }
 }
 

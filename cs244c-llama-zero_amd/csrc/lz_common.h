@@ -99,6 +99,14 @@ __device__ __forceinline__ void lz_dma16(lz_v4i rsrc, uint32_t voff, uint32_t so
                :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0) : "memory");
 }
 
+// 16-byte store with the nontemporal hint (global_store_dwordx4 ... nt): for
+// outputs a kernel writes once and does not read back, so that they do not
+// displace the operand rows the rest of the grid is still reading from L2.
+typedef unsigned int lz_u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_nt16(void* p, const uint4& v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(lz_u32x4_t, v), reinterpret_cast<lz_u32x4_t*>(p));
+}
+
 // Workgroup barrier that publishes LDS written by this workgroup's
 // global_load_lds (direct-to-LDS) loads: each wave first waits until its own
 // loads have landed (vmcnt(0)), then the barrier orders every wave's reads
