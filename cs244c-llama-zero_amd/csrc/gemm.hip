@@ -475,8 +475,8 @@ __device__ __forceinline__ void store_tile16(const GemmArgs& go, typename Acc<MI
           }
         }
         if (go.c_f32) {
-          *reinterpret_cast<uint4*>(static_cast<float*>(go.C) + m * go.ldc + n) = make_uint4(
-              __float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
+          st_nt16(static_cast<float*>(go.C) + m * go.ldc + n, make_uint4(
+              __float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])));
         } else {
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(go.C) + m * go.ldc + n) =
               make_uint2(F::pack2(o[0], o[1]), F::pack2(o[2], o[3]));
@@ -1101,7 +1101,7 @@ __device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t 
   park16<FmtBF16, 16, FM, FN, kRow>(acc, st, lane, 1.0f);
   asm volatile("" ::: "memory");
   constexpr int kIters = TM * kChunks / 64;
-  constexpr int kBlk = 4;  // gate and up pieces of four stores loaded together
+  constexpr int kBlk = 16;  // every gate and up piece of the wave's tile loaded together (acc is free after the park)
   static_assert(kIters % kBlk == 0, "store blocks must tile the wave's rows");
 #pragma unroll
   for (int t0 = 0; t0 < kIters; t0 += kBlk) {

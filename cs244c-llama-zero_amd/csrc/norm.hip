@@ -382,6 +382,73 @@ __global__ void dw_final_kernel(const float* __restrict__ slices, int cols, T* _
   Elem<T>::store(dw, c, s);
 }
 
+// dw from the partial rows in one launch (cols % 4 == 0): each workgroup owns
+// 32 columns; its 256 threads are 8 column quads (16-byte reads) x 32 row
+// groups, each summing every 32nd partial row in order, then the 32 row-group
+// sums are added in a fixed order.  Deterministic: no atomics, and the order
+// does not depend on scheduling.
+constexpr int kColsumCols = 32, kColsumGroups = 32;
+
+template <typename T>
+__global__ void __launch_bounds__(256) dw_colsum_kernel(const float* __restrict__ part, int64_t nparts, int cols,
+                                                        T* __restrict__ dw, int accumulate) {
+  __shared__ float4 red[kColsumGroups][kColsumCols / 4];
+  const int cq = threadIdx.x % (kColsumCols / 4), rg = threadIdx.x / (kColsumCols / 4);
+  const int c = blockIdx.x * kColsumCols + 4 * cq;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < cols) {
+    int64_t p = rg;
+    // four partial rows in flight per thread
+    for (; p + 3 * kColsumGroups < nparts; p += 4 * kColsumGroups) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(part + (p + u * kColsumGroups) * cols + c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s.x += v[u].x;
+        s.y += v[u].y;
+        s.z += v[u].z;
+        s.w += v[u].w;
+      }
+    }
+    for (; p < nparts; p += kColsumGroups) {
+      const float4 v = *reinterpret_cast<const float4*>(part + p * cols + c);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+  }
+  red[rg][cq] = s;
+  __syncthreads();
+  if (rg == 0 && c < cols) {
+    float4 t = red[0][cq];
+    for (int k = 1; k < kColsumGroups; ++k) {
+      const float4 v = red[k][cq];
+      t.x += v.x;
+      t.y += v.y;
+      t.z += v.z;
+      t.w += v.w;
+    }
+    const float o[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Elem<T>::store(dw, c + e, accumulate ? o[e] + Elem<T>::load(dw, c + e) : o[e]);
+  }
+}
+
+// Column sums of `nparts` fp32 partial rows into dw (+= when accumulate).
+template <typename T>
+int dw_from_partials(const float* part, int64_t nparts, int cols, T* dw, int accumulate, float* slices,
+                     hipStream_t s) {
+  if (cols % 4 == 0) {
+    dw_colsum_kernel<T><<<(unsigned)lz_cdiv(cols, kColsumCols), 256, 0, s>>>(part, nparts, cols, dw, accumulate);
+  } else {
+    dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(part, nparts, cols, slices);
+    dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, dw, accumulate);
+  }
+  return lz_check_launch("lz_rmsnorm_bwd(dw)");
+}
+
 // bf16 vector backward: number of workgroups (one dw partial row each), one
 // resident round of them (the register footprint grows with cols: 8, 4, 2, 1
 // workgroups per CU for cols <= 512, 1024, 2048, 4096).
@@ -451,12 +518,7 @@ int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy
       else rmsnorm_bwd16_kernel<T, 8><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, rpb, cols, ldx, lddy, lddx);
       int rc = lz_check_launch("lz_rmsnorm_bwd");
       if (rc) return rc;
-      if (dw) {
-        float* slices = ws + nblk * (int64_t)cols;
-        dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(ws, nblk, cols, slices);
-        dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, (T*)dw, dw_accumulate);
-        rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
-      }
+      if (dw) rc = dw_from_partials<T>(ws, nblk, cols, (T*)dw, dw_accumulate, ws + nblk * (int64_t)cols, s);
       return rc;
     }
   }
@@ -471,12 +533,7 @@ int bwd_dispatch(const void* x, const void* w, const float* rstd, const void* dy
   else rmsnorm_bwd_scalar_kernel<T><<<grid, kThreads, 0, s>>>(xp, wp, rstd, gp, rp, dxp, ws, rows, cols, ldx, lddy, lddx);
   int rc = lz_check_launch("lz_rmsnorm_bwd");
   if (rc) return rc;
-  if (dw) {
-    float* slices = ws + nwaves * (int64_t)cols;
-    dw_slice_kernel<<<dim3((unsigned)lz_cdiv(cols, 64), kSlices), 256, 0, s>>>(ws, nwaves, cols, slices);
-    dw_final_kernel<T><<<(int)lz_cdiv(cols, 256), 256, 0, s>>>(slices, cols, (T*)dw, dw_accumulate);
-    rc = lz_check_launch("lz_rmsnorm_bwd(dw)");
-  }
+  if (dw) rc = dw_from_partials<T>(ws, nwaves, cols, (T*)dw, dw_accumulate, ws + nwaves * (int64_t)cols, s);
   return rc;
 }
 
