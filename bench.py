@@ -5,7 +5,9 @@ Headline (`value`): training tokens/s of the 1B-class model (d2048, 16 layers,
 ZeRO-3 engine at world_size 1, micro-batch 8 x 2048 tokens, bf16 compute with
 an fp32 flat master, synthetic uniform token ids (seed 0) already resident in
 HBM, random-init weights (seed 0).  One step = zero_grad, prepare_forward,
-forward + loss, backward (with ZeRO-3's recomputation; at one rank the
+forward + loss, backward (with ZeRO-3's recomputation, which leaves each
+block's output, the down projection's product, unformed: only autograd.grad
+reads it, so the gradients are the same; at one rank the
 reduce-scatter of the flattened gradients is the identity, so each module's
 bf16 gradients are gathered straight into the fp32 gradient shard instead of
 through 25M-element bf16 buckets), step_with_stats (norm + fused AdamW).
@@ -423,6 +425,31 @@ def _time_ms(fn, iters: int = 20) -> float:
     return start.elapsed_time(end) / iters
 
 
+def _time_graph_ms(fn, iters: int = 20) -> float:
+    """Device time per call of `fn` with the host out of the way: `iters`
+    calls captured into one HIP graph (after 3 eager warm-up calls, so that
+    cached workspaces exist before capture) and the graph replayed between HIP
+    events.  Short kernels (tens of microseconds) launched through the Python
+    wrappers one by one are otherwise partly host-bound."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / iters
+    del graph
+    return ms
+
+
 def bench_ceilings(dev: torch.device) -> dict:
     """What this box's HBM and MFMA deliver, measured, beside the published
     8 TB/s and 2.5 PFLOP/s: a STREAM-style 1 GiB -> 1 GiB copy and a 2 GiB
@@ -465,7 +492,8 @@ def bench_pointwise(dev: torch.device, ceilings=None, rows: int = 16384, dim: in
     tokens): bytes moved (each input read once, each output written once) per
     launch time.  A plain 1 GiB device copy is timed beside them as the
     achievable-bandwidth reference.  Tensors under ~256 MB can be partly
-    served from the 256 MB Infinity Cache, so those rates may exceed HBM's."""
+    served from the 256 MB Infinity Cache, so those rates may exceed HBM's.
+    Each rate is the device time of 20 calls replayed from one HIP graph."""
     from lzhip import ops
 
     g = torch.Generator(device=dev).manual_seed(0)
@@ -482,29 +510,29 @@ def bench_pointwise(dev: torch.device, ceilings=None, rows: int = 16384, dim: in
     # kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters)
     a = torch.ones(1 << 14, 1 << 15, dtype=bf, device=dev)
     b = torch.empty_like(a)
-    rec("device copy 1 GiB (copy2d_vec_kernel)", _time_ms(lambda: ops.copy2d(a, b), 10), 2 * 2 * a.numel())
+    rec("device copy 1 GiB (copy2d_vec_kernel)", _time_graph_ms(lambda: ops.copy2d(a, b), 10), 2 * 2 * a.numel())
     del a, b
     x = torch.randn(rows, dim, device=dev, generator=g).to(bf)
     w = (1 + 0.02 * torch.randn(dim, device=dev, generator=g)).to(bf)
     dy = torch.randn(rows, dim, device=dev, generator=g).to(bf)
     n = rows * dim
-    rec(f"rmsnorm fwd [{rows},{dim}]", _time_ms(lambda: ops.rmsnorm_fwd(x, w, 1e-5)), 4 * n)
+    rec(f"rmsnorm fwd [{rows},{dim}]", _time_graph_ms(lambda: ops.rmsnorm_fwd(x, w, 1e-5)), 4 * n)
     _, rstd = ops.rmsnorm_fwd(x, w, 1e-5)
-    rec(f"rmsnorm bwd [{rows},{dim}]", _time_ms(lambda: ops.rmsnorm_bwd(x, w, rstd, dy)), 6 * n)
+    rec(f"rmsnorm bwd [{rows},{dim}]", _time_graph_ms(lambda: ops.rmsnorm_bwd(x, w, rstd, dy)), 6 * n)
     hd = dim // heads
     inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32, device=dev) / hd))
     cos, sin = ops.rope_table(2048, hd, inv, bf)
-    rec(f"rope fwd [{rows},{heads}x{hd}] in place", _time_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin)), 4 * n)
+    rec(f"rope fwd [{rows},{heads}x{hd}] in place", _time_graph_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin)), 4 * n)
     rec(f"rope bwd [{rows},{heads}x{hd}] in place",
-        _time_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin, backward=True)), 4 * n)
+        _time_graph_ms(lambda: ops.rope_(x, 2048, heads, hd, cos, sin, backward=True)), 4 * n)
     del x, dy
     gu = torch.randn(rows, 2 * ffn, device=dev, generator=g).to(bf)
     gate, up = gu[:, :ffn], gu[:, ffn:]
-    rec(f"swiglu fwd [{rows},{ffn}]", _time_ms(lambda: ops.swiglu_fwd(gate, up)), 6 * rows * ffn)
+    rec(f"swiglu fwd [{rows},{ffn}]", _time_graph_ms(lambda: ops.swiglu_fwd(gate, up)), 6 * rows * ffn)
     dh = torch.randn(rows, ffn, device=dev, generator=g).to(bf)
     dgu = torch.empty_like(gu)
     rec(f"swiglu bwd [{rows},{ffn}]",
-        _time_ms(lambda: ops.swiglu_bwd(gate, up, dh, dgu[:, :ffn], dgu[:, ffn:])), 10 * rows * ffn)
+        _time_graph_ms(lambda: ops.swiglu_bwd(gate, up, dh, dgu[:, :ffn], dgu[:, ffn:])), 10 * rows * ffn)
     return out
 
 
@@ -668,7 +696,10 @@ def main() -> int:
     tokens = B * S
     value = tokens * args.steps / elapsed
     model_flops = estimate_transformer_train_flops(cfg, B, S, stage=0)
-    hw_flops = estimate_transformer_train_flops(cfg, B, S, stage=3)
+    # executed flops: the stage-3 formula's recompute (a fourth forward) less
+    # each layer's down projection, which the recompute leaves unformed (only
+    # autograd.grad reads the recomputed block output)
+    hw_flops = estimate_transformer_train_flops(cfg, B, S, stage=3) - 2.0 * B * S * cfg.ffn_dim * cfg.dim * cfg.n_layers
     n_launch, gemm_flops, gemm_ms = probe.summary()
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
     # the dominant GEMM kernel: the one with the most launch time in the steps

@@ -9,12 +9,37 @@ over the concatenated weight rows.
 from __future__ import annotations
 
 import math
-from typing import List, Optional, Sequence, Tuple
+import threading
+from contextlib import contextmanager
+from typing import Iterator, List, Optional, Sequence, Tuple
 
 import torch
 from torch.autograd import Function
 
 from . import ops
+
+_local = threading.local()
+
+
+@contextmanager
+def output_unused() -> Iterator[None]:
+    """Marks a module call whose output value nobody reads: the ZeRO-3
+    recompute in backward (reference zero/stage3_optimizer.py:213-237) runs the
+    module again only to take autograd.grad of its output with the incoming
+    gradient, which needs the output's graph, not its value.  The op that
+    produces a module's output may then leave the value uncomputed (its
+    backward must not need it); the gradients are the same."""
+    prev = getattr(_local, "output_unused", False)
+    _local.output_unused = True
+    try:
+        yield
+    finally:
+        _local.output_unused = prev
+
+
+def output_is_unused() -> bool:
+    """Whether the current module call runs under output_unused()."""
+    return getattr(_local, "output_unused", False)
 
 
 def _rows(t: torch.Tensor) -> torch.Tensor:
@@ -399,7 +424,8 @@ class MLPFn(Function):
     projection."""
 
     @staticmethod
-    def forward(ctx, x, wg, wu, wd, residual, grad_wanted=True, dropout_p: float = 0.0, seed: int = 0):
+    def forward(ctx, x, wg, wu, wd, residual, grad_wanted=True, dropout_p: float = 0.0, seed: int = 0,
+                compute_output: bool = True):
         x2 = _rows(x)
         F_ = wg.shape[0]
         w = fused_weight([wg, wu])
@@ -415,7 +441,12 @@ class MLPFn(Function):
             ops.dropout_(m, dropout_p, seed)  # the saved m is the dropped-out input of down_proj
         ctx.dropout = (dropout_p, seed)
         r2 = _rows(residual) if residual is not None else None
-        y = _linear_fwd(m, wd, r2)
+        if compute_output:
+            y = _linear_fwd(m, wd, r2)
+        else:
+            # the caller reads only the graph (output_unused): the down
+            # projection's product is not formed; the backward needs m, not y
+            y = torch.empty((m.shape[0], wd.shape[0]), dtype=m.dtype, device=m.device)
         if grad_wanted:
             ctx.save_for_backward(x2, wg, wu, wd, gu, m)
         ctx.has_residual = residual is not None
@@ -447,7 +478,7 @@ class MLPFn(Function):
             dwg, dwu = dw[:F_], dw[F_:]
         dx = dx2.view(ctx.in_shape) if dx2 is not None else None
         dres = dy if (ctx.has_residual and ctx.needs_input_grad[4]) else None
-        return dx, dwg, dwu, dwd, dres, None, None, None
+        return dx, dwg, dwu, dwd, dres, None, None, None, None
 
 
 class DropoutFn(Function):

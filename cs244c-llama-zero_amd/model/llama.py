@@ -186,12 +186,15 @@ class SwiGLU(nn.Module):
         self.down_proj = HipLinear(cfg.ffn_dim, cfg.dim, bias=False)
         self.dropout = nn.Dropout(cfg.dropout)
 
-    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                compute_output: bool = True) -> torch.Tensor:
+        """compute_output=False (the caller only takes gradients through the
+        result): the down projection's product is left uncomputed."""
         ops.require_gpu(x)
         p = float(self.dropout.p) if self.training else 0.0  # nn.Dropout on the gated activations
         seed = ops.dropout_seed(x.device) if p > 0.0 else 0
         return LF.MLPFn.apply(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight, residual,
-                              torch.is_grad_enabled(), p, seed)
+                              torch.is_grad_enabled(), p, seed, compute_output)
 
 
 class TransformerBlock(nn.Module):
@@ -208,7 +211,9 @@ class TransformerBlock(nn.Module):
         h, x = self.input_norm.forward_with_residual(x)
         x = self.attn(h, attention_mask=attention_mask, residual=x)
         h, x = self.post_attn_norm.forward_with_residual(x)
-        return self.mlp(h, residual=x)
+        # the block's output is the MLP's: under output_unused() (the ZeRO-3
+        # recompute) its value is not formed
+        return self.mlp(h, residual=x, compute_output=not LF.output_is_unused())
 
 
 @dataclass

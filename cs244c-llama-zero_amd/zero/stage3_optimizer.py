@@ -41,6 +41,7 @@ import torch.nn as nn
 
 from collectives import CollectiveOps, LocalCollectives
 from lzhip import ops
+from lzhip.functional import output_unused
 from profiler import MemoryTracker
 
 from ._fused import FusedStep
@@ -303,7 +304,10 @@ class _ShardedModuleFunction(torch.autograd.Function):
                         grad_inputs.append(t)
                     rebuilt.append(t)
                 use_ac = ctx.autocast_enabled and runner.device.type in {"cpu", "cuda"}
-                with torch.autocast(device_type=runner.device.type, dtype=ctx.autocast_dtype, enabled=use_ac):
+                # only autograd.grad reads `out` below (its graph, not its
+                # value): modules may skip forming the value (output_unused)
+                with torch.autocast(device_type=runner.device.type, dtype=ctx.autocast_dtype, enabled=use_ac), \
+                        output_unused():
                     out = runner.module(*rebuilt)
                 params = list(h.meta.params)
                 grads = torch.autograd.grad(outputs=out, inputs=grad_inputs + params, grad_outputs=grad_output,

@@ -252,6 +252,40 @@ def test_stage3_recompute_off_matches_recompute_on():
     assert eb._forward_allgather_ms == 0.0
 
 
+def test_block_gradients_unchanged_when_output_unused():
+    """Under lzhip.functional.output_unused() (the stage-3 recompute) a
+    TransformerBlock leaves its MLP's down projection unformed; the gradients
+    of its input and parameters taken through that output are bit for bit
+    those of the full forward, and the GEMM probe sees one launch fewer."""
+    from lzhip import functional as LF
+
+    m = _model(21)
+    block = m.layers[0]
+    torch.manual_seed(3)
+    x0 = torch.randn(3, 64, 128, device=DEV).to(torch.bfloat16)
+    dy = torch.randn(3, 64, 128, device=DEV).to(torch.bfloat16)
+    params = list(block.parameters())
+    res = []
+    for unused in (False, True):
+        x = x0.clone().requires_grad_(True)
+        probe = ops.LaunchProbe()
+        ops.set_gemm_probe(probe)
+        try:
+            if unused:
+                with LF.output_unused():
+                    out = block(x)
+            else:
+                out = block(x)
+        finally:
+            ops.set_gemm_probe(None)
+        launches = len(probe.records)
+        grads = torch.autograd.grad(out, [x] + params, grad_outputs=dy)
+        res.append((grads, launches))
+    for a, b in zip(res[0][0], res[1][0]):
+        assert torch.equal(a, b)
+    assert res[1][1] == res[0][1] - 1  # the down projection's forward product is the one launch left out
+
+
 def test_stage3_recompute_off_checkpoint_restore():
     kw = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01, recompute=False)
     m_src = _model(31)
