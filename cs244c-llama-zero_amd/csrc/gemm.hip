@@ -1329,10 +1329,14 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
   }
   if (p.cfg != 2 && K >= 1024) {
     // Long K: split it when that fills the chip better.  Same unit; a split
-    // product also pays its fp32 slabs' round trip through HBM (written, then
-    // read by the reduce) and its output write, at about 10 MB per unit, plus
-    // 3 units for the reduce launch.  Splits are whole multiples of 64 in K
-    // and at least 256 deep.
+    // product also pays its fp32 slabs' round trip through HBM (written by
+    // the product, read by the reduce: about 2 MB of slab per unit), the
+    // reduce's output write (about 10 MB per unit) and 3 units for the
+    // reduce launch.  Fitted to weight-gradient sweeps over K = 16384 on
+    // MI355X (768x768 ... 2048x5632 outputs, 1 ... 32 splits), whose measured
+    // order of plans it reproduces: e.g. 768x768 is fastest at 16 splits
+    // (42 us; 26 splits 50 us), 2048x5632 unsplit (1.2 PFLOP/s; 4 splits
+    // 1.05).  Splits are whole multiples of 64 in K and at least 256 deep.
     const double mn = (double)M * (double)N;
     double best = 1e30;
     for (int sp = 1; sp <= 32; ++sp) {
@@ -1340,7 +1344,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, bool ak, bool bk) {
       if (sp > 1 && kper < 256) break;
       if (lz_cdiv(K, kper) != sp || sp < min_splits) continue;
       double cost = (double)lz_cdiv(big * sp, cus) * (double)(kper / 64 + 2);
-      if (sp > 1) cost += (2.0 * sp * mn * 4.0 + mn * 4.0) / 10e6 + 3.0;
+      if (sp > 1) cost += sp * mn * 4.0 / 2e6 + mn * 4.0 / 10e6 + 3.0;
       if (cost < best - 1e-9) {
         best = cost;
         p.splits = sp;
