@@ -566,8 +566,14 @@ class LaunchProbe:
     products.  Used by the benchmark to measure the MFMA
     kernels inside a timed training step."""
 
-    def __init__(self) -> None:
+    def __init__(self, only=None) -> None:
+        """only: a kernel key; when set, events are recorded around that
+        key's launches alone (every other launch runs without them)."""
         self.records = []
+        self.only = only
+
+    def wants(self, key) -> bool:
+        return self.only is None or key == self.only
 
     def add(self, flops: float, start, end, key=None) -> None:
         self.records.append((flops, start, end, key))
@@ -673,6 +679,10 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
     ws = torch.empty(((ws_bytes + 15) // 16) * 4, dtype=torch.float32, device=a.device) if ws_bytes else None
     probe = _gemm_probe
     if probe is not None:
+        key = (bool(a_kmajor), bool(b_kmajor), int(lib.lz_gemm_plan(M, N, Kp, int(a_kmajor), int(b_kmajor))))
+        if not probe.wants(key):
+            probe = None
+    if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
@@ -682,8 +692,7 @@ def gemm(a: torch.Tensor, b: torch.Tensor, a_kmajor: bool = True, b_kmajor: bool
               ws_bytes if ws is not None else 0, stream_ptr(a.device))
     if probe is not None:
         end.record()
-        probe.add(2.0 * M * N * K, start, end, (bool(a_kmajor), bool(b_kmajor),
-                                                int(lib.lz_gemm_plan(M, N, Kp, int(a_kmajor), int(b_kmajor)))))
+        probe.add(2.0 * M * N * K, start, end, key)
     return out
 
 
@@ -717,6 +726,8 @@ def _gemm_f32(a, b, a_kmajor, b_kmajor, out, out_dtype, residual, alpha, beta) -
     ws_bytes = int(lib.lz_gemm_f32_workspace(M, N, K))
     ws = torch.empty(((ws_bytes + 15) // 16) * 4, dtype=torch.float32, device=a.device) if ws_bytes else None
     probe = _gemm_probe
+    if probe is not None and not probe.wants((bool(a_kmajor), bool(b_kmajor), "f32")):
+        probe = None
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -756,6 +767,8 @@ def gemm_swiglu(x2: torch.Tensor, w: torch.Tensor, gu: Optional[torch.Tensor] = 
         raise ValueError("gu must be an aligned bf16 [M, 2F] view")
     h = torch.empty((M, F), dtype=torch.bfloat16, device=x2.device)
     probe = _gemm_probe
+    if probe is not None and not probe.wants((True, True, "swiglu")):
+        probe = None
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -801,6 +814,8 @@ def gemm_swiglu_bwd(dy2: torch.Tensor, wd: torch.Tensor, gu: torch.Tensor,
           or _row_stride(dgu) % 8 or dgu.data_ptr() % 16):
         raise ValueError("dgu must be an aligned bf16 [M, 2F] view")
     probe = _gemm_probe
+    if probe is not None and not probe.wants((True, False, "swiglu_bwd")):
+        probe = None
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -842,6 +857,8 @@ def gemm_rope(x2: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.T
     N = w.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x2.device)
     probe = _gemm_probe
+    if probe is not None and not probe.wants((True, True, "rope")):
+        probe = None
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
