@@ -123,54 +123,54 @@ struct Vec4<_Float16> {
 // memory); the n % 4 tail goes to the scalar kernel.
 constexpr int kAdamThreads = 128;
 
+// `part` (optional): one float64 per workgroup, the sum of the squares of the
+// gradient values it read (before the clip scale), for a step that reports
+// the norm without clipping: the norm then costs no pass of its own.
 template <typename G, typename PO>
 __global__ void __launch_bounds__(kAdamThreads) adamw_vec_kernel(float* __restrict__ p, float* __restrict__ m,
                                                                   float* __restrict__ v, const G* __restrict__ g,
                                                                   PO* __restrict__ pout, int64_t n4, AdamArgs a0,
                                                                   const float* __restrict__ scale_ptr,
-                                                                  const float* __restrict__ hyper) {
+                                                                  const float* __restrict__ hyper,
+                                                                  double* __restrict__ part) {
   const int64_t q = (int64_t)blockIdx.x * kAdamThreads + threadIdx.x;
-  if (q >= n4) return;
-  const AdamArgs a = with_hyper(a0, hyper);
-  const int64_t i = q << 2;
-  float pp[4], mm[4], vv[4], gg[4];
-  Vec4<float>::load(p, i, pp);
-  Vec4<float>::load(m, i, mm);
-  Vec4<float>::load(v, i, vv);
-  Vec4<G>::load(g, i, gg);
-  const float scale = scale_ptr ? *scale_ptr : 1.0f;
+  float gg[4] = {0.f, 0.f, 0.f, 0.f};
+  if (q < n4) {
+    const AdamArgs a = with_hyper(a0, hyper);
+    const int64_t i = q << 2;
+    float pp[4], mm[4], vv[4];
+    Vec4<float>::load(p, i, pp);
+    Vec4<float>::load(m, i, mm);
+    Vec4<float>::load(v, i, vv);
+    Vec4<G>::load(g, i, gg);
+    const float scale = scale_ptr ? *scale_ptr : 1.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float gj = scale_ptr ? gg[j] * scale : gg[j];
-    adam_elem(pp[j], mm[j], vv[j], gj, a);
+    for (int j = 0; j < 4; ++j) {
+      const float gj = scale_ptr ? gg[j] * scale : gg[j];
+      adam_elem(pp[j], mm[j], vv[j], gj, a);
+    }
+    Vec4<float>::store(p, i, pp);
+    Vec4<float>::store(m, i, mm);
+    Vec4<float>::store(v, i, vv);
+    if (pout) Vec4<PO>::store(pout, i, pp);
   }
-  Vec4<float>::store(p, i, pp);
-  Vec4<float>::store(m, i, mm);
-  Vec4<float>::store(v, i, vv);
-  if (pout) Vec4<PO>::store(pout, i, pp);
-}
-
-template <typename G, typename PO>
-int launch_adamw(float* p, float* m, float* v, const void* g, void* pout, int64_t n, const AdamArgs& a,
-                 const float* scale, const float* hyper, hipStream_t s) {
-  const G* gp = static_cast<const G*>(g);
-  PO* po = static_cast<PO*>(pout);
-  const bool vec = lz_aligned16(p) && lz_aligned16(m) && lz_aligned16(v) &&
-                   ((reinterpret_cast<uintptr_t>(g) & (4 * sizeof(G) - 1)) == 0) &&
-                   (pout == nullptr || (reinterpret_cast<uintptr_t>(pout) & (4 * sizeof(PO) - 1)) == 0);
-  if (vec) {
-    const int64_t n4 = n / 4, tail = n - 4 * n4;
-    LZ_REQUIRE(lz_cdiv(n4, kAdamThreads) < (1ll << 31), "lz_adamw: too many elements");
-    if (n4 > 0)
-      adamw_vec_kernel<G, PO><<<(unsigned)lz_cdiv(n4, kAdamThreads), kAdamThreads, 0, s>>>(p, m, v, gp, po, n4, a, scale, hyper);
-    if (tail > 0)
-      adamw_scalar_kernel<G, PO><<<1, kThreads, 0, s>>>(p + 4 * n4, m + 4 * n4, v + 4 * n4, gp + 4 * n4,
-                                                        po ? po + 4 * n4 : nullptr, tail, a, scale, hyper);
-  } else {
-    int grid = stream_grid(n);
-    adamw_scalar_kernel<G, PO><<<grid, kThreads, 0, s>>>(p, m, v, gp, po, n, a, scale, hyper);
+  if (part) {
+    // every thread joins (those past the end with zeros), after its stores
+    // are issued; the barrier orders LDS only, so it does not wait for them
+    __shared__ double red[kAdamThreads / 64];
+    const float sq = fmaf(gg[0], gg[0], fmaf(gg[1], gg[1], fmaf(gg[2], gg[2], gg[3] * gg[3])));
+    const double d = wave_sum_d((double)sq);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = d;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (threadIdx.x == 0) {
+      double t = 0.0;
+#pragma unroll
+      for (int w = 0; w < kAdamThreads / 64; ++w) t += red[w];
+      part[blockIdx.x] = t;
+    }
   }
-  return lz_check_launch("lz_adamw");
 }
 
 // ---------------------------------------------------------------------------
@@ -193,6 +193,83 @@ __global__ void __launch_bounds__(kThreads) sumsq_kernel(const T* __restrict__ x
     for (int w = 0; w < kThreads / 64; ++w) s += red[w];
     atomicAdd(acc, s);
   }
+}
+
+// Sum of the workgroup partials of adamw_vec_kernel (and the squares of the
+// n % 4 tail it leaves to the scalar kernel) added to *acc, in a fixed order:
+// kNormBlocks workgroups reduce contiguous ranges into part2, then one
+// workgroup sums part2 and the tail.
+constexpr int kNormBlocks = 256;
+
+__global__ void __launch_bounds__(256) norm_partials_kernel(const double* __restrict__ part, int64_t nparts,
+                                                            double* __restrict__ part2) {
+  __shared__ double red[4];
+  const int64_t per = lz_cdiv(nparts, kNormBlocks);
+  const int64_t b0 = (int64_t)blockIdx.x * per, b1 = min(nparts, b0 + per);
+  double t = 0.0;
+  for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) t += part[i];
+  t = wave_sum_d(t);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  __syncthreads();
+  if (threadIdx.x == 0) part2[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <typename G>
+__global__ void __launch_bounds__(256) norm_final_kernel(const double* __restrict__ part2, const G* __restrict__ tail,
+                                                         int ntail, double* __restrict__ acc) {
+  __shared__ double red[4];
+  double t = threadIdx.x < kNormBlocks ? part2[threadIdx.x] : 0.0;
+  if (threadIdx.x < ntail) {
+    const float x = Elem<G>::load(tail, threadIdx.x);
+    t += (double)(x * x);
+  }
+  t = wave_sum_d(t);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  __syncthreads();
+  if (threadIdx.x == 0) *acc += (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Float64 words of workspace the norm-accumulating AdamW takes for n
+// elements: one partial per workgroup, then kNormBlocks second-level sums.
+inline int64_t adamw_norm_words(int64_t n) { return lz_cdiv(n / 4, kAdamThreads) + kNormBlocks; }
+
+template <typename G, typename PO>
+int launch_adamw(float* p, float* m, float* v, const void* g, void* pout, int64_t n, const AdamArgs& a,
+                 const float* scale, const float* hyper, hipStream_t s, double* sumsq = nullptr,
+                 double* ws = nullptr) {
+  const G* gp = static_cast<const G*>(g);
+  PO* po = static_cast<PO*>(pout);
+  const bool vec = lz_aligned16(p) && lz_aligned16(m) && lz_aligned16(v) &&
+                   ((reinterpret_cast<uintptr_t>(g) & (4 * sizeof(G) - 1)) == 0) &&
+                   (pout == nullptr || (reinterpret_cast<uintptr_t>(pout) & (4 * sizeof(PO) - 1)) == 0);
+  if (sumsq && !vec) {
+    // unaligned operands take the scalar kernel: the sum of squares gets a
+    // pass of its own first (the update does not change g)
+    sumsq_kernel<G><<<stream_grid(n), kThreads, 0, s>>>(gp, n, sumsq);
+    const int rc = lz_check_launch("lz_adamw_norm");
+    if (rc) return rc;
+    sumsq = nullptr;
+  }
+  if (vec) {
+    const int64_t n4 = n / 4, tail = n - 4 * n4;
+    LZ_REQUIRE(lz_cdiv(n4, kAdamThreads) < (1ll << 31), "lz_adamw: too many elements");
+    const int64_t nblk = lz_cdiv(n4, kAdamThreads);
+    double* part = sumsq ? ws : nullptr;
+    if (n4 > 0)
+      adamw_vec_kernel<G, PO><<<(unsigned)nblk, kAdamThreads, 0, s>>>(p, m, v, gp, po, n4, a, scale, hyper, part);
+    if (sumsq) {
+      double* part2 = ws + nblk;
+      norm_partials_kernel<<<kNormBlocks, 256, 0, s>>>(ws, n4 > 0 ? nblk : 0, part2);
+      norm_final_kernel<G><<<1, 256, 0, s>>>(part2, gp + 4 * n4, (int)tail, sumsq);
+    }
+    if (tail > 0)
+      adamw_scalar_kernel<G, PO><<<1, kThreads, 0, s>>>(p + 4 * n4, m + 4 * n4, v + 4 * n4, gp + 4 * n4,
+                                                        po ? po + 4 * n4 : nullptr, tail, a, scale, hyper);
+  } else {
+    int grid = stream_grid(n);
+    adamw_scalar_kernel<G, PO><<<grid, kThreads, 0, s>>>(p, m, v, gp, po, n, a, scale, hyper);
+  }
+  return lz_check_launch("lz_adamw");
 }
 
 __global__ void sumsq_vec4_f32_kernel(const float* __restrict__ x, int64_t n, double* __restrict__ acc) {
@@ -721,7 +798,8 @@ namespace {
 
 int adamw_entry(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype, int64_t n,
                 double lr, double beta1, double beta2, double eps, double weight_decay, int64_t step,
-                const float* grad_scale, const float* hyper, void* stream) {
+                const float* grad_scale, const float* hyper, void* stream, double* sumsq = nullptr,
+                double* ws = nullptr) {
   if (n == 0) return LZ_OK;
   LZ_REQUIRE(p && m && v && g && n > 0, "lz_adamw: bad arguments");
   const double bc1 = 1.0 - pow(beta1, (double)step);
@@ -741,17 +819,17 @@ int adamw_entry(float* p, float* m, float* v, const void* g, int g_dtype, void* 
   LZ_REQUIRE(g_dtype == LZ_BF16 || g_dtype == LZ_F32 || g_dtype == LZ_F16, "lz_adamw: bad grad dtype %d", g_dtype);
   if (gh) {  // fp16 models: fp16 gradients, fp16 (or no) parameter copy
     if (p_out == nullptr || p_out_dtype == LZ_F32)
-      return launch_adamw<_Float16, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+      return launch_adamw<_Float16, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s, sumsq, ws);
     LZ_REQUIRE(p_out_dtype == LZ_F16, "lz_adamw: bad output dtype %d for fp16 gradients", p_out_dtype);
-    return launch_adamw<_Float16, _Float16>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+    return launch_adamw<_Float16, _Float16>(p, m, v, g, p_out, n, a, grad_scale, hyper, s, sumsq, ws);
   }
   if (p_out == nullptr || p_out_dtype == LZ_F32) {
-    return gb ? launch_adamw<uint16_t, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s)
-              : launch_adamw<float, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+    return gb ? launch_adamw<uint16_t, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s, sumsq, ws)
+              : launch_adamw<float, float>(p, m, v, g, p_out, n, a, grad_scale, hyper, s, sumsq, ws);
   }
   LZ_REQUIRE(p_out_dtype == LZ_BF16, "lz_adamw: bad output dtype %d", p_out_dtype);
-  return gb ? launch_adamw<uint16_t, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, hyper, s)
-            : launch_adamw<float, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, hyper, s);
+  return gb ? launch_adamw<uint16_t, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, hyper, s, sumsq, ws)
+            : launch_adamw<float, uint16_t>(p, m, v, g, p_out, n, a, grad_scale, hyper, s, sumsq, ws);
 }
 
 // One thread: advances the device step counter and writes the factors that
@@ -776,6 +854,22 @@ LZ_EXPORT int lz_adamw(float* p, float* m, float* v, const void* g, int g_dtype,
   LZ_REQUIRE(step >= 1, "lz_adamw: step must be >= 1");
   return adamw_entry(p, m, v, g, g_dtype, p_out, p_out_dtype, n, lr, beta1, beta2, eps, weight_decay, step, grad_scale,
                      nullptr, stream);
+}
+
+LZ_EXPORT int64_t lz_adamw_norm_workspace(int64_t n) { return n > 0 ? adamw_norm_words(n) : 0; }
+
+LZ_EXPORT int lz_adamw_norm(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype,
+                            int64_t n, double lr, double beta1, double beta2, double eps, double weight_decay,
+                            int64_t step, const float* grad_scale, double* acc, double* workspace,
+                            int64_t workspace_words, void* stream) {
+  LZ_REQUIRE(step >= 1, "lz_adamw_norm: step must be >= 1");
+  LZ_REQUIRE(acc, "lz_adamw_norm: null accumulator");
+  LZ_REQUIRE(n >= 0, "lz_adamw_norm: bad element count");
+  LZ_REQUIRE(workspace && workspace_words >= lz_adamw_norm_workspace(n),
+             "lz_adamw_norm: workspace of %lld float64 words, %lld needed", (long long)workspace_words,
+             (long long)lz_adamw_norm_workspace(n));
+  return adamw_entry(p, m, v, g, g_dtype, p_out, p_out_dtype, n, lr, beta1, beta2, eps, weight_decay, step, grad_scale,
+                     nullptr, stream, acc, workspace);
 }
 
 LZ_EXPORT int lz_adamw_step(int64_t* step, double lr, double beta1, double beta2, double weight_decay, float* hyper,

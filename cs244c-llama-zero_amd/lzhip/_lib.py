@@ -37,6 +37,9 @@ SIGNATURES = {
     "lz_adamw_step": (_i32, [_vp, _f64, _f64, _f64, _f64, _vp, _vp]),
     "lz_adamw_dev": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _f64, _f64, _f64, _f64, _vp, _vp, _vp]),
     "lz_sumsq": (_i32, [_vp, _i32, _i64, _vp, _vp]),
+    "lz_adamw_norm_workspace": (_i64, [_i64]),
+    "lz_adamw_norm": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _f64, _f64, _f64, _f64, _f64, _i64, _vp, _vp,
+                             _vp, _i64, _vp]),
     "lz_adamw_multi": (_i32, [_vp, _i32, _i32, _i32, _f64, _f64, _f64, _f64, _f64, _i64, _vp, _vp, _vp]),
     "lz_sumsq_multi": (_i32, [_vp, _i32, _i32, _vp, _vp]),
     "lz_clip_finalize": (_i32, [_vp, _f32, _f32, _vp, _vp, _vp]),

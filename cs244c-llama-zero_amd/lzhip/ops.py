@@ -111,6 +111,56 @@ def adamw_(
     )
 
 
+def adamw_norm_workspace_words(n: int) -> int:
+    """float64 words of workspace adamw_norm_ needs for n elements."""
+    return int(_lib.load().lz_adamw_norm_workspace(int(n)))
+
+
+def adamw_norm_(
+    p: torch.Tensor,
+    m: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    acc: torch.Tensor,
+    workspace: torch.Tensor,
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    step: int,
+    grad_scale: Optional[torch.Tensor] = None,
+    p_out: Optional[torch.Tensor] = None,
+) -> None:
+    """adamw_ that also adds sum(g^2) (g as stored) to acc (float64 device
+    scalar) from the same read of g, in a fixed summation order; `workspace`
+    is a float64 device buffer of at least adamw_norm_workspace_words(n)."""
+    require_gpu(p, m, v, g, acc, workspace, grad_scale, p_out)
+    n = p.numel()
+    for t, name in ((m, "exp_avg"), (v, "exp_avg_sq"), (g, "grad")):
+        if t.numel() != n:
+            raise ValueError(f"{name} has {t.numel()} elements, expected {n}")
+    for t in (p, m, v):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("AdamW master/moment buffers must be contiguous float32")
+    if not g.is_contiguous():
+        raise ValueError("gradient must be contiguous")
+    if acc.dtype != torch.float64 or workspace.dtype != torch.float64 or not workspace.is_contiguous():
+        raise ValueError("accumulator and workspace must be float64")
+    if grad_scale is not None and (grad_scale.dtype != torch.float32 or grad_scale.numel() < 1):
+        raise ValueError("grad_scale must be a float32 device scalar")
+    if p_out is not None and (p_out.numel() != n or not p_out.is_contiguous()):
+        raise ValueError("p_out must be contiguous with the same number of elements")
+    _lib.call(
+        "lz_adamw_norm",
+        p.data_ptr(), m.data_ptr(), v.data_ptr(), g.data_ptr(), dtype_code(g),
+        _ptr(p_out), dtype_code(p_out) if p_out is not None else F32, n,
+        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(step),
+        _ptr(grad_scale), acc.data_ptr(), workspace.data_ptr(), workspace.numel(), stream_ptr(p.device),
+    )
+
+
 def adamw_step_(step: torch.Tensor, lr: float, beta1: float, beta2: float, weight_decay: float,
                 hyper: torch.Tensor) -> None:
     """step (int64 device scalar) += 1 and hyper (float32 [3]) = the AdamW

@@ -68,6 +68,19 @@ int lz_adamw_dev(float* p, float* m, float* v, const void* g, int g_dtype, void*
  * (zero/stage0_ddp.py:66) and sum(g*g) (zero/stage2_optimizer.py:162-166,
  * zero/stage3_optimizer.py:438-444). */
 int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* stream);
+
+/* lz_adamw that also adds sum(g^2) (g as stored, before grad_scale) to *acc,
+ * for a step whose norm is reported but does not clip: the reference's
+ * default max_grad_norm = 0.0 (zero/stage0_ddp.py:62-71, stage1/2/3 alike)
+ * computes the norm and never uses it in the update, so the update's own read
+ * of g serves both instead of a second pass (lz_sumsq + lz_adamw).  The sum
+ * is taken in a fixed order (workgroup partials into `workspace`, then two
+ * reduction launches), so it is the same from run to run;
+ * lz_adamw_norm_workspace(n) gives the float64 words `workspace` must hold. */
+int64_t lz_adamw_norm_workspace(int64_t n);
+int lz_adamw_norm(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype, int64_t n,
+                  double lr, double beta1, double beta2, double eps, double weight_decay, int64_t step,
+                  const float* grad_scale, double* acc, double* workspace, int64_t workspace_words, void* stream);
 /* Multi-tensor forms of lz_adamw and lz_sumsq for per-parameter optimizers
  * (reference train.py:206-211,259-271: torch.optim.AdamW over the model's
  * parameter list and clip_grad_norm_ over their gradients): one launch per 24

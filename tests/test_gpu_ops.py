@@ -979,6 +979,50 @@ def test_adamw_multi_matches_per_tensor():
         assert abs(float(acc1.item()) - float(acc2.item())) <= 1e-6 * ref
 
 
+@pytest.mark.parametrize("n,gdtype,off", [(1_000_003, torch.float32, 0), (262_147, torch.bfloat16, 0),
+                                          (3 * 512, torch.bfloat16, 0), (5, torch.float32, 0),
+                                          (10_001, torch.bfloat16, 1)])
+def test_adamw_norm_matches_adamw_and_sumsq(n, gdtype, off):
+    """adamw_norm_ (the update plus the sum of squares of g from the same
+    read) against adamw_ then float64 sums: p, m, v and the bf16 copy bit for
+    bit over 3 steps with a grad scale; the accumulated sum to 1e-6 (fp32
+    squares of 4 elements, float64 after), added onto what acc held, and the
+    same bits on a second run over the same gradient (fixed summation order).
+    off=1 puts every operand one element into its buffer: not 16-byte
+    aligned, so the scalar update runs after a separate sum-of-squares pass."""
+    g = _seed(n % 1000 + off)
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    scale = torch.tensor([0.5], device=DEV)
+
+    def at_offset(t):
+        buf = torch.zeros(t.numel() + off, dtype=t.dtype, device=DEV)
+        buf[off:].copy_(t.to(DEV))
+        return buf[off:]
+
+    p0 = 0.02 * torch.randn(n, generator=g)
+    pa, ma, va = p0.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+    pb, mb, vb = at_offset(p0), at_offset(torch.zeros(n)), at_offset(torch.zeros(n))
+    oa = torch.zeros(n, dtype=torch.bfloat16, device=DEV)
+    ob = at_offset(torch.zeros(n, dtype=torch.bfloat16))
+    ws = torch.full((ops.adamw_norm_workspace_words(n),), float("nan"), dtype=torch.float64, device=DEV)
+    for t in range(1, 4):
+        gr = (1e-3 * torch.randn(n, generator=g)).to(gdtype)
+        gd = at_offset(gr)
+        acc = torch.full((1,), 2.5, dtype=torch.float64, device=DEV)
+        ops.adamw_(pa, ma, va, gr.to(DEV), step=t, grad_scale=scale, p_out=oa, **hp)
+        ops.adamw_norm_(pb, mb, vb, gd, acc, ws, step=t, grad_scale=scale, p_out=ob, **hp)
+        assert torch.equal(pa, pb) and torch.equal(ma, mb) and torch.equal(va, vb) and torch.equal(oa, ob)
+        ref = float(gr.double().pow(2).sum())
+        assert abs(float(acc.item()) - 2.5 - ref) <= 1e-6 * ref
+        if off == 0:
+            # same gradient, fresh copies of the state: the same sum bit for bit
+            acc2 = torch.full((1,), 2.5, dtype=torch.float64, device=DEV)
+            ops.adamw_norm_(pb.clone(), mb.clone(), vb.clone(), gd, acc2, ws, step=t, **hp)
+            assert torch.equal(acc, acc2)
+    with pytest.raises(RuntimeError, match="workspace"):
+        ops.adamw_norm_(pb, mb, vb, gd, acc, ws[:1], step=4, **hp)
+
+
 def test_sumsq_and_clip():
     g = _seed(4)
     a = torch.randn(3_000_001, generator=g)

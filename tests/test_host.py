@@ -349,6 +349,21 @@ def test_library_exports_every_declared_symbol():
     assert lib.lz_version() == 1
 
 
+def test_adamw_norm_workspace_size():
+    """One float64 partial per 128-thread AdamW workgroup (4 elements per
+    thread) plus the 256 second-level sums; host arithmetic only."""
+    import lzhip._lib as L
+
+    if not L.LIB_PATH.exists():
+        pytest.skip("libllamazero_hip.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(L.LIB_PATH))
+    fn = lib.lz_adamw_norm_workspace
+    fn.restype, fn.argtypes = ctypes.c_int64, [ctypes.c_int64]
+    assert fn(0) == 0
+    for n in (1, 3, 4, 511, 512, 513, 1_100_048_384):
+        assert fn(n) == -(-(n // 4) // 128) + 256
+
+
 def test_library_defines_every_kernel_launch_stub():
     """Every kernel the library launches has its host launch stub: an undefined
     __device_stub__ symbol would only fail when the library is loaded."""
