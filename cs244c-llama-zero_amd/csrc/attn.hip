@@ -121,6 +121,18 @@ __device__ __forceinline__ f32x16_t mfma16(const bf16x8_t& a, const bf16x8_t& b,
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// x combined with the value of lane ^ 32 (both halves get the same result):
+// v_permlane32_swap exchanges the halves of two registers without an LDS
+// round trip.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ bf16x8_t lds_frag16(const char* p) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
 }
@@ -361,7 +373,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
           }
           mx = fmaxf(mx, s[t][r]);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = max_halves(mx);
       const float m_new = fmaxf(m, mx * c);
       const float nm = -m_new;
       float rs = 0.f;
@@ -373,7 +385,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
           s[t][r] = p;
           rs += p;
         }
-      rs += __shfl_xor(rs, 32, 64);
+      rs = sum_halves(rs);
       if (__builtin_amdgcn_read_exec() & __ballot(m_new != m)) {  // some lane's max moved
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
         l *= alpha;
@@ -695,7 +707,9 @@ __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, char* 
   for (int q = 0; q < kPer; ++q) {
     const int r = (wave * kPer + q) * kRowsPerLoad + lane / kChunks;
     const int c = (lane % kChunks) ^ tswz<HD>(r);
-    lds_dma16(rsrc, (uint32_t)((r * ld + c * 8) * 2), dst + (wave * kPer + q) * 1024);
+    const uint32_t voff = (uint32_t)((r * ld + c * 8) * 2);
+    if (q == 0) lz_dma16_first(rsrc, voff, 0, dst + (wave * kPer + q) * 1024);
+    else lds_dma16(rsrc, voff, dst + (wave * kPer + q) * 1024);
   }
 }
 
@@ -783,6 +797,11 @@ template <int HD, bool MASK, typename F>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[HD / 32], float& m, float& l,
                                                const TileOffsets<HD>& to, const char* Vt, float c, int lim, int half) {
   constexpr int BKV = 64;
+  // the V^T fragments of the first 16 keys, read now so that the first P.V
+  // MFMAs do not wait for LDS after the softmax
+  bf16x8_t vf[2][HD / 32];
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i) vf[0][i] = to.frag_t(Vt, 0, i);
   float mx = -INFINITY;
 #pragma unroll
   for (int t = 0; t < 2; ++t)
@@ -794,7 +813,7 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[H
       }
       mx = fmaxf(mx, s[t][r]);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = max_halves(mx);
   const float m_step = mx * c;
   if (__builtin_amdgcn_read_exec() & __ballot(m_step > m)) {  // some lane's max moved
     const float m_new = fmaxf(m, m_step);
@@ -816,19 +835,21 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16_t (&s)[2], f32x16_t (&o)[H
       s[t][r] = p;
       rs += p;
     }
-  rs += __shfl_xor(rs, 32, 64);
-  l += rs;
+  l += sum_halves(rs);
 #pragma unroll
   for (int ks = 0; ks < BKV / 16; ++ks) {
+    if (ks + 1 < BKV / 16)  // the next 16 keys' fragments while these MFMAs run
+#pragma unroll
+      for (int i = 0; i < HD / 32; ++i) vf[(ks + 1) & 1][i] = to.frag_t(Vt, ks + 1, i);
     const bf16x8_t pb = pack8<F>(s[ks >> 1], 8 * (ks & 1));
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i)
-      o[i] = mfma16<F>(to.frag_t(Vt, ks, i), pb, o[i]);
+      o[i] = mfma16<F>(vf[ks & 1][i], pb, o[i]);
   }
 }
 
 template <int HD, typename F>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_tile_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2, HD == 64 ? 4 : 2))) attn_fwd_tile_kernel(AttnArgs a) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int kTile = BKV * HD * 2;
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];  // K slots 0, 1; V slots 0, 1

@@ -99,6 +99,16 @@ __device__ __forceinline__ void lz_dma16(lz_v4i rsrc, uint32_t voff, uint32_t so
                :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0) : "memory");
 }
 
+// lz_dma16 for the first load after `rsrc` was formed: its SGPRs may have
+// just been written by v_readfirstlane, and a VALU write of an SGPR must be
+// followed by 5 wait states before a vector-memory instruction reads it (the
+// compiler pads for its own instructions, not for inline assembly).
+__device__ __forceinline__ void lz_dma16_first(lz_v4i rsrc, uint32_t voff, uint32_t soff, void* dst) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst;
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0) : "memory");
+}
+
 // 16-byte store with the nontemporal hint (global_store_dwordx4 ... nt): for
 // outputs a kernel writes once and does not read back, so that they do not
 // displace the operand rows the rest of the grid is still reading from L2.
