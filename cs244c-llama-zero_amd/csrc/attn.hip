@@ -1002,7 +1002,7 @@ __device__ __forceinline__ void dkdv_step(f32x16_t (&dk)[HD / 32], f32x16_t (&dv
       dp = mfma16<F>(to.frag(dOt, t, kk), to.frag(Vt, wave, kk), dp);
       // keeps the fragment reads next to their MFMAs: two waves per SIMD
       // hide the latency, and the register budget is 256
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (HD == 128) __builtin_amdgcn_sched_barrier(0);
     }
     // lane holds key column kvrow; query rows t*32 + 8*(r/4) + 4*half + r%4
 #pragma unroll
@@ -1030,7 +1030,7 @@ __device__ __forceinline__ void dkdv_step(f32x16_t (&dk)[HD / 32], f32x16_t (&dv
       for (int i = 0; i < HD / 32; ++i) {
         dv[i] = mfma16<F>(to.frag_t(dOt, ks, i), pb, dv[i]);
         dk[i] = mfma16<F>(to.frag_t(Qt, ks, i), dsb, dk[i]);
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (HD == 128) __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
@@ -1146,6 +1146,11 @@ __device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffse
       st = mfma16<F>(to.frag(Kt, t, kk), qf[kk], st);
       dpt = mfma16<F>(to.frag(Vt, t, kk), df[kk], dpt);
     }
+    // the K^T fragments of the first 16 keys, read before dS is formed so
+    // that the dQ MFMAs do not wait for LDS; the next 16 keys' during them
+    bf16x8_t kt[2][HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) kt[0][i] = to.frag_t(Kt, 2 * t, i);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       float p = __builtin_amdgcn_exp2f(fmaf(st[r], c, nl2));
@@ -1157,11 +1162,13 @@ __device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffse
     }
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
-      const int ks = 2 * t + kh;
+      if (kh == 0)
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i) kt[1][i] = to.frag_t(Kt, 2 * t + 1, i);
       const bf16x8_t dsb = pack8<F>(dpt, 8 * kh);
 #pragma unroll
       for (int i = 0; i < HD / 32; ++i)
-        dq[i] = mfma16<F>(to.frag_t(Kt, ks, i), dsb, dq[i]);
+        dq[i] = mfma16<F>(kt[kh][i], dsb, dq[i]);
     }
   }
 }
