@@ -21,6 +21,16 @@ constexpr int kThreads = 64 * kRowsPerBlock;
 template <typename T>
 struct Pack8;
 
+// 16-byte nontemporal load: the rows are read once.  Against plain loads,
+// on inputs that come from HBM as they do in a training step (a rotation of
+// buffers larger than the 256 MB Infinity Cache): backward with the residual
+// gradient 60.5 -> 57.1 us, forward 25.9 -> 24.7 us at [16384, 2048].
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+  typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+  const v4u_t t = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(p));
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+
 // 16-bit formats: T is the storage type (uint16_t = bf16, _Float16 = fp16),
 // F the format policy.
 template <typename T, typename F>
@@ -34,6 +44,7 @@ struct Pack8H {
   static __device__ __forceinline__ void load(const T* p, float (&r)[8]) {
     unpack(*reinterpret_cast<const uint4*>(p), r);
   }
+  static __device__ __forceinline__ void load_nt(const T* p, float (&r)[8]) { unpack(ld_nt16(p), r); }
   static __device__ __forceinline__ void store(T* p, const float (&r)[8]) {
     *reinterpret_cast<uint4*>(p) = make_uint4(F::pack2(r[0], r[1]), F::pack2(r[2], r[3]),
                                               F::pack2(r[4], r[5]), F::pack2(r[6], r[7]));
@@ -64,6 +75,7 @@ struct Pack8<float> {
     reinterpret_cast<float4*>(p)[1] = make_float4(r[4], r[5], r[6], r[7]);
   }
   static __device__ __forceinline__ void store_nt(float* p, const float (&r)[8]) { store(p, r); }
+  static __device__ __forceinline__ void load_nt(const float* p, float (&r)[8]) { load(p, r); }
 };
 
 // NC = number of 8-element chunks per lane; cols == NC * 512 at most, and the
@@ -84,7 +96,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(const T* __restri
   for (int j = 0; j < NC; ++j) {
     const int c = lane + 64 * j;
     if (c < nchunk) {
-      Pack8<T>::load(xr + 8 * c, v[j]);
+      Pack8<T>::load_nt(xr + 8 * c, v[j]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);
     }
@@ -137,9 +149,9 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd16_kernel(
     for (int j = 0; j < NC; ++j) {
       const int c = lane + 64 * j;
       if (c < nchunk) {
-        xn[j] = *reinterpret_cast<const uint4*>(x + row * ldx + 8 * c);
-        gn[j] = *reinterpret_cast<const uint4*>(dy + row * lddy + 8 * c);
-        if (dres) rn[j] = *reinterpret_cast<const uint4*>(dres + row * lddx + 8 * c);
+        xn[j] = ld_nt16(x + row * ldx + 8 * c);
+        gn[j] = ld_nt16(dy + row * lddy + 8 * c);
+        if (dres) rn[j] = ld_nt16(dres + row * lddx + 8 * c);
       }
     }
   };
@@ -398,7 +410,21 @@ __global__ void __launch_bounds__(256) dw_colsum_kernel(const float* __restrict_
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   if (c < cols) {
     int64_t p = rg;
-    // four partial rows in flight per thread
+    // sixteen partial rows in flight per thread (one round trip for the 512
+    // partial rows of a 2048-column backward), then four, then one; the
+    // additions follow p in every case, so the sum's order is fixed
+    for (; p + 15 * kColsumGroups < nparts; p += 16 * kColsumGroups) {
+      float4 v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const float4*>(part + (p + u * kColsumGroups) * cols + c);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        s.x += v[u].x;
+        s.y += v[u].y;
+        s.z += v[u].z;
+        s.w += v[u].w;
+      }
+    }
     for (; p + 3 * kColsumGroups < nparts; p += 4 * kColsumGroups) {
       float4 v[4];
 #pragma unroll
