@@ -203,32 +203,47 @@ def fit_sweep(dev: torch.device, max_batch: int, seq: int = 2048, steps: int = 2
     n_params = sum(h.meta.total_numel for h in engine._handle_order)
     total = torch.cuda.get_device_properties(dev).total_memory
     gen = torch.Generator(device=dev).manual_seed(0)
-    rows = []
-    b = 1
-    while b <= max_batch:
+
+    def run_one(b):
         log(f"7B fit sweep: micro-batch {b}")
+        batches = None
         try:
             torch.cuda.reset_peak_memory_stats(dev)
             batches = [torch.randint(0, cfg.vocab_size, (b, seq), device=dev, generator=gen)]
             el, losses = run_steps(model, engine, batches, steps=steps, warmup=warmup)
             peak = torch.cuda.max_memory_allocated(dev)
             flops = estimate_transformer_train_flops(cfg, b, seq, stage=0)
-            rows.append({"micro_batch": b, "tokens_per_s": b * seq * steps / el, "ms_per_step": el * 1000 / steps,
-                         "mfma_util": flops * steps / el / 1e12 / PEAK_BF16_TFLOPS,
-                         "peak_hbm_gib": peak / 2**30, "loss": losses[-1]})
-            log(f"  {rows[-1]['ms_per_step']:.0f} ms/step, {rows[-1]['tokens_per_s']:,.0f} tok/s, "
-                f"peak {rows[-1]['peak_hbm_gib']:.1f} GiB")
-        except torch.cuda.OutOfMemoryError:
-            rows.append({"micro_batch": b, "oom": True})
-            log("  out of memory")
-            break
+            row = {"micro_batch": b, "tokens_per_s": b * seq * steps / el, "ms_per_step": el * 1000 / steps,
+                   "mfma_util": flops * steps / el / 1e12 / PEAK_BF16_TFLOPS,
+                   "peak_hbm_gib": peak / 2**30, "loss": losses[-1]}
+            log(f"  {row['ms_per_step']:.0f} ms/step, {row['tokens_per_s']:,.0f} tok/s, "
+                f"peak {row['peak_hbm_gib']:.1f} GiB")
+            return row
         finally:
             batches = None
             engine.zero_grad()
             torch.cuda.empty_cache()
-        b *= 2
+
+    rows = sweep_batches(run_one, max_batch)
     return {"metric": "7B ZeRO-3 fit-to-memory sweep (world size 1, S=2048, bf16 + fp32 master)",
             "params": n_params, "device_memory_gib": total / 2**30, "sweep": rows}
+
+
+def sweep_batches(run_one, max_batch: int):
+    """run_one(b) for micro-batch b = 1, 2, 4, ... up to max_batch, one row
+    each; the first size that runs out of device memory ends the sweep with
+    the row {"micro_batch": b, "oom": True} (any other error propagates)."""
+    rows = []
+    b = 1
+    while b <= max_batch:
+        try:
+            rows.append(run_one(b))
+        except torch.cuda.OutOfMemoryError:
+            rows.append({"micro_batch": b, "oom": True})
+            log("  out of memory")
+            break
+        b *= 2
+    return rows
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_1b_zero3_traffic.md")

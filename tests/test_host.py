@@ -475,3 +475,31 @@ def test_loss_scaler_follows_torch_grad_scaler():
     off.step(fake, float("nan"))  # disabled: the step runs whatever the norm
     off.update()
     assert off.scale_value() == 1.0 and fake.steps == torch_steps + 1 and off.state_dict() == {}
+
+
+def test_fit_sweep_stops_at_the_first_out_of_memory():
+    """bench.py's 7B fit sweep doubles the micro-batch until a size runs out
+    of device memory: that size is recorded as {"oom": True} and the sweep
+    ends; the sizes before it keep their rows, and errors other than
+    out-of-memory are not swallowed (host logic only: the run is a stub)."""
+    import bench
+
+    seen = []
+
+    def run_one(b):
+        seen.append(b)
+        if b == 8:
+            raise torch.cuda.OutOfMemoryError("stub: out of memory")
+        return {"micro_batch": b, "tokens_per_s": 1.0}
+
+    rows = bench.sweep_batches(run_one, 64)
+    assert seen == [1, 2, 4, 8]
+    assert rows[:3] == [{"micro_batch": b, "tokens_per_s": 1.0} for b in (1, 2, 4)]
+    assert rows[3] == {"micro_batch": 8, "oom": True}
+    assert [r["micro_batch"] for r in bench.sweep_batches(lambda b: {"micro_batch": b}, 5)] == [1, 2, 4]
+
+    def broken(b):
+        raise ValueError("not a memory error")
+
+    with pytest.raises(ValueError):
+        bench.sweep_batches(broken, 4)
