@@ -73,10 +73,12 @@ int lz_sumsq(const void* x, int dtype, int64_t n, double* acc, void* stream);
  * for a step whose norm is reported but does not clip: the reference's
  * default max_grad_norm = 0.0 (zero/stage0_ddp.py:62-71, stage1/2/3 alike)
  * computes the norm and never uses it in the update, so the update's own read
- * of g serves both instead of a second pass (lz_sumsq + lz_adamw).  The sum
- * is taken in a fixed order (workgroup partials into `workspace`, then two
- * reduction launches), so it is the same from run to run;
- * lz_adamw_norm_workspace(n) gives the float64 words `workspace` must hold. */
+ * of g serves both instead of a second pass (lz_sumsq + lz_adamw).  With
+ * p, m, v, g (and p_out) 16-byte aligned the sum is taken in a fixed order
+ * (workgroup partials into `workspace`, then two reduction launches), so it
+ * is the same from run to run; otherwise the update takes the scalar kernel
+ * and the sum a separate lz_sumsq-style pass.  lz_adamw_norm_workspace(n)
+ * gives the float64 words `workspace` must hold. */
 int64_t lz_adamw_norm_workspace(int64_t n);
 int lz_adamw_norm(float* p, float* m, float* v, const void* g, int g_dtype, void* p_out, int p_out_dtype, int64_t n,
                   double lr, double beta1, double beta2, double eps, double weight_decay, int64_t step,
