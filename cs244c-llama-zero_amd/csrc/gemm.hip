@@ -1198,6 +1198,9 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
   const char* s2 = s1 + kWaveBytes;
   const int r0 = (wn & 1) ? TM / 2 : 0;
   uint16_t* out = static_cast<uint16_t*>(g.C) + n0 + (wn >> 1) * kHd;
+  // position of the wave's first row; later rows count up from it (one
+  // division per wave, not one per row)
+  const int64_t pos0 = (mrow0 + r0) % r.S;
 #pragma unroll
   for (int t = 0; t < (TM / 2) * kChunks / 64; ++t) {
     const int idx = t * 64 + lane, row = r0 + idx / kChunks, chunk = idx % kChunks;
@@ -1205,7 +1208,9 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
     const uint4 av = *reinterpret_cast<const uint4*>(s1 + off);
     const uint4 bv = *reinterpret_cast<const uint4*>(s2 + off);
     const int64_t m = mrow0 + row;
-    const int64_t tab = (m % r.S) * kHd + chunk * 8;
+    int64_t pos = pos0 + (row - r0);  // below pos0 + TM / 2
+    while (pos >= r.S) pos -= r.S;    // once at most for S >= TM / 2
+    const int64_t tab = pos * kHd + chunk * 8;
     const uint4 c1 = *reinterpret_cast<const uint4*>(r.cos + tab), c2 = *reinterpret_cast<const uint4*>(r.cos + tab + TN);
     const uint4 n1 = *reinterpret_cast<const uint4*>(r.sin + tab), n2 = *reinterpret_cast<const uint4*>(r.sin + tab + TN);
     const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
