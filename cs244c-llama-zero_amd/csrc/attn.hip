@@ -46,6 +46,7 @@ struct AttnArgs {
   int64_t lddo;
   const uint16_t* dot;  // dO^T [B,H,hd,S]
   const float* delta;   // [B,H,S] rowsum(dO*O)
+  float* delta_w;       // the same rows, written by the dQ kernel that computes them (with o as O)
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
@@ -1174,7 +1175,11 @@ __device__ __forceinline__ void dq_step(f32x16_t (&dq)[HD / 32], const TileOffse
 }
 
 // dQ on tiles: 128 queries per workgroup, 64-key steps up to the diagonal.
-template <int HD, typename F>
+// kDelta: delta = rowsum(dO * O) of the workgroup's queries is computed here
+// (from the dO fragments held in registers and the same columns of O, a.o)
+// and written to a.delta_w for the dK/dV kernel that runs next, instead of
+// read from a.delta.
+template <int HD, typename F, bool kDelta = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_bwd_dq_tile_kernel(AttnArgs a) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int kTile = BKV * HD * 2;
@@ -1207,7 +1212,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   }
   const float nl2 = -a.lse[((int64_t)b * H + h) * S + qc] * kLog2e;
-  const float Dq = a.delta[((int64_t)b * H + h) * S + qc];
+  float Dq;
+  if constexpr (kDelta) {
+    // each half of the wave holds half of the row's columns (8 of every 16)
+    const uint16_t* op = a.o + ((int64_t)b * S + qc) * a.ldo + (int64_t)h * HD + 8 * half;
+    float acc = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      const uint4 ov = *reinterpret_cast<const uint4*>(op + kk * 16);
+      const uint4 dv = __builtin_bit_cast(uint4, df[kk]);
+      const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2) {
+        acc = fmaf(F::to_f(ow[k2] & 0xffff), F::to_f(dw[k2] & 0xffff), acc);
+        acc = fmaf(F::to_f(ow[k2] >> 16), F::to_f(dw[k2] >> 16), acc);
+      }
+    }
+    Dq = sum_halves(acc);
+    if (qrow < S && half == 0) a.delta_w[((int64_t)b * H + h) * S + qrow] = Dq;
+  } else {
+    Dq = a.delta[((int64_t)b * H + h) * S + qc];
+  }
   f32x16_t dq[HD / 32];
 #pragma unroll
   for (int i = 0; i < HD / 32; ++i)
@@ -1925,7 +1950,8 @@ int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const 
                   int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
                   void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
                   int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin,
-                  int dtype, hipStream_t s, bool& rope_done);
+                  int dtype, hipStream_t s, bool& rope_done, const void* o = nullptr, int64_t ldo = 0,
+                  float* delta_w = nullptr);
 
 }  // namespace
 
@@ -1958,15 +1984,40 @@ LZ_EXPORT int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk
   return lz_rope(dk, dtype, lddk, B * S, S, KV, hd, rope_cos, rope_sin, 0, 1, stream);
 }
 
+// lz_attn_delta + lz_attn_bwd in one call for the LDS-tile kernels
+// (lz_attn_path 2): the dQ kernel computes delta = rowsum(dO * O) from the
+// dO rows it loads anyway and writes it to `delta` ([B, H, S] fp32, output),
+// then the dK/dV kernel reads it.  Other shapes are refused.
+LZ_EXPORT int lz_attn_bwd_with_o(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                 const void* o, int64_t ldo, const void* dout, int64_t lddo, const float* lse,
+                                 float* delta, void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
+                                 int64_t B, int64_t S, int64_t H, int64_t KV, int64_t hd, float scale,
+                                 const void* rope_cos, const void* rope_sin, int dtype, void* stream) {
+  int rc = check_shape(B, S, H, KV, hd);
+  if (rc) return rc;
+  LZ_REQUIRE(q && k && v && o && dout && lse && delta && dq && dk && dv, "lz_attn_bwd_with_o: null pointer");
+  LZ_REQUIRE(lz_aligned16(o) && ldo % 8 == 0 && ldo >= H * hd, "lz_attn_bwd_with_o: O rows must be 16-byte aligned");
+  LZ_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), "lz_attn_bwd_with_o: give both RoPE tables or neither");
+  LZ_REQUIRE(rope_cos == nullptr || (hd % 2 == 0 && ((reinterpret_cast<uintptr_t>(rope_cos) |
+                                                        reinterpret_cast<uintptr_t>(rope_sin)) & 7) == 0),
+             "lz_attn_bwd_with_o: RoPE needs an even head dim and 8-byte aligned tables");
+  bool rope_done = false;
+  return attn_bwd_impl(q, ldq, k, ldk, v, ldv, dout, lddo, lse, delta, nullptr, nullptr, nullptr, dq, lddq, dk, lddk,
+                       dv, lddv, B, S, H, KV, hd, scale, rope_cos, rope_sin, dtype, lz_stream(stream), rope_done, o,
+                       ldo, delta);
+}
+
 namespace {
 
 int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, const void* dout,
                   int64_t lddo, const float* lse, const float* delta, const void* qt, const void* kt, const void* dot,
                   void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
                   int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin,
-                  int dtype, hipStream_t s, bool& rope_done) {
+                  int dtype, hipStream_t s, bool& rope_done, const void* o, int64_t ldo, float* delta_w) {
   const bool mfma = mfma_ok(dtype, hd, ldq, ldk, ldv, lddo, q, k, v, dout) && lddq % 4 == 0 && lddk % 4 == 0 &&
                     lddv % 4 == 0;
+  LZ_REQUIRE(delta_w == nullptr || (mfma && S % 64 == 0),
+             "lz_attn_bwd_with_o: this shape takes the other kernels (use lz_attn_delta + lz_attn_bwd)");
   if (mfma && S % 64 == 0) {
     AttnArgs a{};
     a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
@@ -1980,6 +2031,30 @@ int attn_bwd_impl(const void* q, int64_t ldq, const void* k, int64_t ldk, const 
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.KV = (int)KV; a.scale = scale;
     const unsigned grid_kv = (unsigned)(lz_cdiv(S, 256) * B * KV);
     const unsigned grid_q = (unsigned)(lz_cdiv(S, 128) * B * H);
+    if (delta_w) {
+      // the dQ pass computes delta (rowsum(dO * O)) and runs first; dK/dV reads it
+      a.o = (uint16_t*)const_cast<void*>(o);
+      a.ldo = ldo;
+      a.delta_w = delta_w;
+      a.delta = delta_w;
+      if (dtype == LZ_F16) {
+        if (hd == 128) attn_bwd_dq_tile_kernel<128, FmtF16, true><<<grid_q, 256, 0, s>>>(a);
+        else attn_bwd_dq_tile_kernel<64, FmtF16, true><<<grid_q, 256, 0, s>>>(a);
+      } else {
+        if (hd == 128) attn_bwd_dq_tile_kernel<128, FmtBF16, true><<<grid_q, 256, 0, s>>>(a);
+        else attn_bwd_dq_tile_kernel<64, FmtBF16, true><<<grid_q, 256, 0, s>>>(a);
+      }
+      const int rc = lz_check_launch("lz_attn_bwd_with_o");
+      if (rc) return rc;
+      if (dtype == LZ_F16) {
+        if (hd == 128) attn_bwd_dkdv_wide_kernel<128, FmtF16><<<grid_kv, 512, 0, s>>>(a);
+        else attn_bwd_dkdv_wide_kernel<64, FmtF16><<<grid_kv, 512, 0, s>>>(a);
+      } else {
+        if (hd == 128) attn_bwd_dkdv_wide_kernel<128, FmtBF16><<<grid_kv, 512, 0, s>>>(a);
+        else attn_bwd_dkdv_wide_kernel<64, FmtBF16><<<grid_kv, 512, 0, s>>>(a);
+      }
+      return lz_check_launch("lz_attn_bwd_with_o");
+    }
     if (dtype == LZ_F16) {
       if (hd == 128) {
         attn_bwd_dkdv_wide_kernel<128, FmtF16><<<grid_kv, 512, 0, s>>>(a);

@@ -103,6 +103,13 @@ SIGNATURES = {
             _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
         ],
     ),
+    "lz_attn_bwd_with_o": (
+        _i32,
+        [
+            _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
+            _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _i32, _vp,
+        ],
+    ),
     "lz_dropout": (_i32, [_vp, _vp, _i64, _f32, _u64, _i32, _vp]),
     "lz_dropout_mask": (_i32, [_vp, _i64, _f32, _u64, _vp]),
     "lz_attn_bwd": (

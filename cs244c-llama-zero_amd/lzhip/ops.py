@@ -1097,6 +1097,18 @@ def attn_bwd(q2, k2, v2, o2, do2, lse, B, S, H, KV, hd, scale, dq2, dk2, dv2, qt
                 or rs.shape != rc.shape or not (rc.is_contiguous() and rs.is_contiguous()):
             raise ValueError("RoPE tables must be contiguous [>= S, hd] in the activation dtype")
     delta = torch.empty((B, H, S), dtype=torch.float32, device=q2.device)
+    strides = [_row_stride(t) for t in (q2, k2, v2, do2, o2, dq2, dk2, dv2)]
+    if (attn_path(q2.dtype, S, hd, *strides[:4]) == 2 and strides[4] % 8 == 0
+            and all(st % 4 == 0 for st in strides[5:])
+            and all(t.data_ptr() % 16 == 0 for t in (q2, k2, v2, o2, do2))):
+        # LDS-tile kernels: the dQ pass computes delta from the O and dO rows
+        # and runs first (no separate delta launch)
+        _lib.call("lz_attn_bwd_with_o", q2.data_ptr(), strides[0], k2.data_ptr(), strides[1], v2.data_ptr(),
+                  strides[2], o2.data_ptr(), strides[4], do2.data_ptr(), strides[3], lse.data_ptr(),
+                  delta.data_ptr(), dq2.data_ptr(), strides[5], dk2.data_ptr(), strides[6], dv2.data_ptr(),
+                  strides[7], B, S, H, KV, hd, float(scale), _ptr(rc), _ptr(rs), dtype_code(q2),
+                  stream_ptr(q2.device))
+        return
     _lib.call("lz_attn_delta", o2.data_ptr(), _row_stride(o2), do2.data_ptr(), _row_stride(do2), delta.data_ptr(),
               B, S, H, hd, dtype_code(o2), stream_ptr(q2.device))
     _lib.call("lz_attn_bwd", q2.data_ptr(), _row_stride(q2), k2.data_ptr(), _row_stride(k2), v2.data_ptr(),

@@ -333,6 +333,17 @@ int lz_attn_bwd(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
                 void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
                 int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin, int dtype,
                 void* stream);
+/* lz_attn_delta + lz_attn_bwd in one call, for the shapes lz_attn_path
+ * reports as 2 (LDS-tile kernels; others are refused): the same backward of
+ * model/llama.py:88-117, with delta = rowsum(dO * O) computed by the dQ
+ * kernel from the dO rows it loads anyway (O: [B*S, ldo] rows like dout, 16-byte
+ * aligned) and written to `delta` ([B, H, S] fp32, an output), which the
+ * dK/dV kernel then reads; saves the separate pass over O and dO. */
+int lz_attn_bwd_with_o(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                       const void* o, int64_t ldo, const void* dout, int64_t lddo, const float* lse, float* delta,
+                       void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, int64_t B, int64_t S,
+                       int64_t H, int64_t KV, int64_t hd, float scale, const void* rope_cos, const void* rope_sin,
+                       int dtype, void* stream);
 
 /* ---- dropout (model/llama.py:142,146 on the MLP's gated activations and
  * :175,213 on the token embeddings: nn.Dropout in training mode) ----

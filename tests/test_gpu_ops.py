@@ -765,6 +765,57 @@ def test_attention_delta(B, S, H, hd, pad):
     assert _rel_err(delta, want) < 1e-5
 
 
+@pytest.mark.parametrize("B,S,H,KV,hd,dtype", [(2, 256, 4, 2, 128, torch.bfloat16), (1, 192, 6, 2, 64, torch.bfloat16),
+                                               (1, 128, 4, 4, 64, torch.float16), (1, 320, 4, 2, 128, torch.bfloat16)])
+def test_attention_bwd_with_o_matches_separate_delta(B, S, H, KV, hd, dtype):
+    """lz_attn_bwd_with_o (delta computed by the dQ kernel, which then runs
+    before dK/dV) against lz_attn_delta + lz_attn_bwd on the same inputs:
+    delta to 1e-6 relative (the same fp32 sums over the head dim in another
+    order) and dq/dk/dv to the 16-bit format's rounding of that difference;
+    with RoPE tables both return the pre-RoPE gradients.  S = 320 leaves the
+    last 128-query block half outside the sequence."""
+    g = _seed(B * S * H + hd)
+    ld = (H + 2 * KV) * hd
+    qkv = torch.randn(B * S, ld, generator=g).to(dtype).to(DEV)
+    q, k, v = qkv[:, : H * hd], qkv[:, H * hd : (H + KV) * hd], qkv[:, (H + KV) * hd :]
+    scale = hd ** -0.5
+    o, lse = ops.attn_fwd(q, k, v, B, S, H, KV, hd, scale, None)
+    do = torch.randn(B * S, H * hd, generator=g).to(dtype).to(DEV)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32, device=DEV) / hd))
+    cos, sin = ops.rope_table(S, hd, inv, dtype)
+    st = ops.stream_ptr(q.device)
+    for tables in (None, (cos, sin)):
+        rc, rs = (None, None) if tables is None else (tables[0].data_ptr(), tables[1].data_ptr())
+        outs = []
+        for fused in (True, False):
+            dq = torch.empty(B * S, H * hd, dtype=dtype, device=DEV)
+            dk = torch.empty(B * S, KV * hd, dtype=dtype, device=DEV)
+            dv = torch.empty_like(dk)
+            delta = torch.full((B, H, S), float("nan"), dtype=torch.float32, device=DEV)
+            if fused:
+                _lib.call("lz_attn_bwd_with_o", q.data_ptr(), ld, k.data_ptr(), ld, v.data_ptr(), ld, o.data_ptr(),
+                          H * hd, do.data_ptr(), H * hd, lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), H * hd,
+                          dk.data_ptr(), KV * hd, dv.data_ptr(), KV * hd, B, S, H, KV, hd, scale, rc, rs,
+                          ops.dtype_code(q), st)
+            else:
+                _lib.call("lz_attn_delta", o.data_ptr(), H * hd, do.data_ptr(), H * hd, delta.data_ptr(), B, S, H, hd,
+                          ops.dtype_code(o), st)
+                _lib.call("lz_attn_bwd", q.data_ptr(), ld, k.data_ptr(), ld, v.data_ptr(), ld, do.data_ptr(), H * hd,
+                          lse.data_ptr(), delta.data_ptr(), None, None, None, dq.data_ptr(), H * hd, dk.data_ptr(),
+                          KV * hd, dv.data_ptr(), KV * hd, B, S, H, KV, hd, scale, rc, rs, ops.dtype_code(q), st)
+            outs.append((delta, dq, dk, dv))
+        (d1, *g1), (d2, *g2) = outs
+        assert bool(torch.isfinite(d1).all())
+        assert _rel_err(d1, d2) < 1e-6
+        for a, b in zip(g1, g2):
+            assert _rel_err(a, b) < 1e-2 and float((a.float() - b.float()).abs().max()) <= 0.02 * float(b.float().abs().max())
+    # shapes outside the tile kernels are refused, not taken another way
+    with pytest.raises(RuntimeError, match="lz_attn_bwd_with_o"):
+        _lib.call("lz_attn_bwd_with_o", q.data_ptr(), ld, k.data_ptr(), ld, v.data_ptr(), ld, o.data_ptr(), H * hd,
+                  do.data_ptr(), H * hd, lse.data_ptr(), d1.data_ptr(), g1[0].data_ptr(), H * hd, g1[1].data_ptr(),
+                  KV * hd, g1[2].data_ptr(), KV * hd, B, S - 1, H, KV, hd, scale, None, None, ops.dtype_code(q), st)
+
+
 @pytest.mark.parametrize("hd,S,H,KV", [(32, 130, 4, 2), (16, 64, 2, 1), (32, 1, 2, 2)])
 def test_attention_fp32_small_head(hd, S, H, KV):
     """Head dims 16 and 32 (a quad of lanes per row, rows staged through LDS) in
