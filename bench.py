@@ -631,10 +631,11 @@ def cpu_baseline(cfg, tokens: int = 2048, seq: int = 2048, warmup: int = 1):
 def gemm_sweep(dev: torch.device) -> dict:
     """The 1B step's GEMM shapes (16384 tokens) one product at a time, with HIP
     events around 20 launches each: forward x.W^T (with and without the
-    block's residual), input gradient dy.W and weight gradient dy^T.x, next to
-    hipBLASLt (torch.matmul) on the same operands; and the O-projection shape
-    at K = 64 ... 2048, whose intercept is the fixed per-launch cost (prologue,
-    epilogue, launch) and whose slope is the main loop's rate."""
+    block's residual), input gradient dy.W and weight gradient dy^T.x, each
+    next to hipBLASLt (torch.matmul) on the same operands; the 125M step's
+    weight gradients the same way; and the O-projection shape at K = 64 ...
+    2048, whose intercept is the fixed per-launch cost (prologue, epilogue,
+    launch) and whose slope is the main loop's rate."""
     from lzhip import ops
 
     bf = torch.bfloat16
@@ -650,12 +651,24 @@ def gemm_sweep(dev: torch.device) -> dict:
         r = {"forward": f / _time_ms(lambda: ops.gemm(x, w)),
              "input_grad": f / _time_ms(lambda: ops.gemm(dy, w, b_kmajor=False)),
              "weight_grad": f / _time_ms(lambda: ops.gemm(dy, x, a_kmajor=False, b_kmajor=False)),
-             "hipblaslt_forward": f / _time_ms(lambda: torch.matmul(x, w.t()))}
+             "hipblaslt_forward": f / _time_ms(lambda: torch.matmul(x, w.t())),
+             "hipblaslt_input_grad": f / _time_ms(lambda: torch.matmul(dy, w)),
+             "hipblaslt_weight_grad": f / _time_ms(lambda: torch.matmul(dy.t(), x))}
         if N == 2048:
             res = torch.randn(T, N, device=dev, generator=g).to(bf)
             r["forward_residual"] = f / _time_ms(lambda: ops.gemm(x, w, residual=res))
         out["products_TFLOP/s"][name] = {k: round(v, 1) for k, v in r.items()}
         del x, w, dy
+    out["weight_grad_125m_TFLOP/s"] = {}
+    for name, (M, N) in {"qkv": (1280, 768), "o": (768, 768), "gate|up": (4096, 768), "down": (768, 2048),
+                         "lm_head": (32000, 768)}.items():
+        dy = torch.randn(T, M, device=dev, generator=g).to(bf)
+        x = torch.randn(T, N, device=dev, generator=g).to(bf)
+        f = 2.0 * T * M * N / 1e9
+        out["weight_grad_125m_TFLOP/s"][name] = {
+            "ours": round(f / _time_ms(lambda: ops.gemm(dy, x, a_kmajor=False, b_kmajor=False)), 1),
+            "hipblaslt": round(f / _time_ms(lambda: torch.matmul(dy.t(), x)), 1)}
+        del dy, x
     N = 2048
     for K in (64, 128, 256, 512, 1024, 2048):
         x = torch.randn(T, K, device=dev, generator=g).to(bf)
