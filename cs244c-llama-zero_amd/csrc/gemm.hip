@@ -929,13 +929,13 @@ struct SwigluBwdIn {
   int64_t F;
 };
 
-enum { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2, kEpiSwiGLUBwd = 3 };
+enum { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2, kEpiSwiGLUBwd = 3, kEpiRope64 = 4 };
 
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut& o,
                                              f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t tn,
                                              char* smem, int lane, int wave);
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int HD>
 __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
                                            f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t n0,
                                            char* smem, int lane, int wave);
@@ -946,8 +946,8 @@ __device__ __forceinline__ void store_swiglu_bwd(const SwigluBwdIn& sb, f32x4_t 
 // One workgroup's 256 x BN tile of the direct-to-LDS GEMM (main loop, then
 // the epilogue).  kEpiSwiGLU: the tile's 256 B rows are 128 gate rows and the
 // matching 128 up rows of a [gate; up] weight (o.F rows apart), and the
-// epilogue writes silu(gate) * up.  kEpiRope: the epilogue rotates the tile's
-// columns below r.nrope as RoPE heads of 128.  kEpiSwiGLUBwd: the product is
+// epilogue writes silu(gate) * up.  kEpiRope / kEpiRope64: the epilogue
+// rotates the tile's columns below r.nrope as RoPE heads of 128 / 64.  kEpiSwiGLUBwd: the product is
 // the down projection's input gradient and the epilogue runs SwiGLU's
 // backward on it (sb).  BN = 192 (plain epilogue only): waves of 128x48.
 template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST, int kEpi, int BN = 256>
@@ -1042,8 +1042,8 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g, const SwigluOut
 
   if constexpr (kSwiGLU) {
     store_swiglu<BM, BN, WM, WN>(g, o, acc, m0, tn, smem, lane, wave);
-  } else if constexpr (kEpi == kEpiRope) {
-    store_rope<BM, BN, WM, WN>(g, rope, acc, m0, n0, smem, lane, wave);
+  } else if constexpr (kEpi == kEpiRope || kEpi == kEpiRope64) {
+    store_rope<BM, BN, WM, WN, kEpi == kEpiRope ? 128 : 64>(g, rope, acc, m0, n0, smem, lane, wave);
   } else if constexpr (kEpi == kEpiSwiGLUBwd) {
     store_swiglu_bwd<BM, BN, WM, WN>(sb, acc, m0, n0, smem, lane, wave);
   } else {
@@ -1073,9 +1073,10 @@ __global__ void __launch_bounds__(512) gemm_swiglu_kernel(GemmArgs g, SwigluOut 
 }
 
 // Fused QKV projection + RoPE on the q and k heads (both operands K-major,
-// M and N multiples of 256, head dim 128).
+// M and N multiples of 256, head dim HD = 128 or 64).
+template <int HD>
 __global__ void __launch_bounds__(512) gemm_rope_kernel(GemmArgs g, RopeIn r) {
-  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, kEpiRope>(g, SwigluOut{}, r, SwigluBwdIn{});
+  gemm_dma_tile<FmtBF16, 2, 4, true, true, 64, 2, HD == 128 ? kEpiRope : kEpiRope64>(g, SwigluOut{}, r, SwigluBwdIn{});
 }
 
 // Down projection input gradient + SwiGLU backward (dy K-major, W_down read
@@ -1177,12 +1178,40 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs& g, const SwigluOut&
 //   y1 = r(r(x1*c) + r(-x2*s)),  y2 = r(r(x2*c) + r(x1*s))
 // with the table row of the output row's position: the reference's bf16
 // per-op rounding, as the RoPE kernel computes it.
-template <int BM, int BN, int WM, int WN>
+// RoPE on 8 (x1, x2) pairs of bf16 values with their cos/sin table pieces
+// (c1, n1 at x1's columns, c2, n2 at x2's): each product rounded to bf16,
+// then the sum, as the reference's separate bf16 ops round them.
+__device__ __forceinline__ void rope_pair8(const uint4& av, const uint4& bv, const uint4& c1, const uint4& c2,
+                                           const uint4& n1, const uint4& n2, uint4& y1, uint4& y2) {
+  const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+  const uint32_t c1w[4] = {c1.x, c1.y, c1.z, c1.w}, c2w[4] = {c2.x, c2.y, c2.z, c2.w};
+  const uint32_t s1w[4] = {n1.x, n1.y, n1.z, n1.w}, s2w[4] = {n2.x, n2.y, n2.z, n2.w};
+  uint32_t o1w[4], o2w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float o1[2], o2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float a = bf2f((uint16_t)(aw[k] >> (16 * e))), b = bf2f((uint16_t)(bw[k] >> (16 * e)));
+      const float cc1 = bf2f((uint16_t)(c1w[k] >> (16 * e))), cc2 = bf2f((uint16_t)(c2w[k] >> (16 * e)));
+      const float ss1 = bf2f((uint16_t)(s1w[k] >> (16 * e))), ss2 = bf2f((uint16_t)(s2w[k] >> (16 * e)));
+      o1[e] = __fadd_rn(round_bf(__fmul_rn(a, cc1)), round_bf(__fmul_rn(-b, ss1)));
+      o2[e] = __fadd_rn(round_bf(__fmul_rn(b, cc2)), round_bf(__fmul_rn(a, ss2)));
+    }
+    o1w[k] = pack_bf16x2(o1[0], o1[1]);
+    o2w[k] = pack_bf16x2(o2[0], o2[1]);
+  }
+  y1 = make_uint4(o1w[0], o1w[1], o1w[2], o1w[3]);
+  y2 = make_uint4(o2w[0], o2w[1], o2w[2], o2w[3]);
+}
+
+template <int BM, int BN, int WM, int WN, int HD>
 __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
                                            f32x4_t (&acc)[BM / WM / 16][BN / WN / 16], int64_t m0, int64_t n0,
                                            char* smem, int lane, int wave) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
-  static_assert(WN == 4 && TN == 64, "a head of 128 is two 64-column waves");
+  static_assert(WN == 4 && TN == 64, "a head of 128 is two 64-column waves, a head of 64 one");
+  static_assert(HD == 128 || HD == 64, "heads of 128 or 64");
   if (n0 >= r.nrope) {
     store_tile<FmtBF16, 16, BM, BN, WM, WN>(g, acc, m0, n0, smem, lane, wave);
     return;
@@ -1192,6 +1221,31 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
   const int64_t mrow0 = m0 + wm * TM;
   char* st = smem + wave * kWaveBytes;
   park16<FmtBF16, 16, FM, FN, kRow>(acc, st, lane, 1.0f);
+  if constexpr (HD == 64) {
+    // A head is the wave's own 64 columns: x1 in chunks 0-3 and x2 in chunks
+    // 4-7 of each parked row, so the wave reads back only its own region.
+    asm volatile("" ::: "memory");
+    constexpr int kHalf = kChunks / 2;
+    uint16_t* out = static_cast<uint16_t*>(g.C) + n0 + wn * TN;
+    const int64_t pos0 = mrow0 % r.S;
+#pragma unroll
+    for (int t = 0; t < TM * kHalf / 64; ++t) {
+      const int idx = t * 64 + lane, row = idx / kHalf, chunk = idx % kHalf;
+      const uint4 av = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk));
+      const uint4 bv = *reinterpret_cast<const uint4*>(st + epi_off<kRow>(row, chunk + kHalf));
+      int64_t pos = pos0 + row;
+      while (pos >= r.S) pos -= r.S;
+      const int64_t tab = pos * HD + chunk * 8;
+      const uint4 c1 = *reinterpret_cast<const uint4*>(r.cos + tab), c2 = *reinterpret_cast<const uint4*>(r.cos + tab + HD / 2);
+      const uint4 n1 = *reinterpret_cast<const uint4*>(r.sin + tab), n2 = *reinterpret_cast<const uint4*>(r.sin + tab + HD / 2);
+      uint4 y1, y2;
+      rope_pair8(av, bv, c1, c2, n1, n2, y1, y2);
+      uint16_t* dst = out + (mrow0 + row) * g.ldc + chunk * 8;
+      st_nt16(dst, y1);
+      st_nt16(dst + HD / 2, y2);
+    }
+    return;
+  }
   __syncthreads();
   const int xw = wave & ~1;  // the wave holding x1 of this head
   const char* s1 = smem + xw * kWaveBytes;
@@ -1213,27 +1267,11 @@ __device__ __forceinline__ void store_rope(const GemmArgs& g, const RopeIn& r,
     const int64_t tab = pos * kHd + chunk * 8;
     const uint4 c1 = *reinterpret_cast<const uint4*>(r.cos + tab), c2 = *reinterpret_cast<const uint4*>(r.cos + tab + TN);
     const uint4 n1 = *reinterpret_cast<const uint4*>(r.sin + tab), n2 = *reinterpret_cast<const uint4*>(r.sin + tab + TN);
-    const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
-    const uint32_t c1w[4] = {c1.x, c1.y, c1.z, c1.w}, c2w[4] = {c2.x, c2.y, c2.z, c2.w};
-    const uint32_t s1w[4] = {n1.x, n1.y, n1.z, n1.w}, s2w[4] = {n2.x, n2.y, n2.z, n2.w};
-    uint32_t y1[4], y2[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float o1[2], o2[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float a = bf2f((uint16_t)(aw[k] >> (16 * e))), b = bf2f((uint16_t)(bw[k] >> (16 * e)));
-        const float cc1 = bf2f((uint16_t)(c1w[k] >> (16 * e))), cc2 = bf2f((uint16_t)(c2w[k] >> (16 * e)));
-        const float ss1 = bf2f((uint16_t)(s1w[k] >> (16 * e))), ss2 = bf2f((uint16_t)(s2w[k] >> (16 * e)));
-        o1[e] = __fadd_rn(round_bf(__fmul_rn(a, cc1)), round_bf(__fmul_rn(-b, ss1)));
-        o2[e] = __fadd_rn(round_bf(__fmul_rn(b, cc2)), round_bf(__fmul_rn(a, ss2)));
-      }
-      y1[k] = pack_bf16x2(o1[0], o1[1]);
-      y2[k] = pack_bf16x2(o2[0], o2[1]);
-    }
+    uint4 y1, y2;
+    rope_pair8(av, bv, c1, c2, n1, n2, y1, y2);
     uint16_t* dst = out + m * g.ldc + chunk * 8;
-    st_nt16(dst, make_uint4(y1[0], y1[1], y1[2], y1[3]));
-    st_nt16(dst + TN, make_uint4(y2[0], y2[1], y2[2], y2[3]));
+    st_nt16(dst, y1);
+    st_nt16(dst + TN, y2);
   }
 }
 
@@ -1409,6 +1447,8 @@ template __global__ void gemm_dma_n192_kernel<FmtBF16, true>(GemmArgs);
 template __global__ void gemm_dma_n192_kernel<FmtBF16, false>(GemmArgs);
 template __global__ void gemm_dma_n192_kernel<FmtF16, true>(GemmArgs);
 template __global__ void gemm_dma_n192_kernel<FmtF16, false>(GemmArgs);
+template __global__ void gemm_rope_kernel<128>(GemmArgs, RopeIn);
+template __global__ void gemm_rope_kernel<64>(GemmArgs, RopeIn);
 
 template <typename F, int WM, int WN, bool AK, bool BK, int DBK, int NST>
 int launch_dma(const GemmArgs& g, int splits, hipStream_t s) {
@@ -1655,10 +1695,11 @@ LZ_EXPORT int lz_gemm_swiglu_bwd(const void* dy, int64_t lddy, const void* w, in
 // the reference's cache is).  Every value equals lz_gemm (bf16 output)
 // followed by lz_rope on those columns.  Needs M % 256 == 0, N % 256 == 0,
 // nrope % 256 == 0, K % 64 == 0 and 16-byte aligned rows.
-LZ_EXPORT int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
-                           const void* cos_t, const void* sin_t, int64_t S, int64_t nrope, int64_t M, int64_t N,
-                           int64_t K, void* stream) {
+LZ_EXPORT int lz_gemm_rope_hd(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
+                              const void* cos_t, const void* sin_t, int64_t S, int64_t nrope, int64_t hd, int64_t M,
+                              int64_t N, int64_t K, void* stream) {
   LZ_REQUIRE(x && w && out && cos_t && sin_t, "lz_gemm_rope: null pointer");
+  LZ_REQUIRE(hd == 128 || hd == 64, "lz_gemm_rope: head dim %lld (needs 128 or 64)", (long long)hd);
   LZ_REQUIRE(M > 0 && N > 0 && K > 0 && S > 0 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0,
              "lz_gemm_rope: needs M %% 256, N %% 256 and K %% 64 == 0 (M %lld, N %lld, K %lld)", (long long)M,
              (long long)N, (long long)K);
@@ -1690,7 +1731,14 @@ LZ_EXPORT int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ld
   g.vec16 = 1;
   g.kper = K;
   g.slab = 0;
-  gemm_rope_kernel<<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(
-      g, RopeIn{(const uint16_t*)cos_t, (const uint16_t*)sin_t, S, nrope});
+  const RopeIn r{(const uint16_t*)cos_t, (const uint16_t*)sin_t, S, nrope};
+  if (hd == 128) gemm_rope_kernel<128><<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(g, r);
+  else gemm_rope_kernel<64><<<dim3((unsigned)tiles, 1), 512, 0, lz_stream(stream)>>>(g, r);
   return lz_check_launch("lz_gemm_rope");
+}
+
+LZ_EXPORT int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
+                           const void* cos_t, const void* sin_t, int64_t S, int64_t nrope, int64_t M, int64_t N,
+                           int64_t K, void* stream) {
+  return lz_gemm_rope_hd(x, ldx, w, ldw, out, ldo, cos_t, sin_t, S, nrope, 128, M, N, K, stream);
 }

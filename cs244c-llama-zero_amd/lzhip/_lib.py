@@ -74,6 +74,7 @@ SIGNATURES = {
     "lz_gemm_nt": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
     "lz_gemm_swiglu": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "lz_gemm_rope": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "lz_gemm_rope_hd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "lz_gemm_swiglu_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "lz_gemm": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _i64, _f32, _f32,
                        _vp, _i64, _vp]),

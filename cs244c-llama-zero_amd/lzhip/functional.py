@@ -357,7 +357,7 @@ class AttnProjFn(Function):
         w = fused_weight([wq, wk, wv])
         nrope = (n_heads + n_kv) * hd
         if ops.rope_fusable(h2, w, nrope, hd, cos):
-            qkv = ops.gemm_rope(h2, w, cos, sin, S, nrope)   # RoPE in the GEMM's epilogue
+            qkv = ops.gemm_rope(h2, w, cos, sin, S, nrope, hd)  # RoPE in the GEMM's epilogue
         else:
             qkv = _linear_fwd(h2, w)                         # [B*S, (H+2KV)*hd]
             ops.rope_(qkv, S, n_heads + n_kv, hd, cos, sin)  # q and k heads, in place

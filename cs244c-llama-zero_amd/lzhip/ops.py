@@ -647,7 +647,9 @@ def gemm_kernel_name(key) -> str:
     if code == "swiglu":
         return "gemm_swiglu_kernel"
     if code == "rope":
-        return "gemm_rope_kernel"
+        return "gemm_rope_kernel<128>"
+    if code == "rope64":
+        return "gemm_rope_kernel<64>"
     if code == "swiglu_bwd":
         return "gemm_swiglu_bwd_kernel"
     if code == "f32":
@@ -880,44 +882,46 @@ def gemm_swiglu_bwd(dy2: torch.Tensor, wd: torch.Tensor, gu: torch.Tensor,
 
 def rope_fusable(x2: torch.Tensor, w: torch.Tensor, nrope: int, hd: int, cos: torch.Tensor) -> bool:
     """Whether gemm_rope takes x2 [M, K] and w [N, K] with RoPE on the first
-    nrope columns: head dim 128, M, N and nrope multiples of 256, K % 64 == 0,
-    bf16, contiguous [>= S, 128] tables and 16-byte aligned rows."""
-    if hd != 128 or x2.dim() != 2 or w.dim() != 2 or x2.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+    nrope columns: head dim 128 or 64, M, N and nrope multiples of 256,
+    K % 64 == 0, bf16, contiguous [>= S, hd] tables and 16-byte aligned
+    rows."""
+    if hd not in (128, 64) or x2.dim() != 2 or w.dim() != 2 or x2.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         return False
     M, K = x2.shape
     N, k2 = w.shape
     if k2 != K or M % 256 or N % 256 or K % 64 or nrope % 256 or nrope > N or M == 0:
         return False
-    if cos.dtype != torch.bfloat16 or cos.dim() != 2 or cos.size(1) != 128 or not cos.is_contiguous():
+    if cos.dtype != torch.bfloat16 or cos.dim() != 2 or cos.size(1) != hd or not cos.is_contiguous():
         return False
     return all(t.stride(1) == 1 and _row_stride(t) % 8 == 0 and t.data_ptr() % 16 == 0 for t in (x2, w))
 
 
 def gemm_rope(x2: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, seq: int,
-              nrope: int) -> torch.Tensor:
+              nrope: int, hd: int = 128) -> torch.Tensor:
     """x2 . w^T ([M, N] bf16) with RoPE (rows b*S+s at position s) applied to
-    columns [0, nrope) as heads of 128, in one kernel.  Bit-identical to
-    gemm(x2, w) followed by rope_ on those columns."""
+    columns [0, nrope) as heads of hd (128 or 64), in one kernel.
+    Bit-identical to gemm(x2, w) followed by rope_ on those columns."""
     require_gpu(x2, w, cos, sin)
-    if not rope_fusable(x2, w, nrope, 128, cos) or sin.shape != cos.shape or not sin.is_contiguous():
+    if not rope_fusable(x2, w, nrope, hd, cos) or sin.shape != cos.shape or not sin.is_contiguous():
         raise ValueError(f"gemm_rope: unsupported shapes/layout x {tuple(x2.shape)}, w {tuple(w.shape)}")
     if cos.size(0) < seq:
         raise ValueError("RoPE table too short")
     M, K = x2.shape
     N = w.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x2.device)
+    key = (True, True, "rope" if hd == 128 else "rope64")
     probe = _gemm_probe
-    if probe is not None and not probe.wants((True, True, "rope")):
+    if probe is not None and not probe.wants(key):
         probe = None
     if probe is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
-    _lib.call("lz_gemm_rope", x2.data_ptr(), _row_stride(x2), w.data_ptr(), _row_stride(w), out.data_ptr(), N,
-              cos.data_ptr(), sin.data_ptr(), seq, nrope, M, N, K, stream_ptr(x2.device))
+    _lib.call("lz_gemm_rope_hd", x2.data_ptr(), _row_stride(x2), w.data_ptr(), _row_stride(w), out.data_ptr(), N,
+              cos.data_ptr(), sin.data_ptr(), seq, nrope, hd, M, N, K, stream_ptr(x2.device))
     if probe is not None:
         end.record()
-        probe.add(2.0 * M * N * K, start, end, (True, True, "rope"))
+        probe.add(2.0 * M * N * K, start, end, key)
     return out
 
 

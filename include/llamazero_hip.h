@@ -280,6 +280,13 @@ int lz_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, void*
  * 256, K % 64 == 0 and 16-byte aligned rows. */
 int lz_gemm_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo, const void* cos_t,
                  const void* sin_t, int64_t S, int64_t nrope, int64_t M, int64_t N, int64_t K, void* stream);
+/* lz_gemm_rope for heads of hd = 128 or 64 (the same call sites,
+ * model/llama.py:95-103, at the 125M model's head dim 64): tables
+ * [>= S, hd]; lz_gemm_rope is this with hd = 128.  Bit-identical to lz_gemm
+ * (bf16 out) followed by lz_rope on columns [0, nrope). */
+int lz_gemm_rope_hd(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
+                    const void* cos_t, const void* sin_t, int64_t S, int64_t nrope, int64_t hd, int64_t M, int64_t N,
+                    int64_t K, void* stream);
 /* Down projection input gradient fused with SwiGLU's backward
  * (model/llama.py:136-146: autograd of down_proj(silu(gate_proj x) *
  * up_proj x)): dm = dy.W_down (dy [M, K], W_down [K, F] row-major) meets

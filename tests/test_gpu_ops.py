@@ -449,22 +449,26 @@ def test_gemm_swiglu_bwd_fused_matches_unfused(M, F_, K, pad):
         ops.gemm_swiglu_bwd(dyd[:128], wdd, gud[:128])  # M not a multiple of 256
 
 
-@pytest.mark.parametrize("M,N,nrope,K,S", [(256, 512, 256, 64, 256), (512, 1024, 768, 192, 128), (768, 512, 512, 2048, 384)])
-def test_gemm_rope_fused_matches_unfused(M, N, nrope, K, S):
+@pytest.mark.parametrize("M,N,nrope,K,S,hd", [(256, 512, 256, 64, 256, 128), (512, 1024, 768, 192, 128, 128),
+                                               (768, 512, 512, 2048, 384, 128),
+                                               # head dim 64: the 125M layout (12 q + 4 k heads rotated, 4 v heads),
+                                               # and sequences shorter than a wave's 128 rows
+                                               (2048, 1280, 1024, 768, 1024, 64), (768, 1280, 1024, 768, 96, 64),
+                                               (256, 512, 256, 128, 64, 64)])
+def test_gemm_rope_fused_matches_unfused(M, N, nrope, K, S, hd):
     """The fused QKV GEMM + RoPE equals gemm followed by the RoPE kernel bit
     for bit (rotated q/k columns and the plain v columns), and the rotation
     matches the float64 oracle on the same bf16 product within bf16
     rounding."""
-    g = _seed(M + N + K)
+    g = _seed(M + N + K + hd)
     x = (0.5 * torch.randn(M, K, generator=g)).to(torch.bfloat16)
     w = (0.05 * torch.randn(N, K, generator=g)).to(torch.bfloat16)
     xd, wd = x.to(DEV), w.to(DEV)
-    hd = 128
     inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
     cos, sin = ops.rope_table(S, hd, inv.to(DEV), torch.bfloat16)
     ref = ops.gemm(xd, wd)
     ops.rope_(ref, S, nrope // hd, hd, cos, sin)
-    got = ops.gemm_rope(xd, wd, cos, sin, S, nrope)
+    got = ops.gemm_rope(xd, wd, cos, sin, S, nrope, hd)
     assert torch.equal(got.cpu(), ref.cpu())
     prod = (x.double() @ w.double().t()).view(M // S, S, N)
     heads = prod[:, :, :nrope].reshape(M // S, S, nrope // hd, hd).transpose(1, 2)
