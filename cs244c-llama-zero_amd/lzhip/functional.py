@@ -476,20 +476,26 @@ class MLPFn(Function):
         if dropout_p == 0.0 and ops.swiglu_bwd_fusable(dy2, wd, gu):
             # dm = dy . W_down goes straight into SwiGLU's backward in the
             # GEMM's epilogue (same bits as the two kernels, dm never stored).
-            # W_down's gradient runs beside it on a second stream: that
-            # kernel's epilogue phases are HBM-bound with the matrix cores
-            # idle, the weight gradient's main loop is the opposite (1B
-            # shapes: 752 -> 709 us for the pair; other layers' input and
-            # weight gradients run slower side by side, so they do not).
-            main = torch.cuda.current_stream(dy2.device)
-            side = _side_stream(dy2.device)
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
+            # An unsplit W_down gradient runs beside it on a second stream:
+            # that kernel's epilogue phases are HBM-bound with the matrix
+            # cores idle, the weight gradient's main loop is the opposite
+            # (1B shapes: 752 -> 709 us for the pair).  A split one (125M:
+            # 8 ways and a reduce) already fills the chip and measured no
+            # gain; other layers' input and weight gradients run slower
+            # side by side, so they do not.
+            if ctx.needs_input_grad[3] and ops.gemm_unsplit(wd.shape[0], wd.shape[1], dy2.shape[0], False, False):
+                main = torch.cuda.current_stream(dy2.device)
+                side = _side_stream(dy2.device)
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    _, dwd = _linear_bwd(dy2, m, wd, False, True, [wd])
+                dgu = ops.gemm_swiglu_bwd(dy2, wd, gu)
+                main.wait_stream(side)
+                if dwd is not None:
+                    dwd.record_stream(main)  # made on the side stream, read on this one
+            else:
+                dgu = ops.gemm_swiglu_bwd(dy2, wd, gu)
                 _, dwd = _linear_bwd(dy2, m, wd, False, ctx.needs_input_grad[3], [wd])
-            dgu = ops.gemm_swiglu_bwd(dy2, wd, gu)
-            main.wait_stream(side)
-            if dwd is not None:
-                dwd.record_stream(main)  # made on the side stream, read on this one
         else:
             dm, dwd = _linear_bwd(dy2, m, wd, True, ctx.needs_input_grad[3], [wd])
             if dropout_p > 0.0:

@@ -640,6 +640,11 @@ class LaunchProbe:
         return {k: self.summary(k) for k in {r[3] for r in self.records}}
 
 
+def gemm_unsplit(M: int, N: int, K: int, a_kmajor: bool, b_kmajor: bool) -> bool:
+    """Whether lz_gemm runs this product without splitting K."""
+    return int(_lib.load().lz_gemm_plan(M, N, K, int(a_kmajor), int(b_kmajor))) % 64 == 1
+
+
 def gemm_kernel_name(key) -> str:
     """Kernel name (as profilers print it, namespaces dropped) of a
     LaunchProbe key of a bf16 product."""

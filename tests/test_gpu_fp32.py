@@ -128,7 +128,7 @@ def test_fp32_model_vs_oracle(dim, H, KV, ffn, L, V, B, S, chunk):
     out.loss.backward()
     ref = OM.loss(P, _ocfg(cfg), ids, chunk_size=chunk)
     ref.backward()
-    assert abs(float(out.loss.detach()) - float(ref)) <= 1e-5 * abs(float(ref))
+    assert abs(float(out.loss.detach()) - float(ref.detach())) <= 1e-5 * abs(float(ref.detach()))
     worst = min((float(F.cosine_similarity(p.grad.double().cpu().view(-1), P[n].grad.view(-1), dim=0)), n)
                 for n, p in model.named_parameters())
     assert worst[0] >= 0.99999, worst
