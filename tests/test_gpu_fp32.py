@@ -170,7 +170,7 @@ def test_plumbing_fp32_100_steps_vs_oracle():
         for i in range(GA):
             ids = batches[(step - 1) * GA + i][:, :-1].contiguous().to(DEV)
             l = model(input_ids=ids, labels=ids, return_logits=False).loss
-            losses.append(float(l))
+            losses.append(float(l.detach()))
             (l / GA).backward()
             fl = free(input_ids=ids, labels=ids, return_logits=False).loss
             flosses.append(float(fl))

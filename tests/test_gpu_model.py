@@ -38,7 +38,7 @@ def _compare(model, P, ocfg, ids, chunk):
     out.loss.backward()
     ref = OM.loss(P, ocfg, ids, chunk_size=chunk)
     ref.backward()
-    loss, rloss = float(out.loss), float(ref)
+    loss, rloss = float(out.loss.detach()), float(ref.detach())
     assert abs(loss - rloss) <= 1e-2 * abs(rloss), (loss, rloss)
     worst = (1.0, "")
     for name, p in model.named_parameters():
@@ -118,7 +118,7 @@ def test_reference_golden_config_in_bf16():
     ids = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5, 8, 9, 7, 9, 3], [2, 7, 1, 8, 2, 8, 1, 8, 2, 8, 4, 5, 9, 0, 4, 5]])
     out = model(input_ids=ids.to(DEV), labels=ids.to(DEV), return_logits=False)
     assert out.logits is None
-    assert abs(float(out.loss) - 4.901787757873535) <= 1e-2 * 4.901787757873535
+    assert abs(float(out.loss.detach()) - 4.901787757873535) <= 1e-2 * 4.901787757873535
 
 
 def test_logits_and_causality():
@@ -224,7 +224,7 @@ def test_model_with_attention_mask(stage3):
         else:
             loss.backward()
             g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
-        return float(loss), g
+        return float(loss.detach()), g
 
     l0, g0 = run(None)
     l1, g1 = run(causal)
@@ -285,9 +285,9 @@ def test_model_dropout_vs_oracle(monkeypatch, dim, H, KV, S):
     drop = _oracle_drop(cfg, keys, B, S)
     ref = OM.loss(P, _ocfg(cfg), ids, drop=drop)
     ref.backward()
-    assert abs(float(out.loss) - float(ref)) <= 1e-2 * abs(float(ref))
+    assert abs(float(out.loss.detach()) - float(ref.detach())) <= 1e-2 * abs(float(ref.detach()))
     nodrop = OM.loss({k: v.detach() for k, v in P.items()}, _ocfg(cfg), ids)
-    assert abs(float(nodrop) - float(ref)) > 1e-4 * abs(float(ref))  # the masks matter
+    assert abs(float(nodrop) - float(ref.detach())) > 1e-4 * abs(float(ref.detach()))  # the masks matter
     for name, prm in model.named_parameters():
         cos = float(F.cosine_similarity(prm.grad.detach().double().cpu().view(-1), P[name].grad.view(-1), dim=0))
         assert cos >= 0.999, (name, cos)

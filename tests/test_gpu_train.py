@@ -122,7 +122,7 @@ def test_plumbing_100_steps_gradient_fidelity():
         for i in range(GA):
             ids = batches[(step - 1) * GA + i][:, :-1].contiguous().to(DEV)
             l = model(input_ids=ids, labels=ids, return_logits=False).loss
-            losses.append(float(l))
+            losses.append(float(l.detach()))
             (l / GA).backward()
         g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
         rel.append(abs(sum(losses) / GA - loss) / abs(loss))
