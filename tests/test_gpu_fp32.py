@@ -173,7 +173,7 @@ def test_plumbing_fp32_100_steps_vs_oracle():
             losses.append(float(l.detach()))
             (l / GA).backward()
             fl = free(input_ids=ids, labels=ids, return_logits=False).loss
-            flosses.append(float(fl))
+            flosses.append(float(fl.detach()))
             fl.backward(gradient=seed)
         sink.finish()
         opt.clip_grad_norm_(1.0)
