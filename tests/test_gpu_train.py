@@ -173,7 +173,7 @@ def test_fused_epilogues_30_steps_gradient_fidelity():
         l = model(input_ids=ids, labels=ids, return_logits=False).loss
         l.backward()
         g = torch.cat([p.grad.double().reshape(-1).cpu() for p in model.parameters()])
-        rel.append(abs(float(l) - loss) / abs(loss))
+        rel.append(abs(float(l.detach()) - loss) / abs(loss))
         cos.append(float(F.cosine_similarity(g, _flat_grad(grads, order), dim=0)))
 
     OE.train_reference(ocfg, P, iter(batches), steps=steps, grad_accum_steps=GA, lr=3e-4, betas=(0.9, 0.95),
@@ -372,7 +372,7 @@ def test_graphed_step_replays_match_eager():
             (loss / GA).backward()
         oa.clip_grad_norm_(1.0)
         oa.step()
-        ref_loss.append(float(loss))
+        ref_loss.append(float(loss.detach()))
         ref_master.append(masters(ma, oa).clone())
 
     mg, og = make(True)
