@@ -378,12 +378,12 @@ def test_graphed_step_replays_match_eager():
     mg, og = make(True)
     gs = GraphedTrainStep(mg, og, (B, S), GA, 1.0, DEV)
     for i in range(warm):
-        loss = float(gs.warmup(batches[i]))
+        loss = float(gs.warmup(batches[i]).detach())
         assert abs(loss - ref_loss[i]) <= 1e-4 * abs(ref_loss[i]), (i, loss, ref_loss[i])
     gs.capture()
     junk = torch.randn(512, 512, device=DEV)
     for i in range(warm, steps):
-        loss = float(gs(batches[i]))
+        loss = float(gs(batches[i]).detach())
         junk = torch.mm(junk, junk.t().contiguous()).tanh()
         torch.cuda.synchronize()
         upd = (ref_master[i] - ref_master[i - 1]).abs().max().item()
