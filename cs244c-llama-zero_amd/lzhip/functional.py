@@ -483,7 +483,9 @@ class MLPFn(Function):
             # 8 ways and a reduce) already fills the chip and measured no
             # gain; other layers' input and weight gradients run slower
             # side by side, so they do not.
-            if ctx.needs_input_grad[3] and ops.gemm_unsplit(wd.shape[0], wd.shape[1], dy2.shape[0], False, False):
+            # (one stream while a graph is being captured)
+            if (ctx.needs_input_grad[3] and not torch.cuda.is_current_stream_capturing()
+                    and ops.gemm_unsplit(wd.shape[0], wd.shape[1], dy2.shape[0], False, False)):
                 main = torch.cuda.current_stream(dy2.device)
                 side = _side_stream(dy2.device)
                 side.wait_stream(main)
