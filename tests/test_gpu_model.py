@@ -100,7 +100,7 @@ def test_fused_lm_head_loss_matches_unfused(chunk):
     la, lb = float(out_a.loss.detach()), float(out_b.loss.detach())
     assert abs(la - lb) <= 1e-6 * abs(lb), (la, lb)
     with torch.no_grad():  # the no-grad pass forms no gradients and gives the same loss
-        assert float(ma(input_ids=ids.to(DEV), labels=labels.to(DEV), return_logits=False).loss) == la
+        assert float(ma(input_ids=ids.to(DEV), labels=labels.to(DEV), return_logits=False).loss.detach()) == la
     for (n, pa), (_, pb) in zip(ma.named_parameters(), mb.named_parameters()):
         ga, gb = pa.grad.double().view(-1), pb.grad.double().view(-1)
         assert float(F.cosine_similarity(ga, gb, dim=0)) >= 0.9999, n
@@ -150,7 +150,7 @@ def test_activation_checkpointing_matches_plain():
     ids = torch.randint(0, 256, (2, 128), generator=torch.Generator().manual_seed(3)).to(DEV)
     l1 = m1(ids, labels=ids).loss
     l2 = m2(ids, labels=ids).loss
-    assert float(l1) == float(l2)
+    assert float(l1.detach()) == float(l2.detach())
     l1.backward()
     l2.backward()
     for (n, p1), (_, p2) in zip(m1.named_parameters(), m2.named_parameters()):
@@ -311,7 +311,7 @@ def test_model_dropout_replay_and_eval():
     l1 = m1(ids, labels=ids).loss
     torch.manual_seed(100)
     l2 = m2(ids, labels=ids).loss
-    assert float(l1) == float(l2)
+    assert float(l1.detach()) == float(l2.detach())
     l1.backward()
     l2.backward()
     for (n, p1), (_, p2) in zip(m1.named_parameters(), m2.named_parameters()):
@@ -322,5 +322,5 @@ def test_model_dropout_replay_and_eval():
     base = m0(ids, labels=ids).loss
     m1.eval()
     ev = m1(ids, labels=ids).loss
-    assert float(again) == float(l1) and float(other) != float(l1)
-    assert float(ev) == float(base) and float(ev) != float(l1)
+    assert float(again.detach()) == float(l1.detach()) and float(other.detach()) != float(l1.detach())
+    assert float(ev.detach()) == float(base.detach()) and float(ev.detach()) != float(l1.detach())
